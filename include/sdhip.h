@@ -1,0 +1,142 @@
+/*
+ * sdhip.h - C ABI of the MI355X (gfx950) engine for the strands-decider torso.
+ *
+ * This is the drop-in boundary for the reference crate's engine (mircodz/strands-decider-rs,
+ * src/engine.rs).  Each entry point below replaces one item of the reference's `Engine` API; the
+ * reference item is cited next to it.  A Rust `engine.rs` shim binds these 1:1 (see
+ * INTEGRATION.md); the crate's `Decider::new/load/ask/ask_all` (src/lib.rs:113-145) then run
+ * unchanged on top.
+ *
+ * Conventions (as in the reference):
+ *  - Functions returning int return 0 on success and nonzero on failure, writing a
+ *    NUL-terminated message into err[0..errlen) (the reference's `crate::Error(String)`).
+ *  - `sd_engine_forward` is synchronous and exclusive per engine (the reference's `&mut self`):
+ *    it returns after the device is idle.  One engine handle must not be used from two threads
+ *    at once.
+ *  - The engine owns weights, caches and activation buffers; a snapshot owns copies of the
+ *    prefix state until `sd_snapshot_free`, and must be freed before its engine; output memory
+ *    is caller-owned.
+ */
+#ifndef SDHIP_H
+#define SDHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Context capacity of the KV cache and RoPE table, in tokens (src/engine.rs:16 `CONTEXT`). */
+#define SD_CONTEXT 4096
+
+typedef struct sd_engine sd_engine;     /* src/engine.rs:104-132 `Engine` */
+typedef struct sd_snapshot sd_snapshot; /* src/engine.rs:81-87 `Snapshot` */
+typedef struct sd_head sd_head;         /* src/head.rs:11-14 `Head` */
+
+/* Layer kinds of `Config::layer_types` (src/engine.rs:243-247). */
+enum { SD_LINEAR_ATTENTION = 0, SD_FULL_ATTENTION = 1, SD_ADAPTER = 2 };
+
+/* The torso fields of `model::Config` (src/model.rs:31-47). */
+typedef struct {
+    size_t hidden_size, intermediate_size, n_layers;
+    const uint8_t* layer_types; /* n_layers entries: SD_LINEAR_ATTENTION / SD_FULL_ATTENTION / SD_ADAPTER */
+    size_t num_attention_heads, num_key_value_heads, head_dim, rotary_dim;
+    size_t linear_num_key_heads, linear_key_head_dim, linear_value_head_dim;
+    double rope_theta;
+    const double* unrotate; /* nullable; hidden_size entries (`Config::unrotate`) */
+} sd_config;
+
+/* One manifest tensor, `model::Tensor` (src/model.rs:58-83). */
+typedef struct {
+    const char* name;
+    uint64_t offset, bytes;
+    uint32_t N, K, bits, group, asym;
+    int32_t had; /* online Hadamard size, -1 when absent (rejected, as in src/engine.rs:248-250) */
+} sd_tensor;
+
+/* The embedding rows file, `model::Embed` (src/model.rs:92-103), rows already in GPU layout. */
+typedef struct {
+    const char* rows_path;
+    uint64_t vocab, row_bytes;
+    size_t n_parts;
+    const char* const* part_names; /* e.g. "embed.q", "embed.s" */
+    const uint64_t* part_bytes;    /* bytes per row of each part */
+} sd_embed;
+
+/* `Engine::load(dir, &Manifest)` (src/engine.rs:175-303): uploads the shards (shard i holds the
+ * manifest bytes [shard_starts[i], shard_starts[i] + shard_bytes[i])), the embedding parts, and
+ * allocates the recurrent state, conv history and K/V cache. */
+int sd_engine_load(const sd_config* cfg, const sd_tensor* tensors, size_t n_tensors, const char* const* shard_paths,
+                   const uint64_t* shard_starts, const uint64_t* shard_bytes, size_t n_shards, const sd_embed* embed,
+                   sd_engine** out, char* err, size_t errlen);
+
+/* Drop of `Engine`. */
+void sd_engine_free(sd_engine* e);
+
+/* `Engine::hidden_size` (src/engine.rs:305-307). */
+size_t sd_engine_hidden_size(const sd_engine* e);
+
+/* `Engine::adapter` (src/engine.rs:107-108): the device in use, for display. */
+const char* sd_engine_adapter(const sd_engine* e);
+
+/* `Engine::forward(ids, rows, cache, keep, timed)` (src/engine.rs:529-662).
+ * Runs the torso on ids[0..n), continuing from `cache` (nullable prefix snapshot).  Writes the
+ * final hidden rows `rows` (indices into ids) to hidden_out[n_rows * hidden_size] (f32, in the
+ * head's basis after the optional unrotate).  gpu_ms (nullable) receives the device time when
+ * `timed`, NaN otherwise.  With `keep`, *snap_out receives a snapshot of the prefix + ids. */
+int sd_engine_forward(sd_engine* e, const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows,
+                      const sd_snapshot* cache, int keep, int timed, float* hidden_out, double* gpu_ms,
+                      sd_snapshot** snap_out, char* err, size_t errlen);
+
+/* `Snapshot::len` (src/engine.rs:82): prefix + forwarded tokens. */
+size_t sd_snapshot_len(const sd_snapshot* s);
+
+/* Drop of `Snapshot`. */
+void sd_snapshot_free(sd_snapshot* s);
+
+/* `Engine::profile(ids)` (src/engine.rs:668-711): device ms per kernel label, slowest first.
+ * Fills up to `cap` (label, ms) pairs; *n_out receives the number of labels.  Labels are static
+ * strings owned by the library. */
+int sd_engine_profile(sd_engine* e, const uint32_t* ids, size_t n, const char** labels, double* ms, size_t cap,
+                      size_t* n_out, char* err, size_t errlen);
+
+/* `Head::load(bytes)` (src/head.rs:25-52): head.safetensors, all tensors F32. */
+int sd_head_load(const uint8_t* bytes, size_t len, sd_head** out, char* err, size_t errlen);
+void sd_head_free(sd_head* h);
+
+/* `Head::probs(hidden, d, temperature)` (src/head.rs:66-77): hidden = [options..., answer] rows;
+ * probs_out receives n_rows - 1 option probabilities. */
+int sd_head_probs(const sd_head* h, const float* hidden, size_t n_rows, size_t d, double temperature,
+                  double* probs_out, char* err, size_t errlen);
+
+/* The engine half of `Decider::run` (src/lib.rs:183-199) on token ids: one question is a single
+ * forward of state ++ question; several share one forward of the state (keep = true) and continue
+ * from its snapshot.  options[i][0..n_options[i]) are option token indices into question i;
+ * probs_out receives sum(n_options) probabilities, question by question. */
+int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_state, size_t n_questions,
+               const uint32_t* const* q_ids, const size_t* q_lens, const size_t* const* options,
+               const size_t* n_options, const double* temperatures, double* probs_out, char* err, size_t errlen);
+
+/* ---- kernel-level entry points on device buffers (per-configuration benchmarks and tests) ---- */
+
+/* Y[M,N] f16 = A[M,K] f16 . deq(W)^T, W int4 group-32 symmetric in the model layout
+ * ([N][K/32] blocks of 4 u32, scales [N][K/32] f16): the reference's matmul_gemv/matmul_tiled
+ * (src/kernels.rs:590-709).  exact = 1 selects the GEMV's f32 dequant, 0 the tiled f16 dequant;
+ * cfg < 0 picks the kernel configuration by M. */
+int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, int N, int K, int exact, int cfg,
+                 void* stream, char* err, size_t errlen);
+
+/* One gated-delta-net recurrence, the reference's Gdn kernel (src/kernels.rs:257-372), on device
+ * buffers: qkv [L][2*H*dk + H*dv] f32, a/b gates f16 in big [L][stride] at a_off + h / b_off + h,
+ * negA[H], dt_bias[H] f32; state [H][dk][dv] f32 (read when load_state, always written);
+ * o [L][H*dv] f32. */
+int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off, const void* negA, const void* dtb,
+              int L, int H, int dk, int dv, void* state, int load_state, void* o, void* stream, char* err,
+              size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDHIP_H */

@@ -1,0 +1,316 @@
+"""Python host binding of the MI355X engine (libsdhip.so, C ABI in include/sdhip.h).
+
+Mirrors the reference crate's engine API (src/engine.rs): `Engine.load(dir)` (Engine::load,
+175-303), `hidden_size` (305-307), `adapter`, `forward(ids, rows, cache, keep, timed)` -> `Output`
+(529-662), `profile(ids)` (668-711) and `Snapshot` (81-87); the pointer head `Head` (src/head.rs)
+and `ask_ids`, the engine half of `Decider::run` (src/lib.rs:183-199).  It is the same binding a
+Rust `engine.rs` shim makes over the C ABI, used here by the tests and bench.py.
+
+There is no fallback: if libsdhip.so is missing or fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import model as _model
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsdhip.so")
+CONTEXT = 4096
+
+SYMBOLS = [
+    "sd_engine_load", "sd_engine_free", "sd_engine_hidden_size", "sd_engine_adapter", "sd_engine_forward",
+    "sd_snapshot_len", "sd_snapshot_free", "sd_engine_profile", "sd_head_load", "sd_head_free", "sd_head_probs",
+    "sd_ask_ids", "sd_op_matmul", "sd_op_gdn",
+]
+
+
+class EngineError(RuntimeError):
+    """The reference's `crate::Error` (src/lib.rs:23-30)."""
+
+
+class sd_config(C.Structure):
+    _fields_ = [
+        ("hidden_size", C.c_size_t), ("intermediate_size", C.c_size_t), ("n_layers", C.c_size_t),
+        ("layer_types", C.POINTER(C.c_uint8)),
+        ("num_attention_heads", C.c_size_t), ("num_key_value_heads", C.c_size_t), ("head_dim", C.c_size_t),
+        ("rotary_dim", C.c_size_t), ("linear_num_key_heads", C.c_size_t), ("linear_key_head_dim", C.c_size_t),
+        ("linear_value_head_dim", C.c_size_t), ("rope_theta", C.c_double), ("unrotate", C.POINTER(C.c_double)),
+    ]
+
+
+class sd_tensor(C.Structure):
+    _fields_ = [
+        ("name", C.c_char_p), ("offset", C.c_uint64), ("bytes", C.c_uint64), ("N", C.c_uint32), ("K", C.c_uint32),
+        ("bits", C.c_uint32), ("group", C.c_uint32), ("asym", C.c_uint32), ("had", C.c_int32),
+    ]
+
+
+class sd_embed(C.Structure):
+    _fields_ = [
+        ("rows_path", C.c_char_p), ("vocab", C.c_uint64), ("row_bytes", C.c_uint64), ("n_parts", C.c_size_t),
+        ("part_names", C.POINTER(C.c_char_p)), ("part_bytes", C.POINTER(C.c_uint64)),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded libsdhip.so; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise EngineError(f"{LIB_PATH} is missing: build it with `make -C strands-decider-rs_amd` "
+                              "(or __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        vp, sz, i32, err = C.c_void_p, C.c_size_t, C.c_int, C.c_char_p
+        L.sd_engine_load.argtypes = [C.POINTER(sd_config), C.POINTER(sd_tensor), sz, C.POINTER(C.c_char_p),
+                                     C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), sz, C.POINTER(sd_embed),
+                                     C.POINTER(vp), err, sz]
+        L.sd_engine_free.argtypes = [vp]
+        L.sd_engine_hidden_size.argtypes = [vp]
+        L.sd_engine_hidden_size.restype = sz
+        L.sd_engine_adapter.argtypes = [vp]
+        L.sd_engine_adapter.restype = C.c_char_p
+        L.sd_engine_forward.argtypes = [vp, vp, sz, vp, sz, vp, i32, i32, vp, C.POINTER(C.c_double), C.POINTER(vp),
+                                        err, sz]
+        L.sd_snapshot_len.argtypes = [vp]
+        L.sd_snapshot_len.restype = sz
+        L.sd_snapshot_free.argtypes = [vp]
+        L.sd_engine_profile.argtypes = [vp, vp, sz, C.POINTER(C.c_char_p), C.POINTER(C.c_double), sz,
+                                        C.POINTER(sz), err, sz]
+        L.sd_head_load.argtypes = [vp, sz, C.POINTER(vp), err, sz]
+        L.sd_head_free.argtypes = [vp]
+        L.sd_head_probs.argtypes = [vp, vp, sz, sz, C.c_double, vp, err, sz]
+        L.sd_ask_ids.argtypes = [vp, vp, vp, sz, sz, C.POINTER(vp), vp, C.POINTER(vp), vp, vp, vp, err, sz]
+        L.sd_op_matmul.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, err, sz]
+        L.sd_op_gdn.argtypes = [vp, vp, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, err, sz]
+        for name in SYMBOLS:
+            if name not in ("sd_engine_free", "sd_snapshot_free", "sd_head_free", "sd_engine_hidden_size",
+                            "sd_engine_adapter", "sd_snapshot_len"):
+                getattr(L, name).restype = i32
+        _lib = L
+    return _lib
+
+
+def _call(fn, *args):
+    buf = C.create_string_buffer(1024)
+    rc = fn(*args, buf, len(buf))
+    if rc != 0:
+        raise EngineError(buf.value.decode(errors="replace"))
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class Snapshot:
+    """The torso state after a prefix (src/engine.rs:81-87); continue with Engine.forward(cache=)."""
+
+    def __init__(self, handle, engine):
+        self._h, self._engine = handle, engine
+
+    @property
+    def len(self) -> int:
+        return lib().sd_snapshot_len(self._h)
+
+    def free(self):
+        if self._h:
+            lib().sd_snapshot_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        # A snapshot must be freed before its engine; the engine keeps a reference to live ones.
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class Output:
+    """src/engine.rs:89-96."""
+    hidden: np.ndarray  # [len(rows), d] f32
+    d: int
+    gpu_ms: float | None
+    snapshot: Snapshot | None
+
+
+class Engine:
+    def __init__(self, handle, manifest):
+        self._h = handle
+        self.manifest = manifest
+        self._snaps = []
+
+    @staticmethod
+    def load(model_dir: str, manifest: _model.Manifest | None = None) -> "Engine":
+        """src/engine.rs:175-303: read the manifest, upload shards and the embedding."""
+        m = manifest or _model.read_manifest(model_dir)
+        c = m.config
+        kinds = []
+        for k in c.layer_types:
+            if k not in _model.LAYER_KIND:
+                raise EngineError(f"unsupported layer type {k}")
+            kinds.append(_model.LAYER_KIND[k])
+        lt = (C.c_uint8 * len(kinds))(*kinds)
+        unrot = (C.c_double * len(c.unrotate))(*c.unrotate) if c.unrotate else None
+        cfg = sd_config(c.hidden_size, c.intermediate_size, len(kinds), lt, c.num_attention_heads,
+                        c.num_key_value_heads, c.head_dim, c.rotary_dim, c.linear_num_key_heads,
+                        c.linear_key_head_dim, c.linear_value_head_dim, c.rope_theta, unrot)
+        names = list(m.tensors)
+        ts = (sd_tensor * len(names))()
+        keep = []
+        for i, n in enumerate(names):
+            t = m.tensors[n]
+            b = n.encode()
+            keep.append(b)
+            ts[i] = sd_tensor(b, t.offset, t.bytes, t.N, t.K, t.bits, t.group, int(t.asym),
+                              -1 if t.had is None else int(t.had))
+        for s in m.shards:
+            if s.wire is not None:
+                raise EngineError(f"{s.path}: packed (wire) shards are a download format; convert them first")
+        paths = [os.path.join(model_dir, _model.shard_file(i)).encode() for i in range(len(m.shards))]
+        cpaths = (C.c_char_p * len(paths))(*paths)
+        starts = (C.c_uint64 * len(m.shards))(*[s.start for s in m.shards])
+        sizes = (C.c_uint64 * len(m.shards))(*[s.bytes for s in m.shards])
+        e = m.embed
+        if e is None:
+            raise EngineError("manifest has no embedding")
+        if e.u8 or e.wire_row_bytes is not None:
+            raise EngineError("packed (wire) embedding rows are a download format; convert them first")
+        pn = [p[0].encode() for p in e.parts]
+        emb = sd_embed(os.path.join(model_dir, e.rows).encode(), e.vocab, e.row_bytes, len(pn),
+                       (C.c_char_p * len(pn))(*pn), (C.c_uint64 * len(pn))(*[p[1] for p in e.parts]))
+        h = C.c_void_p()
+        _call(lib().sd_engine_load, C.byref(cfg), ts, len(names), cpaths, starts, sizes, len(m.shards),
+              C.byref(emb), C.byref(h))
+        return Engine(h, m)
+
+    def hidden_size(self) -> int:
+        return lib().sd_engine_hidden_size(self._h)
+
+    @property
+    def adapter(self) -> str:
+        return lib().sd_engine_adapter(self._h).decode()
+
+    def forward(self, ids, rows, cache: Snapshot | None = None, keep: bool = False, timed: bool = False) -> Output:
+        """src/engine.rs:529-662."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        rows_a = np.ascontiguousarray(rows, dtype=np.uintp)
+        d = self.hidden_size()
+        hidden = np.empty((len(rows_a), d), np.float32)
+        ms = C.c_double(math.nan)
+        snap = C.c_void_p()
+        _call(lib().sd_engine_forward, self._h, _ptr(ids), len(ids), _ptr(rows_a), len(rows_a),
+              cache._h if cache is not None else None, int(keep), int(timed), _ptr(hidden), C.byref(ms),
+              C.byref(snap) if keep else None)
+        s = None
+        if keep:
+            s = Snapshot(snap, self)
+            self._snaps.append(s)
+        return Output(hidden, d, ms.value if timed else None, s)
+
+    def profile(self, ids):
+        """src/engine.rs:668-711: [(label, ms)], slowest first."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        cap = 64
+        labels = (C.c_char_p * cap)()
+        ms = (C.c_double * cap)()
+        n = C.c_size_t()
+        _call(lib().sd_engine_profile, self._h, _ptr(ids), len(ids), labels, ms, cap, C.byref(n))
+        return [(labels[i].decode(), ms[i]) for i in range(min(n.value, cap))]
+
+    def free(self):
+        if self._h:
+            for s in self._snaps:
+                s.free()
+            self._snaps = []
+            lib().sd_engine_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Head:
+    """src/head.rs: the pointer head, CPU f64."""
+
+    def __init__(self, handle):
+        self._h = handle
+
+    @staticmethod
+    def load(data: bytes) -> "Head":
+        h = C.c_void_p()
+        buf = (C.c_uint8 * len(data)).from_buffer_copy(data)
+        _call(lib().sd_head_load, buf, len(data), C.byref(h))
+        return Head(h)
+
+    def probs(self, hidden: np.ndarray, d: int, temperature: float) -> np.ndarray:
+        hidden = np.ascontiguousarray(hidden, dtype=np.float32)
+        n = hidden.size // d
+        out = np.empty(n - 1, np.float64)
+        _call(lib().sd_head_probs, self._h, _ptr(hidden), n, d, float(temperature), _ptr(out))
+        return out
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().sd_head_free(self._h)
+                self._h = None
+        except Exception:
+            pass
+
+
+def ask_ids(engine: Engine, head: Head, state, questions, options, temperatures):
+    """The engine half of Decider::run (src/lib.rs:183-199) over token ids: one list of option
+    probabilities per question."""
+    st = np.ascontiguousarray(state, dtype=np.uint32)
+    qs = [np.ascontiguousarray(q, dtype=np.uint32) for q in questions]
+    ops = [np.ascontiguousarray(o, dtype=np.uintp) for o in options]
+    nq = len(qs)
+    qptr = (C.c_void_p * nq)(*[q.ctypes.data for q in qs])
+    qlen = np.array([len(q) for q in qs], np.uintp)
+    optr = (C.c_void_p * nq)(*[o.ctypes.data for o in ops])
+    nopt = np.array([len(o) for o in ops], np.uintp)
+    temps = np.ascontiguousarray(temperatures, dtype=np.float64)
+    out = np.empty(int(nopt.sum()), np.float64)
+    _call(lib().sd_ask_ids, engine._h, head._h, _ptr(st), len(st), nq, qptr, _ptr(qlen), optr, _ptr(nopt),
+          _ptr(temps), _ptr(out))
+    res, o = [], 0
+    for n in nopt:
+        res.append(out[o:o + n])
+        o += n
+    return res
+
+
+def load_decider(model_dir: str):
+    """Engine + Head + decider settings of a model directory (the engine half of Decider::load,
+    src/lib.rs:120-134; tokenizer and prompt rendering stay with the caller)."""
+    import json
+    eng = Engine.load(model_dir)
+    with open(os.path.join(model_dir, "head.safetensors"), "rb") as f:
+        head = Head.load(f.read())
+    with open(os.path.join(model_dir, "hobson_config.json")) as f:
+        cfg = json.load(f)
+    return eng, head, cfg
+
+
+# ---- kernel-level entry points (device pointers as ints; stream handle as int or None) ----------
+
+def op_matmul(A, Wq, Sc, Y, M, N, K, exact=False, cfg=-1, stream=None):
+    _call(lib().sd_op_matmul, C.c_void_p(A), C.c_void_p(Wq), C.c_void_p(Sc), C.c_void_p(Y), M, N, K, int(exact), cfg,
+          C.c_void_p(stream) if stream else None)
+
+
+def op_gdn(qkv, big, stride, a_off, b_off, negA, dtb, L, H, dk, dv, state, load_state, o, stream=None):
+    _call(lib().sd_op_gdn, C.c_void_p(qkv), C.c_void_p(big), stride, a_off, b_off, C.c_void_p(negA), C.c_void_p(dtb),
+          L, H, dk, dv, C.c_void_p(state), int(load_state), C.c_void_p(o), C.c_void_p(stream) if stream else None)

@@ -1,0 +1,208 @@
+// extern "C" entry points declared in include/sdhip.h.  Every call catches C++ exceptions and
+// reports them through (err, errlen), the C form of the reference's `crate::Error(String)`.
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <mutex>
+
+#include "engine.h"
+#include "head.h"
+
+namespace {
+
+void put_err(char* err, size_t errlen, const char* msg) {
+    if (!err || errlen == 0) return;
+    std::strncpy(err, msg, errlen - 1);
+    err[errlen - 1] = '\0';
+}
+
+template <class F>
+int guarded(char* err, size_t errlen, F&& f) {
+    try {
+        f();
+        if (err && errlen) err[0] = '\0';
+        return 0;
+    } catch (const std::exception& e) {
+        put_err(err, errlen, e.what());
+    } catch (...) {
+        put_err(err, errlen, "unknown error");
+    }
+    return 1;
+}
+
+sd::Engine* E(sd_engine* e) { return reinterpret_cast<sd::Engine*>(e); }
+const sd::Engine* E(const sd_engine* e) { return reinterpret_cast<const sd::Engine*>(e); }
+sd::Snapshot* S(sd_snapshot* s) { return reinterpret_cast<sd::Snapshot*>(s); }
+const sd::Snapshot* S(const sd_snapshot* s) { return reinterpret_cast<const sd::Snapshot*>(s); }
+const sd::Head* Hd(const sd_head* h) { return reinterpret_cast<const sd::Head*>(h); }
+
+// Device workspace for the kernel-level entry points (grown on demand, kept until exit).
+struct OpWs {
+    std::mutex mu;
+    sd::GemmWs gemm;
+    float* gdn = nullptr;
+    size_t gdn_floats = 0;
+};
+OpWs& op_ws() {
+    static OpWs w;
+    return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sd_engine_load(const sd_config* cfg, const sd_tensor* tensors, size_t n_tensors, const char* const* shard_paths,
+                   const uint64_t* shard_starts, const uint64_t* shard_bytes, size_t n_shards, const sd_embed* embed,
+                   sd_engine** out, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!out) throw sd::Error("sd_engine_load: null output");
+        auto e = std::make_unique<sd::Engine>();
+        e->load(cfg, tensors, n_tensors, shard_paths, shard_starts, shard_bytes, n_shards, embed);
+        *out = reinterpret_cast<sd_engine*>(e.release());
+    });
+}
+
+void sd_engine_free(sd_engine* e) { delete E(e); }
+
+size_t sd_engine_hidden_size(const sd_engine* e) { return e ? (size_t)E(e)->cfg.d : 0; }
+
+const char* sd_engine_adapter(const sd_engine* e) { return e ? E(e)->adapter.c_str() : ""; }
+
+int sd_engine_forward(sd_engine* e, const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows,
+                      const sd_snapshot* cache, int keep, int timed, float* hidden_out, double* gpu_ms,
+                      sd_snapshot** snap_out, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!e || (!ids && n) || (!rows && n_rows) || (!hidden_out && n_rows)) throw sd::Error("sd_engine_forward: null argument");
+        if (keep && !snap_out) throw sd::Error("sd_engine_forward: keep needs snap_out");
+        sd::Snapshot* snap = nullptr;
+        E(e)->forward(ids, n, rows, n_rows, S(cache), keep != 0, timed != 0, hidden_out, gpu_ms, keep ? &snap : nullptr);
+        if (snap_out) *snap_out = reinterpret_cast<sd_snapshot*>(snap);
+    });
+}
+
+size_t sd_snapshot_len(const sd_snapshot* s) { return s ? S(s)->len : 0; }
+
+void sd_snapshot_free(sd_snapshot* s) { delete S(s); }
+
+int sd_engine_profile(sd_engine* e, const uint32_t* ids, size_t n, const char** labels, double* ms, size_t cap,
+                      size_t* n_out, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!e || !ids) throw sd::Error("sd_engine_profile: null argument");
+        const auto by = E(e)->profile(ids, n);
+        for (size_t i = 0; i < by.size() && i < cap; i++) {
+            labels[i] = by[i].first;
+            ms[i] = by[i].second;
+        }
+        if (n_out) *n_out = by.size();
+    });
+}
+
+int sd_head_load(const uint8_t* bytes, size_t len, sd_head** out, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!bytes || !out) throw sd::Error("sd_head_load: null argument");
+        auto h = std::make_unique<sd::Head>();
+        h->load(bytes, len);
+        *out = reinterpret_cast<sd_head*>(h.release());
+    });
+}
+
+void sd_head_free(sd_head* h) { delete reinterpret_cast<sd::Head*>(h); }
+
+int sd_head_probs(const sd_head* h, const float* hidden, size_t n_rows, size_t d, double temperature,
+                  double* probs_out, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!h || !hidden || !probs_out) throw sd::Error("sd_head_probs: null argument");
+        const auto p = Hd(h)->probs(hidden, n_rows, d, temperature);
+        std::memcpy(probs_out, p.data(), p.size() * sizeof(double));
+    });
+}
+
+int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_state, size_t n_questions,
+               const uint32_t* const* q_ids, const size_t* q_lens, const size_t* const* options,
+               const size_t* n_options, const double* temperatures, double* probs_out, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!e || !h || !probs_out) throw sd::Error("sd_ask_ids: null argument");
+        if (n_questions == 0) throw sd::Error("ask at least one question");
+        sd::Engine* eng = E(e);
+        const size_t d = eng->cfg.d;
+        size_t out_off = 0;
+        for (size_t i = 0; i < n_questions; i++)
+            if (q_lens[i] == 0) throw sd::Error("question " + std::to_string(i) + " has no tokens");
+        auto answer = [&](size_t i, const std::vector<size_t>& rows, const std::vector<float>& hidden) {
+            const auto p = Hd(h)->probs(hidden.data(), rows.size(), d, temperatures[i]);
+            std::memcpy(probs_out + out_off, p.data(), p.size() * sizeof(double));
+            out_off += p.size();
+        };
+        if (n_questions == 1) {
+            // src/lib.rs:185-190: one forward of state ++ question.
+            std::vector<uint32_t> ids(state, state + n_state);
+            ids.insert(ids.end(), q_ids[0], q_ids[0] + q_lens[0]);
+            std::vector<size_t> rows;
+            for (size_t k = 0; k < n_options[0]; k++) rows.push_back(n_state + options[0][k]);
+            rows.push_back(ids.size() - 1);
+            std::vector<float> hidden(rows.size() * d);
+            eng->forward(ids.data(), ids.size(), rows.data(), rows.size(), nullptr, false, false, hidden.data(), nullptr, nullptr);
+            answer(0, rows, hidden);
+            return;
+        }
+        // src/lib.rs:192-198: the state once, each question from its snapshot.
+        sd::Snapshot* prefix = nullptr;
+        eng->forward(state, n_state, nullptr, 0, nullptr, true, false, nullptr, nullptr, &prefix);
+        std::unique_ptr<sd::Snapshot> hold(prefix);
+        for (size_t i = 0; i < n_questions; i++) {
+            std::vector<size_t> rows(options[i], options[i] + n_options[i]);
+            rows.push_back(q_lens[i] - 1);
+            std::vector<float> hidden(rows.size() * d);
+            eng->forward(q_ids[i], q_lens[i], rows.data(), rows.size(), prefix, false, false, hidden.data(), nullptr, nullptr);
+            answer(i, rows, hidden);
+        }
+    });
+}
+
+int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, int N, int K, int exact, int cfg,
+                 void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!A || !Wq || !Sc || !Y) throw sd::Error("sd_op_matmul: null argument");
+        if (cfg >= sd::gemm_w4_configs()) throw sd::Error("sd_op_matmul: no configuration " + std::to_string(cfg));
+        OpWs& w = op_ws();
+        std::lock_guard<std::mutex> lock(w.mu);
+        if (!w.gemm.part) {
+            w.gemm.part_elems = size_t(32) << 20;
+            w.gemm.cnt_elems = 65536;
+            SD_HIP(hipMalloc(&w.gemm.part, w.gemm.part_elems * 4));
+            SD_HIP(hipMalloc(&w.gemm.cnt, w.gemm.cnt_elems * 4));
+            SD_HIP(hipMemset(w.gemm.cnt, 0, w.gemm.cnt_elems * 4));
+        }
+        sd::gemm_w4(static_cast<const sd::f16*>(A), static_cast<const uint32_t*>(Wq), static_cast<const sd::f16*>(Sc),
+                    static_cast<sd::f16*>(Y), M, N, K, exact != 0, w.gemm, static_cast<hipStream_t>(stream), cfg);
+    });
+}
+
+int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off, const void* negA, const void* dtb,
+              int L, int H, int dk, int dv, void* state, int load_state, void* o, void* stream, char* err,
+              size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!qkv || !big || !negA || !dtb || !state || !o) throw sd::Error("sd_op_gdn: null argument");
+        if (L < 1 || L > SD_CONTEXT) throw sd::Error("sd_op_gdn: L must be 1 to 4096");
+        if (dk != 128 || dv != 128) throw sd::Error("sd_op_gdn: only 128-wide key/value heads are supported");
+        const sd::GdnShape s{H, dk, dv, stride, a_off, b_off, 0, 2 * H * dk + H * dv};
+        OpWs& w = op_ws();
+        std::lock_guard<std::mutex> lock(w.mu);
+        const size_t need = sd::gdn_ws_floats(L, s);
+        if (need > w.gdn_floats) {
+            if (w.gdn) SD_HIP(hipFree(w.gdn));
+            w.gdn = nullptr;
+            SD_HIP(hipMalloc(&w.gdn, need * 4));
+            w.gdn_floats = need;
+        }
+        sd::GdnWs ws;
+        sd::gdn_ws_carve(w.gdn, L, s, ws);
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        sd::gdn_prep(static_cast<const float*>(qkv), static_cast<const sd::f16*>(big), s, static_cast<const float*>(negA),
+                     static_cast<const float*>(dtb), L, ws, nullptr, st);
+        sd::gdn_scan(s, L, ws, static_cast<float*>(state), nullptr, load_state, static_cast<float*>(o), st);
+    });
+}
+
+}  // extern "C"

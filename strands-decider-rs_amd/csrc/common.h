@@ -1,0 +1,107 @@
+// Shared definitions of the gfx950 engine: vector types, error checks, and the launcher
+// functions each kernel file exports to the engine (engine.cpp drives every kernel through these).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace sd {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define SD_HIP(call)                                                                                   \
+    do {                                                                                               \
+        hipError_t e_ = (call);                                                                        \
+        if (e_ != hipSuccess)                                                                          \
+            throw ::sd::Error(std::string(#call) + ": " + hipGetErrorString(e_) + " (" + __FILE__ + ":" + \
+                              std::to_string(__LINE__) + ")");                                         \
+    } while (0)
+
+#define SD_CHECK(cond, msg)                          \
+    do {                                             \
+        if (!(cond)) throw ::sd::Error(std::string(msg)); \
+    } while (0)
+
+// Launch-time bookkeeping shared with the engine: every kernel launch goes through `launched`
+// so a failed launch is reported at its call site.
+void launched(const char* what);
+
+// ---- quantized matmul (gemm.hip) -----------------------------------------------------------
+// Y[M,N] f16 = A[M,K] f16 . deq(W[N,K])^T with W int4 group-32 symmetric in the reference's
+// layout ([N][K/32] blocks of 4 u32, element e in word e/8 at bits 4(e%8), value (q-8)*scale,
+// scales [N][K/32] f16).  `exact` selects the f32-dequant arithmetic of the reference's GEMV
+// path (used for M <= 20), otherwise the f16 dequant of its tiled path.  `ws`/`cnt` are the
+// split-K workspace (f32) and self-resetting tile counters (zeroed once at allocation).
+struct GemmWs {
+    float* part = nullptr;
+    size_t part_elems = 0;
+    uint32_t* cnt = nullptr;
+    size_t cnt_elems = 0;
+};
+void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, int M, int N, int K, bool exact,
+             const GemmWs& ws, hipStream_t st, int force_cfg = -1);
+// Number of selectable kernel configurations (for tests and tuning sweeps).
+int gemm_w4_configs();
+
+// ---- elementwise / norms (elem.hip) ----------------------------------------------------------
+void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f16* Bi, int d, int bits,
+           int group, bool asym, float* x, hipStream_t st);
+// x[rows[r]] += y (if y), h[r] = rmsnorm(x[rows[r]]) * w -> f16 (h16) or f32 (h32); rows null = identity.
+void add_norm(float* x, const f16* y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16,
+              float* h32, hipStream_t st);
+void silu_mul(const f16* big, int L, int I, f16* mid, hipStream_t st);
+void add_bias(f16* y, int L, int N, const float* c, hipStream_t st);
+void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);
+
+// ---- gated delta net (gdn.hip) ---------------------------------------------------------------
+struct GdnShape {
+    int H, DK, DV, stride, a_off, b_off, z_off, C;
+};
+// Workspace for the chunked recurrence, sized for `cap` tokens.
+struct GdnWs {
+    float* w = nullptr;   // [chunks][H][64][DK]  T (beta k e^G)
+    float* u = nullptr;   // [chunks][H][64][DV]  T (beta v)
+    float* qg = nullptr;  // [chunks][H][64][DK]  qn e^G
+    float* kg = nullptr;  // [chunks][H][64][DK]  kn e^(G_last - G)
+    float* qk = nullptr;  // [chunks][H][64][64]  (qn . kn) e^(G_i - G_j), i >= j
+    float* gl = nullptr;  // [chunks][H]          e^(G_last)
+};
+size_t gdn_ws_floats(int cap, const GdnShape& s);
+void gdn_ws_carve(float* base, int cap, const GdnShape& s, GdnWs& ws);
+void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out,
+               hipStream_t st);
+// hist (nullable) is updated from big afterwards (the reference's hist_update).
+void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
+              const GdnWs& ws, f16* hist, hipStream_t st);
+// lu = device [L, P, ctx, has_cache] (the state is loaded when has_cache); with lu null,
+// load_default decides.
+void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
+              hipStream_t st);
+void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st);
+
+// ---- attention (attn.hip) --------------------------------------------------------------------
+struct AttnShape {
+    int HQ, HK, HD, RD, stride, ctx;
+};
+void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* kw, const float* rope, int L,
+             const uint32_t* lu, f16* Q, f16* Kc, f16* Vc, hipStream_t st);
+// Workspace (floats) of the key-split path for up to `rows` query rows and 8 splits.
+size_t attn_ws_floats(int rows, const AttnShape& s);
+// ks = number of key splits (1: no workspace needed; ks > 1 needs rows = L in the workspace).
+void attention_split(const f16* Q, const f16* Kc, const f16* Vc, const f16* big, const AttnShape& s, int L,
+                     const uint32_t* lu, int ks, float* ws, f16* out, hipStream_t st);
+
+}  // namespace sd

@@ -1,0 +1,146 @@
+// Row-wise and elementwise kernels: embedding gather, residual add + RMSNorm, SiLU gate,
+// adapter bias, and a fill used instead of hipMemsetAsync (safe inside captured graphs).
+#include "common.h"
+
+namespace sd {
+namespace {
+
+// Quant code of element e of block `blk` (src/kernels.rs:63-70).
+__device__ __forceinline__ uint32_t qcode(const uint32_t* __restrict__ Q, size_t blk, int e, int bits) {
+    if (bits == 4) return (Q[blk * 4 + (e >> 3)] >> (4 * (e & 7))) & 15u;
+    uint32_t lo = (Q[blk * bits + (e >> 4)] >> (2 * (e & 15))) & 3u;
+    if (bits == 3) lo |= ((Q[blk * 3 + 2] >> e) & 1u) << 2;
+    return lo;
+}
+
+// x[t, :] = dequantized row ids[t] (src/kernels.rs:63-89).  One thread per 32-element block.
+__global__ void k_embed(const uint32_t* __restrict__ ids, int L, const uint32_t* __restrict__ Q,
+                        const f16* __restrict__ S, const f16* __restrict__ Bi, int d, int bits, int group, int asym,
+                        float* __restrict__ x) {
+    const int t = blockIdx.y;
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    const int nb = d >> 5;
+    if (t >= L || b >= nb) return;
+    const size_t blk = (size_t)ids[t] * nb + b;
+    const size_t gi = group == 32 ? blk : blk / (size_t)(group >> 5);
+    const float sc = (float)S[gi];
+    const float bi = asym ? (float)Bi[gi] : 0.f;
+    const float off = (float)(1 << (bits - 1));
+    float* out = x + (size_t)t * d + b * 32;
+#pragma unroll 8
+    for (int e = 0; e < 32; e++) {
+        const float q = (float)qcode(Q, blk, e, bits);
+        out[e] = asym ? q * sc + bi : (q - off) * sc;
+    }
+}
+
+// One workgroup (256 threads) per output row; D = d / 256 values per thread.
+template <int D>
+__global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f16* __restrict__ y,
+                                                  const float* __restrict__ w, const uint32_t* __restrict__ rows,
+                                                  f16* __restrict__ h16, float* __restrict__ h32) {
+    constexpr int d = D * 256;
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const size_t row = rows ? rows[r] : (size_t)r;
+    float* xr = x + row * d;
+    float v[D];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+        const int c = threadIdx.x + 256 * i;
+        float a = xr[c];
+        if (y) {
+            a += (float)y[row * d + c];
+            xr[c] = a;
+        }
+        v[i] = a;
+        ss += a * a;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / sqrtf(tot / (float)d + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+        const int c = threadIdx.x + 256 * i;
+        const float o = v[i] * inv * w[c];
+        if (h16) h16[(size_t)r * d + c] = (f16)o;
+        else h32[(size_t)r * d + c] = o;
+    }
+}
+
+// mid[t, j] = f16(silu(g) * u), big[t] = [g | u] (src/kernels.rs:123-135).  8 values per thread.
+__global__ void k_silu_mul(const f16* __restrict__ big, int L, int I, f16* __restrict__ mid) {
+    const size_t i8 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i8 >= (size_t)L * I) return;
+    const size_t t = i8 / I, j = i8 % I;
+    const f16x8 gv = *reinterpret_cast<const f16x8*>(big + t * 2 * I + j);
+    const f16x8 uv = *reinterpret_cast<const f16x8*>(big + t * 2 * I + I + j);
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float g = (float)gv[e], u = (float)uv[e];
+        o[e] = (f16)(g / (1.0f + expf(-g)) * u);
+    }
+    *reinterpret_cast<f16x8*>(mid + i8) = o;
+}
+
+__global__ void k_add_bias(f16* __restrict__ y, size_t n, int N, const float* __restrict__ c) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = (f16)((float)y[i] + c[i % N]);
+}
+
+__global__ void k_fill_u32(uint32_t* __restrict__ p, size_t n, uint32_t v) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+}  // namespace
+
+void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f16* Bi, int d, int bits, int group,
+           bool asym, float* x, hipStream_t st) {
+    SD_CHECK(d % 32 == 0 && (bits == 2 || bits == 3 || bits == 4) && group % 32 == 0 && group > 0,
+             "embed: unsupported format");
+    const int nb = d / 32;
+    hipLaunchKernelGGL(k_embed, dim3((nb + 63) / 64, L), dim3(64), 0, st, ids, L, Q, S, Bi, d, bits, group,
+                       (int)asym, x);
+    launched("embed");
+}
+
+void add_norm(float* x, const f16* y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16, float* h32,
+              hipStream_t st) {
+    if (nrows == 0) return;
+    switch (d) {
+#define SD_CASE(D) \
+    case D * 256: hipLaunchKernelGGL(k_add_norm<D>, dim3(nrows), dim3(256), 0, st, x, y, w, rows, h16, h32); break;
+        SD_CASE(1) SD_CASE(2) SD_CASE(3) SD_CASE(4) SD_CASE(5) SD_CASE(6) SD_CASE(8) SD_CASE(10) SD_CASE(12)
+        SD_CASE(16) SD_CASE(20) SD_CASE(24) SD_CASE(32)
+#undef SD_CASE
+        default: throw Error("add_norm: hidden size " + std::to_string(d) + " is not supported");
+    }
+    launched("add_norm");
+}
+
+void silu_mul(const f16* big, int L, int I, f16* mid, hipStream_t st) {
+    SD_CHECK(I % 8 == 0, "silu_mul: intermediate size must be a multiple of 8");
+    const size_t n8 = (size_t)L * I / 8;
+    hipLaunchKernelGGL(k_silu_mul, dim3((n8 + 255) / 256), dim3(256), 0, st, big, L, I, mid);
+    launched("silu_mul");
+}
+
+void add_bias(f16* y, int L, int N, const float* c, hipStream_t st) {
+    const size_t n = (size_t)L * N;
+    hipLaunchKernelGGL(k_add_bias, dim3((n + 255) / 256), dim3(256), 0, st, y, n, N, c);
+    launched("add_bias");
+}
+
+void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st) {
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_fill_u32, dim3((n + 255) / 256), dim3(256), 0, st, p, n, v);
+    launched("fill");
+}
+
+}  // namespace sd

@@ -1,0 +1,592 @@
+// The torso engine on one MI355X: weights resident in HBM, one dispatch plan per token length
+// captured as a hipGraph, prefix snapshots as device-to-device copies.
+// Reference: src/engine.rs (Engine::load 175-303, plan 396-524, forward 529-662, profile 668-711).
+#include "engine.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+namespace sd {
+
+void launched(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error(std::string("launching ") + what + ": " + hipGetErrorString(e));
+}
+
+namespace {
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+bool env_off(const char* name) {
+    const char* v = std::getenv(name);
+    return v && std::strcmp(v, "0") == 0;
+}
+
+// In-place fast Walsh-Hadamard transform, Sylvester order, unnormalized (src/engine.rs:714-727).
+void fwht(float* x, size_t n) {
+    for (size_t h = 1; h < n; h *= 2)
+        for (size_t i = 0; i < n; i += 2 * h)
+            for (size_t j = i; j < i + h; j++) {
+                const float a = x[j], b = x[j + h];
+                x[j] = a + b;
+                x[j + h] = a - b;
+            }
+}
+
+}  // namespace
+
+Engine::~Engine() {
+    for (auto& kv : plans) kv.second.destroy();
+    if (ev0) (void)hipEventDestroy(ev0);
+    if (ev1) (void)hipEventDestroy(ev1);
+    if (st) (void)hipStreamDestroy(st);
+    for (void* p : device_allocs) (void)hipFree(p);
+    if (pool.base) (void)hipFree(pool.base);
+    for (void* p : host_allocs) (void)hipHostFree(p);
+}
+
+void Plan::destroy() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    exec = nullptr;
+    graph = nullptr;
+}
+
+void* Engine::dalloc(size_t bytes) {
+    void* p = nullptr;
+    SD_HIP(hipMalloc(&p, std::max<size_t>(bytes, 256)));
+    device_allocs.push_back(p);
+    return p;
+}
+
+void* Engine::halloc(size_t bytes) {
+    void* p = nullptr;
+    SD_HIP(hipHostMalloc(&p, std::max<size_t>(bytes, 256), hipHostMallocDefault));
+    host_allocs.push_back(p);
+    return p;
+}
+
+const TensorRef& Engine::tensor(const std::string& name) const {
+    auto it = tensors.find(name);
+    if (it == tensors.end()) throw Error("no tensor " + name);
+    return it->second;
+}
+
+const void* Engine::dptr(const std::string& name) const {
+    auto e = embed_parts.find(name);
+    if (e != embed_parts.end()) return e->second;
+    const TensorRef& t = tensor(name);
+    for (const auto& s : shards)
+        if (t.offset >= s.start && t.offset < s.start + s.bytes) {
+            SD_CHECK(t.offset + t.bytes <= s.start + s.bytes, name + " crosses the end of its shard");
+            return static_cast<const uint8_t*>(s.dev) + (t.offset - s.start);
+        }
+    throw Error(name + " is in no shard");
+}
+
+Mat Engine::mat(const std::string& name) const {
+    const TensorRef& t = tensor(name + ".q");
+    if (!(t.bits == 4 && t.group == 32 && !t.asym))
+        throw Error(name + ": matmul weights must be int4, group 32, symmetric (got " + std::to_string(t.bits) +
+                    " bits, group " + std::to_string(t.group) + (t.asym ? ", asymmetric)" : ")"));
+    SD_CHECK(t.K % 128 == 0, name + ": K must be a multiple of 128");
+    Mat m;
+    m.q = static_cast<const uint32_t*>(dptr(name + ".q"));
+    m.s = static_cast<const f16*>(dptr(name + ".s"));
+    SD_CHECK(reinterpret_cast<uintptr_t>(m.q) % 16 == 0, name + ".q is not 16-byte aligned");
+    m.N = (int)t.N;
+    m.K = (int)t.K;
+    return m;
+}
+
+const float* Engine::f32(const std::string& name, size_t count) const {
+    const TensorRef& t = tensor(name);
+    SD_CHECK(t.bytes >= count * 4, name + ": expected at least " + std::to_string(count) + " f32 values");
+    const void* p = dptr(name);
+    SD_CHECK(reinterpret_cast<uintptr_t>(p) % 4 == 0, name + " is not 4-byte aligned");
+    return static_cast<const float*>(p);
+}
+
+void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char* const* shard_paths,
+                  const uint64_t* shard_starts, const uint64_t* shard_bytes, size_t ns, const sd_embed* em) {
+    SD_CHECK(c && ts && em, "sd_engine_load: null argument");
+    cfg.d = (int)c->hidden_size;
+    cfg.inter = (int)c->intermediate_size;
+    cfg.hq = (int)c->num_attention_heads;
+    cfg.hk = (int)c->num_key_value_heads;
+    cfg.hd = (int)c->head_dim;
+    cfg.rd = (int)c->rotary_dim;
+    cfg.H = (int)c->linear_num_key_heads;
+    cfg.dk = (int)c->linear_key_head_dim;
+    cfg.dv = (int)c->linear_value_head_dim;
+    cfg.theta = c->rope_theta;
+    for (size_t i = 0; i < c->n_layers; i++) {
+        const int k = c->layer_types[i];
+        SD_CHECK(k == SD_LINEAR_ATTENTION || k == SD_FULL_ATTENTION || k == SD_ADAPTER,
+                 "unsupported layer type " + std::to_string(k));
+        kinds.push_back(k);
+    }
+    if (c->unrotate) unrotate.assign(c->unrotate, c->unrotate + cfg.d);
+    SD_CHECK(cfg.d % 256 == 0 && cfg.d <= 8192, "hidden_size must be a multiple of 256 (at most 8192)");
+
+    for (size_t i = 0; i < nt; i++) {
+        const sd_tensor& t = ts[i];
+        SD_CHECK(t.name, "tensor without a name");
+        if (t.had >= 0) throw Error(std::string(t.name) + ": online Hadamard rotation is not supported");
+        tensors[t.name] = TensorRef{t.offset, t.bytes, t.N, t.K, t.bits, t.group, t.asym != 0};
+    }
+
+    int dev = 0;
+    SD_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    SD_HIP(hipGetDeviceProperties(&prop, dev));
+    adapter = std::string(prop.name) + " (" + prop.gcnArchName + ", HIP)";
+    SD_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    SD_HIP(hipEventCreate(&ev0));
+    SD_HIP(hipEventCreate(&ev1));
+
+    // Shards: one device buffer each, streamed from the file through a pinned staging buffer.
+    const size_t chunk = size_t(64) << 20;
+    uint8_t* stage = static_cast<uint8_t*>(halloc(chunk));
+    for (size_t i = 0; i < ns; i++) {
+        Shard s;
+        s.start = shard_starts[i];
+        s.bytes = shard_bytes[i];
+        s.dev = dalloc(s.bytes);
+        FILE* f = std::fopen(shard_paths[i], "rb");
+        if (!f) throw Error(std::string(shard_paths[i]) + ": cannot open");
+        for (uint64_t off = 0; off < s.bytes;) {
+            const size_t n = (size_t)std::min<uint64_t>(chunk, s.bytes - off);
+            if (std::fread(stage, 1, n, f) != n) {
+                std::fclose(f);
+                throw Error(std::string(shard_paths[i]) + ": shorter than the manifest says");
+            }
+            SD_HIP(hipMemcpy(static_cast<uint8_t*>(s.dev) + off, stage, n, hipMemcpyHostToDevice));
+            off += n;
+        }
+        std::fclose(f);
+        shards.push_back(s);
+    }
+    // Embedding parts: rows of [part0 | part1 | ...] split into one device array per part
+    // (src/model.rs:260-283).
+    {
+        uint64_t rb = 0;
+        for (size_t p = 0; p < em->n_parts; p++) rb += em->part_bytes[p];
+        SD_CHECK(rb == em->row_bytes, "embed: part sizes do not add up to row_bytes");
+        FILE* f = std::fopen(em->rows_path, "rb");
+        if (!f) throw Error(std::string(em->rows_path) + ": cannot open");
+        std::fseek(f, 0, SEEK_END);
+        const long size = std::ftell(f);
+        std::fseek(f, 0, SEEK_SET);
+        if ((uint64_t)size != em->vocab * em->row_bytes) {
+            std::fclose(f);
+            throw Error(std::string(em->rows_path) + ": " + std::to_string(size) + " bytes, expected " +
+                        std::to_string(em->vocab) + " rows of " + std::to_string(em->row_bytes));
+        }
+        std::vector<std::vector<uint8_t>> parts(em->n_parts);
+        for (size_t p = 0; p < em->n_parts; p++) parts[p].resize(em->vocab * em->part_bytes[p]);
+        std::vector<uint8_t> row(em->row_bytes);
+        const size_t rows_per = std::max<size_t>(1, chunk / em->row_bytes);
+        std::vector<uint8_t> buf(rows_per * em->row_bytes);
+        for (uint64_t r0 = 0; r0 < em->vocab; r0 += rows_per) {
+            const size_t nr = (size_t)std::min<uint64_t>(rows_per, em->vocab - r0);
+            if (std::fread(buf.data(), em->row_bytes, nr, f) != nr) {
+                std::fclose(f);
+                throw Error(std::string(em->rows_path) + ": read failed");
+            }
+            for (size_t r = 0; r < nr; r++) {
+                size_t off = 0;
+                for (size_t p = 0; p < em->n_parts; p++) {
+                    std::memcpy(parts[p].data() + (r0 + r) * em->part_bytes[p], buf.data() + r * em->row_bytes + off,
+                                em->part_bytes[p]);
+                    off += em->part_bytes[p];
+                }
+            }
+        }
+        std::fclose(f);
+        for (size_t p = 0; p < em->n_parts; p++) {
+            void* dptr_ = dalloc(parts[p].size());
+            SD_HIP(hipMemcpy(dptr_, parts[p].data(), parts[p].size(), hipMemcpyHostToDevice));
+            embed_parts[em->part_names[p]] = dptr_;
+        }
+        vocab = (int)em->vocab;
+    }
+    {
+        const TensorRef& t = tensor("embed.q");
+        emb.bits = (int)t.bits;
+        emb.group = (int)t.group;
+        emb.asym = t.asym;
+        emb.q = static_cast<const uint32_t*>(dptr("embed.q"));
+        emb.s = static_cast<const f16*>(dptr("embed.s"));
+        emb.b = emb.asym ? static_cast<const f16*>(dptr("embed.b")) : nullptr;
+    }
+
+    // Per-layer weights and live state.  GDN state and conv history of every linear layer live in
+    // one arena ([all states | all histories]) so that a snapshot is a single copy.
+    const int C = 2 * cfg.H * cfg.dk + cfg.H * cfg.dv;
+    const size_t state_bytes = (size_t)cfg.H * cfg.dk * cfg.dv * 4, hist_bytes = align256((size_t)3 * C * 2);
+    n_linear = 0;
+    for (int k : kinds) n_linear += k == SD_LINEAR_ATTENTION;
+    arena_state_bytes = n_linear * state_bytes;
+    arena_bytes = arena_state_bytes + n_linear * hist_bytes;
+    arena = static_cast<uint8_t*>(dalloc(arena_bytes));
+    SD_HIP(hipMemset(arena, 0, arena_bytes));
+    const size_t kv_bytes = (size_t)cfg.hk * SD_CONTEXT * cfg.hd * 2;
+    int li = 0;
+    for (size_t i = 0; i < kinds.size(); i++) {
+        const std::string p = "layers." + std::to_string(i) + ".";
+        LayerW L;
+        L.kind = kinds[i];
+        L.in_norm = f32(p + "in_norm", cfg.d);
+        if (L.kind == SD_ADAPTER) {
+            L.proj = mat(p + "proj");
+            L.bias = f32(p + "bias", cfg.d);
+            layers.push_back(L);
+            continue;
+        }
+        if (L.kind == SD_LINEAR_ATTENTION) {
+            SD_CHECK(cfg.dk == 128 && cfg.dv == 128, "gated delta net: only 128-wide key/value heads are supported");
+            L.in_proj = mat(p + "in_proj");
+            SD_CHECK(L.in_proj.N >= C + 2 * cfg.H * 1 + cfg.H * cfg.dv, p + "in_proj: too few rows for q|k|v|z|a|b");
+            L.conv = f32(p + "conv", (size_t)C * 4);
+            L.negA = f32(p + "neg_exp_A", cfg.H);
+            L.dtb = f32(p + "dt_bias", cfg.H);
+            L.gnorm = f32(p + "gnorm", cfg.dv);
+            L.out_proj = mat(p + "out_proj");
+            L.state = reinterpret_cast<float*>(arena + li * state_bytes);
+            L.hist = reinterpret_cast<f16*>(arena + arena_state_bytes + li * hist_bytes);
+            li++;
+        } else {
+            SD_CHECK(cfg.hd == 256, "attention: only head_dim 256 is supported");
+            SD_CHECK(cfg.hk > 0 && cfg.hq % cfg.hk == 0, "attention: q heads must be a multiple of kv heads");
+            L.qkv = mat(p + "qkv");
+            SD_CHECK(L.qkv.N >= 2 * cfg.hq * cfg.hd + 2 * cfg.hk * cfg.hd, p + "qkv: too few rows");
+            L.q_norm = f32(p + "q_norm", cfg.hd);
+            L.k_norm = f32(p + "k_norm", cfg.hd);
+            L.o_proj = mat(p + "o_proj");
+            L.kc = static_cast<f16*>(dalloc(kv_bytes));
+            L.vc = static_cast<f16*>(dalloc(kv_bytes));
+            SD_HIP(hipMemset(L.kc, 0, kv_bytes));
+            SD_HIP(hipMemset(L.vc, 0, kv_bytes));
+            attn_layers.push_back((int)i);
+        }
+        L.post_norm = f32(p + "post_norm", cfg.d);
+        L.gate_up = mat(p + "gate_up");
+        L.down = mat(p + "down");
+        SD_CHECK(L.gate_up.N == 2 * cfg.inter && L.down.K == cfg.inter, p + "gate_up/down: shapes do not match intermediate_size");
+        layers.push_back(L);
+    }
+    final_norm = f32("final_norm", cfg.d);
+
+    // RoPE table, angles in f64 (src/engine.rs:259-267).
+    {
+        std::vector<float> table((size_t)SD_CONTEXT * std::max(cfg.rd, 2));
+        for (int t = 0; t < SD_CONTEXT; t++)
+            for (int i = 0; i < cfg.rd / 2; i++) {
+                const double a = (double)t / std::pow(cfg.theta, (double)(2 * i) / (double)cfg.rd);
+                table[(size_t)t * cfg.rd + 2 * i] = (float)std::cos(a);
+                table[(size_t)t * cfg.rd + 2 * i + 1] = (float)std::sin(a);
+            }
+        rope = static_cast<float*>(dalloc(table.size() * 4));
+        SD_HIP(hipMemcpy(rope, table.data(), table.size() * 4, hipMemcpyHostToDevice));
+    }
+    lu = static_cast<uint32_t*>(dalloc(16));
+    lu_h = static_cast<uint32_t*>(halloc(16));
+    use_graphs = !env_off("SD_GRAPHS");
+    for (const LayerW& L : layers) {
+        if (L.kind == SD_LINEAR_ATTENTION) max_n = std::max(max_n, L.in_proj.N);
+        if (L.kind == SD_FULL_ATTENTION) max_n = std::max(max_n, L.qkv.N);
+        if (L.kind != SD_ADAPTER) max_n = std::max(max_n, L.gate_up.N);
+    }
+    max_n = std::max(max_n, cfg.d);
+}
+
+void Engine::ensure_pool(int l) {
+    const int cap = l <= 128 ? 128 : (int)std::min<size_t>(SD_CONTEXT, size_t(1) << (32 - __builtin_clz((unsigned)l - 1)));
+    if (pool.cap >= cap) return;
+    // A bigger pool serves every shorter length too; plans bound to the old one are rebuilt.
+    for (auto& kv : plans) kv.second.destroy();
+    plans.clear();
+    if (pool.base) SD_HIP(hipFree(pool.base));
+    pool = Pool{};
+    const int C = 2 * cfg.H * cfg.dk + cfg.H * cfg.dv;
+    const int orow = std::max({cfg.H * cfg.dv, cfg.hq * cfg.hd, cfg.d});
+    GdnShape gs{cfg.H, cfg.dk, cfg.dv, 0, 0, 0, 0, C};
+    AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, 0, SD_CONTEXT};
+    const size_t gemm_part = size_t(32) << 20, gemm_cnt = 65536;
+    const size_t sizes[] = {
+        (size_t)cap * 4,                               // ids
+        (size_t)cap * 4,                               // rows
+        (size_t)cap * cfg.d * 4,                       // x
+        (size_t)cap * cfg.d * 2,                       // h
+        (size_t)cap * max_n * 2,                       // big
+        (size_t)cap * cfg.inter * 2,                   // mid
+        (size_t)cap * C * 4,                           // qkvc
+        (size_t)cap * cfg.H * cfg.dv * 4,              // of
+        (size_t)cap * orow * 2,                        // o
+        (size_t)cap * cfg.d * 2,                       // y
+        (size_t)cfg.hq * cap * cfg.hd * 2,             // q
+        (size_t)cap * cfg.d * 4,                       // out
+        gdn_ws_floats(cap, gs) * 4,                    // GDN chunk workspace
+        attn_ws_floats(std::min(cap, 256), as) * 4,    // attention key-split workspace
+        gemm_part * 4,                                 // GEMM split-K partials
+        gemm_cnt * 4,                                  // GEMM tile counters
+    };
+    size_t total = 0;
+    for (size_t s : sizes) total += align256(s);
+    void* base = nullptr;
+    SD_HIP(hipMalloc(&base, total));
+    pool.base = base;
+    pool.cap = cap;
+    uint8_t* p = static_cast<uint8_t*>(base);
+    void* ptrs[sizeof(sizes) / sizeof(sizes[0])];
+    for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); i++) {
+        ptrs[i] = p;
+        p += align256(sizes[i]);
+    }
+    pool.ids = (uint32_t*)ptrs[0];
+    pool.rows = (uint32_t*)ptrs[1];
+    pool.x = (float*)ptrs[2];
+    pool.h = (f16*)ptrs[3];
+    pool.big = (f16*)ptrs[4];
+    pool.mid = (f16*)ptrs[5];
+    pool.qkvc = (float*)ptrs[6];
+    pool.of = (float*)ptrs[7];
+    pool.o = (f16*)ptrs[8];
+    pool.y = (f16*)ptrs[9];
+    pool.q = (f16*)ptrs[10];
+    pool.out = (float*)ptrs[11];
+    gdn_ws_carve((float*)ptrs[12], cap, gs, pool.gdn);
+    pool.attn_ws = (float*)ptrs[13];
+    pool.attn_rows = std::min(cap, 256);
+    pool.gemm.part = (float*)ptrs[14];
+    pool.gemm.part_elems = gemm_part;
+    pool.gemm.cnt = (uint32_t*)ptrs[15];
+    pool.gemm.cnt_elems = gemm_cnt;
+    SD_HIP(hipMemset(pool.gemm.cnt, 0, gemm_cnt * 4));
+    SD_HIP(hipMemset(pool.x, 0, (size_t)cap * cfg.d * 4));
+    if (ids_h_cap < cap) {
+        ids_h = static_cast<uint32_t*>(halloc((size_t)cap * 4));
+        rows_h = static_cast<uint32_t*>(halloc((size_t)cap * 4));
+        out_h = static_cast<float*>(halloc((size_t)cap * cfg.d * 4));
+        ids_h_cap = cap;
+    }
+}
+
+void Engine::mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L) {
+    // The reference's GEMV (f32 dequant) serves M <= 20 and N % 64 != 0 (src/engine.rs:419-442).
+    const bool exact = L <= 20 || m.N % 64 != 0;
+    const GemmWs ws = pool.gemm;
+    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, L, m.N, m.K, exact, ws, s); }});
+}
+
+Plan& Engine::plan(int L) {
+    auto it = plans.find(L);
+    if (it != plans.end()) return it->second;
+    Plan pl;
+    pl.L = L;
+    auto& steps = pl.steps;
+    const Pool P = pool;
+    const int d = cfg.d, I = cfg.inter;
+    const int C = 2 * cfg.H * cfg.dk + cfg.H * cfg.dv;
+    const EmbedW E = emb;
+    const uint32_t* luv = lu;
+    steps.push_back({"embed", [=](hipStream_t s) { embed(P.ids, L, E.q, E.s, E.b, d, E.bits, E.group, E.asym, P.x, s); }});
+    for (size_t i = 0; i < layers.size(); i++) {
+        const LayerW W = layers[i];
+        const f16* yin = i > 0 ? P.y : nullptr;
+        steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.in_norm, d, nullptr, L, P.h, nullptr, s); }});
+        if (W.kind == SD_ADAPTER) {
+            mm(steps, "proj", P.h, W.proj, P.y, L);
+            steps.push_back({"bias", [=](hipStream_t s) { add_bias(P.y, L, d, W.bias, s); }});
+            continue;
+        }
+        if (W.kind == SD_LINEAR_ATTENTION) {
+            const int n = W.in_proj.N;
+            const GdnShape gs{cfg.H, cfg.dk, cfg.dv, n, C + cfg.H * cfg.dv, C + cfg.H * cfg.dv + cfg.H, C, C};
+            mm(steps, "in_proj", P.h, W.in_proj, P.big, L);
+            steps.push_back({"conv", [=](hipStream_t s) { conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, s); }});
+            steps.push_back({"gdn", [=](hipStream_t s) { gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, W.hist, s); }});
+            steps.push_back({"gdn", [=](hipStream_t s) { gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, s); }});
+            steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
+            mm(steps, "out_proj", P.o, W.out_proj, P.y, L);
+        } else {
+            const AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, W.qkv.N, SD_CONTEXT};
+            const float* rp = rope;
+            mm(steps, "qkv", P.h, W.qkv, P.big, L);
+            steps.push_back({"qk_prep", [=](hipStream_t s) { qk_prep(P.big, as, W.q_norm, W.k_norm, rp, L, luv, P.q, W.kc, W.vc, s); }});
+            const int nb = (L + 15) / 16;
+            int ks = 1;
+            if (L <= P.attn_rows)
+                while (ks < 8 && nb * cfg.hq * ks < 256) ks *= 2;
+            steps.push_back({"attn", [=](hipStream_t s) { attention_split(P.q, W.kc, W.vc, P.big, as, L, luv, ks, P.attn_ws, P.o, s); }});
+            mm(steps, "o_proj", P.o, W.o_proj, P.y, L);
+        }
+        steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, P.y, W.post_norm, d, nullptr, L, P.h, nullptr, s); }});
+        mm(steps, "gate_up", P.h, W.gate_up, P.big, L);
+        steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, L, I, P.mid, s); }});
+        mm(steps, "down", P.mid, W.down, P.y, L);
+    }
+    if (use_graphs) {
+        SD_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        try {
+            for (auto& s : steps) s.run(st);
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(st, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        SD_HIP(hipStreamEndCapture(st, &pl.graph));
+        SD_HIP(hipGraphInstantiate(&pl.exec, pl.graph, nullptr, nullptr, 0));
+    }
+    return plans.emplace(L, std::move(pl)).first->second;
+}
+
+void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, const Snapshot* cache,
+                     bool keep, bool timed, float* hidden, double* gpu_ms, Snapshot** snap_out) {
+    const size_t P = cache ? cache->len : 0;
+    if (n == 0 || P + n > SD_CONTEXT)
+        throw Error("context of " + std::to_string(P + n) + " tokens: must be 1 to " + std::to_string(SD_CONTEXT));
+    for (size_t r = 0; r < n_rows; r++)
+        if (rows[r] >= n) throw Error("row " + std::to_string(rows[r]) + " out of range for " + std::to_string(n) + " tokens");
+    if (cache && cache->engine != this) throw Error("snapshot belongs to another engine");
+    for (uint32_t i = 0; i < n; i++)
+        if (ids[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(ids[i]) + " out of range for vocab " + std::to_string(vocab));
+    const int L = (int)n;
+    ensure_pool(L);
+    Plan& pl = plan(L);
+
+    std::memcpy(ids_h, ids, n * 4);
+    SD_HIP(hipMemcpyAsync(pool.ids, ids_h, n * 4, hipMemcpyHostToDevice, st));
+    for (size_t r = 0; r < n_rows; r++) rows_h[r] = (uint32_t)rows[r];
+    if (n_rows) SD_HIP(hipMemcpyAsync(pool.rows, rows_h, n_rows * 4, hipMemcpyHostToDevice, st));
+    lu_h[0] = (uint32_t)n;
+    lu_h[1] = (uint32_t)P;
+    lu_h[2] = SD_CONTEXT;
+    lu_h[3] = cache ? 1u : 0u;
+    SD_HIP(hipMemcpyAsync(lu, lu_h, 16, hipMemcpyHostToDevice, st));
+    // Restore (src/engine.rs:552-571): GDN state + conv history in one copy; K/V prefix rows only
+    // when the live cache does not already hold this snapshot's prefix (question forwards write
+    // rows >= P only, so after one restore the prefix stays valid for every later question).
+    if (cache) {
+        SD_HIP(hipMemcpyAsync(arena, cache->arena, arena_bytes, hipMemcpyDeviceToDevice, st));
+        if (kv_owner != cache->id) {
+            const size_t row = (size_t)cfg.hd * 2;
+            for (size_t a = 0; a < attn_layers.size(); a++) {
+                const LayerW& W = layers[attn_layers[a]];
+                const uint8_t* ks = cache->kv(a, 0), *vs = cache->kv(a, 1);
+                SD_HIP(hipMemcpy2DAsync(W.kc, SD_CONTEXT * row, ks, P * row, P * row, cfg.hk, hipMemcpyDeviceToDevice, st));
+                SD_HIP(hipMemcpy2DAsync(W.vc, SD_CONTEXT * row, vs, P * row, P * row, cfg.hk, hipMemcpyDeviceToDevice, st));
+            }
+            kv_owner = cache->id;
+        }
+    } else {
+        fill_u32(reinterpret_cast<uint32_t*>(arena + arena_state_bytes), (arena_bytes - arena_state_bytes) / 4, 0u, st);
+        kv_owner = 0;
+    }
+    if (timed) SD_HIP(hipEventRecord(ev0, st));
+    if (pl.exec) {
+        SD_HIP(hipGraphLaunch(pl.exec, st));
+    } else {
+        for (auto& s : pl.steps) s.run(st);
+    }
+    if (n_rows) add_norm(pool.x, pool.y, final_norm, cfg.d, pool.rows, (int)n_rows, nullptr, pool.out, st);
+    if (timed) SD_HIP(hipEventRecord(ev1, st));
+    if (n_rows) SD_HIP(hipMemcpyAsync(out_h, pool.out, n_rows * cfg.d * 4, hipMemcpyDeviceToHost, st));
+    Snapshot* snap = nullptr;
+    if (keep) {
+        const size_t T = P + n;
+        snap = new Snapshot();
+        snap->engine = this;
+        snap->len = T;
+        snap->id = ++snapshot_ids;
+        snap->kv_stride = (size_t)cfg.hk * T * cfg.hd * 2;
+        snap->arena_bytes = arena_bytes;
+        const size_t bytes = arena_bytes + attn_layers.size() * 2 * snap->kv_stride;
+        const hipError_t e = hipMalloc(&snap->arena, bytes);
+        if (e != hipSuccess) {
+            delete snap;
+            throw Error(std::string("snapshot allocation: ") + hipGetErrorString(e));
+        }
+        SD_HIP(hipMemcpyAsync(snap->arena, arena, arena_bytes, hipMemcpyDeviceToDevice, st));
+        const size_t row = (size_t)cfg.hd * 2;
+        for (size_t a = 0; a < attn_layers.size(); a++) {
+            const LayerW& W = layers[attn_layers[a]];
+            SD_HIP(hipMemcpy2DAsync(snap->kv(a, 0), T * row, W.kc, SD_CONTEXT * row, T * row, cfg.hk, hipMemcpyDeviceToDevice, st));
+            SD_HIP(hipMemcpy2DAsync(snap->kv(a, 1), T * row, W.vc, SD_CONTEXT * row, T * row, cfg.hk, hipMemcpyDeviceToDevice, st));
+        }
+        kv_owner = snap->id;
+    }
+    const hipError_t se = hipStreamSynchronize(st);
+    if (se != hipSuccess) {
+        delete snap;
+        throw Error(std::string("GPU: ") + hipGetErrorString(se));
+    }
+    if (n_rows) {
+        std::memcpy(hidden, out_h, n_rows * cfg.d * 4);
+        // A rotated torso: the head's basis is unrotate * FWHT(row) (src/engine.rs:652-660).
+        if (!unrotate.empty())
+            for (size_t r = 0; r < n_rows; r++) {
+                float* x = hidden + r * cfg.d;
+                fwht(x, cfg.d);
+                for (int j = 0; j < cfg.d; j++) x[j] = (float)((double)x[j] * unrotate[j]);
+            }
+    }
+    if (gpu_ms) {
+        *gpu_ms = NAN;
+        if (timed) {
+            float ms = 0.f;
+            SD_HIP(hipEventElapsedTime(&ms, ev0, ev1));
+            *gpu_ms = ms;
+        }
+    }
+    if (snap_out) *snap_out = snap;
+    else delete snap;
+}
+
+std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids, size_t n) {
+    if (n == 0 || n > SD_CONTEXT) throw Error("profiling needs 1 to 4096 tokens");
+    for (uint32_t i = 0; i < n; i++)
+        if (ids[i] >= (uint32_t)vocab) throw Error("token id out of range");
+    const int L = (int)n;
+    ensure_pool(L);
+    Plan& pl = plan(L);
+    std::memcpy(ids_h, ids, n * 4);
+    SD_HIP(hipMemcpyAsync(pool.ids, ids_h, n * 4, hipMemcpyHostToDevice, st));
+    lu_h[0] = (uint32_t)n;
+    lu_h[1] = 0;
+    lu_h[2] = SD_CONTEXT;
+    lu_h[3] = 0;
+    SD_HIP(hipMemcpyAsync(lu, lu_h, 16, hipMemcpyHostToDevice, st));
+    fill_u32(reinterpret_cast<uint32_t*>(arena + arena_state_bytes), (arena_bytes - arena_state_bytes) / 4, 0u, st);
+    kv_owner = 0;
+    std::vector<hipEvent_t> evs(pl.steps.size() + 1);
+    for (auto& e : evs) SD_HIP(hipEventCreate(&e));
+    SD_HIP(hipEventRecord(evs[0], st));
+    for (size_t i = 0; i < pl.steps.size(); i++) {
+        pl.steps[i].run(st);
+        SD_HIP(hipEventRecord(evs[i + 1], st));
+    }
+    SD_HIP(hipStreamSynchronize(st));
+    std::vector<std::pair<const char*, double>> by;
+    for (size_t i = 0; i < pl.steps.size(); i++) {
+        float ms = 0.f;
+        SD_HIP(hipEventElapsedTime(&ms, evs[i], evs[i + 1]));
+        auto f = std::find_if(by.begin(), by.end(), [&](auto& p) { return std::strcmp(p.first, pl.steps[i].label) == 0; });
+        if (f == by.end()) by.emplace_back(pl.steps[i].label, ms);
+        else f->second += ms;
+    }
+    for (auto& e : evs) (void)hipEventDestroy(e);
+    std::sort(by.begin(), by.end(), [](auto& a, auto& b) { return a.second > b.second; });
+    return by;
+}
+
+Snapshot::~Snapshot() {
+    if (arena) (void)hipFree(arena);
+}
+
+}  // namespace sd

@@ -1,0 +1,153 @@
+// Engine state: the counterpart of the reference's `Engine`, `Pool`, `Plan` and `Snapshot`
+// (src/engine.rs:57-132), laid out for one MI355X.
+#pragma once
+
+#include <functional>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+#include "../../include/sdhip.h"
+#include "common.h"
+
+namespace sd {
+
+struct TensorRef {
+    uint64_t offset, bytes;
+    uint32_t N, K, bits, group;
+    bool asym;
+};
+
+struct Shard {
+    uint64_t start = 0, bytes = 0;
+    void* dev = nullptr;
+};
+
+struct Mat {
+    const uint32_t* q = nullptr;
+    const f16* s = nullptr;
+    int N = 0, K = 0;
+};
+
+struct EmbedW {
+    const uint32_t* q = nullptr;
+    const f16* s = nullptr;
+    const f16* b = nullptr;
+    int bits = 4, group = 32;
+    bool asym = false;
+};
+
+struct LayerW {
+    int kind = 0;
+    const float* in_norm = nullptr;
+    const float* post_norm = nullptr;
+    Mat in_proj, out_proj, qkv, o_proj, gate_up, down, proj;
+    const float *conv = nullptr, *negA = nullptr, *dtb = nullptr, *gnorm = nullptr;
+    const float *q_norm = nullptr, *k_norm = nullptr, *bias = nullptr;
+    float* state = nullptr;  // [H][dk][dv] f32 (in the live arena)
+    f16* hist = nullptr;     // [3][C] f16 (in the live arena)
+    f16* kc = nullptr;       // [hk][CONTEXT][hd] f16
+    f16* vc = nullptr;
+};
+
+struct Cfg {
+    int d = 0, inter = 0, hq = 0, hk = 0, hd = 0, rd = 0, H = 0, dk = 0, dv = 0;
+    double theta = 0;
+};
+
+// Activation buffers for up to `cap` tokens, shared by every plan (src/engine.rs:62-78).
+struct Pool {
+    int cap = 0;
+    void* base = nullptr;
+    uint32_t *ids = nullptr, *rows = nullptr;
+    float *x = nullptr, *qkvc = nullptr, *of = nullptr, *out = nullptr;
+    f16 *h = nullptr, *big = nullptr, *mid = nullptr, *o = nullptr, *y = nullptr, *q = nullptr;
+    GdnWs gdn;
+    float* attn_ws = nullptr;
+    int attn_rows = 0;
+    GemmWs gemm;
+};
+
+struct Step {
+    const char* label;
+    std::function<void(hipStream_t)> run;
+};
+
+// The dispatch list for one token length and its captured graph (src/engine.rs:57-60, 396-524).
+struct Plan {
+    int L = 0;
+    std::vector<Step> steps;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    void destroy();
+};
+
+struct Engine;
+
+// Prefix state after a forward: GDN state + conv history (the live arena image), then compact
+// K/V [hk][len][hd] per attention layer (src/engine.rs:81-87, 592-614).
+struct Snapshot {
+    const Engine* engine = nullptr;
+    size_t len = 0;
+    uint64_t id = 0;
+    void* arena = nullptr;
+    size_t arena_bytes = 0, kv_stride = 0;
+    uint8_t* kv(size_t attn_index, int which) const {
+        return static_cast<uint8_t*>(arena) + arena_bytes + (attn_index * 2 + which) * kv_stride;
+    }
+    ~Snapshot();
+};
+
+struct Engine {
+    Cfg cfg;
+    std::vector<int> kinds;
+    std::vector<double> unrotate;
+    std::string adapter;
+    hipStream_t st = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::unordered_map<std::string, TensorRef> tensors;
+    std::vector<Shard> shards;
+    std::unordered_map<std::string, void*> embed_parts;
+    EmbedW emb;
+    int vocab = 0;
+    std::vector<LayerW> layers;
+    std::vector<int> attn_layers;
+    const float* final_norm = nullptr;
+    float* rope = nullptr;
+    uint32_t* lu = nullptr;  // device [L, P, CONTEXT, has_cache]
+    uint32_t* lu_h = nullptr;
+    uint8_t* arena = nullptr;  // [GDN states | conv histories]
+    size_t arena_bytes = 0, arena_state_bytes = 0;
+    int n_linear = 0;
+    int max_n = 0;
+    uint64_t snapshot_ids = 0, kv_owner = 0;
+    bool use_graphs = true;
+    Pool pool;
+    std::map<int, Plan> plans;
+    uint32_t *ids_h = nullptr, *rows_h = nullptr;
+    float* out_h = nullptr;
+    int ids_h_cap = 0;
+    std::vector<void*> device_allocs, host_allocs;
+
+    ~Engine();
+    void load(const sd_config* c, const sd_tensor* ts, size_t nt, const char* const* shard_paths,
+              const uint64_t* shard_starts, const uint64_t* shard_bytes, size_t ns, const sd_embed* em);
+    void forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, const Snapshot* cache, bool keep,
+                 bool timed, float* hidden, double* gpu_ms, Snapshot** snap_out);
+    std::vector<std::pair<const char*, double>> profile(const uint32_t* ids, size_t n);
+
+   private:
+    void* dalloc(size_t bytes);
+    void* halloc(size_t bytes);
+    const TensorRef& tensor(const std::string& name) const;
+    const void* dptr(const std::string& name) const;
+    Mat mat(const std::string& name) const;
+    const float* f32(const std::string& name, size_t count) const;
+    void ensure_pool(int l);
+    Plan& plan(int L);
+    void mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L);
+};
+
+}  // namespace sd

@@ -1,0 +1,269 @@
+// Fused-dequant int4 (group 32, symmetric) GEMM on gfx950 MFMA:
+//   Y[M,N] f16 = A[M,K] f16 . deq(W[N,K])^T, f32 accumulation.
+// The reference's matmul kernels are src/kernels.rs:590-709 (GEMV with f32 dequant for M <= 20,
+// tiled with f16 dequant otherwise; selection at src/engine.rs:414-444).
+//
+// Design (one kernel family for prefill and the short question suffix):
+//  * a workgroup is 4 waves side by side along N; each wave owns NT 16-column tiles and all MT
+//    16-row tiles of the workgroup, so no two waves ever dequantize the same weights;
+//  * weights go straight from HBM to registers: lane (j = l%16, g = l/16) loads the whole 16-byte
+//    quant block (32 k values) of column j at block kb0+g, i.e. one macro step covers 128 k and
+//    feeds 4 v_mfma_f32_16x16x32_f16; step s uses word s of the block;
+//  * a word's 8 nibbles become 4 f16 pairs with the 0x6400 exponent trick:
+//      ((w >> 4i) & 0x000F000F) | 0x64006400 = (1024 + q_i, 1024 + q_{i+4}),
+//    minus 1032 (exact) gives q - 8, times the f16 scale rounds once: exactly the reference's
+//    f16 dequant (f16(q) - 8) * sc.  The pairs come out in k order [0,4,1,5,2,6,3,7]; the A tile
+//    is stored to LDS in the same order, so the dot products see matching k;
+//  * `EXACT` reproduces the reference GEMV's f32 dequant (q-8)*sc: the value is split into
+//    hi = f16((q-8)*sc) and lo = fma_f16(q-8, sc, -hi) (exact: the residual is a multiple of
+//    2^-24 with at most 5 significant bits), and both are fed to the MFMA;
+//  * A (activations, f16) is staged once per workgroup per macro step in LDS (shared by the 4
+//    waves) with a register prefetch of the next step; B for the next step is prefetched too;
+//  * split-K over workgroups writes f32 partials; the last workgroup of a tile (self-resetting
+//    counter) sums them in a fixed order and writes f16, so results do not depend on timing.
+#include "common.h"
+
+namespace sd {
+namespace {
+
+constexpr int KSTEP = 128;      // k per macro step: 4 quant blocks
+constexpr int LDA = KSTEP + 8;  // LDS row stride in halves (16-byte pad)
+
+__device__ __forceinline__ f16x2 nib_pair(uint32_t w, int sh) {
+    uint32_t v = ((w >> sh) & 0x000F000Fu) | 0x64006400u;
+    return __builtin_bit_cast(f16x2, v) - f16x2{(f16)1032.0f, (f16)1032.0f};
+}
+
+__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
+    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Permute 8 halves [a0..a7] (as 4 words) to [a0,a4,a1,a5,a2,a6,a3,a7].
+__device__ __forceinline__ u32x4 perm_a(u32x4 d) {
+    u32x4 o;
+    o[0] = (d[0] & 0xFFFFu) | (d[2] << 16);
+    o[1] = (d[0] >> 16) | (d[2] & 0xFFFF0000u);
+    o[2] = (d[1] & 0xFFFFu) | (d[3] << 16);
+    o[3] = (d[1] >> 16) | (d[3] & 0xFFFF0000u);
+    return o;
+}
+
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int MT, int NT, bool EXACT>
+__global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, const uint32_t* __restrict__ W,
+                                                 const f16* __restrict__ S, f16* __restrict__ Y,
+                                                 float* __restrict__ part, uint32_t* __restrict__ cnt, int M,
+                                                 int N, int K, int ksplit) {
+    constexpr int BM = MT * 16;
+    constexpr int BN = 4 * NT * 16;
+    constexpr int ACH = BM * 16 / 256;  // 16-byte A chunks per thread per macro step (== MT)
+    __shared__ __attribute__((aligned(16))) f16 As[BM * LDA];
+    __shared__ int last_flag;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int KB = K >> 5;
+    const int steps_total = K / KSTEP;
+    const int steps = steps_total / ksplit;
+    const int step0 = blockIdx.z * steps;
+
+    // B addressing for this lane's NT columns.
+    int ncol[NT];
+    bool nok[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        ncol[t] = n0 + (wave * NT + t) * 16 + j;
+        nok[t] = ncol[t] < N;
+    }
+
+    auto load_b = [&](int step, u32x4* bw, f16* bs) {
+        const int kb = step * 4 + g;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (nok[t]) {
+                const size_t blk = (size_t)ncol[t] * KB + kb;
+                bw[t] = *reinterpret_cast<const u32x4*>(W + blk * 4);
+                bs[t] = S[blk];
+            } else {
+                bw[t] = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+                bs[t] = (f16)0.0f;
+            }
+        }
+    };
+    auto load_a = [&](int step, u32x4* ar) {
+#pragma unroll
+        for (int c = 0; c < ACH; c++) {
+            const int idx = tid + 256 * c;
+            const int row = idx >> 4, c16 = idx & 15;
+            const int m = m0 + row;
+            if (m < M)
+                ar[c] = *reinterpret_cast<const u32x4*>(A + (size_t)m * K + step * KSTEP + c16 * 8);
+            else
+                ar[c] = u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[a][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 areg[ACH], bcur[NT], bnext[NT];
+    f16 scur[NT], snext[NT];
+    load_a(step0, areg);
+    load_b(step0, bcur, scur);
+
+    for (int it = 0; it < steps; it++) {
+        __syncthreads();  // the previous step's LDS reads are done
+#pragma unroll
+        for (int c = 0; c < ACH; c++) {
+            const int idx = tid + 256 * c;
+            const int row = idx >> 4, c16 = idx & 15;
+            *reinterpret_cast<u32x4*>(&As[row * LDA + c16 * 8]) = perm_a(areg[c]);
+        }
+        if (it + 1 < steps) {
+            load_a(step0 + it + 1, areg);
+            load_b(step0 + it + 1, bnext, snext);
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            f16x8 b[NT];
+            f16x8 blo[NT];
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const uint32_t w = bcur[t][s];
+                const f16x2 sc2 = f16x2{scur[t], scur[t]};
+                const f16x2 p0 = nib_pair(w, 0), p1 = nib_pair(w, 4), p2 = nib_pair(w, 8), p3 = nib_pair(w, 12);
+                const f16x2 h0 = p0 * sc2, h1 = p1 * sc2, h2 = p2 * sc2, h3 = p3 * sc2;
+                b[t] = cat4(h0, h1, h2, h3);
+                if constexpr (EXACT) {
+                    blo[t] = cat4(__builtin_elementwise_fma(p0, sc2, -h0), __builtin_elementwise_fma(p1, sc2, -h1),
+                                  __builtin_elementwise_fma(p2, sc2, -h2), __builtin_elementwise_fma(p3, sc2, -h3));
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < MT; a++) {
+                const u32x4 araw = *reinterpret_cast<const u32x4*>(&As[(a * 16 + j) * LDA + g * 32 + s * 8]);
+                const f16x8 av = __builtin_bit_cast(f16x8, araw);
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[t], acc[a][t], 0, 0, 0);
+                    if constexpr (EXACT) acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, blo[t], acc[a][t], 0, 0, 0);
+                }
+            }
+        }
+        if (it + 1 < steps) {
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                bcur[t] = bnext[t];
+                scur[t] = snext[t];
+            }
+        }
+    }
+
+    // Output: acc[a][t][r] is row m0 + 16a + 4g + r, column ncol[t].
+    if (ksplit == 1) {
+#pragma unroll
+        for (int a = 0; a < MT; a++)
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + a * 16 + g * 4 + r;
+                    if (m < M && nok[t]) Y[(size_t)m * N + ncol[t]] = (f16)acc[a][t][r];
+                }
+        return;
+    }
+    float* mine = part + (size_t)blockIdx.z * M * N;
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + a * 16 + g * 4 + r;
+                if (m < M && nok[t]) mine[(size_t)m * N + ncol[t]] = acc[a][t][r];
+            }
+    __threadfence();
+    __syncthreads();
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    if (tid == 0) {
+        const uint32_t old = atomicAdd(&cnt[tile], 1u);
+        last_flag = old == (uint32_t)(ksplit - 1);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + a * 16 + g * 4 + r;
+                if (m < M && nok[t]) {
+                    float sum = 0.f;
+                    for (int z = 0; z < ksplit; z++) sum += ld_coherent(part + ((size_t)z * M + m) * N + ncol[t]);
+                    Y[(size_t)m * N + ncol[t]] = (f16)sum;
+                }
+            }
+    if (tid == 0) cnt[tile] = 0u;
+}
+
+struct Cfg {
+    int mt, nt;
+    bool exact;
+    void (*fn)(const f16*, const uint32_t*, const f16*, f16*, float*, uint32_t*, int, int, int, int);
+};
+
+#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX>}
+const Cfg kCfgs[] = {
+    SD_CFG(1, 1, true), SD_CFG(2, 1, true),                                           // M <= 20: f32 dequant
+    SD_CFG(1, 1, false), SD_CFG(2, 1, false), SD_CFG(3, 1, false), SD_CFG(4, 1, false),  // skinny
+    SD_CFG(8, 2, false), SD_CFG(8, 4, false), SD_CFG(4, 2, false), SD_CFG(8, 1, false),  // prefill
+};
+#undef SD_CFG
+constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+
+int pick_cfg(int M, bool exact) {
+    if (exact) return M <= 16 ? 0 : 1;
+    if (M <= 16) return 2;
+    if (M <= 32) return 3;
+    if (M <= 48) return 4;
+    if (M <= 64) return 5;
+    return 6;
+}
+
+}  // namespace
+
+int gemm_w4_configs() { return kNumCfgs; }
+
+void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, int M, int N, int K, bool exact,
+             const GemmWs& ws, hipStream_t st, int force_cfg) {
+    SD_CHECK(M >= 1 && N >= 1 && K >= KSTEP && K % KSTEP == 0, "gemm_w4: need M, N >= 1 and K a multiple of 128");
+    int ci = force_cfg >= 0 ? force_cfg : pick_cfg(M, exact);
+    SD_CHECK(ci < kNumCfgs, "gemm_w4: bad configuration index");
+    const Cfg& c = kCfgs[ci];
+    SD_CHECK(c.exact == exact, "gemm_w4: configuration does not match the dequant mode");
+    const int bm = c.mt * 16, bn = 4 * c.nt * 16;
+    const int gx = (N + bn - 1) / bn, gy = (M + bm - 1) / bm;
+    const int steps = K / KSTEP;
+    // Split K until the grid covers the chip twice over, keeping >= 2 macro steps per split and
+    // the partials within the workspace.
+    int ks = 1;
+    while (gx * gy * ks < 512 && steps % (ks * 2) == 0 && steps / (ks * 2) >= 2 &&
+           (size_t)(ks * 2) * M * N <= ws.part_elems && (size_t)gx * gy <= ws.cnt_elems)
+        ks *= 2;
+    dim3 grid(gx, gy, ks);
+    hipLaunchKernelGGL(c.fn, grid, dim3(256), 0, st, A, W, S, Y, ws.part, ws.cnt, M, N, K, ks);
+    launched("gemm_w4");
+}
+
+}  // namespace sd

@@ -1,0 +1,22 @@
+// Pointer head (src/head.rs), CPU f64.
+#pragma once
+
+#include <algorithm>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace sd {
+
+struct Head {
+    std::map<std::string, std::vector<float>> t;
+    size_t dim = 0;
+    void load(const uint8_t* bytes, size_t len);
+    std::vector<double> project(const char* which, const float* x, size_t d) const;
+    // Option probabilities from rows [option 0 .. option n-2, answer], each d wide.
+    std::vector<double> probs(const float* hidden, size_t n_rows, size_t d, double temperature) const;
+};
+
+}  // namespace sd

@@ -1,0 +1,100 @@
+"""Engine-level parity on the GPU through the C ABI: forward vs the oracle's forward on the same
+seeded model, snapshot continuation vs a full forward (tests/engine_parity.rs:58-85), ask_all
+probabilities, error paths of Engine::forward (src/engine.rs:530-537)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+HIDDEN_TOL = 2e-2   # per-row activations / hidden states, absolute
+PROB_TOL = 2e-3     # answer probabilities, absolute
+
+
+@pytest.fixture(scope="module")
+def tiny(sdamd, tiny_model, oracle):
+    eng, head, cfg = sdamd.load_decider(tiny_model)
+    om = oracle.OracleModel(tiny_model)
+    yield eng, head, om
+    eng.free()
+
+
+def ids_for(seed, n, vocab=4096):
+    return np.random.default_rng(seed).integers(0, vocab, n).astype(np.uint32)
+
+
+@pytest.mark.parametrize("L", [1, 7, 20, 21, 64, 100, 300])
+def test_forward_matches_oracle(tiny, L):
+    eng, head, om = tiny
+    ids = ids_for(L, L)
+    rows = sorted({0, L // 2, L - 1})
+    got = eng.forward(ids, rows).hidden
+    want, _ = om.forward(ids, rows)
+    err = np.abs(got - want).max()
+    assert err < HIDDEN_TOL, f"L={L}: max |dh| {err}"
+
+
+def test_snapshot_continuation_matches_full_forward(tiny, oracle):
+    eng, head, om = tiny
+    state, q = ids_for(1, 150), ids_for(2, 40)
+    opts = [3, 10, 20]
+    rows = opts + [len(q) - 1]
+    prefix = eng.forward(state, [], keep=True).snapshot
+    assert prefix.len == 150
+    cached = eng.forward(q, rows, cache=prefix).hidden
+    full = eng.forward(np.concatenate([state, q]), [150 + r for r in rows]).hidden
+    assert np.abs(cached - full).max() < HIDDEN_TOL
+    pa, pb = head.probs(cached, cached.shape[1], 1.0), head.probs(full, full.shape[1], 1.0)
+    assert np.abs(pa - pb).max() < PROB_TOL
+    # the same snapshot twice in a row (the K/V prefix is not restored the second time)
+    again = eng.forward(q, rows, cache=prefix).hidden
+    np.testing.assert_array_equal(again, cached)
+    # the oracle's own continuation agrees with the GPU's
+    _, osnap = om.forward(state, [], keep=True)
+    ocached, _ = om.forward(q, rows, cache=osnap)
+    assert np.abs(cached - ocached).max() < HIDDEN_TOL
+    prefix.free()
+
+
+def test_ask_ids_matches_oracle(tiny, sdamd):
+    eng, head, om = tiny
+    state = ids_for(3, 120)
+    qs = [ids_for(10 + i, 30 + 5 * i) for i in range(3)]
+    options = [[2, 5], [1, 4, 9], [3, 6, 12, 18, 25]]
+    temps = [1.0, 0.7, 1.3]
+    got = sdamd.ask_ids(eng, head, state, qs, options, temps)
+    _, snap = om.forward(state, [], keep=True)
+    for q, o, t, g in zip(qs, options, temps, got):
+        rows = list(o) + [len(q) - 1]
+        h, _ = om.forward(q, rows, cache=snap)
+        want = om.probs(h, t)
+        assert np.abs(g - want).max() < PROB_TOL
+        assert int(np.argmax(g)) == int(np.argmax(want)) or np.sort(want)[-1] - np.sort(want)[-2] < PROB_TOL
+    # one question: a single forward of state ++ question
+    one = sdamd.ask_ids(eng, head, state, qs[:1], options[:1], temps[:1])[0]
+    assert np.abs(one - got[0]).max() < PROB_TOL
+
+
+def test_forward_errors(tiny, sdamd):
+    eng, head, om = tiny
+    with pytest.raises(sdamd.EngineError, match="must be 1 to 4096"):
+        eng.forward(np.zeros(0, np.uint32), [])
+    with pytest.raises(sdamd.EngineError, match="out of range"):
+        eng.forward(ids_for(4, 5), [5])
+    with pytest.raises(sdamd.EngineError, match="must be 1 to 4096"):
+        eng.forward(ids_for(5, 4097), [0])
+    snap = eng.forward(ids_for(6, 4000), [], keep=True).snapshot
+    with pytest.raises(sdamd.EngineError, match="context of 4100"):
+        eng.forward(ids_for(7, 100), [0], cache=snap)
+    snap.free()
+    # the engine still works after the errors
+    h = eng.forward(ids_for(8, 10), [9]).hidden
+    assert np.isfinite(h).all()
+
+
+def test_profile_labels(tiny):
+    eng, _, _ = tiny
+    prof = eng.profile(ids_for(9, 64))
+    labels = {k for k, _ in prof}
+    assert {"embed", "norm", "in_proj", "conv", "gdn", "gnorm", "out_proj", "qkv", "qk_prep", "attn", "o_proj",
+            "gate_up", "silu", "down"} <= labels
+    assert all(ms >= 0 for _, ms in prof)

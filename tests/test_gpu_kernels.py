@@ -1,0 +1,138 @@
+"""Kernel-level parity on the GPU: the int4 GEMM (BASELINE configs 0 and 1) and the gated delta
+rule (config 2), through the C ABI (sd_op_matmul / sd_op_gdn), against the C oracle."""
+import numpy as np
+import pytest
+
+from conftest import f16_ulp
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a):
+    """numpy array -> device bytes (torch is only the allocator here)."""
+    a = np.ascontiguousarray(a)
+    return torch.from_numpy(a.view(np.uint8).reshape(-1).copy()).cuda()
+
+
+def host(t, dtype, shape):
+    return t.cpu().numpy().view(dtype).reshape(shape)
+
+
+def gemm_case(synth, rng, M, N, K, lo=0, smin=0.005, smax=0.02):
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    W = synth.pack_nibbles(rng.integers(lo, 16, size=(N, K), dtype=np.uint32))
+    S = rng.uniform(smin, smax, size=(N, K // 32)).astype(np.float16)
+    return A, W, S
+
+
+def run_gemm(sdamd, A, W, S, M, N, K, exact, cfg=-1):
+    dA, dW, dS = dev(A), dev(W), dev(S)
+    dY = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
+    sdamd.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, exact, cfg)
+    torch.cuda.synchronize()
+    return host(dY, np.float16, (M, N))
+
+
+def check_gemm(oracle, A, W, S, Y, N, K, exact):
+    want = oracle.h2f(oracle.matmul(A.view(np.uint16), W, S.view(np.uint16), N, K, f16_deq=not exact))
+    got = Y.astype(np.float32)
+    err = np.abs(got - want)
+    tol = 1.01 * f16_ulp(want) + 2e-5
+    bad = err > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside 1 f16 ulp; max err {err.max()} at {np.argmax(err)}"
+
+
+# M <= 20 uses the reference GEMV's f32 dequant (exact), larger M the tiled kernel's f16 dequant.
+@pytest.mark.parametrize("M,N,K", [
+    (128, 6144, 2048),
+    (1, 64, 128), (5, 320, 256), (17, 200, 384), (40, 2048, 2048), (64, 8256, 2048),
+    (100, 1000, 512), (512, 2048, 6144), (300, 5120, 2048),
+])
+def test_gemm_matches_oracle(sdamd, synth, oracle, M, N, K):
+    rng = np.random.default_rng(M * 7919 + N * 31 + K)
+    A, W, S = gemm_case(synth, rng, M, N, K)
+    exact = M <= 20
+    Y = run_gemm(sdamd, A, W, S, M, N, K, exact)
+    check_gemm(oracle, A, W, S, Y, N, K, exact)
+
+
+def test_gemm_every_config(sdamd, synth, oracle):
+    """Each kernel configuration (tile shape, dequant mode) on ragged shapes."""
+    rng = np.random.default_rng(5)
+    cfg, ran = 0, 0
+    while True:
+        for (M, N, K) in [(3, 100, 256), (37, 330, 640), (130, 72, 1024)]:
+            A, W, S = gemm_case(synth, rng, M, N, K)
+            for exact in (False, True):
+                try:
+                    Y = run_gemm(sdamd, A, W, S, M, N, K, exact, cfg)
+                except sdamd.EngineError as e:
+                    if "no configuration" in str(e):
+                        assert cfg >= 2 and ran > 0
+                        return
+                    assert "does not match" in str(e)
+                    continue
+                check_gemm(oracle, A, W, S, Y, N, K, exact)
+                ran += 1
+        cfg += 1
+
+
+@pytest.mark.parametrize("M", [512, 8])
+def test_layer_gemm_set(sdamd, synth, oracle, M):
+    """q, k, v, o, gate, up, down of a 2048-wide layer at M = 512 and 8."""
+    rng = np.random.default_rng(M)
+    for (N, K) in [(2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (6144, 2048), (6144, 2048), (2048, 6144)]:
+        A, W, S = gemm_case(synth, rng, M, N, K)
+        exact = M <= 20
+        Y = run_gemm(sdamd, A, W, S, M, N, K, exact)
+        check_gemm(oracle, A, W, S, Y, N, K, exact)
+
+
+def gdn_case(rng, L, H, dk=128, dv=128, negA=-1.0, dtb=0.0, a_scale=1.0):
+    C = 2 * H * dk + H * dv
+    qkv = rng.standard_normal((L, C)).astype(np.float32)
+    stride = 2 * H
+    big = np.zeros((L, stride), np.float16)
+    big[:, :H] = (a_scale * rng.standard_normal((L, H))).astype(np.float16)  # a (decay input)
+    big[:, H:] = rng.standard_normal((L, H)).astype(np.float16)  # b (beta logit)
+    nA = np.full(H, negA, np.float32)
+    db = np.full(H, dtb, np.float32)
+    return qkv, big, stride, nA, db
+
+
+def run_gdn(sdamd, qkv, big, stride, nA, db, L, H, state0, load):
+    dq, db_, dn, dd = dev(qkv), dev(big), dev(nA), dev(db)
+    dst = dev(state0)
+    do = torch.empty(L * H * 128 * 4, dtype=torch.uint8, device="cuda")
+    sdamd.op_gdn(dq.data_ptr(), db_.data_ptr(), stride, 0, H, dn.data_ptr(), dd.data_ptr(), L, H, 128, 128,
+                 dst.data_ptr(), load, do.data_ptr())
+    torch.cuda.synchronize()
+    return host(do, np.float32, (L, H * 128)), host(dst, np.float32, state0.shape)
+
+
+def oracle_gdn(oracle, qkv, big, stride, nA, db, L, H, state0, load):
+    import ctypes
+    st = state0.copy()
+    o = np.empty((L, H * 128), np.float32)
+    I = ctypes.c_int
+    oracle.lib().or_gdn(oracle.P(qkv), oracle.P(big.view(np.uint16)), I(stride), I(0), I(H), oracle.P(nA),
+                        oracle.P(db), I(L), I(H), I(128), I(128), oracle.P(st), I(int(load)), oracle.P(o))
+    return o, st
+
+
+@pytest.mark.parametrize("L,H,load,negA,a_scale", [
+    (512, 16, False, -1.0, 1.0),
+    (1, 2, False, -1.0, 1.0), (3, 2, True, -1.0, 1.0), (63, 2, False, -1.0, 1.0), (64, 2, True, -1.0, 1.0),
+    (65, 2, False, -1.0, 1.0), (130, 4, True, -1.0, 1.0), (200, 2, True, -16.0, 3.0),
+])
+def test_gdn_matches_sequential_oracle(sdamd, oracle, L, H, load, negA, a_scale):
+    """The chunked recurrence equals the reference's token-by-token recurrence (fp32)."""
+    rng = np.random.default_rng(L * 131 + H)
+    qkv, big, stride, nA, db = gdn_case(rng, L, H, negA=negA, a_scale=a_scale)
+    state0 = (0.1 * rng.standard_normal((H, 128, 128))).astype(np.float32)
+    o, st = run_gdn(sdamd, qkv, big, stride, nA, db, L, H, state0, load)
+    wo, wst = oracle_gdn(oracle, qkv, big, stride, nA, db, L, H, state0, load)
+    np.testing.assert_allclose(o, wo, rtol=2e-4, atol=2e-4)
+    np.testing.assert_allclose(st, wst, rtol=2e-4, atol=2e-4)
