@@ -39,7 +39,8 @@ const sd::Head* Hd(const sd_head* h) { return reinterpret_cast<const sd::Head*>(
 // Device workspace for the kernel-level entry points (grown on demand, kept until exit).
 struct OpWs {
     std::mutex mu;
-    sd::GemmWs gemm;
+    float* part = nullptr;
+    size_t part_floats = 0;
     float* gdn = nullptr;
     size_t gdn_floats = 0;
 };
@@ -165,17 +166,28 @@ int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, 
     return guarded(err, errlen, [&] {
         if (!A || !Wq || !Sc || !Y) throw sd::Error("sd_op_matmul: null argument");
         if (cfg >= sd::gemm_w4_configs()) throw sd::Error("sd_op_matmul: no configuration " + std::to_string(cfg));
+        if (M < 1 || N < 1 || K < 128 || K % 128) throw sd::Error("sd_op_matmul: need M, N >= 1 and K a multiple of 128");
         OpWs& w = op_ws();
         std::lock_guard<std::mutex> lock(w.mu);
-        if (!w.gemm.part) {
-            w.gemm.part_elems = size_t(32) << 20;
-            w.gemm.cnt_elems = 65536;
-            SD_HIP(hipMalloc(&w.gemm.part, w.gemm.part_elems * 4));
-            SD_HIP(hipMalloc(&w.gemm.cnt, w.gemm.cnt_elems * 4));
-            SD_HIP(hipMemset(w.gemm.cnt, 0, w.gemm.cnt_elems * 4));
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        const int c = cfg >= 0 ? cfg : sd::gemm_w4_cfg(M, exact != 0);
+        const size_t cap = size_t(64) << 20;
+        const int ks = sd::gemm_w4_split(M, N, K, c, 256, cap);
+        const auto* a = static_cast<const sd::f16*>(A);
+        const auto* wq = static_cast<const uint32_t*>(Wq);
+        const auto* sc = static_cast<const sd::f16*>(Sc);
+        if (ks == 1) {
+            sd::gemm_w4(a, wq, sc, static_cast<sd::f16*>(Y), nullptr, M, N, K, exact != 0, 1, st, c);
+            return;
         }
-        sd::gemm_w4(static_cast<const sd::f16*>(A), static_cast<const uint32_t*>(Wq), static_cast<const sd::f16*>(Sc),
-                    static_cast<sd::f16*>(Y), M, N, K, exact != 0, w.gemm, static_cast<hipStream_t>(stream), cfg);
+        if (w.part_floats < (size_t)ks * M * N) {
+            if (w.part) SD_HIP(hipFree(w.part));
+            w.part = nullptr;
+            SD_HIP(hipMalloc(&w.part, cap * 4));
+            w.part_floats = cap;
+        }
+        sd::gemm_w4(a, wq, sc, nullptr, w.part, M, N, K, exact != 0, ks, st, c);
+        sd::reduce_partials(w.part, ks, (size_t)M * N, static_cast<sd::f16*>(Y), st);
     });
 }
 

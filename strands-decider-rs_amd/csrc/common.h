@@ -43,25 +43,32 @@ void launched(const char* what);
 // Y[M,N] f16 = A[M,K] f16 . deq(W[N,K])^T with W int4 group-32 symmetric in the reference's
 // layout ([N][K/32] blocks of 4 u32, element e in word e/8 at bits 4(e%8), value (q-8)*scale,
 // scales [N][K/32] f16).  `exact` selects the f32-dequant arithmetic of the reference's GEMV
-// path (used for M <= 20), otherwise the f16 dequant of its tiled path.  `ws`/`cnt` are the
-// split-K workspace (f32) and self-resetting tile counters (zeroed once at allocation).
-struct GemmWs {
-    float* part = nullptr;
-    size_t part_elems = 0;
-    uint32_t* cnt = nullptr;
-    size_t cnt_elems = 0;
-};
-void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, int M, int N, int K, bool exact,
-             const GemmWs& ws, hipStream_t st, int force_cfg = -1);
-// Number of selectable kernel configurations (for tests and tuning sweeps).
+// path (used for M <= 20), otherwise the f16 dequant of its tiled path.  With `part` non-null the
+// k range is split over ks workgroups that write f32 partials part[ks][M][N] instead of Y (ks = 1
+// allowed); the consumer sums them in slot order (add_norm, or reduce_partials).  cfg < 0 picks
+// the tile shape by M.
+void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part, int M, int N, int K, bool exact,
+             int ks, hipStream_t st, int cfg = -1);
 int gemm_w4_configs();
+int gemm_w4_cfg(int M, bool exact);
+// Split count that brings the grid to about target_groups workgroups (power of 2, <= 8).
+int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_part_elems);
+void reduce_partials(const float* part, int ks, size_t n, f16* Y, hipStream_t st);
 
 // ---- elementwise / norms (elem.hip) ----------------------------------------------------------
 void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f16* Bi, int d, int bits,
            int group, bool asym, float* x, hipStream_t st);
-// x[rows[r]] += y (if y), h[r] = rmsnorm(x[rows[r]]) * w -> f16 (h16) or f32 (h32); rows null = identity.
-void add_norm(float* x, const f16* y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16,
-              float* h32, hipStream_t st);
+// The sublayer output to add: f16 rows y16, or ks f32 partial slots yp[ks][L][d] whose slot-order
+// sum rounded to f16 is the same value (null both: no add).
+struct YIn {
+    const f16* y16 = nullptr;
+    const float* yp = nullptr;
+    int ks = 0;
+    size_t slot = 0;  // elements per slot (L * d)
+};
+// x[rows[r]] += y, h[r] = rmsnorm(x[rows[r]]) * w -> f16 (h16) or f32 (h32); rows null = identity.
+void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16, float* h32,
+              hipStream_t st);
 void silu_mul(const f16* big, int L, int I, f16* mid, hipStream_t st);
 void add_bias(f16* y, int L, int N, const float* c, hipStream_t st);
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);

@@ -35,8 +35,11 @@ __global__ void k_embed(const uint32_t* __restrict__ ids, int L, const uint32_t*
 }
 
 // One workgroup (256 threads) per output row; D = d / 256 values per thread.
+// The sublayer output y is f16 rows, or ks f32 partial slots whose slot-order sum rounded to f16
+// is that same f16 value.
 template <int D>
 __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f16* __restrict__ y,
+                                                  const float* __restrict__ yp, int ks, size_t slot,
                                                   const float* __restrict__ w, const uint32_t* __restrict__ rows,
                                                   f16* __restrict__ h16, float* __restrict__ h32) {
     constexpr int d = D * 256;
@@ -52,6 +55,11 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
         float a = xr[c];
         if (y) {
             a += (float)y[row * d + c];
+            xr[c] = a;
+        } else if (yp) {
+            float s = yp[row * d + c];
+            for (int z = 1; z < ks; z++) s += yp[z * slot + row * d + c];
+            a += (float)(f16)s;
             xr[c] = a;
         }
         v[i] = a;
@@ -110,12 +118,15 @@ void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f1
     launched("embed");
 }
 
-void add_norm(float* x, const f16* y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16, float* h32,
+void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16, float* h32,
               hipStream_t st) {
     if (nrows == 0) return;
     switch (d) {
-#define SD_CASE(D) \
-    case D * 256: hipLaunchKernelGGL(k_add_norm<D>, dim3(nrows), dim3(256), 0, st, x, y, w, rows, h16, h32); break;
+#define SD_CASE(D)                                                                                                  \
+    case D * 256:                                                                                                   \
+        hipLaunchKernelGGL(k_add_norm<D>, dim3(nrows), dim3(256), 0, st, x, y.y16, y.yp, y.ks, y.slot, w, rows, h16, \
+                           h32);                                                                                    \
+        break;
         SD_CASE(1) SD_CASE(2) SD_CASE(3) SD_CASE(4) SD_CASE(5) SD_CASE(6) SD_CASE(8) SD_CASE(10) SD_CASE(12)
         SD_CASE(16) SD_CASE(20) SD_CASE(24) SD_CASE(32)
 #undef SD_CASE

@@ -316,7 +316,7 @@ void Engine::ensure_pool(int l) {
     const int orow = std::max({cfg.H * cfg.dv, cfg.hq * cfg.hd, cfg.d});
     GdnShape gs{cfg.H, cfg.dk, cfg.dv, 0, 0, 0, 0, C};
     AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, 0, SD_CONTEXT};
-    const size_t gemm_part = size_t(32) << 20, gemm_cnt = 65536;
+    const size_t ypart = (size_t)8 * cap * cfg.d;
     const size_t sizes[] = {
         (size_t)cap * 4,                               // ids
         (size_t)cap * 4,                               // rows
@@ -332,8 +332,7 @@ void Engine::ensure_pool(int l) {
         (size_t)cap * cfg.d * 4,                       // out
         gdn_ws_floats(cap, gs) * 4,                    // GDN chunk workspace
         attn_ws_floats(std::min(cap, 256), as) * 4,    // attention key-split workspace
-        gemm_part * 4,                                 // GEMM split-K partials
-        gemm_cnt * 4,                                  // GEMM tile counters
+        ypart * 4,                                     // split-K partials of y
     };
     size_t total = 0;
     for (size_t s : sizes) total += align256(s);
@@ -362,11 +361,8 @@ void Engine::ensure_pool(int l) {
     gdn_ws_carve((float*)ptrs[12], cap, gs, pool.gdn);
     pool.attn_ws = (float*)ptrs[13];
     pool.attn_rows = std::min(cap, 256);
-    pool.gemm.part = (float*)ptrs[14];
-    pool.gemm.part_elems = gemm_part;
-    pool.gemm.cnt = (uint32_t*)ptrs[15];
-    pool.gemm.cnt_elems = gemm_cnt;
-    SD_HIP(hipMemset(pool.gemm.cnt, 0, gemm_cnt * 4));
+    pool.ypart = (float*)ptrs[14];
+    pool.ypart_elems = ypart;
     SD_HIP(hipMemset(pool.x, 0, (size_t)cap * cfg.d * 4));
     if (ids_h_cap < cap) {
         ids_h = static_cast<uint32_t*>(halloc((size_t)cap * 4));
@@ -379,8 +375,22 @@ void Engine::ensure_pool(int l) {
 void Engine::mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L) {
     // The reference's GEMV (f32 dequant) serves M <= 20 and N % 64 != 0 (src/engine.rs:419-442).
     const bool exact = L <= 20 || m.N % 64 != 0;
-    const GemmWs ws = pool.gemm;
-    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, L, m.N, m.K, exact, ws, s); }});
+    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, nullptr, L, m.N, m.K, exact, 1, s); }});
+}
+
+YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L) {
+    // A projection whose output only feeds the residual add: split K until the grid covers the
+    // chip, the add + RMSNorm sums the partials.
+    const bool exact = L <= 20 || m.N % 64 != 0;
+    const int cfg_ = gemm_w4_cfg(L, exact);
+    const int ks = gemm_w4_split(L, m.N, m.K, cfg_, 256, pool.ypart_elems);
+    float* part = pool.ypart;
+    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, nullptr, part, L, m.N, m.K, exact, ks, s, cfg_); }});
+    YIn y;
+    y.yp = part;
+    y.ks = ks;
+    y.slot = (size_t)L * m.N;
+    return y;
 }
 
 Plan& Engine::plan(int L) {
@@ -395,13 +405,18 @@ Plan& Engine::plan(int L) {
     const EmbedW E = emb;
     const uint32_t* luv = lu;
     steps.push_back({"embed", [=](hipStream_t s) { embed(P.ids, L, E.q, E.s, E.b, d, E.bits, E.group, E.asym, P.x, s); }});
+    YIn y;  // the sublayer output the next add + norm consumes (none before layer 0)
     for (size_t i = 0; i < layers.size(); i++) {
         const LayerW W = layers[i];
-        const f16* yin = i > 0 ? P.y : nullptr;
-        steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.in_norm, d, nullptr, L, P.h, nullptr, s); }});
+        {
+            const YIn yin = y;
+            steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.in_norm, d, nullptr, L, P.h, nullptr, s); }});
+        }
         if (W.kind == SD_ADAPTER) {
             mm(steps, "proj", P.h, W.proj, P.y, L);
             steps.push_back({"bias", [=](hipStream_t s) { add_bias(P.y, L, d, W.bias, s); }});
+            y = YIn{};
+            y.y16 = P.y;
             continue;
         }
         if (W.kind == SD_LINEAR_ATTENTION) {
@@ -412,7 +427,7 @@ Plan& Engine::plan(int L) {
             steps.push_back({"gdn", [=](hipStream_t s) { gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, W.hist, s); }});
             steps.push_back({"gdn", [=](hipStream_t s) { gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, s); }});
             steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
-            mm(steps, "out_proj", P.o, W.out_proj, P.y, L);
+            y = mm_y(steps, "out_proj", P.o, W.out_proj, L);
         } else {
             const AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, W.qkv.N, SD_CONTEXT};
             const float* rp = rope;
@@ -423,13 +438,17 @@ Plan& Engine::plan(int L) {
             if (L <= P.attn_rows)
                 while (ks < 8 && nb * cfg.hq * ks < 256) ks *= 2;
             steps.push_back({"attn", [=](hipStream_t s) { attention_split(P.q, W.kc, W.vc, P.big, as, L, luv, ks, P.attn_ws, P.o, s); }});
-            mm(steps, "o_proj", P.o, W.o_proj, P.y, L);
+            y = mm_y(steps, "o_proj", P.o, W.o_proj, L);
         }
-        steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, P.y, W.post_norm, d, nullptr, L, P.h, nullptr, s); }});
+        {
+            const YIn yin = y;
+            steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.post_norm, d, nullptr, L, P.h, nullptr, s); }});
+        }
         mm(steps, "gate_up", P.h, W.gate_up, P.big, L);
         steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, L, I, P.mid, s); }});
-        mm(steps, "down", P.mid, W.down, P.y, L);
+        y = mm_y(steps, "down", P.mid, W.down, L);
     }
+    pl.last_y = y;
     if (use_graphs) {
         SD_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         try {
@@ -494,7 +513,7 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
     } else {
         for (auto& s : pl.steps) s.run(st);
     }
-    if (n_rows) add_norm(pool.x, pool.y, final_norm, cfg.d, pool.rows, (int)n_rows, nullptr, pool.out, st);
+    if (n_rows) add_norm(pool.x, pl.last_y, final_norm, cfg.d, pool.rows, (int)n_rows, nullptr, pool.out, st);
     if (timed) SD_HIP(hipEventRecord(ev1, st));
     if (n_rows) SD_HIP(hipMemcpyAsync(out_h, pool.out, n_rows * cfg.d * 4, hipMemcpyDeviceToHost, st));
     Snapshot* snap = nullptr;

@@ -67,7 +67,8 @@ struct Pool {
     GdnWs gdn;
     float* attn_ws = nullptr;
     int attn_rows = 0;
-    GemmWs gemm;
+    float* ypart = nullptr;  // split-K partials of the projections that feed the residual add
+    size_t ypart_elems = 0;
 };
 
 struct Step {
@@ -79,6 +80,7 @@ struct Step {
 struct Plan {
     int L = 0;
     std::vector<Step> steps;
+    YIn last_y;  // where the last sublayer output lives (read by the final norm)
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     void destroy();
@@ -148,6 +150,7 @@ struct Engine {
     void ensure_pool(int l);
     Plan& plan(int L);
     void mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L);
+    YIn mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L);
 };
 
 }  // namespace sd

@@ -19,8 +19,10 @@
 //    2^-24 with at most 5 significant bits), and both are fed to the MFMA;
 //  * A (activations, f16) is staged once per workgroup per macro step in LDS (shared by the 4
 //    waves) with a register prefetch of the next step; B for the next step is prefetched too;
-//  * split-K over workgroups writes f32 partials; the last workgroup of a tile (self-resetting
-//    counter) sums them in a fixed order and writes f16, so results do not depend on timing.
+//  * split-K over workgroups writes f32 partials [ks][M][N] with plain stores and no cross-
+//    workgroup synchronisation (on MI355X a device-scope fence writes back the whole XCD L2); the
+//    consumer sums the ks slots in a fixed order: the residual add + RMSNorm does it for the
+//    projections that feed it, `reduce_partials` for everything else.
 #include "common.h"
 
 namespace sd {
@@ -48,20 +50,14 @@ __device__ __forceinline__ u32x4 perm_a(u32x4 d) {
     return o;
 }
 
-__device__ __forceinline__ float ld_coherent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-template <int MT, int NT, bool EXACT>
+template <int MT, int NT, bool EXACT, bool PARTIAL>
 __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, const uint32_t* __restrict__ W,
                                                  const f16* __restrict__ S, f16* __restrict__ Y,
-                                                 float* __restrict__ part, uint32_t* __restrict__ cnt, int M,
-                                                 int N, int K, int ksplit) {
+                                                 float* __restrict__ part, int M, int N, int K, int ksplit) {
     constexpr int BM = MT * 16;
     constexpr int BN = 4 * NT * 16;
     constexpr int ACH = BM * 16 / 256;  // 16-byte A chunks per thread per macro step (== MT)
     __shared__ __attribute__((aligned(16))) f16 As[BM * LDA];
-    __shared__ int last_flag;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
@@ -169,7 +165,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
     }
 
     // Output: acc[a][t][r] is row m0 + 16a + 4g + r, column ncol[t].
-    if (ksplit == 1) {
+    if constexpr (!PARTIAL) {
 #pragma unroll
         for (int a = 0; a < MT; a++)
 #pragma unroll
@@ -191,39 +187,36 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
                 const int m = m0 + a * 16 + g * 4 + r;
                 if (m < M && nok[t]) mine[(size_t)m * N + ncol[t]] = acc[a][t][r];
             }
-    __threadfence();
-    __syncthreads();
-    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
-    if (tid == 0) {
-        const uint32_t old = atomicAdd(&cnt[tile], 1u);
-        last_flag = old == (uint32_t)(ksplit - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-#pragma unroll
-    for (int a = 0; a < MT; a++)
-#pragma unroll
-        for (int t = 0; t < NT; t++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + a * 16 + g * 4 + r;
-                if (m < M && nok[t]) {
-                    float sum = 0.f;
-                    for (int z = 0; z < ksplit; z++) sum += ld_coherent(part + ((size_t)z * M + m) * N + ncol[t]);
-                    Y[(size_t)m * N + ncol[t]] = (f16)sum;
-                }
-            }
-    if (tid == 0) cnt[tile] = 0u;
 }
 
+// Y[i] = f16(sum_z part[z][i]) in slot order.
+__global__ void k_reduce_partials(const float* __restrict__ part, int ks, size_t n, f16* __restrict__ Y) {
+    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= n) return;
+    if (i + 4 <= n && (n & 3) == 0) {
+        float4 s = *reinterpret_cast<const float4*>(part + i);
+        for (int z = 1; z < ks; z++) {
+            const float4 v = *reinterpret_cast<const float4*>(part + (size_t)z * n + i);
+            s.x += v.x, s.y += v.y, s.z += v.z, s.w += v.w;
+        }
+        *reinterpret_cast<f16x4*>(Y + i) = f16x4{(f16)s.x, (f16)s.y, (f16)s.z, (f16)s.w};
+        return;
+    }
+    for (size_t e = i; e < n && e < i + 4; e++) {
+        float s = part[e];
+        for (int z = 1; z < ks; z++) s += part[(size_t)z * n + e];
+        Y[e] = (f16)s;
+    }
+}
+
+typedef void (*GemmFn)(const f16*, const uint32_t*, const f16*, f16*, float*, int, int, int, int);
 struct Cfg {
     int mt, nt;
     bool exact;
-    void (*fn)(const f16*, const uint32_t*, const f16*, f16*, float*, uint32_t*, int, int, int, int);
+    GemmFn f16_out, part_out;
 };
 
-#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX>}
+#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX, false>, k_gemm_w4<MT, NT, EX, true>}
 const Cfg kCfgs[] = {
     SD_CFG(1, 1, true), SD_CFG(2, 1, true),                                           // M <= 20: f32 dequant
     SD_CFG(1, 1, false), SD_CFG(2, 1, false), SD_CFG(3, 1, false), SD_CFG(4, 1, false),  // skinny
@@ -245,25 +238,39 @@ int pick_cfg(int M, bool exact) {
 
 int gemm_w4_configs() { return kNumCfgs; }
 
-void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, int M, int N, int K, bool exact,
-             const GemmWs& ws, hipStream_t st, int force_cfg) {
+int gemm_w4_cfg(int M, bool exact) { return pick_cfg(M, exact); }
+
+int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_part_elems) {
+    const Cfg& c = kCfgs[cfg];
+    const int bm = c.mt * 16, bn = 4 * c.nt * 16;
+    const int groups = ((N + bn - 1) / bn) * ((M + bm - 1) / bm);
+    const int steps = K / KSTEP;
+    int ks = 1;
+    while (groups * ks < target_groups && ks < 8 && steps % (ks * 2) == 0 && steps / (ks * 2) >= 2 &&
+           (size_t)(ks * 2) * M * N <= max_part_elems)
+        ks *= 2;
+    return ks;
+}
+
+void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part, int M, int N, int K, bool exact,
+             int ks, hipStream_t st, int cfg) {
     SD_CHECK(M >= 1 && N >= 1 && K >= KSTEP && K % KSTEP == 0, "gemm_w4: need M, N >= 1 and K a multiple of 128");
-    int ci = force_cfg >= 0 ? force_cfg : pick_cfg(M, exact);
+    const int ci = cfg >= 0 ? cfg : pick_cfg(M, exact);
     SD_CHECK(ci < kNumCfgs, "gemm_w4: bad configuration index");
     const Cfg& c = kCfgs[ci];
     SD_CHECK(c.exact == exact, "gemm_w4: configuration does not match the dequant mode");
+    SD_CHECK(ks >= 1 && (K / KSTEP) % ks == 0, "gemm_w4: split count must divide the k steps");
+    SD_CHECK(part || (Y && ks == 1), "gemm_w4: split-K writes partials and needs a partial buffer");
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
-    const int gx = (N + bn - 1) / bn, gy = (M + bm - 1) / bm;
-    const int steps = K / KSTEP;
-    // Split K until the grid covers the chip twice over, keeping >= 2 macro steps per split and
-    // the partials within the workspace.
-    int ks = 1;
-    while (gx * gy * ks < 512 && steps % (ks * 2) == 0 && steps / (ks * 2) >= 2 &&
-           (size_t)(ks * 2) * M * N <= ws.part_elems && (size_t)gx * gy <= ws.cnt_elems)
-        ks *= 2;
-    dim3 grid(gx, gy, ks);
-    hipLaunchKernelGGL(c.fn, grid, dim3(256), 0, st, A, W, S, Y, ws.part, ws.cnt, M, N, K, ks);
+    dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, ks);
+    hipLaunchKernelGGL(part ? c.part_out : c.f16_out, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks);
     launched("gemm_w4");
+}
+
+void reduce_partials(const float* part, int ks, size_t n, f16* Y, hipStream_t st) {
+    const size_t threads = (n + 3) / 4;
+    hipLaunchKernelGGL(k_reduce_partials, dim3((threads + 255) / 256), dim3(256), 0, st, part, ks, n, Y);
+    launched("reduce_partials");
 }
 
 }  // namespace sd

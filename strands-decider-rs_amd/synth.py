@@ -11,7 +11,8 @@ Layouts written (the reference's, src/kernels.rs:550-586, 640-709; src/engine.rs
   * attention qkv rows: [q head s (hd) | gate head s (hd)] for each q head, then K heads, V heads;
   * gate_up rows: [gate (I) | up (I)].
 
-Value distributions (seeded per tensor name): codes uniform in 1..15 (values -7..7); scales uniform in
+Value distributions (seeded per tensor name): uniform nibbles with code 0 remapped to 8 (values -7..7,
+zero mean); scales uniform in
 [0.5, 1] * s0 / sqrt(K) (s0 chosen so a sublayer's output has roughly unit scale); norm weights
 1 + 0.1 N(0,1) (the reference bakes "1 + w" into the file); conv taps N(0, 0.5); A_log-style decay
 negA = -U(0, 16) and dt_bias = 1 (Qwen's initialisation); head projections N(0, 1/d).
@@ -72,11 +73,16 @@ def pack_nibbles(q: np.ndarray) -> np.ndarray:
     return w.reshape(*q.shape[:-2], q.shape[-2] // 4, 4)
 
 
-def quant(rng: np.random.Generator, n: int, k: int, s0: float = S0, lo: int = 1):
-    """int4 g32 codes [N][K/32][4] u32 (values q - 8 uniform in lo-8..7) and fp16 scales [N][K/32].
-    The model uses lo = 1 (values -7..7, zero mean, so a 24-layer residual stream stays bounded);
-    the single-GEMM configs use lo = 0 (-8..7)."""
-    codes = pack_nibbles(rng.integers(lo, 16, size=(n, k), dtype=np.uint32))
+# byte -> byte with each zero nibble replaced by 8
+_NIB_FIX = np.array([((b & 15) or 8) | (((b >> 4) or 8) << 4) for b in range(256)], np.uint8)
+
+
+def quant(rng: np.random.Generator, n: int, k: int, s0: float = S0):
+    """int4 g32 codes [N][K/32][4] u32 and fp16 scales [N][K/32].  Codes are uniform nibbles with
+    code 0 (value -8) replaced by code 8 (value 0): values -7..7, zero mean, so a 24-layer residual
+    stream stays bounded."""
+    b = rng.integers(0, np.iinfo(np.uint64).max, size=n * k // 16, dtype=np.uint64, endpoint=True).view(np.uint8)
+    codes = _NIB_FIX[b].view(np.uint32).reshape(n, k // 32, 4)
     scales = (rng.uniform(0.5, 1.0, size=(n, k // 32)) * (s0 / np.sqrt(k))).astype(np.float16)
     return codes, scales
 
@@ -138,7 +144,7 @@ def write_model(out_dir: str, cfg: dict | None = None, vocab: int = 4096, seed: 
                 head_dim_out: int = 256, temperature: float = 1.0) -> str:
     """Writes a seeded model directory; returns it.  Skips the work if the same model is there."""
     cfg = dict(CONFIG_TINY if cfg is None else cfg)
-    key = hashlib.sha1(json.dumps([cfg, vocab, seed, head_dim_out, temperature, 3], sort_keys=True).encode()).hexdigest()
+    key = hashlib.sha1(json.dumps([cfg, vocab, seed, head_dim_out, temperature, 5], sort_keys=True).encode()).hexdigest()
     stamp = os.path.join(out_dir, ".synth")
     if os.path.exists(stamp) and open(stamp).read() == key:
         return out_dir
