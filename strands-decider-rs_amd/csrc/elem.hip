@@ -37,9 +37,9 @@ __global__ void k_embed(const uint32_t* __restrict__ ids, int L, const uint32_t*
 // One workgroup (256 threads) per output row; D = d / 256 values per thread.
 // The sublayer output y is f16 rows, or ks f32 partial slots whose slot-order sum rounded to f16
 // is that same f16 value.
-template <int D>
+template <int D, int KS>
 __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f16* __restrict__ y,
-                                                  const float* __restrict__ yp, int ks, size_t slot,
+                                                  const float* __restrict__ yp, size_t slot,
                                                   const float* __restrict__ w, const uint32_t* __restrict__ rows,
                                                   f16* __restrict__ h16, float* __restrict__ h32) {
     constexpr int d = D * 256;
@@ -48,18 +48,32 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
     const size_t row = rows ? rows[r] : (size_t)r;
     float* xr = x + row * d;
     float v[D];
+    float part[D][KS > 0 ? KS : 1];
+    // issue every load of the row before using any
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+        const int c = threadIdx.x + 256 * i;
+        v[i] = xr[c];
+        if constexpr (KS > 0) {
+#pragma unroll
+            for (int z = 0; z < KS; z++) part[i][z] = yp[z * slot + row * d + c];
+        } else {
+            part[i][0] = y ? (float)y[row * d + c] : 0.f;
+        }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < D; i++) {
         const int c = threadIdx.x + 256 * i;
-        float a = xr[c];
-        if (y) {
-            a += (float)y[row * d + c];
-            xr[c] = a;
-        } else if (yp) {
-            float s = yp[row * d + c];
-            for (int z = 1; z < ks; z++) s += yp[z * slot + row * d + c];
+        float a = v[i];
+        if constexpr (KS > 0) {
+            float s = part[i][0];
+#pragma unroll
+            for (int z = 1; z < KS; z++) s += part[i][z];
             a += (float)(f16)s;
+            xr[c] = a;
+        } else if (y) {
+            a += part[i][0];
             xr[c] = a;
         }
         v[i] = a;
@@ -121,17 +135,20 @@ void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f1
 void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16, float* h32,
               hipStream_t st) {
     if (nrows == 0) return;
-    switch (d) {
-#define SD_CASE(D)                                                                                                  \
-    case D * 256:                                                                                                   \
-        hipLaunchKernelGGL(k_add_norm<D>, dim3(nrows), dim3(256), 0, st, x, y.y16, y.yp, y.ks, y.slot, w, rows, h16, \
-                           h32);                                                                                    \
-        break;
-        SD_CASE(1) SD_CASE(2) SD_CASE(3) SD_CASE(4) SD_CASE(5) SD_CASE(6) SD_CASE(8) SD_CASE(10) SD_CASE(12)
-        SD_CASE(16) SD_CASE(20) SD_CASE(24) SD_CASE(32)
-#undef SD_CASE
-        default: throw Error("add_norm: hidden size " + std::to_string(d) + " is not supported");
+    const int ks = y.yp ? y.ks : 0;
+    SD_CHECK(ks == 0 || ks == 1 || ks == 2 || ks == 4 || ks == 8, "add_norm: unsupported partial count");
+    bool done = false;
+#define SD_CASE(D, KS)                                                                                            \
+    if (!done && d == D * 256 && ks == KS) {                                                                      \
+        hipLaunchKernelGGL((k_add_norm<D, KS>), dim3(nrows), dim3(256), 0, st, x, y.y16, y.yp, y.slot, w, rows, h16, \
+                           h32);                                                                                  \
+        done = true;                                                                                              \
     }
+#define SD_KS(D) SD_CASE(D, 0) SD_CASE(D, 1) SD_CASE(D, 2) SD_CASE(D, 4) SD_CASE(D, 8)
+    SD_KS(1) SD_KS(2) SD_KS(3) SD_KS(4) SD_KS(6) SD_KS(8) SD_KS(10) SD_KS(12) SD_KS(16)
+#undef SD_KS
+#undef SD_CASE
+    if (!done) throw Error("add_norm: hidden size " + std::to_string(d) + " is not supported");
     launched("add_norm");
 }
 

@@ -130,7 +130,11 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         kinds.push_back(k);
     }
     if (c->unrotate) unrotate.assign(c->unrotate, c->unrotate + cfg.d);
-    SD_CHECK(cfg.d % 256 == 0 && cfg.d <= 8192, "hidden_size must be a multiple of 256 (at most 8192)");
+    {
+        const int dd = cfg.d / 256;
+        SD_CHECK(cfg.d % 256 == 0 && (dd <= 4 || dd == 6 || dd == 8 || dd == 10 || dd == 12 || dd == 16),
+                 "hidden_size must be 256 x {1, 2, 3, 4, 6, 8, 10, 12, 16}");
+    }
 
     for (size_t i = 0; i < nt; i++) {
         const sd_tensor& t = ts[i];

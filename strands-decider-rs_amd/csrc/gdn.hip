@@ -12,15 +12,15 @@
 //  * gdn_prep: one workgroup per (chunk, head), fully parallel: norms, decays, A (blocked 16x16
 //    inversion of I - A), W, U, Qk, qn e^G, (kn e^(G_last - G))^T.  Block (0,0) also performs the
 //    reference's hist_update (the conv already consumed the old history).
-//  * gdn_scan: one workgroup per (head, 16 value columns), sequential over chunks; the state
-//    slice lives in LDS.
+//  * gdn_scan: one workgroup per (head, 8 value columns), sequential over chunks; the state
+//    slice lives in LDS, each chunk's operands are staged in LDS by one pass of coalesced loads.
 #include "common.h"
 
 namespace sd {
 namespace {
 
-constexpr int CH = 64;   // chunk length
-constexpr int DVS = 16;  // value columns per scan workgroup
+constexpr int CH = 64;  // chunk length
+constexpr int DVS = 8;  // value columns per scan workgroup
 
 __device__ __forceinline__ float warp_sum4(float v) {  // sum over aligned groups of 4 lanes
     v += __shfl_xor(v, 1);
@@ -51,10 +51,12 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
                                                   const float* __restrict__ dtb, int L, GdnWs ws, f16* hist) {
     static_assert(DK == 128 && DV == 128, "gdn_prep is written for 128-wide heads");
     constexpr int KP = DK + 4;  // padded LDS row
-    __shared__ __attribute__((aligned(16))) float Ks[CH * KP];  // kn rows, later v rows
+    __shared__ __attribute__((aligned(16))) float Qs[CH * KP];  // q rows, then qn
+    __shared__ __attribute__((aligned(16))) float Ks[CH * KP];  // k rows, then kn
+    __shared__ __attribute__((aligned(16))) float Vs[CH * KP];  // v rows
     __shared__ float Ts[CH][CH + 1];                           // A, then T = (I - A)^-1
     __shared__ float Xs[16][17];
-    __shared__ float rq[CH], beta[CH], G[CH], eG[CH];
+    __shared__ float rq[CH], rk[CH], beta[CH], G[CH], eG[CH];
 
     const int tid = threadIdx.x;
     const int c = blockIdx.x, h = blockIdx.y, H = gridDim.y;
@@ -68,32 +70,19 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     float* KgT = ws.kg + wsb * CH * DK;
     float* Qk = ws.qk + wsb * CH * CH;
 
-    // ---- phase 0: norms, kn rows into LDS, gates, cumulative decay
-    {
-        const int i = tid >> 2, p = tid & 3;
-        float kr[32];
-        float sq = 0.f, sk = 0.f;
+    // ---- phase 0: the chunk's q, k, v rows into LDS in one pass of coalesced loads; gates
+    for (int e = tid; e < CH * DK / 4; e += 256) {
+        const int i = e / (DK / 4), c4 = (e % (DK / 4)) * 4;
+        float4 q4 = {0.f, 0.f, 0.f, 0.f}, k4 = q4, v4 = q4;
         if (i < Lc) {
-            const float* qrow = qkvc + (size_t)(t0 + i) * C + h * DK + p * 32;
-            const float* krow = qkvc + (size_t)(t0 + i) * C + sh.H * DK + h * DK + p * 32;
-#pragma unroll
-            for (int e = 0; e < 32; e += 4) {
-                const float4 q4 = *reinterpret_cast<const float4*>(qrow + e);
-                const float4 k4 = *reinterpret_cast<const float4*>(krow + e);
-                sq += q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w;
-                sk += k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w;
-                kr[e] = k4.x, kr[e + 1] = k4.y, kr[e + 2] = k4.z, kr[e + 3] = k4.w;
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 32; e++) kr[e] = 0.f;
+            const float* row = qkvc + (size_t)(t0 + i) * C;
+            q4 = *reinterpret_cast<const float4*>(row + h * DK + c4);
+            k4 = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + c4);
+            v4 = *reinterpret_cast<const float4*>(row + 2 * sh.H * DK + h * DV + c4);
         }
-        sq = warp_sum4(sq);
-        sk = warp_sum4(sk);
-        const float rk = i < Lc ? 1.0f / sqrtf(sk + 1e-6f) : 0.f;
-#pragma unroll
-        for (int e = 0; e < 32; e++) Ks[i * KP + p * 32 + e] = kr[e] * rk;
-        if (p == 0) rq[i] = i < Lc ? (1.0f / sqrtf(sq + 1e-6f)) * (1.0f / sqrtf((float)DK)) : 0.f;
+        *reinterpret_cast<float4*>(&Qs[i * KP + c4]) = q4;
+        *reinterpret_cast<float4*>(&Ks[i * KP + c4]) = k4;
+        *reinterpret_cast<float4*>(&Vs[i * KP + c4]) = v4;
     }
     if (tid < CH) {
         const int i = tid;
@@ -118,20 +107,43 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
         eG[i] = expf(s);
     }
     __syncthreads();
+    // row norms: qn = q rsqrt(|q|^2 + 1e-6) / sqrt(DK), kn = k rsqrt(|k|^2 + 1e-6)
+    {
+        const int i = tid >> 2, p = tid & 3;
+        float sq = 0.f, sk = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; e += 4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(&Qs[i * KP + p * 32 + e]);
+            const float4 k4 = *reinterpret_cast<const float4*>(&Ks[i * KP + p * 32 + e]);
+            sq += q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w;
+            sk += k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w;
+        }
+        sq = warp_sum4(sq);
+        sk = warp_sum4(sk);
+        if (p == 0) {
+            rq[i] = i < Lc ? (1.0f / sqrtf(sq + 1e-6f)) * (1.0f / sqrtf((float)DK)) : 0.f;
+            rk[i] = i < Lc ? 1.0f / sqrtf(sk + 1e-6f) : 0.f;
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < CH * DK; e += 256) {
+        const int i = e / DK, d = e % DK;
+        Qs[i * KP + d] *= rq[i];
+        Ks[i * KP + d] *= rk[i];
+    }
+    __syncthreads();
 
     // ---- phase 1: A (into Ts) and Qk (to global); thread = 4 rows x 4 columns
     {
         const int ib = tid >> 4, jb = tid & 15;
         float ak[4][4] = {}, aq[4][4] = {};
-        const float* qbase = qkvc + (size_t)t0 * C + h * DK;
         for (int d = 0; d < DK; d += 4) {
             float4 kr[4], kc[4], qr[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 kr[r] = *reinterpret_cast<const float4*>(&Ks[(4 * ib + r) * KP + d]);
+                qr[r] = *reinterpret_cast<const float4*>(&Qs[(4 * ib + r) * KP + d]);
                 kc[r] = *reinterpret_cast<const float4*>(&Ks[(4 * jb + r) * KP + d]);
-                const int i = 4 * ib + r;
-                qr[r] = i < Lc ? *reinterpret_cast<const float4*>(qbase + (size_t)i * C + d) : float4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
             for (int r = 0; r < 4; r++)
@@ -142,14 +154,19 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
                 }
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+        for (int r = 0; r < 4; r++) {
+            const int i = 4 * ib + r;
+            float4 qo;
+            float* qov = reinterpret_cast<float*>(&qo);
 #pragma unroll
             for (int cc = 0; cc < 4; cc++) {
-                const int i = 4 * ib + r, j = 4 * jb + cc;
+                const int j = 4 * jb + cc;
                 const float dec = i >= j ? expf(G[i] - G[j]) : 0.f;
                 Ts[i][j] = i > j ? -beta[i] * ak[r][cc] * dec : (i == j ? 1.f : 0.f);
-                Qk[i * CH + j] = i >= j ? aq[r][cc] * rq[i] * dec : 0.f;
+                qov[cc] = i >= j ? aq[r][cc] * dec : 0.f;
             }
+            *reinterpret_cast<float4*>(Qk + i * CH + 4 * jb) = qo;
+        }
     }
     __syncthreads();
 
@@ -187,60 +204,41 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
             }
     }
 
-    // ---- phase 3: W = T (beta e^G kn), and (kn e^(G_last - G))^T; thread = 1 row x 32 columns
+    // ---- phase 3: W = T (beta e^G kn), U = T (beta v), qn e^G and (kn e^(G_last - G))^T;
+    // thread = 1 row x 32 columns
     const float Glast = G[Lc - 1];
     {
         const int i = tid >> 2, p = tid & 3;
-        float acc[32] = {};
+        float aw[32] = {}, au[32] = {};
         for (int j = 0; j <= i; j++) {
-            const float coef = Ts[i][j] * beta[j] * eG[j];
+            const float cu = Ts[i][j] * beta[j];
+            const float cw = cu * eG[j];
 #pragma unroll
             for (int e = 0; e < 32; e += 4) {
                 const float4 k4 = *reinterpret_cast<const float4*>(&Ks[j * KP + p * 32 + e]);
-                acc[e] += coef * k4.x, acc[e + 1] += coef * k4.y, acc[e + 2] += coef * k4.z, acc[e + 3] += coef * k4.w;
+                const float4 v4 = *reinterpret_cast<const float4*>(&Vs[j * KP + p * 32 + e]);
+                aw[e] += cw * k4.x, aw[e + 1] += cw * k4.y, aw[e + 2] += cw * k4.z, aw[e + 3] += cw * k4.w;
+                au[e] += cu * v4.x, au[e + 1] += cu * v4.y, au[e + 2] += cu * v4.z, au[e + 3] += cu * v4.w;
             }
         }
-#pragma unroll
-        for (int e = 0; e < 32; e += 4)
-            *reinterpret_cast<float4*>(Wo + i * DK + p * 32 + e) = float4{acc[e], acc[e + 1], acc[e + 2], acc[e + 3]};
-        // kgT[d][i] = kn_i[d] e^(G_last - G_i): thread handles d = tid % 128, rows in halves
-        const int d = tid & 127, half = tid >> 7;
-        for (int r = half * 32; r < half * 32 + 32; r++) KgT[d * CH + r] = Ks[r * KP + d] * expf(Glast - G[r]);
-    }
-    __syncthreads();
-    // v rows into the Ks region
-    {
-        const int i = tid >> 2, p = tid & 3;
-        const float* vrow = qkvc + (size_t)(t0 + i) * C + 2 * sh.H * DK + h * DV + p * 32;
+        const float sc = eG[i];
 #pragma unroll
         for (int e = 0; e < 32; e += 4) {
-            const float4 v4 = i < Lc ? *reinterpret_cast<const float4*>(vrow + e) : float4{0.f, 0.f, 0.f, 0.f};
-            *reinterpret_cast<float4*>(&Ks[i * KP + p * 32 + e]) = v4;
-        }
-    }
-    __syncthreads();
-    {
-        const int i = tid >> 2, p = tid & 3;
-        float acc[32] = {};
-        for (int j = 0; j <= i; j++) {
-            const float coef = Ts[i][j] * beta[j];
-#pragma unroll
-            for (int e = 0; e < 32; e += 4) {
-                const float4 v4 = *reinterpret_cast<const float4*>(&Ks[j * KP + p * 32 + e]);
-                acc[e] += coef * v4.x, acc[e + 1] += coef * v4.y, acc[e + 2] += coef * v4.z, acc[e + 3] += coef * v4.w;
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 32; e += 4)
-            *reinterpret_cast<float4*>(Uo + i * DV + p * 32 + e) = float4{acc[e], acc[e + 1], acc[e + 2], acc[e + 3]};
-        // qg[i] = qn_i e^(G_i)
-        const float sc = rq[i] * eG[i];
-        const float* qrow = qkvc + (size_t)(t0 + i) * C + h * DK + p * 32;
-#pragma unroll
-        for (int e = 0; e < 32; e += 4) {
-            float4 q4 = i < Lc ? *reinterpret_cast<const float4*>(qrow + e) : float4{0.f, 0.f, 0.f, 0.f};
+            *reinterpret_cast<float4*>(Wo + i * DK + p * 32 + e) = float4{aw[e], aw[e + 1], aw[e + 2], aw[e + 3]};
+            *reinterpret_cast<float4*>(Uo + i * DV + p * 32 + e) = float4{au[e], au[e + 1], au[e + 2], au[e + 3]};
+            float4 q4 = *reinterpret_cast<const float4*>(&Qs[i * KP + p * 32 + e]);
             q4.x *= sc, q4.y *= sc, q4.z *= sc, q4.w *= sc;
             *reinterpret_cast<float4*>(Qg + i * DK + p * 32 + e) = q4;
+        }
+        // kgT[d][r] = kn_r[d] e^(G_last - G_r): thread (d, half) writes 32 consecutive r
+        const int d = tid & 127, half = tid >> 7;
+        for (int r0 = half * 32; r0 < half * 32 + 32; r0 += 4) {
+            float4 o4;
+            o4.x = Ks[(r0 + 0) * KP + d] * expf(Glast - G[r0 + 0]);
+            o4.y = Ks[(r0 + 1) * KP + d] * expf(Glast - G[r0 + 1]);
+            o4.z = Ks[(r0 + 2) * KP + d] * expf(Glast - G[r0 + 2]);
+            o4.w = Ks[(r0 + 3) * KP + d] * expf(Glast - G[r0 + 3]);
+            *reinterpret_cast<float4*>(KgT + d * CH + r0) = o4;
         }
     }
     if (tid == 0) ws.gl[wsb] = expf(Glast);
@@ -260,24 +258,34 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     }
 }
 
-template <int DK, int DV>
+// Sequential over chunks for one head and DVS value columns: each chunk's W, qn e^G, KgT and Qk
+// (shared by all column slices of the head) and its U columns arrive in LDS with one pass of
+// coalesced loads, then V' = U - W S, o = Qg S + Qk V', S <- e^(G_last) S + KgT V' from LDS.
+template <int DK, int DV, int DVS>
 __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, float* __restrict__ state,
                                                   const uint32_t* __restrict__ lu, int load_default,
                                                   float* __restrict__ o) {
+    static_assert(DK == 128 && (DVS == 8 || DVS == 16), "scan layout");
+    constexpr int KP = DK + 4, CP = CH + 4;
+    constexpr int OC = DVS / 4;   // output columns per thread (64 rows x DVS columns, 256 threads)
+    constexpr int SC = DVS / 2;   // state columns per thread (128 rows x DVS columns)
+    __shared__ __attribute__((aligned(16))) float Wc[CH * KP];
+    __shared__ __attribute__((aligned(16))) float Qc[CH * KP];
+    __shared__ __attribute__((aligned(16))) float Kc[DK * CP];  // KgT rows
+    __shared__ __attribute__((aligned(16))) float Ac[CH * CP];  // Qk
+    __shared__ __attribute__((aligned(16))) float Uc[CH][DVS];
     __shared__ __attribute__((aligned(16))) float Ss[DK][DVS];
     __shared__ __attribute__((aligned(16))) float Vn[CH][DVS];
     const int tid = threadIdx.x;
     const int h = blockIdx.x, sl = blockIdx.y, H = gridDim.x;
     const int c0 = sl * DVS;
     const bool load = lu ? lu[3] != 0u : load_default != 0;
-    // thread owns S rows k = tid / 2, columns 8 (tid & 1) .. + 7
-    const int sk = tid >> 1, sc0 = (tid & 1) * 8;
+    const int sk = tid >> 1, sc0 = (tid & 1) * SC;
     float* Sg = state + (size_t)h * DK * DV;
 #pragma unroll
-    for (int e = 0; e < 8; e++) Ss[sk][sc0 + e] = load ? Sg[sk * DV + c0 + sc0 + e] : 0.f;
-    __syncthreads();
+    for (int e = 0; e < SC; e++) Ss[sk][sc0 + e] = load ? Sg[sk * DV + c0 + sc0 + e] : 0.f;
     const int nch = (L + CH - 1) / CH;
-    const int oi = tid >> 2, oc = (tid & 3) * 4;  // output row and 4 columns
+    const int oi = tid >> 2, oc = (tid & 3) * OC;
     for (int c = 0; c < nch; c++) {
         const size_t wsb = (size_t)c * H + h;
         const float* W = ws.w + wsb * CH * DK;
@@ -286,57 +294,76 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         const float* KgT = ws.kg + wsb * CH * DK;
         const float* Qk = ws.qk + wsb * CH * CH;
         const int Lc = min(CH, L - c * CH);
-        // V' = U - W S
-        float vp[4] = {0.f, 0.f, 0.f, 0.f}, oq[4] = {0.f, 0.f, 0.f, 0.f};
+        __syncthreads();  // the previous chunk is done with the LDS tiles
+        for (int e = tid; e < CH * DK / 4; e += 256) {
+            const int r = e / (DK / 4), c4 = (e % (DK / 4)) * 4;
+            *reinterpret_cast<float4*>(&Wc[r * KP + c4]) = *reinterpret_cast<const float4*>(W + r * DK + c4);
+            *reinterpret_cast<float4*>(&Qc[r * KP + c4]) = *reinterpret_cast<const float4*>(Qg + r * DK + c4);
+        }
+        for (int e = tid; e < DK * CH / 4; e += 256) {
+            const int r = e / (CH / 4), c4 = (e % (CH / 4)) * 4;
+            *reinterpret_cast<float4*>(&Kc[r * CP + c4]) = *reinterpret_cast<const float4*>(KgT + r * CH + c4);
+        }
+        for (int e = tid; e < CH * CH / 4; e += 256) {
+            const int r = e / (CH / 4), c4 = (e % (CH / 4)) * 4;
+            *reinterpret_cast<float4*>(&Ac[r * CP + c4]) = *reinterpret_cast<const float4*>(Qk + r * CH + c4);
+        }
+        for (int e = tid; e < CH * DVS / 4; e += 256) {
+            const int r = e / (DVS / 4), c4 = (e % (DVS / 4)) * 4;
+            *reinterpret_cast<float4*>(&Uc[r][c4]) = *reinterpret_cast<const float4*>(U + r * DV + c0 + c4);
+        }
+        __syncthreads();
+        // V' = U - W S and the inter-chunk part of o, Qg S
+        float vp[OC], oq[OC];
+#pragma unroll
+        for (int e = 0; e < OC; e++) vp[e] = oq[e] = 0.f;
         for (int k = 0; k < DK; k += 4) {
-            const float4 w4 = *reinterpret_cast<const float4*>(W + oi * DK + k);
-            const float4 q4 = *reinterpret_cast<const float4*>(Qg + oi * DK + k);
+            const float4 w4 = *reinterpret_cast<const float4*>(&Wc[oi * KP + k]);
+            const float4 q4 = *reinterpret_cast<const float4*>(&Qc[oi * KP + k]);
             const float wk[4] = {w4.x, w4.y, w4.z, w4.w}, qk[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const float4 s4 = *reinterpret_cast<const float4*>(&Ss[k + kk][oc]);
-                vp[0] += wk[kk] * s4.x, vp[1] += wk[kk] * s4.y, vp[2] += wk[kk] * s4.z, vp[3] += wk[kk] * s4.w;
-                oq[0] += qk[kk] * s4.x, oq[1] += qk[kk] * s4.y, oq[2] += qk[kk] * s4.z, oq[3] += qk[kk] * s4.w;
-            }
+            for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+                for (int e = 0; e < OC; e++) {
+                    const float sv = Ss[k + kk][oc + e];
+                    vp[e] += wk[kk] * sv;
+                    oq[e] += qk[kk] * sv;
+                }
         }
-        {
-            const float4 u4 = *reinterpret_cast<const float4*>(U + oi * DV + c0 + oc);
-            *reinterpret_cast<float4*>(&Vn[oi][oc]) = float4{u4.x - vp[0], u4.y - vp[1], u4.z - vp[2], u4.w - vp[3]};
-        }
+#pragma unroll
+        for (int e = 0; e < OC; e++) Vn[oi][oc + e] = Uc[oi][oc + e] - vp[e];
         __syncthreads();
         // o = Qg S + Qk V'
         for (int j = 0; j <= oi; j++) {
-            const float a = Qk[oi * CH + j];
-            const float4 v4 = *reinterpret_cast<const float4*>(&Vn[j][oc]);
-            oq[0] += a * v4.x, oq[1] += a * v4.y, oq[2] += a * v4.z, oq[3] += a * v4.w;
+            const float a = Ac[oi * CP + j];
+#pragma unroll
+            for (int e = 0; e < OC; e++) oq[e] += a * Vn[j][oc + e];
         }
         if (oi < Lc) {
             float* orow = o + (size_t)(c * CH + oi) * sh.H * DV + h * DV + c0 + oc;
-            *reinterpret_cast<float4*>(orow) = float4{oq[0], oq[1], oq[2], oq[3]};
+#pragma unroll
+            for (int e = 0; e < OC; e++) orow[e] = oq[e];
         }
         // S <- e^(G_last) S + KgT V'
         const float gl = ws.gl[wsb];
-        float sn[8];
+        float sn[SC];
 #pragma unroll
-        for (int e = 0; e < 8; e++) sn[e] = gl * Ss[sk][sc0 + e];
+        for (int e = 0; e < SC; e++) sn[e] = gl * Ss[sk][sc0 + e];
         for (int i = 0; i < CH; i += 4) {
-            const float4 k4 = *reinterpret_cast<const float4*>(KgT + sk * CH + i);
+            const float4 k4 = *reinterpret_cast<const float4*>(&Kc[sk * CP + i]);
             const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
-            for (int ii = 0; ii < 4; ii++) {
-                const float4 a4 = *reinterpret_cast<const float4*>(&Vn[i + ii][sc0]);
-                const float4 b4 = *reinterpret_cast<const float4*>(&Vn[i + ii][sc0 + 4]);
-                sn[0] += kv[ii] * a4.x, sn[1] += kv[ii] * a4.y, sn[2] += kv[ii] * a4.z, sn[3] += kv[ii] * a4.w;
-                sn[4] += kv[ii] * b4.x, sn[5] += kv[ii] * b4.y, sn[6] += kv[ii] * b4.z, sn[7] += kv[ii] * b4.w;
-            }
+            for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+                for (int e = 0; e < SC; e++) sn[e] += kv[ii] * Vn[i + ii][sc0 + e];
         }
-        __syncthreads();  // all reads of Ss and Vn for this chunk are done
+        __syncthreads();  // all reads of Ss for this chunk are done
 #pragma unroll
-        for (int e = 0; e < 8; e++) Ss[sk][sc0 + e] = sn[e];
-        __syncthreads();
+        for (int e = 0; e < SC; e++) Ss[sk][sc0 + e] = sn[e];
     }
+    __syncthreads();
 #pragma unroll
-    for (int e = 0; e < 8; e++) Sg[sk * DV + c0 + sc0 + e] = Ss[sk][sc0 + e];
+    for (int e = 0; e < SC; e++) Sg[sk * DV + c0 + sc0 + e] = Ss[sk][sc0 + e];
 }
 
 // out[t, h*DV + c] = f16(w[c] o rsqrt(mean(o^2) + 1e-6) silu(z)); one wave per (t, h), DV = 128.
@@ -391,7 +418,7 @@ void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float*
 
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
               hipStream_t st) {
-    hipLaunchKernelGGL((k_gdn_scan<128, 128>), dim3(s.H, s.DV / DVS), dim3(256), 0, st, s, L, ws, state, lu,
+    hipLaunchKernelGGL((k_gdn_scan<128, 128, DVS>), dim3(s.H, s.DV / DVS), dim3(256), 0, st, s, L, ws, state, lu,
                        load_default, o);
     launched("gdn_scan");
 }
