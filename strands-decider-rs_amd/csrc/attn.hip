@@ -2,12 +2,11 @@
 // write (reference: src/kernels.rs:400-448), and causal GQA attention with a sigmoid output gate
 // (reference: src/kernels.rs:453-541).
 //
-// Attention: a workgroup takes 16 queries of one q head and walks the keys in tiles of 64: the
-// K tile is staged in LDS as f16, scores are f32, the softmax is online (running max and sum per
-// query), and each thread accumulates one head dimension for the 16 queries.  When the query
-// blocks alone cannot fill the GPU (the short question suffix over a long cached prefix), the
-// key range is split over workgroups and a combine kernel merges the partial (max, sum, acc).
-// As in the reference, q is pre-scaled by 1/sqrt(hd) and rounded to f16 before the dot products.
+// Attention runs on MFMA (k_attn below).  When the query blocks alone cannot fill the GPU (the
+// short question suffix over a long cached prefix), the key range is also split over workgroups
+// and a combine kernel merges the partial (max, sum, acc).  As in the reference, q is pre-scaled
+// by 1/sqrt(hd) and rounded to f16 before the dot products.  The V cache is kept transposed,
+// [hk][hd][ctx].
 #include <cmath>
 
 #include "common.h"
@@ -16,7 +15,6 @@ namespace sd {
 namespace {
 
 constexpr int BQ = 16;  // queries per workgroup
-constexpr int KT = 64;  // keys per tile
 
 template <int HD>
 __global__ __launch_bounds__(HD) void k_qk_prep(const f16* __restrict__ big, AttnShape s, const float* __restrict__ qw,
@@ -30,9 +28,9 @@ __global__ __launch_bounds__(HD) void k_qk_prep(const f16* __restrict__ big, Att
     const bool isq = slot < s.HQ;
     const int k_off = 2 * s.HQ * HD, v_off = k_off + s.HK * HD;
     const f16* row = big + (size_t)t * s.stride;
-    if (!isq) {
+    if (!isq) {  // V cache is stored transposed, [hk][hd][ctx]
         const int kh = slot - s.HQ;
-        Vc[((size_t)kh * s.ctx + pos) * HD + d] = row[v_off + kh * HD + d];
+        Vc[((size_t)kh * HD + d) * s.ctx + pos] = row[v_off + kh * HD + d];
     }
     const float v = (float)row[isq ? slot * 2 * HD + d : k_off + (slot - s.HQ) * HD + d];
     float ss = v * v;
@@ -57,118 +55,155 @@ __global__ __launch_bounds__(HD) void k_qk_prep(const f16* __restrict__ big, Att
     else Kc[((size_t)(slot - s.HQ) * s.ctx + pos) * HD + d] = (f16)r;
 }
 
+__device__ __forceinline__ float wave_max16(float v) {  // max over lanes {l, l^16, l^32, l^48}
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float wave_sum16(float v) {
+    v += __shfl_xor(v, 16);
+    return v + __shfl_xor(v, 32);
+}
+
+// Causal GQA attention on MFMA.  A workgroup takes 16 queries of one q head; its 4 waves split the
+// key range in blocks of 32 keys (wave w takes blocks w, w+4, ...) and merge their online-softmax
+// states in LDS at the end.  Per 32-key block a wave computes S^T = K Q^T (keys x queries, 2 x 8
+// v_mfma_f32_16x16x32_f16 over the 256 dims), the online softmax per query (column), then
+// O^T += V^T P^T (256 dims x 16 queries); with S^T in the MFMA output layout, P^T is already in
+// the B-operand layout (lane = query, 8 keys), and the V cache is stored transposed so V^T
+// fragments are contiguous.  P is split into f16 hi + lo (two MFMAs) so that the product keeps the
+// reference's f32 P.V to about 22 bits.  With ks > 1 the workgroups along z also split the keys
+// and write unnormalised (acc, max, sum) for k_attn_combine.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f16* __restrict__ Kc,
-                                              const f16* __restrict__ Vc, const f16* __restrict__ big, AttnShape s,
+                                              const f16* __restrict__ Vt, const f16* __restrict__ big, AttnShape s,
                                               int L, const uint32_t* __restrict__ lu, f16* __restrict__ out,
                                               float* __restrict__ pacc, float* __restrict__ pml, int ks) {
-    static_assert(HD == 256, "attention is written for 256-wide heads (one thread per dimension)");
-    constexpr int QP = HD + 4;  // padded f32 row
-    constexpr int KP = HD + 8;  // padded f16 row
-    __shared__ __attribute__((aligned(16))) float Qs[BQ * QP];
-    __shared__ __attribute__((aligned(16))) f16 Ks[KT * KP];
-    __shared__ float Ps[BQ][KT + 1];
-    __shared__ float alpha_s[BQ];
-    const int tid = threadIdx.x;
+    static_assert(HD == 256, "attention is written for 256-wide heads");
+    constexpr int ND = HD / 16;   // 16 output dimension tiles
+    constexpr int NS = HD / 32;   // 8 k steps over the head dimension
+    constexpr int KB = 32;        // keys per block
+    __shared__ float Om[4][16][HD + 4];  // per-wave unnormalised outputs [query][dim]
+    __shared__ float Mm[4][16], Lm[4][16];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int fq = lane & 15, fg = lane >> 4;
     const int P = (int)lu[1];
-    const int t0 = blockIdx.x * BQ, h = blockIdx.y, z = blockIdx.z;
+    const int t0 = blockIdx.x * 16, h = blockIdx.y, z = blockIdx.z;
     const int kh = h / (s.HQ / s.HK);
-    const int nq = min(BQ, L - t0);
+    const int nq = min(16, L - t0);
     const int nkeys = P + t0 + nq;  // keys 0 .. P + t0 + nq - 1 can be attended
-    const int span = ((nkeys + ks - 1) / ks + KT - 1) / KT * KT;
+    const int span = ((nkeys + ks - 1) / ks + KB - 1) / KB * KB;
     const int kbeg = z * span, kend = min(nkeys, kbeg + span);
     const float scale = 1.0f / sqrtf((float)HD);
+    const int qpos = P + t0 + fq;  // absolute position of this lane's query
+    const bool qok = fq < nq;
 
-    for (int e = tid; e < BQ * HD; e += 256) {
-        const int i = e / HD, d = e % HD;
-        float q = 0.f;
-        if (i < nq) q = (float)(f16)((float)Q[((size_t)h * L + t0 + i) * HD + d] * scale);
-        Qs[i * QP + d] = q;
+    // Q^T fragments (B operand): lane (query fq, group fg) holds Q[fq][32s + 8fg .. +8], pre-scaled
+    // by 1/sqrt(hd) and rounded to f16 as the reference does.
+    f16x8 qf[NS];
+    {
+        const f16* qrow = Q + ((size_t)h * L + t0 + min(fq, nq - 1)) * HD;
+#pragma unroll
+        for (int st = 0; st < NS; st++) {
+            const f16x8 v = *reinterpret_cast<const f16x8*>(qrow + st * 32 + fg * 8);
+#pragma unroll
+            for (int e = 0; e < 8; e++) qf[st][e] = (f16)((float)v[e] * scale);
+        }
     }
-    // score lanes: query qi, keys kj .. kj + 3 of the tile
-    const int qi = tid >> 4, kj = (tid & 15) * 4;
-    float m_run = -INFINITY, l_run = 0.f;  // valid in the 16 lanes owning query qi
-    float acc[BQ];
+    f32x4 acc[ND];
 #pragma unroll
-    for (int i = 0; i < BQ; i++) acc[i] = 0.f;
-    const f16* Kbase = Kc + (size_t)kh * s.ctx * HD;
-    const f16* Vbase = Vc + (size_t)kh * s.ctx * HD;
+    for (int dt = 0; dt < ND; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    const f16* Kb = Kc + (size_t)kh * s.ctx * HD;
+    const f16* Vb = Vt + (size_t)kh * HD * s.ctx;
 
-    for (int j0 = kbeg; j0 < kend; j0 += KT) {
-        __syncthreads();  // previous tile's Ks / Ps reads are done (and Qs is written)
-        for (int e = tid; e < KT * HD / 8; e += 256) {
-            const int j = e / (HD / 8), c8 = e % (HD / 8);
-            f16x8 v = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-            if (j0 + j < kend) v = *reinterpret_cast<const f16x8*>(Kbase + (size_t)(j0 + j) * HD + c8 * 8);
-            *reinterpret_cast<f16x8*>(&Ks[j * KP + c8 * 8]) = v;
-        }
-        __syncthreads();
-        float sc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int d = 0; d < HD; d += 8) {
-            const float4 qa = *reinterpret_cast<const float4*>(&Qs[qi * QP + d]);
-            const float4 qb = *reinterpret_cast<const float4*>(&Qs[qi * QP + d + 4]);
+    for (int j0 = kbeg + wv * KB; j0 < kend; j0 += 4 * KB) {
+        // S^T for keys j0 .. j0+31: two 16-key tiles; lane (query fq) holds keys j0 + 16tt + 4fg + r
+        f32x4 st2[2];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const f16x8 k8 = *reinterpret_cast<const f16x8*>(&Ks[(kj + r) * KP + d]);
-                sc[r] += qa.x * (float)k8[0] + qa.y * (float)k8[1] + qa.z * (float)k8[2] + qa.w * (float)k8[3] +
-                         qb.x * (float)k8[4] + qb.y * (float)k8[5] + qb.z * (float)k8[6] + qb.w * (float)k8[7];
-            }
+        for (int tt = 0; tt < 2; tt++) {
+            const int key = min(j0 + tt * 16 + fq, kend - 1);
+            const f16* krow = Kb + (size_t)key * HD + fg * 8;
+            f16x8 kf[NS];
+#pragma unroll
+            for (int st = 0; st < NS; st++) kf[st] = *reinterpret_cast<const f16x8*>(krow + st * 32);
+            f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < NS; st++) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[st], qf[st], a, 0, 0, 0);
+            st2[tt] = a;
         }
+        float sv[8];
         float tmax = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int j = j0 + kj + r;
-            if (!(j < kend && j <= P + t0 + qi && qi < nq)) sc[r] = -INFINITY;
-            tmax = fmaxf(tmax, sc[r]);
-        }
+        for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o));
+            for (int r = 0; r < 4; r++) {
+                const int j = j0 + tt * 16 + fg * 4 + r;
+                const float v = (qok && j < kend && j <= qpos) ? st2[tt][r] : -INFINITY;
+                sv[tt * 4 + r] = v;
+                tmax = fmaxf(tmax, v);
+            }
+        tmax = wave_max16(tmax);
         const float m_new = fmaxf(m_run, tmax);
+        const float alpha = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
         float psum = 0.f;
+        f16x8 ph, pl;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float p = sc[r] == -INFINITY ? 0.f : expf(sc[r] - m_new);
-            Ps[qi][kj + r] = p;
-            psum += p;
+        for (int e = 0; e < 8; e++) {
+            const float pv = sv[e] == -INFINITY ? 0.f : expf(sv[e] - m_new);
+            psum += pv;
+            const f16 hi = (f16)pv;
+            ph[e] = hi;
+            pl[e] = (f16)(pv - (float)hi);
         }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) psum += __shfl_xor(psum, o);
-        const float al = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
-        l_run = l_run * al + psum;
+        l_run = l_run * alpha + wave_sum16(psum);
         m_run = m_new;
-        if ((tid & 15) == 0) alpha_s[qi] = al;
-        __syncthreads();
-        const int d = tid;
+        // O^T += V^T P^T; A operand lane (dim 16dt + fq, group fg): keys j0 + 4fg .. +3, j0 + 16 + 4fg .. +3
 #pragma unroll
-        for (int i = 0; i < BQ; i++) acc[i] *= alpha_s[i];
-        const int jn = min(KT, kend - j0);
-        for (int jj = 0; jj < jn; jj++) {
-            const float v = (float)Vbase[(size_t)(j0 + jj) * HD + d];
-#pragma unroll
-            for (int i = 0; i < BQ; i++) acc[i] += Ps[i][jj] * v;
+        for (int dt = 0; dt < ND; dt++) {
+            const f16* vrow = Vb + (size_t)(dt * 16 + fq) * s.ctx + j0 + fg * 4;
+            const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow);
+            const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16);
+            const f16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            f32x4 a = acc[dt];
+            a[0] *= alpha, a[1] *= alpha, a[2] *= alpha, a[3] *= alpha;
+            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, a, 0, 0, 0);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, a, 0, 0, 0);
         }
     }
-    // per-query (m, l) to LDS so that the dimension threads can read them
-    __shared__ float m_s[BQ], l_s[BQ];
-    if ((tid & 15) == 0) {
-        m_s[qi] = m_run;
-        l_s[qi] = l_run;
+    // merge the 4 waves: acc[dt][r] is O[query fq][dim 16dt + 4fg + r]
+#pragma unroll
+    for (int dt = 0; dt < ND; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) Om[wv][fq][dt * 16 + fg * 4 + r] = acc[dt][r];
+    if (fg == 0) {
+        Mm[wv][fq] = m_run;
+        Lm[wv][fq] = l_run;
     }
     __syncthreads();
-    const int d = tid;
-    if (ks == 1) {
-        for (int i = 0; i < nq; i++) {
-            const int t = t0 + i;
+    const int d = tid;  // one output dimension per thread, all 16 queries
+    for (int q = 0; q < nq; q++) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            if (Lm[w][q] > 0.f) m = fmaxf(m, Mm[w][q]);
+        float l = 0.f, a = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            if (Lm[w][q] > 0.f) {
+                const float f = expf(Mm[w][q] - m);
+                l += Lm[w][q] * f;
+                a += Om[w][q][d] * f;
+            }
+        const int t = t0 + q;
+        if (ks == 1) {
             const float g = (float)big[(size_t)t * s.stride + h * 2 * HD + HD + d];
-            out[(size_t)t * s.HQ * HD + h * HD + d] = (f16)(acc[i] / l_s[i] / (1.0f + expf(-g)));
-        }
-    } else {
-        for (int i = 0; i < nq; i++) {
-            const size_t r = ((size_t)z * L + t0 + i) * s.HQ + h;
-            pacc[r * HD + d] = acc[i];
+            out[(size_t)t * s.HQ * HD + h * HD + d] = (f16)(a / l / (1.0f + expf(-g)));
+        } else {
+            const size_t r = ((size_t)z * L + t) * s.HQ + h;
+            pacc[r * HD + d] = a;
             if (d == 0) {
-                pml[r * 2] = m_s[i];
-                pml[r * 2 + 1] = l_s[i];
+                pml[r * 2] = m;
+                pml[r * 2 + 1] = l;
             }
         }
     }

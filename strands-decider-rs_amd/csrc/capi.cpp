@@ -41,8 +41,8 @@ struct OpWs {
     std::mutex mu;
     float* part = nullptr;
     size_t part_floats = 0;
-    float* gdn = nullptr;
-    size_t gdn_floats = 0;
+    void* gdn = nullptr;
+    size_t gdn_bytes = 0;
 };
 OpWs& op_ws() {
     static OpWs w;
@@ -201,12 +201,12 @@ int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off
         const sd::GdnShape s{H, dk, dv, stride, a_off, b_off, 0, 2 * H * dk + H * dv};
         OpWs& w = op_ws();
         std::lock_guard<std::mutex> lock(w.mu);
-        const size_t need = sd::gdn_ws_floats(L, s);
-        if (need > w.gdn_floats) {
+        const size_t need = sd::gdn_ws_bytes(L, s);
+        if (need > w.gdn_bytes) {
             if (w.gdn) SD_HIP(hipFree(w.gdn));
             w.gdn = nullptr;
-            SD_HIP(hipMalloc(&w.gdn, need * 4));
-            w.gdn_floats = need;
+            SD_HIP(hipMalloc(&w.gdn, need));
+            w.gdn_bytes = need;
         }
         sd::GdnWs ws;
         sd::gdn_ws_carve(w.gdn, L, s, ws);

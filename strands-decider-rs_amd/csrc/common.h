@@ -69,7 +69,8 @@ struct YIn {
 // x[rows[r]] += y, h[r] = rmsnorm(x[rows[r]]) * w -> f16 (h16) or f32 (h32); rows null = identity.
 void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16, float* h32,
               hipStream_t st);
-void silu_mul(const f16* big, int L, int I, f16* mid, hipStream_t st);
+// gate_up output in big (f16, [L][2I]) or as ks f32 split-K slots in part.
+void silu_mul(const f16* big, const float* part, int ks, int L, int I, f16* mid, hipStream_t st);
 void add_bias(f16* y, int L, int N, const float* c, hipStream_t st);
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);
 
@@ -77,17 +78,18 @@ void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);
 struct GdnShape {
     int H, DK, DV, stride, a_off, b_off, z_off, C;
 };
-// Workspace for the chunked recurrence, sized for `cap` tokens.
+// Workspace of the chunked recurrence, sized for `cap` tokens: per (chunk, head) the scan's A
+// operands split into f16 hi/lo in MFMA fragment order, U (fp32) and e^(G_last).
 struct GdnWs {
-    float* w = nullptr;   // [chunks][H][64][DK]  T (beta k e^G)
-    float* u = nullptr;   // [chunks][H][64][DV]  T (beta v)
-    float* qg = nullptr;  // [chunks][H][64][DK]  qn e^G
-    float* kg = nullptr;  // [chunks][H][64][DK]  kn e^(G_last - G)
-    float* qk = nullptr;  // [chunks][H][64][64]  (qn . kn) e^(G_i - G_j), i >= j
-    float* gl = nullptr;  // [chunks][H]          e^(G_last)
+    f16* wf = nullptr;   // W = T diag(beta e^G) Kn
+    f16* qgf = nullptr;  // qn e^G
+    f16* qkf = nullptr;  // (qn . kn) e^(G_i - G_j), i >= j
+    f16* kgf = nullptr;  // (kn e^(G_last - G))^T
+    float* u = nullptr;  // T diag(beta) V, [64][dv] fp32
+    float* gl = nullptr; // e^(G_last)
 };
-size_t gdn_ws_floats(int cap, const GdnShape& s);
-void gdn_ws_carve(float* base, int cap, const GdnShape& s, GdnWs& ws);
+size_t gdn_ws_bytes(int cap, const GdnShape& s);
+void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws);
 void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out,
                hipStream_t st);
 // hist (nullable) is updated from big afterwards (the reference's hist_update).

@@ -95,18 +95,45 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
 }
 
 // mid[t, j] = f16(silu(g) * u), big[t] = [g | u] (src/kernels.rs:123-135).  8 values per thread.
-__global__ void k_silu_mul(const f16* __restrict__ big, int L, int I, f16* __restrict__ mid) {
+// With KS > 0 the gate_up output arrives as KS f32 split-K slots of [L][2I]; their slot-order
+// sum rounded to f16 is the f16 value the reference stores in `big`.
+template <int KS>
+__global__ void k_silu_mul(const f16* __restrict__ big, const float* __restrict__ part, int L, int I,
+                           f16* __restrict__ mid) {
     const size_t i8 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
     if (i8 >= (size_t)L * I) return;
     const size_t t = i8 / I, j = i8 % I;
-    const f16x8 gv = *reinterpret_cast<const f16x8*>(big + t * 2 * I + j);
-    const f16x8 uv = *reinterpret_cast<const f16x8*>(big + t * 2 * I + I + j);
+    float gv[8], uv[8];
+    if constexpr (KS == 0) {
+        const f16x8 g8 = *reinterpret_cast<const f16x8*>(big + t * 2 * I + j);
+        const f16x8 u8 = *reinterpret_cast<const f16x8*>(big + t * 2 * I + I + j);
+#pragma unroll
+        for (int e = 0; e < 8; e++) gv[e] = (float)g8[e], uv[e] = (float)u8[e];
+    } else {
+        const size_t slot = (size_t)L * 2 * I;
+        float4 g4[KS][2], u4[KS][2];
+#pragma unroll
+        for (int z = 0; z < KS; z++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                g4[z][h] = *reinterpret_cast<const float4*>(part + z * slot + t * 2 * I + j + 4 * h);
+                u4[z][h] = *reinterpret_cast<const float4*>(part + z * slot + t * 2 * I + I + j + 4 * h);
+            }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float4 gs = g4[0][h], us = u4[0][h];
+#pragma unroll
+            for (int z = 1; z < KS; z++) {
+                gs.x += g4[z][h].x, gs.y += g4[z][h].y, gs.z += g4[z][h].z, gs.w += g4[z][h].w;
+                us.x += u4[z][h].x, us.y += u4[z][h].y, us.z += u4[z][h].z, us.w += u4[z][h].w;
+            }
+            gv[4 * h] = (float)(f16)gs.x, gv[4 * h + 1] = (float)(f16)gs.y, gv[4 * h + 2] = (float)(f16)gs.z, gv[4 * h + 3] = (float)(f16)gs.w;
+            uv[4 * h] = (float)(f16)us.x, uv[4 * h + 1] = (float)(f16)us.y, uv[4 * h + 2] = (float)(f16)us.z, uv[4 * h + 3] = (float)(f16)us.w;
+        }
+    }
     f16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const float g = (float)gv[e], u = (float)uv[e];
-        o[e] = (f16)(g / (1.0f + expf(-g)) * u);
-    }
+    for (int e = 0; e < 8; e++) o[e] = (f16)(gv[e] / (1.0f + expf(-gv[e])) * uv[e]);
     *reinterpret_cast<f16x8*>(mid + i8) = o;
 }
 
@@ -152,10 +179,19 @@ void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* row
     launched("add_norm");
 }
 
-void silu_mul(const f16* big, int L, int I, f16* mid, hipStream_t st) {
+void silu_mul(const f16* big, const float* part, int ks, int L, int I, f16* mid, hipStream_t st) {
     SD_CHECK(I % 8 == 0, "silu_mul: intermediate size must be a multiple of 8");
     const size_t n8 = (size_t)L * I / 8;
-    hipLaunchKernelGGL(k_silu_mul, dim3((n8 + 255) / 256), dim3(256), 0, st, big, L, I, mid);
+    const dim3 grid((n8 + 255) / 256);
+    const int k = part ? ks : 0;
+    switch (k) {
+        case 0: hipLaunchKernelGGL(k_silu_mul<0>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
+        case 1: hipLaunchKernelGGL(k_silu_mul<1>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
+        case 2: hipLaunchKernelGGL(k_silu_mul<2>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
+        case 4: hipLaunchKernelGGL(k_silu_mul<4>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
+        case 8: hipLaunchKernelGGL(k_silu_mul<8>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
+        default: throw Error("silu_mul: unsupported partial count");
+    }
     launched("silu_mul");
 }
 

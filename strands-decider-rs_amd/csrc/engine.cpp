@@ -321,6 +321,8 @@ void Engine::ensure_pool(int l) {
     GdnShape gs{cfg.H, cfg.dk, cfg.dv, 0, 0, 0, 0, C};
     AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, 0, SD_CONTEXT};
     const size_t ypart = (size_t)8 * cap * cfg.d;
+    // gate_up partials: 8 slots for short inputs, fewer for long ones (whose grids need no split)
+    const size_t gpart = (size_t)(cap <= 256 ? 8 : 1) * cap * 2 * cfg.inter;
     const size_t sizes[] = {
         (size_t)cap * 4,                               // ids
         (size_t)cap * 4,                               // rows
@@ -334,9 +336,10 @@ void Engine::ensure_pool(int l) {
         (size_t)cap * cfg.d * 2,                       // y
         (size_t)cfg.hq * cap * cfg.hd * 2,             // q
         (size_t)cap * cfg.d * 4,                       // out
-        gdn_ws_floats(cap, gs) * 4,                    // GDN chunk workspace
+        gdn_ws_bytes(cap, gs),                         // GDN chunk workspace
         attn_ws_floats(std::min(cap, 256), as) * 4,    // attention key-split workspace
         ypart * 4,                                     // split-K partials of y
+        gpart * 4,                                     // split-K partials of gate_up
     };
     size_t total = 0;
     for (size_t s : sizes) total += align256(s);
@@ -362,11 +365,13 @@ void Engine::ensure_pool(int l) {
     pool.y = (f16*)ptrs[9];
     pool.q = (f16*)ptrs[10];
     pool.out = (float*)ptrs[11];
-    gdn_ws_carve((float*)ptrs[12], cap, gs, pool.gdn);
+    gdn_ws_carve(ptrs[12], cap, gs, pool.gdn);
     pool.attn_ws = (float*)ptrs[13];
     pool.attn_rows = std::min(cap, 256);
     pool.ypart = (float*)ptrs[14];
     pool.ypart_elems = ypart;
+    pool.gpart = (float*)ptrs[15];
+    pool.gpart_elems = gpart;
     SD_HIP(hipMemset(pool.x, 0, (size_t)cap * cfg.d * 4));
     if (ids_h_cap < cap) {
         ids_h = static_cast<uint32_t*>(halloc((size_t)cap * 4));
@@ -387,7 +392,7 @@ YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, cons
     // chip, the add + RMSNorm sums the partials.
     const bool exact = L <= 20 || m.N % 64 != 0;
     const int cfg_ = gemm_w4_cfg(L, exact);
-    const int ks = gemm_w4_split(L, m.N, m.K, cfg_, 256, pool.ypart_elems);
+    const int ks = gemm_w4_split(L, m.N, m.K, cfg_, 512, pool.ypart_elems);
     float* part = pool.ypart;
     steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, nullptr, part, L, m.N, m.K, exact, ks, s, cfg_); }});
     YIn y;
@@ -448,8 +453,18 @@ Plan& Engine::plan(int L) {
             const YIn yin = y;
             steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.post_norm, d, nullptr, L, P.h, nullptr, s); }});
         }
-        mm(steps, "gate_up", P.h, W.gate_up, P.big, L);
-        steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, L, I, P.mid, s); }});
+        {
+            // gate_up only feeds silu * mul, which sums split-K partials itself
+            const bool exact = L <= 20 || W.gate_up.N % 64 != 0;
+            const int cg = gemm_w4_cfg(L, exact);
+            const int ks = gemm_w4_split(L, W.gate_up.N, W.gate_up.K, cg, 512, P.gpart_elems);
+            const Mat m = W.gate_up;
+            float* gp = ks > 1 ? P.gpart : nullptr;  // unsplit: f16 straight into big
+            steps.push_back({"gate_up", [=](hipStream_t s) {
+                gemm_w4(P.h, m.q, m.s, P.big, gp, L, m.N, m.K, exact, ks, s, cg);
+            }});
+            steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, gp, ks, L, I, P.mid, s); }});
+        }
         y = mm_y(steps, "down", P.mid, W.down, L);
     }
     pl.last_y = y;
@@ -498,12 +513,14 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
     if (cache) {
         SD_HIP(hipMemcpyAsync(arena, cache->arena, arena_bytes, hipMemcpyDeviceToDevice, st));
         if (kv_owner != cache->id) {
+            // K rows [hk][t][hd]; V transposed [hk][hd][t] (the attention kernel's layout)
             const size_t row = (size_t)cfg.hd * 2;
             for (size_t a = 0; a < attn_layers.size(); a++) {
                 const LayerW& W = layers[attn_layers[a]];
                 const uint8_t* ks = cache->kv(a, 0), *vs = cache->kv(a, 1);
                 SD_HIP(hipMemcpy2DAsync(W.kc, SD_CONTEXT * row, ks, P * row, P * row, cfg.hk, hipMemcpyDeviceToDevice, st));
-                SD_HIP(hipMemcpy2DAsync(W.vc, SD_CONTEXT * row, vs, P * row, P * row, cfg.hk, hipMemcpyDeviceToDevice, st));
+                SD_HIP(hipMemcpy2DAsync(W.vc, SD_CONTEXT * 2, vs, P * 2, P * 2, (size_t)cfg.hk * cfg.hd,
+                                        hipMemcpyDeviceToDevice, st));
             }
             kv_owner = cache->id;
         }
@@ -540,7 +557,8 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
         for (size_t a = 0; a < attn_layers.size(); a++) {
             const LayerW& W = layers[attn_layers[a]];
             SD_HIP(hipMemcpy2DAsync(snap->kv(a, 0), T * row, W.kc, SD_CONTEXT * row, T * row, cfg.hk, hipMemcpyDeviceToDevice, st));
-            SD_HIP(hipMemcpy2DAsync(snap->kv(a, 1), T * row, W.vc, SD_CONTEXT * row, T * row, cfg.hk, hipMemcpyDeviceToDevice, st));
+            SD_HIP(hipMemcpy2DAsync(snap->kv(a, 1), T * 2, W.vc, SD_CONTEXT * 2, T * 2, (size_t)cfg.hk * cfg.hd,
+                                    hipMemcpyDeviceToDevice, st));
         }
         kv_owner = snap->id;
     }

@@ -49,7 +49,7 @@ struct LayerW {
     float* state = nullptr;  // [H][dk][dv] f32 (in the live arena)
     f16* hist = nullptr;     // [3][C] f16 (in the live arena)
     f16* kc = nullptr;       // [hk][CONTEXT][hd] f16
-    f16* vc = nullptr;
+    f16* vc = nullptr;       // [hk][hd][CONTEXT] f16 (transposed for the attention kernel)
 };
 
 struct Cfg {
@@ -69,6 +69,8 @@ struct Pool {
     int attn_rows = 0;
     float* ypart = nullptr;  // split-K partials of the projections that feed the residual add
     size_t ypart_elems = 0;
+    float* gpart = nullptr;  // split-K partials of gate_up (summed by silu * mul)
+    size_t gpart_elems = 0;
 };
 
 struct Step {
@@ -89,7 +91,7 @@ struct Plan {
 struct Engine;
 
 // Prefix state after a forward: GDN state + conv history (the live arena image), then compact
-// K/V [hk][len][hd] per attention layer (src/engine.rs:81-87, 592-614).
+// K [hk][len][hd] and V [hk][hd][len] per attention layer (src/engine.rs:81-87, 592-614).
 struct Snapshot {
     const Engine* engine = nullptr;
     size_t len = 0;

@@ -1,31 +1,72 @@
 // Gated delta net on gfx950: depthwise conv + SiLU, the chunked gated delta rule (chunk 64,
-// fp32 throughout), and the gated RMSNorm.  Reference kernels: src/kernels.rs:152-190 (conv,
+// fp32 accuracy), and the gated RMSNorm.  Reference kernels: src/kernels.rs:152-190 (conv,
 // hist_update), 257-372 (the delta rule, sequential over tokens), 377-396 (gnorm).
 //
 // The reference runs the delta rule token by token: S <- e^g S; delta = (v - S^T kn) beta;
 // S <- S + kn delta^T; o = S^T qn.  Here the same recurrence is evaluated per chunk of 64 tokens
 // (the WY/UT form): with G the within-chunk cumulative log-decay,
 //   A_ij = -beta_i (kn_i . kn_j) e^(G_i - G_j) (i > j),  T = (I - A)^-1,
-//   W = T (beta kn e^G),  U = T (beta v),  Qk_ij = (qn_i . kn_j) e^(G_i - G_j) (i >= j),
-//   per chunk:  V' = U - W S;  o = (qn e^G) S + Qk V';  S <- e^(G_last) S + (kn e^(G_last - G))^T V'.
+//   W = T diag(beta e^G) Kn,  U = T diag(beta) V,  Qk_ij = (qn_i . kn_j) e^(G_i - G_j) (i >= j),
+//   per chunk:  V' = U - W S;  o = (qn e^G) S + Qk V';  S <- e^(G_last) S + (Kn e^(G_last - G))^T V'.
 // Every exponent above is <= 0, so nothing overflows for any decay.
-//  * gdn_prep: one workgroup per (chunk, head), fully parallel: norms, decays, A (blocked 16x16
-//    inversion of I - A), W, U, Qk, qn e^G, (kn e^(G_last - G))^T.  Block (0,0) also performs the
-//    reference's hist_update (the conv already consumed the old history).
-//  * gdn_scan: one workgroup per (head, 8 value columns), sequential over chunks; the state
-//    slice lives in LDS, each chunk's operands are staged in LDS by one pass of coalesced loads.
+//
+// All matrix products run on v_mfma_f32_16x16x32_f16 with each fp32 operand split into
+// hi = f16(x) and lo = f16(x - hi) and three MFMAs per product (hi.hi + hi.lo + lo.hi, f32
+// accumulation): about 22 significant bits per operand, well inside the fp32 parity tolerance.
+// Normalised q/k are scaled by 2^8 before the split (exact) so that small components stay in the
+// f16 normal range.
+//  * gdn_prep: one workgroup per (chunk, head), fully parallel: norms, decays, Kn Kn^T and Qn Kn^T,
+//    T by a blocked inversion (16x16 diagonal blocks as (I+N)(I+N^2)(I+N^4)(I+N^8), then block
+//    rows), W and U.  It writes the scan's A operands (W, qn e^G, Qk, (Kn e^(G_last-G))^T) already
+//    split, in MFMA fragment order, so the scan reads each fragment with one 16-byte load per lane.
+//    Block (0,0) also performs the reference's hist_update (the conv already consumed the old
+//    history).
+//  * gdn_scan: one workgroup per (head, 16 value columns), sequential over chunks; the state slice
+//    lives in LDS (transposed, the B operand of every product).
 #include "common.h"
 
 namespace sd {
 namespace {
 
-constexpr int CH = 64;  // chunk length
-constexpr int DVS = 8;  // value columns per scan workgroup
+constexpr int CH = 64;   // chunk length
+constexpr int DVS = 16;  // value columns per scan workgroup (one MFMA column tile)
+constexpr float QK_SCALE = 256.0f;
 
 __device__ __forceinline__ float warp_sum4(float v) {  // sum over aligned groups of 4 lanes
     v += __shfl_xor(v, 1);
     v += __shfl_xor(v, 2);
     return v;
+}
+
+__device__ __forceinline__ void split8(const float* v, f16x8& hi, f16x8& lo) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const f16 h = (f16)v[e];
+        hi[e] = h;
+        lo[e] = (f16)(v[e] - (float)h);
+    }
+}
+
+__device__ __forceinline__ f32x4 mma3(const f16x8& ah, const f16x8& al, const f16x8& bh, const f16x8& bl, f32x4 acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
+    return acc;
+}
+
+// A-operand fragment store: matrix with KS k-steps of 32, layout [row tile][k step][hi|lo][lane][8].
+__device__ __forceinline__ void put_frag(f16* base, int KS, int rt, int s, int lane, const float* v8) {
+    f16x8 hi, lo;
+    split8(v8, hi, lo);
+    f16* p = base + ((size_t)((rt * KS + s) * 2) * 64 + lane) * 8;
+    *reinterpret_cast<f16x8*>(p) = hi;
+    *reinterpret_cast<f16x8*>(p + 64 * 8) = lo;
+}
+
+__device__ __forceinline__ void get_frag(const f16* base, int KS, int rt, int s, int lane, f16x8& hi, f16x8& lo) {
+    const f16* p = base + ((size_t)((rt * KS + s) * 2) * 64 + lane) * 8;
+    hi = *reinterpret_cast<const f16x8*>(p);
+    lo = *reinterpret_cast<const f16x8*>(p + 64 * 8);
 }
 
 // qkvc[t, c] = silu(sum_j w[c][j] x[t + j - 3, c]), rows before 0 from hist (src/kernels.rs:152-170).
@@ -45,45 +86,47 @@ __global__ void k_conv(const f16* __restrict__ big, int stride, int L, int C, co
     out[(size_t)t * C + c] = s / (1.0f + expf(-s));
 }
 
-template <int DK, int DV>
+// Workspace slot sizes (halves / floats) per (chunk, head).
+constexpr size_t WF_H = 4 * 4 * 2 * 64 * 8;   // W: 4 row tiles x 4 k steps
+constexpr size_t QGF_H = WF_H;                // qn e^G
+constexpr size_t QKF_H = 4 * 2 * 2 * 64 * 8;  // Qk: 4 row tiles x 2 k steps
+constexpr size_t KGF_H = 8 * 2 * 2 * 64 * 8;  // KgT: 8 row tiles x 2 k steps
+constexpr size_t U_F = 64 * 128;              // U, fp32 row-major
+
 __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc, const f16* __restrict__ big,
                                                   GdnShape sh, const float* __restrict__ negA,
                                                   const float* __restrict__ dtb, int L, GdnWs ws, f16* hist) {
-    static_assert(DK == 128 && DV == 128, "gdn_prep is written for 128-wide heads");
-    constexpr int KP = DK + 4;  // padded LDS row
-    __shared__ __attribute__((aligned(16))) float Qs[CH * KP];  // q rows, then qn
-    __shared__ __attribute__((aligned(16))) float Ks[CH * KP];  // k rows, then kn
-    __shared__ __attribute__((aligned(16))) float Vs[CH * KP];  // v rows
-    __shared__ float Ts[CH][CH + 1];                           // A, then T = (I - A)^-1
-    __shared__ float Xs[16][17];
-    __shared__ float rq[CH], rk[CH], beta[CH], G[CH], eG[CH];
+    constexpr int DK = 128, DV = 128;
+    constexpr int RP = DK + 8;  // f16 row pitch of row-major tiles
+    constexpr int TP = CH + 8;  // f16 row pitch of transposed tiles
+    constexpr int FP = CH + 4;  // fp32 pitch of T
+    // LDS regions: R1 = K rows (hi, lo), later W staging (fp32); R2 = Q rows (hi, lo), later Qk
+    // staging (fp32), then V^T (hi, lo); R3 = K^T (hi, lo); T; scratch.
+    __shared__ __attribute__((aligned(16))) uint8_t R1[2 * CH * RP * 2 > CH * (DK + 4) * 4 ? 2 * CH * RP * 2 : CH * (DK + 4) * 4];
+    __shared__ __attribute__((aligned(16))) uint8_t R2[2 * DK * TP * 2];
+    __shared__ __attribute__((aligned(16))) f16 KT[2][DK * TP];
+    __shared__ __attribute__((aligned(16))) float Ts[CH * FP];
+    __shared__ float Xs[4][16][17], Ys[4][16][17];
+    __shared__ float beta[CH], G[CH], eG[CH], eL[CH];
+    f16* Kh = reinterpret_cast<f16*>(R1);
+    f16* Kl = Kh + CH * RP;
+    f16* Qh = reinterpret_cast<f16*>(R2);
+    f16* Ql = Qh + CH * RP;
 
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int fr = lane & 15, fg = lane >> 4;  // fragment row / k group of this lane
     const int c = blockIdx.x, h = blockIdx.y, H = gridDim.y;
     const int t0 = c * CH;
     const int Lc = min(CH, L - t0);
     const int C = sh.C;
-    const size_t wsb = (size_t)c * H + h;  // workspace slot
-    float* Wo = ws.w + wsb * CH * DK;
-    float* Uo = ws.u + wsb * CH * DV;
-    float* Qg = ws.qg + wsb * CH * DK;
-    float* KgT = ws.kg + wsb * CH * DK;
-    float* Qk = ws.qk + wsb * CH * CH;
+    const size_t slot = (size_t)c * H + h;
+    f16* Wf = ws.wf + slot * WF_H;
+    f16* Qgf = ws.qgf + slot * QGF_H;
+    f16* Qkf = ws.qkf + slot * QKF_H;
+    f16* Kgf = ws.kgf + slot * KGF_H;
+    float* Uo = ws.u + slot * U_F;
 
-    // ---- phase 0: the chunk's q, k, v rows into LDS in one pass of coalesced loads; gates
-    for (int e = tid; e < CH * DK / 4; e += 256) {
-        const int i = e / (DK / 4), c4 = (e % (DK / 4)) * 4;
-        float4 q4 = {0.f, 0.f, 0.f, 0.f}, k4 = q4, v4 = q4;
-        if (i < Lc) {
-            const float* row = qkvc + (size_t)(t0 + i) * C;
-            q4 = *reinterpret_cast<const float4*>(row + h * DK + c4);
-            k4 = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + c4);
-            v4 = *reinterpret_cast<const float4*>(row + 2 * sh.H * DK + h * DV + c4);
-        }
-        *reinterpret_cast<float4*>(&Qs[i * KP + c4]) = q4;
-        *reinterpret_cast<float4*>(&Ks[i * KP + c4]) = k4;
-        *reinterpret_cast<float4*>(&Vs[i * KP + c4]) = v4;
-    }
+    // ---- phase 0: gates (wave 0), normalised q/k rows: thread (i, p) owns columns 32p..32p+31
     if (tid < CH) {
         const int i = tid;
         float b = 0.f, gl = 0.f;
@@ -95,153 +138,272 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
             const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
             gl = negA[h] * sp;
         }
-        // inclusive prefix sum over the 64 lanes of wave 0
-        float s = gl;
+        float sc = gl;  // inclusive prefix sum over the 64 lanes of wave 0
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const float v = __shfl_up(s, o);
-            if (i >= o) s += v;
+            const float v = __shfl_up(sc, o);
+            if (i >= o) sc += v;
         }
+        const float glast = __shfl(sc, Lc - 1);
         beta[i] = b;
-        G[i] = s;
-        eG[i] = expf(s);
+        G[i] = sc;
+        eG[i] = expf(sc);
+        eL[i] = expf(glast - sc);
     }
-    __syncthreads();
-    // row norms: qn = q rsqrt(|q|^2 + 1e-6) / sqrt(DK), kn = k rsqrt(|k|^2 + 1e-6)
+    const int ri = tid >> 2, rp = tid & 3;
+    float qv[32], kv[32];
     {
-        const int i = tid >> 2, p = tid & 3;
         float sq = 0.f, sk = 0.f;
+        const float* row = qkvc + (size_t)(t0 + ri) * C;
 #pragma unroll
         for (int e = 0; e < 32; e += 4) {
-            const float4 q4 = *reinterpret_cast<const float4*>(&Qs[i * KP + p * 32 + e]);
-            const float4 k4 = *reinterpret_cast<const float4*>(&Ks[i * KP + p * 32 + e]);
+            float4 q4 = {0.f, 0.f, 0.f, 0.f}, k4 = q4;
+            if (ri < Lc) {
+                q4 = *reinterpret_cast<const float4*>(row + h * DK + rp * 32 + e);
+                k4 = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + rp * 32 + e);
+            }
+            qv[e] = q4.x, qv[e + 1] = q4.y, qv[e + 2] = q4.z, qv[e + 3] = q4.w;
+            kv[e] = k4.x, kv[e + 1] = k4.y, kv[e + 2] = k4.z, kv[e + 3] = k4.w;
             sq += q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w;
             sk += k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w;
         }
         sq = warp_sum4(sq);
         sk = warp_sum4(sk);
-        if (p == 0) {
-            rq[i] = i < Lc ? (1.0f / sqrtf(sq + 1e-6f)) * (1.0f / sqrtf((float)DK)) : 0.f;
-            rk[i] = i < Lc ? 1.0f / sqrtf(sk + 1e-6f) : 0.f;
+        const float rq = ri < Lc ? (1.0f / sqrtf(sq + 1e-6f)) * (1.0f / sqrtf((float)DK)) : 0.f;
+        const float rk = ri < Lc ? 1.0f / sqrtf(sk + 1e-6f) : 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; e++) {
+            qv[e] *= rq;
+            kv[e] *= rk;
+        }
+#pragma unroll
+        for (int e = 0; e < 32; e += 8) {
+            float q8[8], k8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) q8[u] = qv[e + u] * QK_SCALE, k8[u] = kv[e + u] * QK_SCALE;
+            f16x8 hi, lo;
+            split8(q8, hi, lo);
+            *reinterpret_cast<f16x8*>(&Qh[ri * RP + rp * 32 + e]) = hi;
+            *reinterpret_cast<f16x8*>(&Ql[ri * RP + rp * 32 + e]) = lo;
+            split8(k8, hi, lo);
+            *reinterpret_cast<f16x8*>(&Kh[ri * RP + rp * 32 + e]) = hi;
+            *reinterpret_cast<f16x8*>(&Kl[ri * RP + rp * 32 + e]) = lo;
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                KT[0][(rp * 32 + e + u) * TP + ri] = hi[u];
+                KT[1][(rp * 32 + e + u) * TP + ri] = lo[u];
+            }
         }
     }
     __syncthreads();
-    for (int e = tid; e < CH * DK; e += 256) {
-        const int i = e / DK, d = e % DK;
-        Qs[i * KP + d] *= rq[i];
-        Ks[i * KP + d] *= rk[i];
-    }
-    __syncthreads();
-
-    // ---- phase 1: A (into Ts) and Qk (to global); thread = 4 rows x 4 columns
+    // qn e^G as A fragments: (row tile ri/16, k step rp, lanes (ri%16) + 16g)
     {
-        const int ib = tid >> 4, jb = tid & 15;
-        float ak[4][4] = {}, aq[4][4] = {};
-        for (int d = 0; d < DK; d += 4) {
-            float4 kr[4], kc[4], qr[4];
+        const float e = eG[ri];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            float v8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v8[u] = qv[g * 8 + u] * e;
+            put_frag(Qgf, 4, ri >> 4, rp, (ri & 15) + 16 * g, v8);
+        }
+    }
+    // (Kn e^(G_last - G))^T as A fragments: rows d (8 tiles), k = token (2 steps); 4 per thread
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int slotf = tid + 256 * q;  // (tile, step, lane)
+        const int ln = slotf & 63, st = (slotf >> 6) & 1, kt = slotf >> 7;
+        const int d = kt * 16 + (ln & 15), i0 = st * 32 + (ln >> 4) * 8;
+        const f16x8 hi = *reinterpret_cast<const f16x8*>(&KT[0][d * TP + i0]);
+        const f16x8 lo = *reinterpret_cast<const f16x8*>(&KT[1][d * TP + i0]);
+        float v8[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v8[u] = ((float)hi[u] + (float)lo[u]) * (1.0f / QK_SCALE) * eL[i0 + u];
+        put_frag(Kgf, 2, kt, st, ln, v8);
+    }
+
+    // ---- phase 1: Kn Kn^T and Qn Kn^T; wave w computes row tile w x 4 column tiles
+    {
+        f32x4 akk[4], aqk[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) akk[t] = aqk[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int ar = (wv * 16 + fr) * RP + s * 32 + fg * 8;
+            const f16x8 kah = *reinterpret_cast<const f16x8*>(&Kh[ar]), kal = *reinterpret_cast<const f16x8*>(&Kl[ar]);
+            const f16x8 qah = *reinterpret_cast<const f16x8*>(&Qh[ar]), qal = *reinterpret_cast<const f16x8*>(&Ql[ar]);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int br = (t * 16 + fr) * RP + s * 32 + fg * 8;
+                const f16x8 kbh = *reinterpret_cast<const f16x8*>(&Kh[br]), kbl = *reinterpret_cast<const f16x8*>(&Kl[br]);
+                akk[t] = mma3(kah, kal, kbh, kbl, akk[t]);
+                aqk[t] = mma3(qah, qal, kbh, kbl, aqk[t]);
+            }
+        }
+        __syncthreads();  // Q rows are consumed: R2 becomes the Qk staging area
+        float* Qs = reinterpret_cast<float*>(R2);
+        constexpr float UNS = 1.0f / (QK_SCALE * QK_SCALE);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                kr[r] = *reinterpret_cast<const float4*>(&Ks[(4 * ib + r) * KP + d]);
-                qr[r] = *reinterpret_cast<const float4*>(&Qs[(4 * ib + r) * KP + d]);
-                kc[r] = *reinterpret_cast<const float4*>(&Ks[(4 * jb + r) * KP + d]);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int cc = 0; cc < 4; cc++) {
-                    ak[r][cc] += kr[r].x * kc[cc].x + kr[r].y * kc[cc].y + kr[r].z * kc[cc].z + kr[r].w * kc[cc].w;
-                    aq[r][cc] += qr[r].x * kc[cc].x + qr[r].y * kc[cc].y + qr[r].z * kc[cc].z + qr[r].w * kc[cc].w;
-                }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int i = 4 * ib + r;
-            float4 qo;
-            float* qov = reinterpret_cast<float*>(&qo);
-#pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const int j = 4 * jb + cc;
+                const int i = wv * 16 + fg * 4 + r, j = t * 16 + fr;
                 const float dec = i >= j ? expf(G[i] - G[j]) : 0.f;
-                Ts[i][j] = i > j ? -beta[i] * ak[r][cc] * dec : (i == j ? 1.f : 0.f);
-                qov[cc] = i >= j ? aq[r][cc] * dec : 0.f;
+                Ts[i * FP + j] = i > j ? -beta[i] * (akk[t][r] * UNS) * dec : (i == j ? 1.f : 0.f);
+                Qs[i * FP + j] = i >= j ? aqk[t][r] * UNS * dec : 0.f;
             }
-            *reinterpret_cast<float4*>(Qk + i * CH + 4 * jb) = qo;
+        __syncthreads();
+        // Qk as A fragments: 4 row tiles x 2 k steps x 64 lanes, 2 per thread
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int slotf = tid + 256 * q;
+            const int ln = slotf & 63, st = (slotf >> 6) & 1, rt = slotf >> 7;
+            const float* src = &Qs[(rt * 16 + (ln & 15)) * FP + st * 32 + (ln >> 4) * 8];
+            float v8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v8[u] = src[u];
+            put_frag(Qkf, 2, rt, st, ln, v8);
+        }
+        __syncthreads();  // R2 becomes V^T (hi, lo)
+        f16* VTh = reinterpret_cast<f16*>(R2);
+        f16* VTl = VTh + DK * TP;
+        const float* row = qkvc + (size_t)(t0 + ri) * C + 2 * sh.H * DK + h * DV + rp * 32;
+#pragma unroll
+        for (int e = 0; e < 32; e += 8) {
+            float v8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u += 4) {
+                float4 v4 = {0.f, 0.f, 0.f, 0.f};
+                if (ri < Lc) v4 = *reinterpret_cast<const float4*>(row + e + u);
+                v8[u] = v4.x, v8[u + 1] = v4.y, v8[u + 2] = v4.z, v8[u + 3] = v4.w;
+            }
+            f16x8 hi, lo;
+            split8(v8, hi, lo);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                VTh[(rp * 32 + e + u) * TP + ri] = hi[u];
+                VTl[(rp * 32 + e + u) * TP + ri] = lo[u];
+            }
         }
     }
-    __syncthreads();
 
-    // ---- phase 2: T = (I - A)^-1 in place.  Diagonal 16x16 blocks by row substitution
-    // (wave p inverts block p, lanes 0..15 are the columns), then the off-diagonal blocks
-    // T_pq = T_pp sum_{r=q}^{p-1} A_pr T_rq, rows p = 1..3 in order and q ascending.
+    // ---- phase 2: T = (I - A)^-1 in place (Ts holds I + A, A strictly lower).
+    // Diagonal blocks: wave w turns block w (I + N) into (I+N)(I+N^2)(I+N^4)(I+N^8).
     {
-        const int wv = tid >> 6, ln = tid & 63;
+        float(&Mb)[16][17] = Xs[wv];
+        float(&Pb)[16][17] = Ys[wv];
         const int base = wv * 16;
-        for (int i = 1; i < 16; i++) {
-            float v = 0.f;
-            const int jj = ln;
-            if (jj < i && ln < 16) {
-                v = Ts[base + i][base + jj];
-                for (int k = jj + 1; k < i; k++) v += Ts[base + i][base + k] * Ts[base + k][base + jj];
+        for (int e = lane; e < 256; e += 64) {
+            const int a = e >> 4, b = e & 15;
+            Mb[a][b] = a > b ? Ts[(base + a) * FP + base + b] : 0.f;
+            Pb[a][b] = Ts[(base + a) * FP + base + b];
+        }
+        __syncthreads();
+        const int a = lane >> 2, b0 = (lane & 3) * 4;
+        for (int step = 0; step < 3; step++) {
+            float m2[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float x = Mb[a][k];
+#pragma unroll
+                for (int u = 0; u < 4; u++) m2[u] += x * Mb[k][b0 + u];
             }
             __syncthreads();
-            if (jj < i && ln < 16) Ts[base + i][base + jj] = v;
+#pragma unroll
+            for (int u = 0; u < 4; u++) Mb[a][b0 + u] = m2[u];
+            __syncthreads();
+            float pn[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) pn[u] = Pb[a][b0 + u];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float x = Pb[a][k];
+#pragma unroll
+                for (int u = 0; u < 4; u++) pn[u] += x * Mb[k][b0 + u];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < 4; u++) Pb[a][b0 + u] = pn[u];
             __syncthreads();
         }
-        const int a = tid >> 4, b = tid & 15;
-        for (int p = 1; p < 4; p++)
-            for (int q = 0; q < p; q++) {
-                float x = 0.f;
-                for (int r = q; r < p; r++)
-#pragma unroll 4
-                    for (int k = 0; k < 16; k++) x += Ts[16 * p + a][16 * r + k] * Ts[16 * r + k][16 * q + b];
-                Xs[a][b] = x;
-                __syncthreads();
-                float y = 0.f;
-#pragma unroll 4
-                for (int k = 0; k < 16; k++) y += Ts[16 * p + a][16 * p + k] * Xs[k][b];
-                Ts[16 * p + a][16 * q + b] = y;
-                __syncthreads();
-            }
+        for (int e = lane; e < 256; e += 64) Ts[(base + (e >> 4)) * FP + base + (e & 15)] = Pb[e >> 4][e & 15];
+        __syncthreads();
+    }
+    // Block rows p = 1..3: X_q = sum_{r=q}^{p-1} A_pr T_rq for every q < p at once, then
+    // T_pq = T_pp X_q (A_pq is overwritten only after every X of the row is formed).
+    for (int p = 1; p < 4; p++) {
+        const int nq = p;  // blocks q = 0..p-1
+        for (int e = tid; e < nq * 256; e += 256) {
+            const int q = e >> 8, a = (e >> 4) & 15, b = e & 15;
+            float x = 0.f;
+            for (int r = q; r < p; r++)
+#pragma unroll
+                for (int k = 0; k < 16; k++) x += Ts[(16 * p + a) * FP + 16 * r + k] * Ts[(16 * r + k) * FP + 16 * q + b];
+            Xs[q][a][b] = x;
+        }
+        __syncthreads();
+        for (int e = tid; e < nq * 256; e += 256) {
+            const int q = e >> 8, a = (e >> 4) & 15, b = e & 15;
+            float y = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; k++) y += Ts[(16 * p + a) * FP + 16 * p + k] * Xs[q][k][b];
+            Ts[(16 * p + a) * FP + 16 * q + b] = y;
+        }
+        __syncthreads();
     }
 
-    // ---- phase 3: W = T (beta e^G kn), U = T (beta v), qn e^G and (kn e^(G_last - G))^T;
-    // thread = 1 row x 32 columns
-    const float Glast = G[Lc - 1];
+    // ---- phase 3: W = T diag(beta e^G) Kn and U = T diag(beta) V; wave w: row tile w x 8 column tiles
     {
-        const int i = tid >> 2, p = tid & 3;
-        float aw[32] = {}, au[32] = {};
-        for (int j = 0; j <= i; j++) {
-            const float cu = Ts[i][j] * beta[j];
-            const float cw = cu * eG[j];
+        const f16* VTh = reinterpret_cast<const f16*>(R2);
+        const f16* VTl = VTh + DK * TP;
+        f32x4 aw[8], au[8];
 #pragma unroll
-            for (int e = 0; e < 32; e += 4) {
-                const float4 k4 = *reinterpret_cast<const float4*>(&Ks[j * KP + p * 32 + e]);
-                const float4 v4 = *reinterpret_cast<const float4*>(&Vs[j * KP + p * 32 + e]);
-                aw[e] += cw * k4.x, aw[e + 1] += cw * k4.y, aw[e + 2] += cw * k4.z, aw[e + 3] += cw * k4.w;
-                au[e] += cu * v4.x, au[e + 1] += cu * v4.y, au[e + 2] += cu * v4.z, au[e + 3] += cu * v4.w;
+        for (int t = 0; t < 8; t++) aw[t] = au[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int i = wv * 16 + fr, j0 = s * 32 + fg * 8;
+            float xw[8], xu[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float tv = Ts[i * FP + j0 + u] * beta[j0 + u];
+                xu[u] = tv;
+                xw[u] = tv * eG[j0 + u];
+            }
+            f16x8 wh, wl, uh, ul;
+            split8(xw, wh, wl);
+            split8(xu, uh, ul);
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int br = (t * 16 + fr) * TP + s * 32 + fg * 8;
+                const f16x8 kh = *reinterpret_cast<const f16x8*>(&KT[0][br]), kl = *reinterpret_cast<const f16x8*>(&KT[1][br]);
+                const f16x8 vh = *reinterpret_cast<const f16x8*>(&VTh[br]), vl = *reinterpret_cast<const f16x8*>(&VTl[br]);
+                aw[t] = mma3(wh, wl, kh, kl, aw[t]);
+                au[t] = mma3(uh, ul, vh, vl, au[t]);
             }
         }
-        const float sc = eG[i];
+        // U straight to global (fp32 row-major); W through LDS (R1: K rows are no longer needed)
+        float* Ws = reinterpret_cast<float*>(R1);
+        constexpr int WP = DK + 4;
 #pragma unroll
-        for (int e = 0; e < 32; e += 4) {
-            *reinterpret_cast<float4*>(Wo + i * DK + p * 32 + e) = float4{aw[e], aw[e + 1], aw[e + 2], aw[e + 3]};
-            *reinterpret_cast<float4*>(Uo + i * DV + p * 32 + e) = float4{au[e], au[e + 1], au[e + 2], au[e + 3]};
-            float4 q4 = *reinterpret_cast<const float4*>(&Qs[i * KP + p * 32 + e]);
-            q4.x *= sc, q4.y *= sc, q4.z *= sc, q4.w *= sc;
-            *reinterpret_cast<float4*>(Qg + i * DK + p * 32 + e) = q4;
-        }
-        // kgT[d][r] = kn_r[d] e^(G_last - G_r): thread (d, half) writes 32 consecutive r
-        const int d = tid & 127, half = tid >> 7;
-        for (int r0 = half * 32; r0 < half * 32 + 32; r0 += 4) {
-            float4 o4;
-            o4.x = Ks[(r0 + 0) * KP + d] * expf(Glast - G[r0 + 0]);
-            o4.y = Ks[(r0 + 1) * KP + d] * expf(Glast - G[r0 + 1]);
-            o4.z = Ks[(r0 + 2) * KP + d] * expf(Glast - G[r0 + 2]);
-            o4.w = Ks[(r0 + 3) * KP + d] * expf(Glast - G[r0 + 3]);
-            *reinterpret_cast<float4*>(KgT + d * CH + r0) = o4;
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int i = wv * 16 + fg * 4 + r, d = t * 16 + fr;
+                Uo[i * DV + d] = au[t][r];
+                Ws[i * WP + d] = aw[t][r] * (1.0f / QK_SCALE);
+            }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int slotf = tid + 256 * q;  // 4 row tiles x 4 k steps x 64 lanes
+            const int ln = slotf & 63, st = (slotf >> 6) & 3, rt = slotf >> 8;
+            const float* src = &Ws[(rt * 16 + (ln & 15)) * WP + st * 32 + (ln >> 4) * 8];
+            float v8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v8[u] = src[u];
+            put_frag(Wf, 4, rt, st, ln, v8);
         }
     }
-    if (tid == 0) ws.gl[wsb] = expf(Glast);
+    if (tid == 0) ws.gl[slot] = eG[Lc - 1];
 
     // ---- the reference's hist_update (src/kernels.rs:173-190), by one workgroup
     if (hist && c == 0 && h == 0) {
@@ -258,112 +420,104 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     }
 }
 
-// Sequential over chunks for one head and DVS value columns: each chunk's W, qn e^G, KgT and Qk
-// (shared by all column slices of the head) and its U columns arrive in LDS with one pass of
-// coalesced loads, then V' = U - W S, o = Qg S + Qk V', S <- e^(G_last) S + KgT V' from LDS.
-template <int DK, int DV, int DVS>
+// Sequential over chunks for one head and 16 value columns; wave w owns rows 16w..16w+15 of the
+// chunk (and state rows 32w..32w+31 for the update).
 __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, float* __restrict__ state,
                                                   const uint32_t* __restrict__ lu, int load_default,
                                                   float* __restrict__ o) {
-    static_assert(DK == 128 && (DVS == 8 || DVS == 16), "scan layout");
-    constexpr int KP = DK + 4, CP = CH + 4;
-    constexpr int OC = DVS / 4;   // output columns per thread (64 rows x DVS columns, 256 threads)
-    constexpr int SC = DVS / 2;   // state columns per thread (128 rows x DVS columns)
-    __shared__ __attribute__((aligned(16))) float Wc[CH * KP];
-    __shared__ __attribute__((aligned(16))) float Qc[CH * KP];
-    __shared__ __attribute__((aligned(16))) float Kc[DK * CP];  // KgT rows
-    __shared__ __attribute__((aligned(16))) float Ac[CH * CP];  // Qk
-    __shared__ __attribute__((aligned(16))) float Uc[CH][DVS];
-    __shared__ __attribute__((aligned(16))) float Ss[DK][DVS];
-    __shared__ __attribute__((aligned(16))) float Vn[CH][DVS];
-    const int tid = threadIdx.x;
+    constexpr int DK = 128, DV = 128;
+    constexpr int SP = DK + 4, VP = CH + 4;
+    __shared__ __attribute__((aligned(16))) float St[DVS * SP];  // S^T: [column][k]
+    __shared__ __attribute__((aligned(16))) float Vt[DVS * VP];  // V'^T: [column][token]
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int fr = lane & 15, fg = lane >> 4;
     const int h = blockIdx.x, sl = blockIdx.y, H = gridDim.x;
     const int c0 = sl * DVS;
     const bool load = lu ? lu[3] != 0u : load_default != 0;
-    const int sk = tid >> 1, sc0 = (tid & 1) * SC;
     float* Sg = state + (size_t)h * DK * DV;
-#pragma unroll
-    for (int e = 0; e < SC; e++) Ss[sk][sc0 + e] = load ? Sg[sk * DV + c0 + sc0 + e] : 0.f;
+    for (int e = tid; e < DK * DVS; e += 256) {
+        const int k = e / DVS, cc = e % DVS;
+        St[cc * SP + k] = load ? Sg[k * DV + c0 + cc] : 0.f;
+    }
     const int nch = (L + CH - 1) / CH;
-    const int oi = tid >> 2, oc = (tid & 3) * OC;
     for (int c = 0; c < nch; c++) {
-        const size_t wsb = (size_t)c * H + h;
-        const float* W = ws.w + wsb * CH * DK;
-        const float* U = ws.u + wsb * CH * DV;
-        const float* Qg = ws.qg + wsb * CH * DK;
-        const float* KgT = ws.kg + wsb * CH * DK;
-        const float* Qk = ws.qk + wsb * CH * CH;
+        const size_t slot = (size_t)c * H + h;
+        const f16* Wf = ws.wf + slot * WF_H;
+        const f16* Qgf = ws.qgf + slot * QGF_H;
+        const f16* Qkf = ws.qkf + slot * QKF_H;
+        const f16* Kgf = ws.kgf + slot * KGF_H;
+        const float* U = ws.u + slot * U_F;
         const int Lc = min(CH, L - c * CH);
-        __syncthreads();  // the previous chunk is done with the LDS tiles
-        for (int e = tid; e < CH * DK / 4; e += 256) {
-            const int r = e / (DK / 4), c4 = (e % (DK / 4)) * 4;
-            *reinterpret_cast<float4*>(&Wc[r * KP + c4]) = *reinterpret_cast<const float4*>(W + r * DK + c4);
-            *reinterpret_cast<float4*>(&Qc[r * KP + c4]) = *reinterpret_cast<const float4*>(Qg + r * DK + c4);
+        f16x8 wh[4], wl[4], qh[4], ql[4];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            get_frag(Wf, 4, wv, s, lane, wh[s], wl[s]);
+            get_frag(Qgf, 4, wv, s, lane, qh[s], ql[s]);
         }
-        for (int e = tid; e < DK * CH / 4; e += 256) {
-            const int r = e / (CH / 4), c4 = (e % (CH / 4)) * 4;
-            *reinterpret_cast<float4*>(&Kc[r * CP + c4]) = *reinterpret_cast<const float4*>(KgT + r * CH + c4);
+        float ur[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) ur[r] = U[(wv * 16 + fg * 4 + r) * DV + c0 + fr];
+        __syncthreads();  // St holds this chunk's starting state; Vt is free
+        f32x4 av = {0.f, 0.f, 0.f, 0.f}, ao = av;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            float s8[8];
+            const float* sp = &St[fr * SP + s * 32 + fg * 8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) s8[u] = sp[u];
+            f16x8 sh8, sl8;
+            split8(s8, sh8, sl8);
+            av = mma3(wh[s], wl[s], sh8, sl8, av);
+            ao = mma3(qh[s], ql[s], sh8, sl8, ao);
         }
-        for (int e = tid; e < CH * CH / 4; e += 256) {
-            const int r = e / (CH / 4), c4 = (e % (CH / 4)) * 4;
-            *reinterpret_cast<float4*>(&Ac[r * CP + c4]) = *reinterpret_cast<const float4*>(Qk + r * CH + c4);
-        }
-        for (int e = tid; e < CH * DVS / 4; e += 256) {
-            const int r = e / (DVS / 4), c4 = (e % (DVS / 4)) * 4;
-            *reinterpret_cast<float4*>(&Uc[r][c4]) = *reinterpret_cast<const float4*>(U + r * DV + c0 + c4);
-        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) Vt[fr * VP + wv * 16 + fg * 4 + r] = ur[r] - av[r];
         __syncthreads();
-        // V' = U - W S and the inter-chunk part of o, Qg S
-        float vp[OC], oq[OC];
+        // V'^T fragments (B operand), used by Qk V' and by the state update
+        f16x8 vh[2], vl[2];
 #pragma unroll
-        for (int e = 0; e < OC; e++) vp[e] = oq[e] = 0.f;
-        for (int k = 0; k < DK; k += 4) {
-            const float4 w4 = *reinterpret_cast<const float4*>(&Wc[oi * KP + k]);
-            const float4 q4 = *reinterpret_cast<const float4*>(&Qc[oi * KP + k]);
-            const float wk[4] = {w4.x, w4.y, w4.z, w4.w}, qk[4] = {q4.x, q4.y, q4.z, q4.w};
+        for (int s = 0; s < 2; s++) {
+            float v8[8];
+            const float* vp = &Vt[fr * VP + s * 32 + fg * 8];
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-#pragma unroll
-                for (int e = 0; e < OC; e++) {
-                    const float sv = Ss[k + kk][oc + e];
-                    vp[e] += wk[kk] * sv;
-                    oq[e] += qk[kk] * sv;
-                }
+            for (int u = 0; u < 8; u++) v8[u] = vp[u];
+            split8(v8, vh[s], vl[s]);
         }
 #pragma unroll
-        for (int e = 0; e < OC; e++) Vn[oi][oc + e] = Uc[oi][oc + e] - vp[e];
-        __syncthreads();
-        // o = Qg S + Qk V'
-        for (int j = 0; j <= oi; j++) {
-            const float a = Ac[oi * CP + j];
-#pragma unroll
-            for (int e = 0; e < OC; e++) oq[e] += a * Vn[j][oc + e];
+        for (int s = 0; s < 2; s++) {
+            f16x8 ah, al;
+            get_frag(Qkf, 2, wv, s, lane, ah, al);
+            ao = mma3(ah, al, vh[s], vl[s], ao);
         }
-        if (oi < Lc) {
-            float* orow = o + (size_t)(c * CH + oi) * sh.H * DV + h * DV + c0 + oc;
 #pragma unroll
-            for (int e = 0; e < OC; e++) orow[e] = oq[e];
+        for (int r = 0; r < 4; r++) {
+            const int i = wv * 16 + fg * 4 + r;
+            if (i < Lc) o[(size_t)(c * CH + i) * sh.H * DV + h * DV + c0 + fr] = ao[r];
         }
-        // S <- e^(G_last) S + KgT V'
-        const float gl = ws.gl[wsb];
-        float sn[SC];
+        // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
+        const float gl = ws.gl[slot];
 #pragma unroll
-        for (int e = 0; e < SC; e++) sn[e] = gl * Ss[sk][sc0 + e];
-        for (int i = 0; i < CH; i += 4) {
-            const float4 k4 = *reinterpret_cast<const float4*>(&Kc[sk * CP + i]);
-            const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
+        for (int q = 0; q < 2; q++) {
+            const int kt = wv * 2 + q;
+            f32x4 as = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ii = 0; ii < 4; ii++)
+            for (int s = 0; s < 2; s++) {
+                f16x8 ah, al;
+                get_frag(Kgf, 2, kt, s, lane, ah, al);
+                as = mma3(ah, al, vh[s], vl[s], as);
+            }
 #pragma unroll
-                for (int e = 0; e < SC; e++) sn[e] += kv[ii] * Vn[i + ii][sc0 + e];
+            for (int r = 0; r < 4; r++) {
+                const int k = kt * 16 + fg * 4 + r;
+                St[fr * SP + k] = gl * St[fr * SP + k] + as[r];
+            }
         }
-        __syncthreads();  // all reads of Ss for this chunk are done
-#pragma unroll
-        for (int e = 0; e < SC; e++) Ss[sk][sc0 + e] = sn[e];
     }
     __syncthreads();
-#pragma unroll
-    for (int e = 0; e < SC; e++) Sg[sk * DV + c0 + sc0 + e] = Ss[sk][sc0 + e];
+    for (int e = tid; e < DK * DVS; e += 256) {
+        const int k = e / DVS, cc = e % DVS;
+        Sg[k * DV + c0 + cc] = St[cc * SP + k];
+    }
 }
 
 // out[t, h*DV + c] = f16(w[c] o rsqrt(mean(o^2) + 1e-6) silu(z)); one wave per (t, h), DV = 128.
@@ -388,19 +542,20 @@ __global__ __launch_bounds__(256) void k_gnorm(const float* __restrict__ o, cons
 
 }  // namespace
 
-size_t gdn_ws_floats(int cap, const GdnShape& s) {
-    const size_t nch = (cap + CH - 1) / CH;
-    return nch * s.H * ((size_t)CH * s.DK * 3 + (size_t)CH * s.DV + (size_t)CH * CH + 1);
+size_t gdn_ws_bytes(int cap, const GdnShape& s) {
+    const size_t slots = (size_t)((cap + CH - 1) / CH) * s.H;
+    return slots * ((WF_H + QGF_H + QKF_H + KGF_H) * 2 + (U_F + 1) * 4) + 1024;
 }
 
-void gdn_ws_carve(float* base, int cap, const GdnShape& s, GdnWs& ws) {
-    const size_t nch = (cap + CH - 1) / CH, slots = nch * s.H;
-    ws.w = base;
-    ws.u = ws.w + slots * CH * s.DK;
-    ws.qg = ws.u + slots * CH * s.DV;
-    ws.kg = ws.qg + slots * CH * s.DK;
-    ws.qk = ws.kg + slots * CH * s.DK;
-    ws.gl = ws.qk + slots * CH * CH;
+void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws) {
+    const size_t slots = (size_t)((cap + CH - 1) / CH) * s.H;
+    f16* p = static_cast<f16*>(base);
+    ws.wf = p;
+    ws.qgf = ws.wf + slots * WF_H;
+    ws.qkf = ws.qgf + slots * QGF_H;
+    ws.kgf = ws.qkf + slots * QKF_H;
+    ws.u = reinterpret_cast<float*>(ws.kgf + slots * KGF_H);
+    ws.gl = ws.u + slots * U_F;
 }
 
 void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out, hipStream_t st) {
@@ -412,14 +567,14 @@ void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float*
               const GdnWs& ws, f16* hist, hipStream_t st) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     const int nch = (L + CH - 1) / CH;
-    hipLaunchKernelGGL((k_gdn_prep<128, 128>), dim3(nch, s.H), dim3(256), 0, st, qkvc, big, s, negA, dtb, L, ws, hist);
+    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H), dim3(256), 0, st, qkvc, big, s, negA, dtb, L, ws, hist);
     launched("gdn_prep");
 }
 
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
               hipStream_t st) {
-    hipLaunchKernelGGL((k_gdn_scan<128, 128, DVS>), dim3(s.H, s.DV / DVS), dim3(256), 0, st, s, L, ws, state, lu,
-                       load_default, o);
+    SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
+    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS), dim3(256), 0, st, s, L, ws, state, lu, load_default, o);
     launched("gdn_scan");
 }
 

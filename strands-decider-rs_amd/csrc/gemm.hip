@@ -10,15 +10,18 @@
 //    quant block (32 k values) of column j at block kb0+g, i.e. one macro step covers 128 k and
 //    feeds 4 v_mfma_f32_16x16x32_f16; step s uses word s of the block;
 //  * a word's 8 nibbles become 4 f16 pairs with the 0x6400 exponent trick:
-//      ((w >> 4i) & 0x000F000F) | 0x64006400 = (1024 + q_i, 1024 + q_{i+4}),
-//    minus 1032 (exact) gives q - 8, times the f16 scale rounds once: exactly the reference's
-//    f16 dequant (f16(q) - 8) * sc.  The pairs come out in k order [0,4,1,5,2,6,3,7]; the A tile
-//    is stored to LDS in the same order, so the dot products see matching k;
+//      (w & 0x000F000F) | 0x64006400 = (1024 + q0, 1024 + q4), minus 1032 (exact) gives q - 8;
+//      (w & 0x00F000F0) | 0x64006400 = (1024 + 16 q1, 1024 + 16 q5), times 1/16 minus 72 (one
+//      exact fma) gives q - 8; the same on w >> 8 gives q2/q6 and q3/q7.  Times the f16 scale
+//    rounds once: exactly the reference's f16 dequant (f16(q) - 8) * sc.  The pairs come out in
+//    k order [0,4,1,5,2,6,3,7]; the A tile is stored to LDS in the same order, so the dot
+//    products see matching k;
 //  * `EXACT` reproduces the reference GEMV's f32 dequant (q-8)*sc: the value is split into
 //    hi = f16((q-8)*sc) and lo = fma_f16(q-8, sc, -hi) (exact: the residual is a multiple of
 //    2^-24 with at most 5 significant bits), and both are fed to the MFMA;
-//  * A (activations, f16) is staged once per workgroup per macro step in LDS (shared by the 4
-//    waves) with a register prefetch of the next step; B for the next step is prefetched too;
+//  * A (activations, f16) is staged once per workgroup per macro step in a double-buffered LDS
+//    tile shared by the 4 waves (one barrier per step), with A two steps and B one step ahead in
+//    registers;
 //  * split-K over workgroups writes f32 partials [ks][M][N] with plain stores and no cross-
 //    workgroup synchronisation (on MI355X a device-scope fence writes back the whole XCD L2); the
 //    consumer sums the ks slots in a fixed order: the residual add + RMSNorm does it for the
@@ -29,11 +32,32 @@ namespace sd {
 namespace {
 
 constexpr int KSTEP = 128;      // k per macro step: 4 quant blocks
-constexpr int LDA = KSTEP + 8;  // LDS row stride in halves (16-byte pad)
+#ifndef SD_LDA_PAD
+#define SD_LDA_PAD 8
+#endif
+constexpr int LDA = KSTEP + SD_LDA_PAD;  // LDS row stride in halves
 
-__device__ __forceinline__ f16x2 nib_pair(uint32_t w, int sh) {
-    uint32_t v = ((w >> sh) & 0x000F000Fu) | 0x64006400u;
-    return __builtin_bit_cast(f16x2, v) - f16x2{(f16)1032.0f, (f16)1032.0f};
+// The 8 nibbles of a weight word as 4 f16 pairs q - 8 (exact), k order [0,4],[1,5],[2,6],[3,7]:
+// the low nibble of each byte lands in the f16 mantissa as 1024 + q, the high nibble as
+// 1024 + 16 q, so two masks per 8-bit shift give all four pairs.
+// (a & m) | c in one v_and_or_b32 (the compiler otherwise emits separate and/or here).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "s"(c));
+    return r;
+}
+
+__device__ __forceinline__ void nib_pairs(uint32_t w, f16x2& p0, f16x2& p1, f16x2& p2, f16x2& p3) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 x0 = __builtin_bit_cast(f16x2, and_or(w, 0x000F000Fu, 0x64006400u));
+    const f16x2 x1 = __builtin_bit_cast(f16x2, and_or(w, 0x00F000F0u, 0x64006400u));
+    const f16x2 x2 = __builtin_bit_cast(f16x2, and_or(w8, 0x000F000Fu, 0x64006400u));
+    const f16x2 x3 = __builtin_bit_cast(f16x2, and_or(w8, 0x00F000F0u, 0x64006400u));
+    const f16x2 c1032 = {(f16)1032.0f, (f16)1032.0f}, c16 = {(f16)0.0625f, (f16)0.0625f}, c72 = {(f16)-72.0f, (f16)-72.0f};
+    p0 = x0 - c1032;
+    p1 = __builtin_elementwise_fma(x1, c16, c72);
+    p2 = x2 - c1032;
+    p3 = __builtin_elementwise_fma(x3, c16, c72);
 }
 
 __device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
@@ -42,11 +66,11 @@ __device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
 
 // Permute 8 halves [a0..a7] (as 4 words) to [a0,a4,a1,a5,a2,a6,a3,a7].
 __device__ __forceinline__ u32x4 perm_a(u32x4 d) {
-    u32x4 o;
-    o[0] = (d[0] & 0xFFFFu) | (d[2] << 16);
-    o[1] = (d[0] >> 16) | (d[2] & 0xFFFF0000u);
-    o[2] = (d[1] & 0xFFFFu) | (d[3] << 16);
-    o[3] = (d[1] >> 16) | (d[3] & 0xFFFF0000u);
+    u32x4 o;  // v_perm_b32: selector bytes 0-3 pick from the second source, 4-7 from the first
+    o[0] = __builtin_amdgcn_perm(d[2], d[0], 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(d[2], d[0], 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(d[3], d[1], 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(d[3], d[1], 0x07060302u);
     return o;
 }
 
@@ -57,7 +81,10 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
     constexpr int BM = MT * 16;
     constexpr int BN = 4 * NT * 16;
     constexpr int ACH = BM * 16 / 256;  // 16-byte A chunks per thread per macro step (== MT)
-    __shared__ __attribute__((aligned(16))) f16 As[BM * LDA];
+    // Double-buffered A tile: two separate arrays so that the compiler can see that the stores of
+    // the next tile never alias the fragment reads of the current one.
+    __shared__ __attribute__((aligned(16))) f16 As0[BM * LDA];
+    __shared__ __attribute__((aligned(16))) f16 As1[BM * LDA];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
@@ -67,7 +94,6 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
     const int steps = steps_total / ksplit;
     const int step0 = blockIdx.z * steps;
 
-    // B addressing for this lane's NT columns.
     int ncol[NT];
     bool nok[NT];
 #pragma unroll
@@ -75,33 +101,22 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
         ncol[t] = n0 + (wave * NT + t) * 16 + j;
         nok[t] = ncol[t] < N;
     }
-
-    auto load_b = [&](int step, u32x4* bw, f16* bs) {
-        const int kb = step * 4 + g;
+    // Loads are branch-free: rows past M and columns past N read the last valid row/column, and
+    // the outputs they feed are never stored.
+    const u32x4* wrow[NT];
+    const f16* srow[NT];
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (nok[t]) {
-                const size_t blk = (size_t)ncol[t] * KB + kb;
-                bw[t] = *reinterpret_cast<const u32x4*>(W + blk * 4);
-                bs[t] = S[blk];
-            } else {
-                bw[t] = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
-                bs[t] = (f16)0.0f;
-            }
-        }
-    };
-    auto load_a = [&](int step, u32x4* ar) {
+    for (int t = 0; t < NT; t++) {
+        const size_t n = (size_t)min(ncol[t], N - 1);
+        wrow[t] = reinterpret_cast<const u32x4*>(W) + n * KB + g;
+        srow[t] = S + n * KB + g;
+    }
+    const f16* arow[ACH];
 #pragma unroll
-        for (int c = 0; c < ACH; c++) {
-            const int idx = tid + 256 * c;
-            const int row = idx >> 4, c16 = idx & 15;
-            const int m = m0 + row;
-            if (m < M)
-                ar[c] = *reinterpret_cast<const u32x4*>(A + (size_t)m * K + step * KSTEP + c16 * 8);
-            else
-                ar[c] = u32x4{0u, 0u, 0u, 0u};
-        }
-    };
+    for (int c = 0; c < ACH; c++) {
+        const int idx = tid + 256 * c;
+        arow[c] = A + (size_t)min(m0 + (idx >> 4), M - 1) * K + (idx & 15) * 8;
+    }
 
     f32x4 acc[MT][NT];
 #pragma unroll
@@ -111,57 +126,90 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 
     u32x4 areg[ACH], bcur[NT], bnext[NT];
     f16 scur[NT], snext[NT];
-    load_a(step0, areg);
-    load_b(step0, bcur, scur);
-
-    for (int it = 0; it < steps; it++) {
-        __syncthreads();  // the previous step's LDS reads are done
+    auto load_a = [&](int step) {
+#pragma unroll
+        for (int c = 0; c < ACH; c++) areg[c] = *reinterpret_cast<const u32x4*>(arow[c] + step * KSTEP);
+    };
+    auto load_b = [&](int step) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            bnext[t] = wrow[t][step * 4];
+            snext[t] = srow[t][step * 4];
+        }
+    };
+    auto store_a = [&](f16* dst) {
 #pragma unroll
         for (int c = 0; c < ACH; c++) {
             const int idx = tid + 256 * c;
-            const int row = idx >> 4, c16 = idx & 15;
-            *reinterpret_cast<u32x4*>(&As[row * LDA + c16 * 8]) = perm_a(areg[c]);
+            *reinterpret_cast<u32x4*>(&dst[(idx >> 4) * LDA + (idx & 15) * 8]) = perm_a(areg[c]);
         }
+    };
+    auto frags = [&](const f16* Acur, int s, f16x8* af) {
+#pragma unroll
+        for (int a = 0; a < MT; a++)
+            af[a] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(&Acur[(a * 16 + j) * LDA + g * 32 + s * 8]));
+    };
+    auto dequant = [&](int s, f16x8* b, f16x8* blo) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const f16x2 sc2 = f16x2{scur[t], scur[t]};
+            f16x2 p0, p1, p2, p3;
+            nib_pairs(bcur[t][s], p0, p1, p2, p3);
+            const f16x2 h0 = p0 * sc2, h1 = p1 * sc2, h2 = p2 * sc2, h3 = p3 * sc2;
+            b[t] = cat4(h0, h1, h2, h3);
+            if constexpr (EXACT)
+                blo[t] = cat4(__builtin_elementwise_fma(p0, sc2, -h0), __builtin_elementwise_fma(p1, sc2, -h1),
+                              __builtin_elementwise_fma(p2, sc2, -h2), __builtin_elementwise_fma(p3, sc2, -h3));
+        }
+    };
+    // One k step (4 sub-steps of 32 k).  The next tile's A store and the next loads are issued
+    // first; sub-step s+1's fragment reads and dequant are issued before sub-step s's MFMAs.
+    auto step = [&](const f16* Acur, f16* Anext, int it) {
+        f16x8 af[2][MT], bf[2][NT], bl[2][EXACT ? NT : 1];
+        frags(Acur, 0, af[0]);
+        dequant(0, bf[0], bl[0]);
         if (it + 1 < steps) {
-            load_a(step0 + it + 1, areg);
-            load_b(step0 + it + 1, bnext, snext);
+            store_a(Anext);
+            load_b(step0 + it + 1);
+            if (it + 2 < steps) load_a(step0 + it + 2);
         }
-        __syncthreads();
-
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            f16x8 b[NT];
-            f16x8 blo[NT];
-#pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const uint32_t w = bcur[t][s];
-                const f16x2 sc2 = f16x2{scur[t], scur[t]};
-                const f16x2 p0 = nib_pair(w, 0), p1 = nib_pair(w, 4), p2 = nib_pair(w, 8), p3 = nib_pair(w, 12);
-                const f16x2 h0 = p0 * sc2, h1 = p1 * sc2, h2 = p2 * sc2, h3 = p3 * sc2;
-                b[t] = cat4(h0, h1, h2, h3);
-                if constexpr (EXACT) {
-                    blo[t] = cat4(__builtin_elementwise_fma(p0, sc2, -h0), __builtin_elementwise_fma(p1, sc2, -h1),
-                                  __builtin_elementwise_fma(p2, sc2, -h2), __builtin_elementwise_fma(p3, sc2, -h3));
-                }
+            const int cu = s & 1, nx = cu ^ 1;
+            if (s < 3) {
+                frags(Acur, s + 1, af[nx]);
+                dequant(s + 1, bf[nx], bl[nx]);
             }
 #pragma unroll
-            for (int a = 0; a < MT; a++) {
-                const u32x4 araw = *reinterpret_cast<const u32x4*>(&As[(a * 16 + j) * LDA + g * 32 + s * 8]);
-                const f16x8 av = __builtin_bit_cast(f16x8, araw);
+            for (int a = 0; a < MT; a++)
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
-                    acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b[t], acc[a][t], 0, 0, 0);
-                    if constexpr (EXACT) acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, blo[t], acc[a][t], 0, 0, 0);
+                    acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[cu][a], bf[cu][t], acc[a][t], 0, 0, 0);
+                    if constexpr (EXACT)
+                        acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[cu][a], bl[cu][t], acc[a][t], 0, 0, 0);
                 }
-            }
         }
-        if (it + 1 < steps) {
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                bcur[t] = bnext[t];
-                scur[t] = snext[t];
-            }
+        for (int t = 0; t < NT; t++) {
+            bcur[t] = bnext[t];
+            scur[t] = snext[t];
         }
+        __syncthreads();  // Anext is complete and Acur is no longer read
+    };
+
+    load_a(step0);
+    load_b(step0);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        bcur[t] = bnext[t];
+        scur[t] = snext[t];
+    }
+    store_a(As0);
+    if (steps > 1) load_a(step0 + 1);
+    __syncthreads();
+    for (int it = 0; it < steps; it += 2) {
+        step(As0, As1, it);
+        if (it + 1 < steps) step(As1, As0, it + 1);
     }
 
     // Output: acc[a][t][r] is row m0 + 16a + 4g + r, column ncol[t].
@@ -221,6 +269,7 @@ const Cfg kCfgs[] = {
     SD_CFG(1, 1, true), SD_CFG(2, 1, true),                                           // M <= 20: f32 dequant
     SD_CFG(1, 1, false), SD_CFG(2, 1, false), SD_CFG(3, 1, false), SD_CFG(4, 1, false),  // skinny
     SD_CFG(8, 2, false), SD_CFG(8, 4, false), SD_CFG(4, 2, false), SD_CFG(8, 1, false),  // prefill
+    SD_CFG(4, 4, false), SD_CFG(6, 2, false), SD_CFG(3, 2, false), SD_CFG(2, 2, false),
 };
 #undef SD_CFG
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -231,7 +280,7 @@ int pick_cfg(int M, bool exact) {
     if (M <= 32) return 3;
     if (M <= 48) return 4;
     if (M <= 64) return 5;
-    return 6;
+    return 8;  // (4, 2): the best prefill tile on MI355X in a sweep over the 2B's shapes
 }
 
 }  // namespace
