@@ -33,54 +33,119 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def gemm_roofline(pkg, cfg, reps=20):
-    """Average launch duration of the prefill GEMM kernel over the 2B's per-layer GEMM mix at
-    M = 512, timed with HIP events on the stream the kernels are launched on."""
-    import torch
-    d, inter = cfg["hidden_size"], cfg["intermediate_size"]
+GEMM_LABELS = ("in_proj", "out_proj", "qkv", "o_proj", "gate_up", "down")
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "gemm_w4_prefill_512_traffic.txt")
+
+
+def gemm_shapes(cfg):
+    """(label, N, K) of every int4 GEMM launch of one forward, in plan order (src/engine.rs:475-518)."""
     import sdamd.synth as synth
-    n_gdn = sum(k == "linear_attention" for k in cfg["layer_types"])
-    n_att = sum(k == "full_attention" for k in cfg["layer_types"])
+    d, inter = cfg["hidden_size"], cfg["intermediate_size"]
     H, dv = cfg["linear_num_key_heads"], cfg["linear_value_head_dim"]
     hq, hd = cfg["num_attention_heads"], cfg["head_dim"]
-    shapes = ([(synth.in_proj_rows(cfg), d), (d, H * dv)] * n_gdn + [(synth.qkv_rows(cfg), d), (d, hq * hd)] * n_att
-              + [(2 * inter, d), (d, inter)] * (n_gdn + n_att))
-    M = STATE_LEN
-    uniq = sorted(set(shapes))
-    bufs = {}
-    for (N, K) in uniq:
-        W = torch.randint(0, 2 ** 31, (N * K // 8,), dtype=torch.int32, device="cuda")
-        S = (torch.rand(N * K // 32, device="cuda") * 0.01 + 0.005).half()
-        bufs[(N, K)] = (W, S, torch.empty(M * N, dtype=torch.float16, device="cuda"))
-    A = torch.randn(M * max(K for _, K in uniq), device="cuda").half()
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
+    out = []
+    for kind in cfg["layer_types"]:
+        if kind == "linear_attention":
+            out += [("in_proj", synth.in_proj_rows(cfg), d), ("out_proj", d, H * dv)]
+        else:
+            out += [("qkv", synth.qkv_rows(cfg), d), ("o_proj", d, hq * hd)]
+        out += [("gate_up", 2 * inter, d), ("down", d, inter)]
+    return out
 
-    def run():
-        for (N, K) in shapes:
-            W, S, Y = bufs[(N, K)]
-            pkg.op_matmul(A.data_ptr(), W.data_ptr(), S.data_ptr(), Y.data_ptr(), M, N, K, False, -1, sp)
 
-    run()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
+def read_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 counter summary, or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def gemm_roofline(eng, state, cfg, reps=5):
+    """The prefill int4 GEMM (k_gemm_w4, M = 512) inside the engine's own 512-token forward: each
+    GEMM is one launch, bracketed by HIP events on the engine's stream (Engine.profile).  achieved =
+    algorithmic flops per launch / average launch duration."""
+    shapes = gemm_shapes(cfg)
+    M = len(state)
+    total_ms = []
     for _ in range(reps):
-        run()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    launches = reps * len(shapes)
-    avg_s = e0.elapsed_time(e1) / 1e3 / launches
-    flops = sum(2.0 * M * N * K for N, K in shapes) / len(shapes)
+        prof = dict(eng.profile(state))
+        total_ms.append(sum(prof[k] for k in GEMM_LABELS))
+    ms = statistics.median(total_ms)
+    launches = len(shapes)
+    avg_s = ms / 1e3 / launches
+    flops = sum(2.0 * M * N * K for _, N, K in shapes) / launches
     achieved = flops / avg_s / 1e12
     return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_MFMA_F16, 4), "traffic": None,
-            "kernel": "k_gemm_w4<8,2,false> (prefill int4 GEMM, M=512)",
-            "avg_launch_us": round(avg_s * 1e6, 2), "flops_per_launch": flops, "launches_timed": launches}
+            "frac": round(achieved / PEAK_MFMA_F16, 4), "traffic": read_traffic(),
+            "kernel": "k_gemm_w4 (int4 g32 fused-dequant MFMA GEMM, prefill M=512, the 2B's 96 GEMMs)",
+            "avg_launch_us": round(avg_s * 1e6, 2), "flops_per_launch": flops,
+            "algorithmic_bytes_per_launch": sum(N * K // 2 + N * K // 16 + 2 * M * K + 2 * M * N
+                                                for _, N, K in shapes) / launches,
+            "launches_timed": launches * reps}
 
 
-def cpu_baseline(model_dir, vocab, n_tokens=64):
-    """The C oracle (a CPU port of the reference kernels) on the host cores: prefill of n_tokens."""
+def pmc_workload(eng, state):
+    """What the rocprofv3 counter runs profile: a plain copy kernel of known size (torch.neg over
+    256 MiB of f32: 256 MiB read + 256 MiB written), then one eager 512-token forward."""
+    import torch
+    n = 64 << 20
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    eng.profile(state)
+    torch.cuda.synchronize()
+    log(f"pmc workload done: copy kernel of {4 * n} bytes each way, one {len(state)}-token forward")
+
+
+def traffic_summary(fetch_dir, write_dir, cfg, state_len):
+    """Reads the per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) of the two counter runs, scales each
+    by the ratio of the copy kernel's known bytes to its counter reading, and prints the summary
+    that read_traffic() parses."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        rows = []
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    if r["Counter_Name"] == counter:
+                        rows.append((r["Kernel_Name"], float(r["Counter_Value"])))
+        if not rows:
+            raise SystemExit(f"no {counter} rows under {d}")
+        copy = [v for k, v in rows if "neg_kernel" in k]
+        gemm = [v for k, v in rows if "k_gemm_w4" in k]
+        if not copy or not gemm:
+            raise SystemExit(f"{counter}: copy kernel or GEMM dispatches missing under {d}")
+        return statistics.median(copy), sum(gemm) / len(gemm), len(gemm)
+
+    copy_bytes = 4 * (64 << 20)
+    fc, fg, nf = per_kernel(fetch_dir, "FETCH_SIZE")
+    wc, wg, nw = per_kernel(write_dir, "WRITE_SIZE")
+    kf, kw = copy_bytes / (fc * 1024), copy_bytes / (wc * 1024)
+    traffic = fg * 1024 * kf + wg * 1024 * kw
+    shapes = gemm_shapes(cfg)
+    alg = sum(N * K // 2 + N * K // 16 + 2 * state_len * K + 2 * state_len * N for _, N, K in shapes) / len(shapes)
+    print(f"# HBM traffic of k_gemm_w4 in one eager {state_len}-token prefill of the 2B (rocprofv3 --pmc)")
+    print(f"# copy kernel (torch.neg, {copy_bytes} B each way): FETCH_SIZE {fc:.1f} KiB -> factor {kf:.4f}; "
+          f"WRITE_SIZE {wc:.1f} KiB -> factor {kw:.4f}")
+    print(f"# k_gemm_w4: {nf} dispatches, mean FETCH_SIZE {fg:.1f} KiB, mean WRITE_SIZE {wg:.1f} KiB")
+    print(f"# algorithmic bytes per launch (weights + scales + A + Y as f16): {alg:.0f}")
+    print(f"fetch_bytes_per_launch: {fg * 1024 * kf:.0f}")
+    print(f"write_bytes_per_launch: {wg * 1024 * kw:.0f}")
+    print(f"traffic_bytes_per_launch: {traffic:.0f}")
+
+
+def cpu_baseline(model_dir, vocab, n_tokens=STATE_LEN):
+    """The C oracle (a CPU port of the reference kernels) on the host cores: one prefill of
+    n_tokens random ids (the 512-token state of the workload; about 15-20 s on 16 cores)."""
     import numpy as np
     from oracle import torso
     om = torso.OracleModel(model_dir)
@@ -103,7 +168,17 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--profile", action="store_true", help="also print the per-kernel-label breakdown")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run only the workload of the rocprofv3 counter runs (copy kernel + one prefill)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the HBM traffic summary from two rocprofv3 --pmc output folders (no GPU)")
     args = ap.parse_args()
+    if args.traffic_summary:
+        import __graft_entry__ as entry
+        entry._import_pkg()
+        import sdamd.synth as synth
+        traffic_summary(*args.traffic_summary, synth.CONFIG_2B, STATE_LEN)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): every state and question is independent, "
               "so more GPUs would each run their own requests; there is no multi-GPU path to measure.", file=sys.stderr)
@@ -128,6 +203,9 @@ def main():
     state = rng.integers(0, synth.VOCAB_2B, STATE_LEN).astype(np.uint32)
     questions = [rng.integers(0, synth.VOCAB_2B, Q_LEN).astype(np.uint32) for _ in range(N_QUESTIONS)]
     temp = float(dcfg["temperature"])
+    if args.pmc_workload:
+        pmc_workload(eng, state)
+        return
 
     def step():
         t0 = time.perf_counter()
@@ -190,7 +268,7 @@ def main():
         prof_q = eng.profile(questions[0])
         res["profile_question_ms"] = {k: round(v, 4) for k, v in prof_q}
     if not args.no_roofline:
-        res["roofline"] = gemm_roofline(pkg, synth.CONFIG_2B)
+        res["roofline"] = gemm_roofline(eng, state, synth.CONFIG_2B)
     if not args.no_cpu_baseline:
         eng.free()
         res["cpu_baseline"] = cpu_baseline(model_dir, synth.VOCAB_2B)

@@ -111,6 +111,12 @@ static void deq_row(const uint32_t* W, const uint16_t* Sc, const uint16_t* Bi, i
     }
 }
 
+/* The dequantized weights W[N][K] as f32 (each f16-representable when f16_deq). */
+void or_dequant(const uint32_t* W, const uint16_t* Sc, const uint16_t* Bi, int N, int K, int bits, int group,
+                int asym, int f16_deq, float* out) {
+    for (int n = 0; n < N; n++) deq_row(W, Sc, Bi, n, K, bits, group, asym, f16_deq, out + (int64_t)n * K);
+}
+
 /* src/kernels.rs:590-709 (gemv and tiled): f32 accumulation, f16 output.  Bi may be NULL. */
 void or_matmul(const uint16_t* A, const uint32_t* W, const uint16_t* Sc, const uint16_t* Bi, int M,
                int N, int K, int bits, int group, int asym, int f16_deq, uint16_t* Y) {

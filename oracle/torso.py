@@ -73,6 +73,14 @@ def matmul(A16, Wq, Sc, N, K, f16_deq, bits=4, group=32, asym=False, Bi=None):
     return Y
 
 
+def dequant(Wq, Sc, N, K, f16_deq, bits=4, group=32, asym=False, Bi=None):
+    """deq(W)[N,K] as f32: the tiled kernel's f16 dequant or the GEMV's f32 dequant."""
+    out = np.empty((N, K), np.float32)
+    lib().or_dequant(P(np.ascontiguousarray(Wq)), P(np.ascontiguousarray(Sc)), P(Bi), I(N), I(K), I(bits), I(group),
+                     I(int(asym)), I(int(f16_deq)), P(out))
+    return out
+
+
 def add_norm(x, y16, w, rows=None, out_f32=False):
     """x += y (if y16 is not None), then RMSNorm of the given rows (src/kernels.rs:93-120)."""
     L, d = x.shape
