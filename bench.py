@@ -134,6 +134,10 @@ def traffic_summary(fetch_dir, write_dir, cfg, state_len):
     shapes = gemm_shapes(cfg)
     alg = sum(N * K // 2 + N * K // 16 + 2 * state_len * K + 2 * state_len * N for _, N, K in shapes) / len(shapes)
     print(f"# HBM traffic of k_gemm_w4 in one eager {state_len}-token prefill of the 2B (rocprofv3 --pmc)")
+    print("# commands (R = repository root, run from /tmp):")
+    print("#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d FETCH_DIR -o run -- python3 $R/bench.py --pmc-workload")
+    print("#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d WRITE_DIR -o run -- python3 $R/bench.py --pmc-workload")
+    print("#   python3 $R/bench.py --traffic-summary FETCH_DIR WRITE_DIR")
     print(f"# copy kernel (torch.neg, {copy_bytes} B each way): FETCH_SIZE {fc:.1f} KiB -> factor {kf:.4f}; "
           f"WRITE_SIZE {wc:.1f} KiB -> factor {kw:.4f}")
     print(f"# k_gemm_w4: {nf} dispatches, mean FETCH_SIZE {fg:.1f} KiB, mean WRITE_SIZE {wg:.1f} KiB")
@@ -212,23 +216,26 @@ def main():
         out = eng.forward(state, [], keep=True, timed=True)
         t1 = time.perf_counter()
         snap = out.snapshot
-        qgpu, probs = [], []
+        qgpu, probs, hs = [], [], 0.0
         for q, opts in zip(questions, OPTIONS):
             o = eng.forward(q, opts + [Q_LEN - 1], cache=snap, timed=True)
+            th = time.perf_counter()
             probs.append(head.probs(o.hidden, d, temp))
+            hs += time.perf_counter() - th
             qgpu.append(o.gpu_ms)
         t2 = time.perf_counter()
         snap.free()
-        return t1 - t0, t2 - t1, out.gpu_ms, qgpu, probs
+        return t1 - t0, t2 - t1, out.gpu_ms, qgpu, probs, hs
 
     for i in range(args.warmup):
         step()
         log(f"warmup {i + 1}/{args.warmup} done")
     torch.cuda.synchronize()
-    pre, qs, pre_gpu, q_gpu = [], [], [], []
+    pre, qs, pre_gpu, q_gpu, head_s = [], [], [], [], []
     t_start = time.perf_counter()
     for i in range(args.steps):
-        a, b, g, qg, probs = step()
+        a, b, g, qg, probs, hs = step()
+        head_s.append(hs)
         pre.append(a)
         qs.append(b)
         pre_gpu.append(g)
@@ -260,6 +267,7 @@ def main():
         "prefill_gpu_ms": round(statistics.mean(pre_gpu), 3),
         "question_ms": round(1e3 * statistics.mean(qs) / N_QUESTIONS, 3),
         "question_gpu_ms": round(statistics.mean(q_gpu), 3),
+        "head_ms": round(1e3 * statistics.mean(head_s) / N_QUESTIONS, 3),
         "probs_last_step": [[round(float(x), 5) for x in p] for p in probs],
     }
     if args.profile:

@@ -88,11 +88,20 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    // XCD-aware tile order: workgroup b runs on XCD b % 8, so XCD x is given the contiguous run of
+    // tiles [x G/8, (x+1) G/8) in column-block-major order (every row block and K split of a column
+    // block together): a column block's weights are then fetched into one XCD's L2 only.
+    const int gy = gridDim.y, gyz = gridDim.y * gridDim.z;
+    const int G = gridDim.x * gyz;
+    const int b = blockIdx.x + gridDim.x * (blockIdx.y + gy * blockIdx.z);
+    const int q8 = G >> 3;
+    const int tile = b < 8 * q8 ? (b & 7) * q8 + (b >> 3) : b;
+    const int bx = tile / gyz, by = (tile % gyz) % gy, bz = (tile % gyz) / gy;
+    const int m0 = by * BM, n0 = bx * BN;
     const int KB = K >> 5;
     const int steps_total = K / KSTEP;
     const int steps = steps_total / ksplit;
-    const int step0 = blockIdx.z * steps;
+    const int step0 = bz * steps;
 
     int ncol[NT];
     bool nok[NT];
@@ -225,7 +234,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
                 }
         return;
     }
-    float* mine = part + (size_t)blockIdx.z * M * N;
+    float* mine = part + (size_t)bz * M * N;
 #pragma unroll
     for (int a = 0; a < MT; a++)
 #pragma unroll

@@ -6,6 +6,8 @@
 #include <cmath>
 #include <cstring>
 
+#include <immintrin.h>
+
 namespace sd {
 namespace {
 
@@ -179,7 +181,7 @@ void Head::load(const uint8_t* bytes, size_t len) {
         if (!t.count(k)) throw Error(std::string("head.safetensors: no ") + k);
 }
 
-std::vector<double> Head::project(const char* which, const float* x, size_t d) const {
+std::vector<double> Head::normalize(const float* x, size_t d) const {
     double mean = 0;
     for (size_t j = 0; j < d; j++) mean += (double)x[j];
     mean /= (double)d;
@@ -191,13 +193,52 @@ std::vector<double> Head::project(const char* which, const float* x, size_t d) c
     const auto& nb = t.at("norm.bias");
     std::vector<double> xn(d);
     for (size_t j = 0; j < d; j++) xn[j] = ((double)x[j] - mean) * r * (double)nw[j] + (double)nb[j];
+    return xn;
+}
+
+// f64 dot product of f32 weights with f64 values; with AVX2 + FMA when the host has them (four
+// 4-wide partial sums).  The reference widens to f64 and sums in f64 too; the summation order only
+// moves the last bits.
+__attribute__((target("avx2,fma"))) static double dot_avx2(const float* a, const double* b, size_t n) {
+    __m256d s0 = _mm256_setzero_pd(), s1 = _mm256_setzero_pd(), s2 = _mm256_setzero_pd(), s3 = _mm256_setzero_pd();
+    size_t j = 0;
+    for (; j + 16 <= n; j += 16) {
+        s0 = _mm256_fmadd_pd(_mm256_cvtps_pd(_mm_loadu_ps(a + j)), _mm256_loadu_pd(b + j), s0);
+        s1 = _mm256_fmadd_pd(_mm256_cvtps_pd(_mm_loadu_ps(a + j + 4)), _mm256_loadu_pd(b + j + 4), s1);
+        s2 = _mm256_fmadd_pd(_mm256_cvtps_pd(_mm_loadu_ps(a + j + 8)), _mm256_loadu_pd(b + j + 8), s2);
+        s3 = _mm256_fmadd_pd(_mm256_cvtps_pd(_mm_loadu_ps(a + j + 12)), _mm256_loadu_pd(b + j + 12), s3);
+    }
+    const __m256d s = _mm256_add_pd(_mm256_add_pd(s0, s1), _mm256_add_pd(s2, s3));
+    double v[4];
+    _mm256_storeu_pd(v, s);
+    double r = (v[0] + v[1]) + (v[2] + v[3]);
+    for (; j < n; j++) r += (double)a[j] * b[j];
+    return r;
+}
+
+static double dot_plain(const float* a, const double* b, size_t n) {
+    double s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    size_t j = 0;
+    for (; j + 8 <= n; j += 8)
+        for (int u = 0; u < 8; u++) s[u] += (double)a[j + u] * b[j + u];
+    for (; j < n; j++) s[0] += (double)a[j] * b[j];
+    return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+}
+
+static double dot(const float* a, const double* b, size_t n) {
+    static const bool avx2 = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    return avx2 ? dot_avx2(a, b, n) : dot_plain(a, b, n);
+}
+
+// out[r][o] = bias[o] + W[o] . xs[r] in f64.  Each weight row is read once for all rows; the dot
+std::vector<std::vector<double>> Head::project(const char* which, const std::vector<std::vector<double>>& xs,
+                                               size_t d) const {
     const auto& w = t.at(std::string(which) + ".weight");
     const auto& b = t.at(std::string(which) + ".bias");
-    std::vector<double> out(dim);
+    std::vector<std::vector<double>> out(xs.size(), std::vector<double>(dim));
     for (size_t o = 0; o < dim; o++) {
-        double s = 0;
-        for (size_t j = 0; j < d; j++) s += (double)w[o * d + j] * xn[j];
-        out[o] = (double)b[o] + s;
+        const float* wr = w.data() + o * d;
+        for (size_t r = 0; r < xs.size(); r++) out[r][o] = (double)b[o] + dot(wr, xs[r].data(), d);
     }
     return out;
 }
@@ -206,13 +247,15 @@ std::vector<double> Head::probs(const float* hidden, size_t n_rows, size_t d, do
     if (n_rows < 2) throw Error("head: need at least one option row and the answer row");
     if (t.at("norm.weight").size() != d || t.at("q.weight").size() != dim * d || t.at("k.weight").size() != dim * d)
         throw Error("head: tensor shapes do not match hidden size " + std::to_string(d));
-    const std::vector<double> q = project("q", hidden + (n_rows - 1) * d, d);
+    std::vector<std::vector<double>> opts;
+    for (size_t i = 0; i + 1 < n_rows; i++) opts.push_back(normalize(hidden + i * d, d));
+    const std::vector<double> q = project("q", {normalize(hidden + (n_rows - 1) * d, d)}, d)[0];
+    const std::vector<std::vector<double>> k = project("k", opts, d);
     const double scale = std::pow((double)dim, -0.5) / std::max(temperature, 1e-6);
     std::vector<double> logits(n_rows - 1);
     for (size_t i = 0; i + 1 < n_rows; i++) {
-        const std::vector<double> k = project("k", hidden + i * d, d);
         double s = 0;
-        for (size_t o = 0; o < dim; o++) s += k[o] * q[o];
+        for (size_t o = 0; o < dim; o++) s += k[i][o] * q[o];
         logits[i] = s * scale;
     }
     double mx = -INFINITY;
