@@ -51,6 +51,12 @@ void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part,
              int ks, hipStream_t st, int cfg = -1);
 int gemm_w4_configs();
 int gemm_w4_cfg(int M, bool exact);
+// Kernel configuration and split-K count for an M x N x K product.  partial_ok: the consumer can
+// sum f32 split-K slots (else ks = 1 and the output is f16).
+struct GemmPlan {
+    int cfg, ks;
+};
+GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t max_part_elems);
 // Split count that brings the grid to about target_groups workgroups (power of 2, <= 8).
 int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_part_elems);
 void reduce_partials(const float* part, int ks, size_t n, f16* Y, hipStream_t st);

@@ -384,15 +384,16 @@ void Engine::ensure_pool(int l) {
 void Engine::mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L) {
     // The reference's GEMV (f32 dequant) serves M <= 20 and N % 64 != 0 (src/engine.rs:419-442).
     const bool exact = L <= 20 || m.N % 64 != 0;
-    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, nullptr, L, m.N, m.K, exact, 1, s); }});
+    const int cfg_ = gemm_w4_plan(L, m.N, m.K, exact, false, 0).cfg;
+    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, nullptr, L, m.N, m.K, exact, 1, s, cfg_); }});
 }
 
 YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L) {
     // A projection whose output only feeds the residual add: split K until the grid covers the
     // chip, the add + RMSNorm sums the partials.
     const bool exact = L <= 20 || m.N % 64 != 0;
-    const int cfg_ = gemm_w4_cfg(L, exact);
-    const int ks = gemm_w4_split(L, m.N, m.K, cfg_, 512, pool.ypart_elems);
+    const GemmPlan gp = gemm_w4_plan(L, m.N, m.K, exact, true, pool.ypart_elems);
+    const int cfg_ = gp.cfg, ks = gp.ks;
     float* part = pool.ypart;
     steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, nullptr, part, L, m.N, m.K, exact, ks, s, cfg_); }});
     YIn y;
@@ -456,8 +457,8 @@ Plan& Engine::plan(int L) {
         {
             // gate_up only feeds silu * mul, which sums split-K partials itself
             const bool exact = L <= 20 || W.gate_up.N % 64 != 0;
-            const int cg = gemm_w4_cfg(L, exact);
-            const int ks = gemm_w4_split(L, W.gate_up.N, W.gate_up.K, cg, 512, P.gpart_elems);
+            const GemmPlan plan_ = gemm_w4_plan(L, W.gate_up.N, W.gate_up.K, exact, true, P.gpart_elems);
+            const int cg = plan_.cfg, ks = plan_.ks;
             const Mat m = W.gate_up;
             float* gp = ks > 1 ? P.gpart : nullptr;  // unsplit: f16 straight into big
             steps.push_back({"gate_up", [=](hipStream_t s) {

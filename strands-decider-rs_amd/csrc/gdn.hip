@@ -19,8 +19,8 @@
 //    T by a blocked inversion (16x16 diagonal blocks as (I+N)(I+N^2)(I+N^4)(I+N^8), then block
 //    rows), W and U.  It writes the scan's A operands (W, qn e^G, Qk, (Kn e^(G_last-G))^T) already
 //    split, in MFMA fragment order, so the scan reads each fragment with one 16-byte load per lane.
-//    Block (0,0) also performs the reference's hist_update (the conv already consumed the old
-//    history).
+//    The workgroups also perform the reference's hist_update, each on a slice of the channels (the
+//    conv already consumed the old history).
 //  * gdn_scan: one workgroup per (head, 16 value columns), sequential over chunks; the state slice
 //    lives in LDS (transposed, the B operand of every product).
 #include "common.h"
@@ -405,9 +405,11 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     }
     if (tid == 0) ws.gl[slot] = eG[Lc - 1];
 
-    // ---- the reference's hist_update (src/kernels.rs:173-190), by one workgroup
-    if (hist && c == 0 && h == 0) {
-        for (int ch = tid; ch < C; ch += 256) {
+    // ---- the reference's hist_update (src/kernels.rs:173-190)
+    if (hist) {  // each workgroup of the grid takes a slice of the channels
+        const int nb = gridDim.x * H, per = (C + nb - 1) / nb, b = c * H + h;
+        const int lo = b * per, hi = min(C, lo + per);
+        for (int ch = lo + tid; ch < hi; ch += 256) {
             f16 v[3];
 #pragma unroll
             for (int r = 0; r < 3; r++) {

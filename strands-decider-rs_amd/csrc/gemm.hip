@@ -279,6 +279,7 @@ const Cfg kCfgs[] = {
     SD_CFG(1, 1, false), SD_CFG(2, 1, false), SD_CFG(3, 1, false), SD_CFG(4, 1, false),  // skinny
     SD_CFG(8, 2, false), SD_CFG(8, 4, false), SD_CFG(4, 2, false), SD_CFG(8, 1, false),  // prefill
     SD_CFG(4, 4, false), SD_CFG(6, 2, false), SD_CFG(3, 2, false), SD_CFG(2, 2, false),
+    SD_CFG(4, 3, false), SD_CFG(3, 3, false), SD_CFG(2, 3, false), SD_CFG(5, 2, false),
 };
 #undef SD_CFG
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -297,6 +298,27 @@ int pick_cfg(int M, bool exact) {
 int gemm_w4_configs() { return kNumCfgs; }
 
 int gemm_w4_cfg(int M, bool exact) { return pick_cfg(M, exact); }
+
+GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t max_part_elems) {
+    GemmPlan p{pick_cfg(M, exact), 1};
+    if (!exact && M >= 256 && M <= 1024) {
+        // Prefill-sized M.  From a sweep of the 2B's shapes at M = 512 on MI355X (256 CUs, two
+        // 256-thread workgroups each): filling whole rounds of workgroup slots matters more than a
+        // tile's own speed, so the tile follows N.
+        if (N >= 10000) p.cfg = 14;      // (4,3): N = 12288 -> 64 column blocks x 8 row blocks = 512
+        else if (N >= 7000) p.cfg = 17;  // (5,2): N = 8256 -> 65 x 7 = 455
+        else if (N >= 4000) p.cfg = 14;  // (4,3): N = 5120 -> 27 x 8 = 216
+        else if (partial_ok) {           // N = 2048: split K so that the grid covers the chip
+            p.cfg = K > 3000 ? 8 : 5;    // (4,2) x 4 splits for K = 6144, (4,1) x 2 for K = 2048
+            p.ks = K > 3000 ? 4 : 2;
+        }
+        const int steps = K / KSTEP;
+        while (p.ks > 1 && (steps % p.ks || (size_t)p.ks * M * N > max_part_elems)) p.ks /= 2;
+        return p;
+    }
+    if (partial_ok) p.ks = gemm_w4_split(M, N, K, p.cfg, 512, max_part_elems);
+    return p;
+}
 
 int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_part_elems) {
     const Cfg& c = kCfgs[cfg];
