@@ -89,6 +89,18 @@ int sd_engine_forward(sd_engine* e, const uint32_t* ids, size_t n, const size_t*
                       const sd_snapshot* cache, int keep, int timed, float* hidden_out, double* gpu_ms,
                       sd_snapshot** snap_out, char* err, size_t errlen);
 
+/* No counterpart in the reference's `Engine`: the questions of `Decider::ask_all` in one forward
+ * (its engine half, src/lib.rs:192-198, forwards each question from the prefix snapshot in turn).
+ * ids holds n_seqs independent sequences back to back (lens[q] tokens each); each one continues
+ * from `cache` (nullable) exactly as its own `sd_engine_forward` would, so the results match
+ * that forward's, while the weights stream once for the whole batch.  rows index the
+ * concatenation; hidden_out as in sd_engine_forward.  No snapshot is kept.  Limits: 1 to 32
+ * sequences; prefix + all sequences <= SD_CONTEXT; either every sequence has <= 20 tokens or every
+ * one has more (the reference's matmul kernel choice depends on the length, src/engine.rs:419). */
+int sd_engine_forward_batch(sd_engine* e, const uint32_t* ids, const size_t* lens, size_t n_seqs, const size_t* rows,
+                            size_t n_rows, const sd_snapshot* cache, int timed, float* hidden_out, double* gpu_ms,
+                            char* err, size_t errlen);
+
 /* `Snapshot::len` (src/engine.rs:82): prefix + forwarded tokens. */
 size_t sd_snapshot_len(const sd_snapshot* s);
 

@@ -26,7 +26,7 @@ CONTEXT = 4096
 SYMBOLS = [
     "sd_engine_load", "sd_engine_free", "sd_engine_hidden_size", "sd_engine_adapter", "sd_engine_forward",
     "sd_snapshot_len", "sd_snapshot_free", "sd_engine_profile", "sd_head_load", "sd_head_free", "sd_head_probs",
-    "sd_ask_ids", "sd_op_matmul", "sd_op_gdn",
+    "sd_ask_ids", "sd_op_matmul", "sd_op_gdn", "sd_engine_forward_batch",
 ]
 
 
@@ -80,6 +80,7 @@ def lib():
         L.sd_engine_adapter.restype = C.c_char_p
         L.sd_engine_forward.argtypes = [vp, vp, sz, vp, sz, vp, i32, i32, vp, C.POINTER(C.c_double), C.POINTER(vp),
                                         err, sz]
+        L.sd_engine_forward_batch.argtypes = [vp, vp, vp, sz, vp, sz, vp, i32, vp, C.POINTER(C.c_double), err, sz]
         L.sd_snapshot_len.argtypes = [vp]
         L.sd_snapshot_len.restype = sz
         L.sd_snapshot_free.argtypes = [vp]
@@ -215,6 +216,27 @@ class Engine:
             s = Snapshot(snap, self)
             self._snaps.append(s)
         return Output(hidden, d, ms.value if timed else None, s)
+
+    def forward_batch(self, seqs, rows, cache: Snapshot | None = None, timed: bool = False):
+        """Several independent sequences in one forward, each continuing from `cache` as its own
+        forward would (no counterpart in the reference's Engine; it replaces the per-question
+        forwards of Decider::ask_all, src/lib.rs:192-198).  rows[q] indexes sequence q.
+        Returns ([hidden rows of sequence q], gpu_ms)."""
+        seqs = [np.ascontiguousarray(q, dtype=np.uint32) for q in seqs]
+        ids = np.ascontiguousarray(np.concatenate(seqs) if seqs else np.zeros(0, np.uint32), dtype=np.uint32)
+        lens = np.array([len(q) for q in seqs], dtype=np.uintp)
+        flat, base, spans = [], 0, []
+        for q, r in zip(seqs, rows):
+            spans.append((len(flat), len(r)))
+            flat.extend(base + int(i) for i in r)
+            base += len(q)
+        rows_a = np.ascontiguousarray(flat, dtype=np.uintp)
+        d = self.hidden_size()
+        hidden = np.empty((len(rows_a), d), np.float32)
+        ms = C.c_double(math.nan)
+        _call(lib().sd_engine_forward_batch, self._h, _ptr(ids), _ptr(lens), len(lens), _ptr(rows_a), len(rows_a),
+              cache._h if cache is not None else None, int(timed), _ptr(hidden), C.byref(ms))
+        return [hidden[a:a + n] for a, n in spans], (ms.value if timed else None)
 
     def profile(self, ids):
         """src/engine.rs:668-711: [(label, ms)], slowest first."""

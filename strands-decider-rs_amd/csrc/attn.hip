@@ -19,12 +19,13 @@ constexpr int BQ = 16;  // queries per workgroup
 template <int HD>
 __global__ __launch_bounds__(HD) void k_qk_prep(const f16* __restrict__ big, AttnShape s, const float* __restrict__ qw,
                                                 const float* __restrict__ kw, const float* __restrict__ rope, int L,
-                                                const uint32_t* __restrict__ lu, f16* __restrict__ Q,
-                                                f16* __restrict__ Kc, f16* __restrict__ Vc) {
+                                                const uint32_t* __restrict__ lu, const uint32_t* __restrict__ rowt,
+                                                f16* __restrict__ Q, f16* __restrict__ Kc, f16* __restrict__ Vc) {
     __shared__ float red[HD / 64];
     __shared__ float nv[HD];
     const int t = blockIdx.x, slot = blockIdx.y, d = threadIdx.x;
-    const int pos = (int)lu[1] + t;
+    const int pos = (int)lu[1] + t;                                        // cache row
+    const int rpos = (int)lu[1] + (rowt ? (int)(rowt[t] & 0xFFFFu) : t);  // RoPE position
     const bool isq = slot < s.HQ;
     const int k_off = 2 * s.HQ * HD, v_off = k_off + s.HK * HD;
     const f16* row = big + (size_t)t * s.stride;
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(HD) void k_qk_prep(const f16* __restrict__ big, Att
     const int rd2 = s.RD / 2;
     if (d < s.RD) {
         const int i = d % rd2;
-        const float c = rope[((size_t)pos * rd2 + i) * 2], sn = rope[((size_t)pos * rd2 + i) * 2 + 1];
+        const float c = rope[((size_t)rpos * rd2 + i) * 2], sn = rope[((size_t)rpos * rd2 + i) * 2 + 1];
         r = d < rd2 ? n * c - nv[d + rd2] * sn : n * c + nv[d - rd2] * sn;
     }
     if (isq) Q[((size_t)slot * L + t) * HD + d] = (f16)r;
@@ -76,7 +77,8 @@ __device__ __forceinline__ float wave_sum16(float v) {
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f16* __restrict__ Kc,
                                               const f16* __restrict__ Vt, const f16* __restrict__ big, AttnShape s,
-                                              int L, const uint32_t* __restrict__ lu, f16* __restrict__ out,
+                                              int L, const uint32_t* __restrict__ lu,
+                                              const uint32_t* __restrict__ rowt, f16* __restrict__ out,
                                               float* __restrict__ pacc, float* __restrict__ pml, int ks) {
     static_assert(HD == 256, "attention is written for 256-wide heads");
     constexpr int ND = HD / 16;   // 16 output dimension tiles
@@ -94,8 +96,10 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     const int span = ((nkeys + ks - 1) / ks + KB - 1) / KB * KB;
     const int kbeg = z * span, kend = min(nkeys, kbeg + span);
     const float scale = 1.0f / sqrtf((float)HD);
-    const int qpos = P + t0 + fq;  // absolute position of this lane's query
+    const int qpos = P + t0 + fq;  // cache row of this lane's query
     const bool qok = fq < nq;
+    // first cache row of the query's own sequence: rows [P, qlo) belong to other sequences
+    const int qlo = P + (rowt ? (int)(rowt[t0 + min(fq, nq - 1)] >> 16) : 0);
 
     // Q^T fragments (B operand): lane (query fq, group fg) holds Q[fq][32s + 8fg .. +8], pre-scaled
     // by 1/sqrt(hd) and rounded to f16 as the reference does.
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int j = j0 + tt * 16 + fg * 4 + r;
-                const float v = (qok && j < kend && j <= qpos) ? st2[tt][r] : -INFINITY;
+                const float v = (qok && j < kend && j <= qpos && (j < P || j >= qlo)) ? st2[tt][r] : -INFINITY;
                 sv[tt * 4 + r] = v;
                 tmax = fmaxf(tmax, v);
             }
@@ -236,10 +240,11 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ p
 }  // namespace
 
 void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* kw, const float* rope, int L,
-             const uint32_t* lu, f16* Q, f16* Kc, f16* Vc, hipStream_t st) {
+             const uint32_t* lu, const Segs& sg, f16* Q, f16* Kc, f16* Vc, hipStream_t st) {
     SD_CHECK(s.HD == 256, "attention: only head_dim 256 is supported");
     SD_CHECK(s.RD % 2 == 0 && s.RD <= s.HD, "attention: bad rotary_dim");
-    hipLaunchKernelGGL(k_qk_prep<256>, dim3(L, s.HQ + s.HK), dim3(256), 0, st, big, s, qw, kw, rope, L, lu, Q, Kc, Vc);
+    hipLaunchKernelGGL(k_qk_prep<256>, dim3(L, s.HQ + s.HK), dim3(256), 0, st, big, s, qw, kw, rope, L, lu, sg.row, Q,
+                       Kc, Vc);
     launched("qk_prep");
 }
 
@@ -247,12 +252,13 @@ void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* k
 size_t attn_ws_floats(int rows, const AttnShape& s) { return (size_t)8 * rows * s.HQ * (s.HD + 2); }
 
 void attention_split(const f16* Q, const f16* Kc, const f16* Vc, const f16* big, const AttnShape& s, int L,
-                     const uint32_t* lu, int ks, float* ws, f16* out, hipStream_t st) {
+                     const uint32_t* lu, const Segs& sg, int ks, float* ws, f16* out, hipStream_t st) {
     SD_CHECK(s.HD == 256 && s.HQ % s.HK == 0, "attention: unsupported head shape");
     const int nb = (L + BQ - 1) / BQ;
     float* pacc = ws;
     float* pml = ws + (size_t)ks * L * s.HQ * s.HD;
-    hipLaunchKernelGGL(k_attn<256>, dim3(nb, s.HQ, ks), dim3(256), 0, st, Q, Kc, Vc, big, s, L, lu, out, pacc, pml, ks);
+    hipLaunchKernelGGL(k_attn<256>, dim3(nb, s.HQ, ks), dim3(256), 0, st, Q, Kc, Vc, big, s, L, lu, sg.row, out, pacc,
+                       pml, ks);
     launched("attn");
     if (ks > 1) {
         hipLaunchKernelGGL(k_attn_combine<256>, dim3(L, s.HQ), dim3(256), 0, st, pacc, pml, big, s, L, ks, out);

@@ -82,6 +82,16 @@ int sd_engine_forward(sd_engine* e, const uint32_t* ids, size_t n, const size_t*
     });
 }
 
+int sd_engine_forward_batch(sd_engine* e, const uint32_t* ids, const size_t* lens, size_t n_seqs, const size_t* rows,
+                            size_t n_rows, const sd_snapshot* cache, int timed, float* hidden_out, double* gpu_ms,
+                            char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!e || !ids || !lens || (!rows && n_rows) || (!hidden_out && n_rows))
+            throw sd::Error("sd_engine_forward_batch: null argument");
+        E(e)->forward_batch(ids, lens, n_seqs, rows, n_rows, S(cache), timed != 0, hidden_out, gpu_ms);
+    });
+}
+
 size_t sd_snapshot_len(const sd_snapshot* s) { return s ? S(s)->len : 0; }
 
 void sd_snapshot_free(sd_snapshot* s) { delete S(s); }
@@ -147,16 +157,53 @@ int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_s
             answer(0, rows, hidden);
             return;
         }
-        // src/lib.rs:192-198: the state once, each question from its snapshot.
+        // src/lib.rs:192-198: the state once, every question continuing from its snapshot.  The
+        // questions run as independent sequences of batched forwards (same results as one forward
+        // each; the weights stream once per batch).  A batch holds questions of one matmul class
+        // (<= 20 tokens or longer) and fits the context after the prefix.
         sd::Snapshot* prefix = nullptr;
         eng->forward(state, n_state, nullptr, 0, nullptr, true, false, nullptr, nullptr, &prefix);
         std::unique_ptr<sd::Snapshot> hold(prefix);
-        for (size_t i = 0; i < n_questions; i++) {
-            std::vector<size_t> rows(options[i], options[i] + n_options[i]);
-            rows.push_back(q_lens[i] - 1);
+        std::vector<std::vector<size_t>> batches;
+        for (int cls = 0; cls < 2; cls++) {
+            std::vector<size_t> cur;
+            size_t tokens = 0;
+            for (size_t i = 0; i < n_questions; i++) {
+                if ((q_lens[i] <= 20) != (cls == 0)) continue;
+                if (!cur.empty() && (cur.size() == (size_t)sd::SD_MAX_SEQS || n_state + tokens + q_lens[i] > SD_CONTEXT)) {
+                    batches.push_back(cur);
+                    cur.clear();
+                    tokens = 0;
+                }
+                cur.push_back(i);
+                tokens += q_lens[i];
+            }
+            if (!cur.empty()) batches.push_back(cur);
+        }
+        std::vector<std::vector<double>> probs(n_questions);
+        for (const auto& b : batches) {
+            std::vector<uint32_t> ids;
+            std::vector<size_t> lens, rows;
+            std::vector<std::pair<size_t, size_t>> spans;  // (question, first hidden row)
+            for (size_t i : b) {
+                const size_t base = ids.size();
+                spans.emplace_back(i, rows.size());
+                for (size_t k = 0; k < n_options[i]; k++) rows.push_back(base + options[i][k]);
+                rows.push_back(base + q_lens[i] - 1);
+                ids.insert(ids.end(), q_ids[i], q_ids[i] + q_lens[i]);
+                lens.push_back(q_lens[i]);
+            }
             std::vector<float> hidden(rows.size() * d);
-            eng->forward(q_ids[i], q_lens[i], rows.data(), rows.size(), prefix, false, false, hidden.data(), nullptr, nullptr);
-            answer(i, rows, hidden);
+            eng->forward_batch(ids.data(), lens.data(), lens.size(), rows.data(), rows.size(), prefix, false,
+                               hidden.data(), nullptr);
+            for (const auto& sp : spans) {
+                const size_t i = sp.first, nr = n_options[i] + 1;
+                probs[i] = Hd(h)->probs(hidden.data() + sp.second * d, nr, d, temperatures[i]);
+            }
+        }
+        for (size_t i = 0; i < n_questions; i++) {
+            std::memcpy(probs_out + out_off, probs[i].data(), probs[i].size() * sizeof(double));
+            out_off += probs[i].size();
         }
     });
 }
@@ -212,8 +259,8 @@ int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off
         sd::gdn_ws_carve(w.gdn, L, s, ws);
         const hipStream_t st = static_cast<hipStream_t>(stream);
         sd::gdn_prep(static_cast<const float*>(qkv), static_cast<const sd::f16*>(big), s, static_cast<const float*>(negA),
-                     static_cast<const float*>(dtb), L, ws, nullptr, st);
-        sd::gdn_scan(s, L, ws, static_cast<float*>(state), nullptr, load_state, static_cast<float*>(o), st);
+                     static_cast<const float*>(dtb), L, ws, nullptr, sd::Segs{}, 0, nullptr, st);
+        sd::gdn_scan(s, L, ws, static_cast<float*>(state), nullptr, load_state, static_cast<float*>(o), sd::Segs{}, 1, st);
     });
 }
 

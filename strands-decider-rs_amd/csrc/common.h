@@ -81,6 +81,20 @@ void add_bias(f16* y, int L, int N, const float* c, hipStream_t st);
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);
 
 // ---- gated delta net (gdn.hip) ---------------------------------------------------------------
+// Several independent token sequences in one forward (the questions of an ask_all, each continuing
+// from the same prefix).  Rows of a sequence are consecutive.  Device tables; all null = one
+// sequence covering every row:
+//   row[r]   = local index i | first row of r's sequence << 16
+//   chunk[c] = first row | length << 16 of chunk c (chunks of <= 64 rows never cross sequences)
+//   seq[q]   = first chunk | chunk count << 16 of sequence q
+// The chunk and sequence counts are lu[4] and lu[5].
+constexpr int SD_MAX_SEQS = 32;  // sequences per forward
+struct Segs {
+    const uint32_t* row = nullptr;
+    const uint32_t* chunk = nullptr;
+    const uint32_t* seq = nullptr;
+};
+
 struct GdnShape {
     int H, DK, DV, stride, a_off, b_off, z_off, C;
 };
@@ -96,27 +110,32 @@ struct GdnWs {
 };
 size_t gdn_ws_bytes(int cap, const GdnShape& s);
 void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws);
+// Every sequence's first rows read the conv history `hist`.
 void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out,
-               hipStream_t st);
-// hist (nullable) is updated from big afterwards (the reference's hist_update).
+               const Segs& sg, hipStream_t st);
+// hist (nullable) is updated from big afterwards (the reference's hist_update; single sequence
+// only).  nch = chunk grid size (chunks past lu[4] exit when sg.chunk is set).
 void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
-              const GdnWs& ws, f16* hist, hipStream_t st);
-// lu = device [L, P, ctx, has_cache] (the state is loaded when has_cache); with lu null,
-// load_default decides.
+              const GdnWs& ws, f16* hist, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st);
+// lu = device [L, P, ctx, has_cache, chunks, sequences] (the state is loaded when has_cache); with
+// lu null, load_default decides.  Every sequence starts from `state`; the final state is written
+// back only for a single sequence (sg.seq null).  nseq = sequence grid size.
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
-              hipStream_t st);
+              const Segs& sg, int nseq, hipStream_t st);
 void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st);
 
 // ---- attention (attn.hip) --------------------------------------------------------------------
 struct AttnShape {
     int HQ, HK, HD, RD, stride, ctx;
 };
+// RoPE position of row r = P + its index in its sequence; cache row = P + r.
 void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* kw, const float* rope, int L,
-             const uint32_t* lu, f16* Q, f16* Kc, f16* Vc, hipStream_t st);
+             const uint32_t* lu, const Segs& sg, f16* Q, f16* Kc, f16* Vc, hipStream_t st);
 // Workspace (floats) of the key-split path for up to `rows` query rows and 8 splits.
 size_t attn_ws_floats(int rows, const AttnShape& s);
 // ks = number of key splits (1: no workspace needed; ks > 1 needs rows = L in the workspace).
+// Row r attends the prefix (cache rows < P) and its own sequence up to itself.
 void attention_split(const f16* Q, const f16* Kc, const f16* Vc, const f16* big, const AttnShape& s, int L,
-                     const uint32_t* lu, int ks, float* ws, f16* out, hipStream_t st);
+                     const uint32_t* lu, const Segs& sg, int ks, float* ws, f16* out, hipStream_t st);
 
 }  // namespace sd

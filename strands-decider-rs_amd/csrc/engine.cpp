@@ -297,8 +297,8 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         rope = static_cast<float*>(dalloc(table.size() * 4));
         SD_HIP(hipMemcpy(rope, table.data(), table.size() * 4, hipMemcpyHostToDevice));
     }
-    lu = static_cast<uint32_t*>(dalloc(16));
-    lu_h = static_cast<uint32_t*>(halloc(16));
+    lu = static_cast<uint32_t*>(dalloc(32));
+    lu_h = static_cast<uint32_t*>(halloc(32));
     use_graphs = !env_off("SD_GRAPHS");
     for (const LayerW& L : layers) {
         if (L.kind == SD_LINEAR_ATTENTION) max_n = std::max(max_n, L.in_proj.N);
@@ -340,6 +340,9 @@ void Engine::ensure_pool(int l) {
         attn_ws_floats(std::min(cap, 256), as) * 4,    // attention key-split workspace
         ypart * 4,                                     // split-K partials of y
         gpart * 4,                                     // split-K partials of gate_up
+        (size_t)cap * 4,                               // Segs: row table
+        (size_t)(cap / 64 + SD_MAX_SEQS) * 4,          // Segs: chunk table
+        (size_t)SD_MAX_SEQS * 4,                       // Segs: sequence table
     };
     size_t total = 0;
     for (size_t s : sizes) total += align256(s);
@@ -372,26 +375,32 @@ void Engine::ensure_pool(int l) {
     pool.ypart_elems = ypart;
     pool.gpart = (float*)ptrs[15];
     pool.gpart_elems = gpart;
+    pool.seg_row = (uint32_t*)ptrs[16];
+    pool.seg_chunk = (uint32_t*)ptrs[17];
+    pool.seg_seq = (uint32_t*)ptrs[18];
+    pool.seg_chunk_cap = cap / 64 + SD_MAX_SEQS;
     SD_HIP(hipMemset(pool.x, 0, (size_t)cap * cfg.d * 4));
     if (ids_h_cap < cap) {
         ids_h = static_cast<uint32_t*>(halloc((size_t)cap * 4));
         rows_h = static_cast<uint32_t*>(halloc((size_t)cap * 4));
         out_h = static_cast<float*>(halloc((size_t)cap * cfg.d * 4));
+        seg_h = static_cast<uint32_t*>(halloc((size_t)(cap + cap / 64 + 2 * SD_MAX_SEQS) * 4));
         ids_h_cap = cap;
     }
 }
 
-void Engine::mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L) {
+void Engine::mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L,
+                bool short_rows) {
     // The reference's GEMV (f32 dequant) serves M <= 20 and N % 64 != 0 (src/engine.rs:419-442).
-    const bool exact = L <= 20 || m.N % 64 != 0;
+    const bool exact = short_rows || m.N % 64 != 0;
     const int cfg_ = gemm_w4_plan(L, m.N, m.K, exact, false, 0).cfg;
     steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, nullptr, L, m.N, m.K, exact, 1, s, cfg_); }});
 }
 
-YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L) {
+YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L, bool short_rows) {
     // A projection whose output only feeds the residual add: split K until the grid covers the
     // chip, the add + RMSNorm sums the partials.
-    const bool exact = L <= 20 || m.N % 64 != 0;
+    const bool exact = short_rows || m.N % 64 != 0;
     const GemmPlan gp = gemm_w4_plan(L, m.N, m.K, exact, true, pool.ypart_elems);
     const int cfg_ = gp.cfg, ks = gp.ks;
     float* part = pool.ypart;
@@ -403,11 +412,16 @@ YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, cons
     return y;
 }
 
-Plan& Engine::plan(int L) {
-    auto it = plans.find(L);
+Plan& Engine::plan(int L, int nseq, bool short_seqs) {
+    const int key = (L << 8) | (nseq << 1) | (short_seqs ? 1 : 0);
+    auto it = plans.find(key);
     if (it != plans.end()) return it->second;
     Plan pl;
     pl.L = L;
+    const bool sr = nseq ? short_seqs : L <= 20;  // the reference's GEMV rows
+    Segs sg;
+    if (nseq) sg = Segs{pool.seg_row, pool.seg_chunk, pool.seg_seq};
+    const int nch = (L + 63) / 64 + (nseq ? nseq - 1 : 0);  // most chunks L rows can split into
     auto& steps = pl.steps;
     const Pool P = pool;
     const int d = cfg.d, I = cfg.inter;
@@ -423,7 +437,7 @@ Plan& Engine::plan(int L) {
             steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.in_norm, d, nullptr, L, P.h, nullptr, s); }});
         }
         if (W.kind == SD_ADAPTER) {
-            mm(steps, "proj", P.h, W.proj, P.y, L);
+            mm(steps, "proj", P.h, W.proj, P.y, L, sr);
             steps.push_back({"bias", [=](hipStream_t s) { add_bias(P.y, L, d, W.bias, s); }});
             y = YIn{};
             y.y16 = P.y;
@@ -432,23 +446,30 @@ Plan& Engine::plan(int L) {
         if (W.kind == SD_LINEAR_ATTENTION) {
             const int n = W.in_proj.N;
             const GdnShape gs{cfg.H, cfg.dk, cfg.dv, n, C + cfg.H * cfg.dv, C + cfg.H * cfg.dv + cfg.H, C, C};
-            mm(steps, "in_proj", P.h, W.in_proj, P.big, L);
-            steps.push_back({"conv", [=](hipStream_t s) { conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, s); }});
-            steps.push_back({"gdn", [=](hipStream_t s) { gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, W.hist, s); }});
-            steps.push_back({"gdn", [=](hipStream_t s) { gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, s); }});
+            mm(steps, "in_proj", P.h, W.in_proj, P.big, L, sr);
+            steps.push_back({"conv", [=](hipStream_t s) { conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, sg, s); }});
+            f16* hist_upd = nseq ? nullptr : W.hist;  // several sequences leave no history
+            steps.push_back({"gdn", [=](hipStream_t s) {
+                gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, hist_upd, sg, nch, luv, s);
+            }});
+            steps.push_back({"gdn", [=](hipStream_t s) { gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s); }});
             steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
-            y = mm_y(steps, "out_proj", P.o, W.out_proj, L);
+            y = mm_y(steps, "out_proj", P.o, W.out_proj, L, sr);
         } else {
             const AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, W.qkv.N, SD_CONTEXT};
             const float* rp = rope;
-            mm(steps, "qkv", P.h, W.qkv, P.big, L);
-            steps.push_back({"qk_prep", [=](hipStream_t s) { qk_prep(P.big, as, W.q_norm, W.k_norm, rp, L, luv, P.q, W.kc, W.vc, s); }});
+            mm(steps, "qkv", P.h, W.qkv, P.big, L, sr);
+            steps.push_back({"qk_prep", [=](hipStream_t s) {
+                qk_prep(P.big, as, W.q_norm, W.k_norm, rp, L, luv, sg, P.q, W.kc, W.vc, s);
+            }});
             const int nb = (L + 15) / 16;
             int ks = 1;
             if (L <= P.attn_rows)
                 while (ks < 8 && nb * cfg.hq * ks < 256) ks *= 2;
-            steps.push_back({"attn", [=](hipStream_t s) { attention_split(P.q, W.kc, W.vc, P.big, as, L, luv, ks, P.attn_ws, P.o, s); }});
-            y = mm_y(steps, "o_proj", P.o, W.o_proj, L);
+            steps.push_back({"attn", [=](hipStream_t s) {
+                attention_split(P.q, W.kc, W.vc, P.big, as, L, luv, sg, ks, P.attn_ws, P.o, s);
+            }});
+            y = mm_y(steps, "o_proj", P.o, W.o_proj, L, sr);
         }
         {
             const YIn yin = y;
@@ -456,7 +477,7 @@ Plan& Engine::plan(int L) {
         }
         {
             // gate_up only feeds silu * mul, which sums split-K partials itself
-            const bool exact = L <= 20 || W.gate_up.N % 64 != 0;
+            const bool exact = sr || W.gate_up.N % 64 != 0;
             const GemmPlan plan_ = gemm_w4_plan(L, W.gate_up.N, W.gate_up.K, exact, true, P.gpart_elems);
             const int cg = plan_.cfg, ks = plan_.ks;
             const Mat m = W.gate_up;
@@ -466,7 +487,7 @@ Plan& Engine::plan(int L) {
             }});
             steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, gp, ks, L, I, P.mid, s); }});
         }
-        y = mm_y(steps, "down", P.mid, W.down, L);
+        y = mm_y(steps, "down", P.mid, W.down, L, sr);
     }
     pl.last_y = y;
     if (use_graphs) {
@@ -482,35 +503,24 @@ Plan& Engine::plan(int L) {
         SD_HIP(hipStreamEndCapture(st, &pl.graph));
         SD_HIP(hipGraphInstantiate(&pl.exec, pl.graph, nullptr, nullptr, 0));
     }
-    return plans.emplace(L, std::move(pl)).first->second;
+    return plans.emplace(key, std::move(pl)).first->second;
 }
 
-void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, const Snapshot* cache,
-                     bool keep, bool timed, float* hidden, double* gpu_ms, Snapshot** snap_out) {
-    const size_t P = cache ? cache->len : 0;
-    if (n == 0 || P + n > SD_CONTEXT)
-        throw Error("context of " + std::to_string(P + n) + " tokens: must be 1 to " + std::to_string(SD_CONTEXT));
-    for (size_t r = 0; r < n_rows; r++)
-        if (rows[r] >= n) throw Error("row " + std::to_string(rows[r]) + " out of range for " + std::to_string(n) + " tokens");
-    if (cache && cache->engine != this) throw Error("snapshot belongs to another engine");
-    for (uint32_t i = 0; i < n; i++)
-        if (ids[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(ids[i]) + " out of range for vocab " + std::to_string(vocab));
-    const int L = (int)n;
-    ensure_pool(L);
-    Plan& pl = plan(L);
-
+void Engine::upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
+                    uint32_t chunks, uint32_t nseq) {
     std::memcpy(ids_h, ids, n * 4);
     SD_HIP(hipMemcpyAsync(pool.ids, ids_h, n * 4, hipMemcpyHostToDevice, st));
     for (size_t r = 0; r < n_rows; r++) rows_h[r] = (uint32_t)rows[r];
     if (n_rows) SD_HIP(hipMemcpyAsync(pool.rows, rows_h, n_rows * 4, hipMemcpyHostToDevice, st));
-    lu_h[0] = (uint32_t)n;
-    lu_h[1] = (uint32_t)P;
-    lu_h[2] = SD_CONTEXT;
-    lu_h[3] = cache ? 1u : 0u;
-    SD_HIP(hipMemcpyAsync(lu, lu_h, 16, hipMemcpyHostToDevice, st));
-    // Restore (src/engine.rs:552-571): GDN state + conv history in one copy; K/V prefix rows only
-    // when the live cache does not already hold this snapshot's prefix (question forwards write
-    // rows >= P only, so after one restore the prefix stays valid for every later question).
+    const uint32_t v[8] = {(uint32_t)n, (uint32_t)P, SD_CONTEXT, has_cache ? 1u : 0u, chunks, nseq, 0u, 0u};
+    std::memcpy(lu_h, v, sizeof(v));
+    SD_HIP(hipMemcpyAsync(lu, lu_h, sizeof(v), hipMemcpyHostToDevice, st));
+}
+
+// Restore (src/engine.rs:552-571): GDN state + conv history in one copy; K/V prefix rows only when
+// the live cache does not already hold this snapshot's prefix (question forwards write rows >= P
+// only, so after one restore the prefix stays valid for every later question).
+void Engine::restore(const Snapshot* cache, size_t P) {
     if (cache) {
         SD_HIP(hipMemcpyAsync(arena, cache->arena, arena_bytes, hipMemcpyDeviceToDevice, st));
         if (kv_owner != cache->id) {
@@ -529,6 +539,9 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
         fill_u32(reinterpret_cast<uint32_t*>(arena + arena_state_bytes), (arena_bytes - arena_state_bytes) / 4, 0u, st);
         kv_owner = 0;
     }
+}
+
+void Engine::launch_and_read(Plan& pl, size_t n_rows, bool timed) {
     if (timed) SD_HIP(hipEventRecord(ev0, st));
     if (pl.exec) {
         SD_HIP(hipGraphLaunch(pl.exec, st));
@@ -538,6 +551,45 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
     if (n_rows) add_norm(pool.x, pl.last_y, final_norm, cfg.d, pool.rows, (int)n_rows, nullptr, pool.out, st);
     if (timed) SD_HIP(hipEventRecord(ev1, st));
     if (n_rows) SD_HIP(hipMemcpyAsync(out_h, pool.out, n_rows * cfg.d * 4, hipMemcpyDeviceToHost, st));
+}
+
+void Engine::finish(size_t n_rows, float* hidden, bool timed, double* gpu_ms) {
+    if (n_rows) {
+        std::memcpy(hidden, out_h, n_rows * cfg.d * 4);
+        // A rotated torso: the head's basis is unrotate * FWHT(row) (src/engine.rs:652-660).
+        if (!unrotate.empty())
+            for (size_t r = 0; r < n_rows; r++) {
+                float* x = hidden + r * cfg.d;
+                fwht(x, cfg.d);
+                for (int j = 0; j < cfg.d; j++) x[j] = (float)((double)x[j] * unrotate[j]);
+            }
+    }
+    if (gpu_ms) {
+        *gpu_ms = NAN;
+        if (timed) {
+            float ms = 0.f;
+            SD_HIP(hipEventElapsedTime(&ms, ev0, ev1));
+            *gpu_ms = ms;
+        }
+    }
+}
+
+void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, const Snapshot* cache,
+                     bool keep, bool timed, float* hidden, double* gpu_ms, Snapshot** snap_out) {
+    const size_t P = cache ? cache->len : 0;
+    if (n == 0 || P + n > SD_CONTEXT)
+        throw Error("context of " + std::to_string(P + n) + " tokens: must be 1 to " + std::to_string(SD_CONTEXT));
+    for (size_t r = 0; r < n_rows; r++)
+        if (rows[r] >= n) throw Error("row " + std::to_string(rows[r]) + " out of range for " + std::to_string(n) + " tokens");
+    if (cache && cache->engine != this) throw Error("snapshot belongs to another engine");
+    for (uint32_t i = 0; i < n; i++)
+        if (ids[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(ids[i]) + " out of range for vocab " + std::to_string(vocab));
+    const int L = (int)n;
+    ensure_pool(L);
+    Plan& pl = plan(L);
+    upload(ids, n, rows, n_rows, P, cache != nullptr, 0, 0);
+    restore(cache, P);
+    launch_and_read(pl, n_rows, timed);
     Snapshot* snap = nullptr;
     if (keep) {
         const size_t T = P + n;
@@ -568,26 +620,64 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
         delete snap;
         throw Error(std::string("GPU: ") + hipGetErrorString(se));
     }
-    if (n_rows) {
-        std::memcpy(hidden, out_h, n_rows * cfg.d * 4);
-        // A rotated torso: the head's basis is unrotate * FWHT(row) (src/engine.rs:652-660).
-        if (!unrotate.empty())
-            for (size_t r = 0; r < n_rows; r++) {
-                float* x = hidden + r * cfg.d;
-                fwht(x, cfg.d);
-                for (int j = 0; j < cfg.d; j++) x[j] = (float)((double)x[j] * unrotate[j]);
-            }
-    }
-    if (gpu_ms) {
-        *gpu_ms = NAN;
-        if (timed) {
-            float ms = 0.f;
-            SD_HIP(hipEventElapsedTime(&ms, ev0, ev1));
-            *gpu_ms = ms;
-        }
-    }
+    finish(n_rows, hidden, timed, gpu_ms);
     if (snap_out) *snap_out = snap;
     else delete snap;
+}
+
+void Engine::forward_batch(const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows, size_t n_rows,
+                           const Snapshot* cache, bool timed, float* hidden, double* gpu_ms) {
+    if (nseq == 0 || nseq > (size_t)SD_MAX_SEQS)
+        throw Error("a batch holds 1 to " + std::to_string(SD_MAX_SEQS) + " sequences");
+    size_t n = 0;
+    bool any_short = false, any_long = false;
+    for (size_t q = 0; q < nseq; q++) {
+        if (lens[q] == 0) throw Error("sequence " + std::to_string(q) + " has no tokens");
+        n += lens[q];
+        (lens[q] <= 20 ? any_short : any_long) = true;
+    }
+    if (any_short && any_long)
+        throw Error("a batch mixes sequences of at most 20 tokens with longer ones (their matmuls differ)");
+    const size_t P = cache ? cache->len : 0;
+    if (P + n > SD_CONTEXT)
+        throw Error("context of " + std::to_string(P + n) + " tokens (prefix + every sequence): must be at most " +
+                    std::to_string(SD_CONTEXT));
+    for (size_t r = 0; r < n_rows; r++)
+        if (rows[r] >= n) throw Error("row " + std::to_string(rows[r]) + " out of range for " + std::to_string(n) + " tokens");
+    if (cache && cache->engine != this) throw Error("snapshot belongs to another engine");
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(ids[i]) + " out of range for vocab " + std::to_string(vocab));
+    const int L = (int)n;
+    ensure_pool(L);
+    Plan& pl = plan(L, (int)nseq, any_short);
+    // sequence tables (see Segs): rows, chunks of <= 64 rows inside each sequence, sequences
+    uint32_t* rowt = seg_h;
+    uint32_t* chunkt = seg_h + n;
+    uint32_t nch = 0;
+    size_t s0 = 0;
+    std::vector<uint32_t> seqt(nseq);
+    for (size_t q = 0; q < nseq; q++) {
+        for (size_t i = 0; i < lens[q]; i++) rowt[s0 + i] = (uint32_t)i | (uint32_t)(s0 << 16);
+        const uint32_t first = nch;
+        for (size_t k = 0; k < lens[q]; k += 64)
+            chunkt[nch++] = (uint32_t)(s0 + k) | (uint32_t)(std::min<size_t>(64, lens[q] - k) << 16);
+        seqt[q] = first | ((nch - first) << 16);
+        s0 += lens[q];
+    }
+    SD_CHECK((int)nch <= pool.seg_chunk_cap, "forward_batch: chunk table overflow");
+    uint32_t* seqh = chunkt + nch;
+    std::memcpy(seqh, seqt.data(), nseq * 4);
+    SD_HIP(hipMemcpyAsync(pool.seg_row, rowt, n * 4, hipMemcpyHostToDevice, st));
+    SD_HIP(hipMemcpyAsync(pool.seg_chunk, chunkt, nch * 4, hipMemcpyHostToDevice, st));
+    SD_HIP(hipMemcpyAsync(pool.seg_seq, seqh, nseq * 4, hipMemcpyHostToDevice, st));
+    upload(ids, n, rows, n_rows, P, cache != nullptr, nch, (uint32_t)nseq);
+    restore(cache, P);
+    launch_and_read(pl, n_rows, timed);
+    // The live K/V prefix rows are untouched (rows >= P only); the GDN state and history are not
+    // meaningful after several sequences, and the next forward restores or clears them.
+    const hipError_t se = hipStreamSynchronize(st);
+    if (se != hipSuccess) throw Error(std::string("GPU: ") + hipGetErrorString(se));
+    finish(n_rows, hidden, timed, gpu_ms);
 }
 
 std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids, size_t n) {
@@ -597,15 +687,8 @@ std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids,
     const int L = (int)n;
     ensure_pool(L);
     Plan& pl = plan(L);
-    std::memcpy(ids_h, ids, n * 4);
-    SD_HIP(hipMemcpyAsync(pool.ids, ids_h, n * 4, hipMemcpyHostToDevice, st));
-    lu_h[0] = (uint32_t)n;
-    lu_h[1] = 0;
-    lu_h[2] = SD_CONTEXT;
-    lu_h[3] = 0;
-    SD_HIP(hipMemcpyAsync(lu, lu_h, 16, hipMemcpyHostToDevice, st));
-    fill_u32(reinterpret_cast<uint32_t*>(arena + arena_state_bytes), (arena_bytes - arena_state_bytes) / 4, 0u, st);
-    kv_owner = 0;
+    upload(ids, n, nullptr, 0, 0, false, 0, 0);
+    restore(nullptr, 0);
     std::vector<hipEvent_t> evs(pl.steps.size() + 1);
     for (auto& e : evs) SD_HIP(hipEventCreate(&e));
     SD_HIP(hipEventRecord(evs[0], st));

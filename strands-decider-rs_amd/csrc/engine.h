@@ -71,6 +71,8 @@ struct Pool {
     size_t ypart_elems = 0;
     float* gpart = nullptr;  // split-K partials of gate_up (summed by silu * mul)
     size_t gpart_elems = 0;
+    uint32_t *seg_row = nullptr, *seg_chunk = nullptr, *seg_seq = nullptr;  // Segs tables
+    int seg_chunk_cap = 0;
 };
 
 struct Step {
@@ -120,7 +122,7 @@ struct Engine {
     std::vector<int> attn_layers;
     const float* final_norm = nullptr;
     float* rope = nullptr;
-    uint32_t* lu = nullptr;  // device [L, P, CONTEXT, has_cache]
+    uint32_t* lu = nullptr;  // device [L, P, CONTEXT, has_cache, chunks, sequences, 0, 0]
     uint32_t* lu_h = nullptr;
     uint8_t* arena = nullptr;  // [GDN states | conv histories]
     size_t arena_bytes = 0, arena_state_bytes = 0;
@@ -130,7 +132,7 @@ struct Engine {
     bool use_graphs = true;
     Pool pool;
     std::map<int, Plan> plans;
-    uint32_t *ids_h = nullptr, *rows_h = nullptr;
+    uint32_t *ids_h = nullptr, *rows_h = nullptr, *seg_h = nullptr;
     float* out_h = nullptr;
     int ids_h_cap = 0;
     std::vector<void*> device_allocs, host_allocs;
@@ -140,6 +142,12 @@ struct Engine {
               const uint64_t* shard_starts, const uint64_t* shard_bytes, size_t ns, const sd_embed* em);
     void forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, const Snapshot* cache, bool keep,
                  bool timed, float* hidden, double* gpu_ms, Snapshot** snap_out);
+    // Several independent sequences (ids = their concatenation, lens[q] tokens each) in one
+    // forward, each continuing from `cache` (nullable) as its own forward would; rows index the
+    // concatenation.  No snapshot.  Every sequence must be <= 20 tokens, or every one longer (the
+    // reference's matmul choice depends on the length).
+    void forward_batch(const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows, size_t n_rows,
+                       const Snapshot* cache, bool timed, float* hidden, double* gpu_ms);
     std::vector<std::pair<const char*, double>> profile(const uint32_t* ids, size_t n);
 
    private:
@@ -150,9 +158,16 @@ struct Engine {
     Mat mat(const std::string& name) const;
     const float* f32(const std::string& name, size_t count) const;
     void ensure_pool(int l);
-    Plan& plan(int L);
-    void mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L);
-    YIn mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L);
+    // The plan for L rows: one sequence (nseq = 0) or nseq independent ones; short: the reference's
+    // GEMV dequant (each sequence <= 20 tokens).
+    Plan& plan(int L, int nseq = 0, bool short_seqs = false);
+    void upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
+                uint32_t chunks, uint32_t nseq);
+    void restore(const Snapshot* cache, size_t P);
+    void launch_and_read(Plan& pl, size_t n_rows, bool timed);
+    void finish(size_t n_rows, float* hidden, bool timed, double* gpu_ms);
+    void mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L, bool short_rows);
+    YIn mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L, bool short_rows);
 };
 
 }  // namespace sd

@@ -70,17 +70,20 @@ __device__ __forceinline__ void get_frag(const f16* base, int KS, int rt, int s,
 }
 
 // qkvc[t, c] = silu(sum_j w[c][j] x[t + j - 3, c]), rows before 0 from hist (src/kernels.rs:152-170).
+// With several sequences, row t is index i of the sequence starting at row s0.
 __global__ void k_conv(const f16* __restrict__ big, int stride, int L, int C, const float* __restrict__ w,
-                       const f16* __restrict__ hist, float* __restrict__ out) {
+                       const f16* __restrict__ hist, float* __restrict__ out, const uint32_t* __restrict__ rowt) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     const int t = blockIdx.y;
     if (c >= C || t >= L) return;
+    const int i = rowt ? (int)(rowt[t] & 0xFFFFu) : t;
+    const int s0 = rowt ? (int)(rowt[t] >> 16) : 0;
     const float kk[4] = {w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int tt = t + j - 3;
-        const float x = tt >= 0 ? (float)big[(size_t)tt * stride + c] : (float)hist[(size_t)(tt + 3) * C + c];
+        const int tt = i + j - 3;
+        const float x = tt >= 0 ? (float)big[(size_t)(s0 + tt) * stride + c] : (float)hist[(size_t)(tt + 3) * C + c];
         s += kk[j] * x;
     }
     out[(size_t)t * C + c] = s / (1.0f + expf(-s));
@@ -95,7 +98,8 @@ constexpr size_t U_F = 64 * 128;              // U, fp32 row-major
 
 __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc, const f16* __restrict__ big,
                                                   GdnShape sh, const float* __restrict__ negA,
-                                                  const float* __restrict__ dtb, int L, GdnWs ws, f16* hist) {
+                                                  const float* __restrict__ dtb, int L, GdnWs ws, f16* hist,
+                                                  const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu) {
     constexpr int DK = 128, DV = 128;
     constexpr int RP = DK + 8;  // f16 row pitch of row-major tiles
     constexpr int TP = CH + 8;  // f16 row pitch of transposed tiles
@@ -116,8 +120,9 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int fr = lane & 15, fg = lane >> 4;  // fragment row / k group of this lane
     const int c = blockIdx.x, h = blockIdx.y, H = gridDim.y;
-    const int t0 = c * CH;
-    const int Lc = min(CH, L - t0);
+    if (chunkt && c >= (int)lu[4]) return;  // the grid is sized for the most chunks L can split into
+    const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
+    const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - t0);
     const int C = sh.C;
     const size_t slot = (size_t)c * H + h;
     f16* Wf = ws.wf + slot * WF_H;
@@ -426,14 +431,16 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
 // chunk (and state rows 32w..32w+31 for the update).
 __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, float* __restrict__ state,
                                                   const uint32_t* __restrict__ lu, int load_default,
-                                                  float* __restrict__ o) {
+                                                  float* __restrict__ o, const uint32_t* __restrict__ chunkt,
+                                                  const uint32_t* __restrict__ seqt) {
     constexpr int DK = 128, DV = 128;
     constexpr int SP = DK + 4, VP = CH + 4;
     __shared__ __attribute__((aligned(16))) float St[DVS * SP];  // S^T: [column][k]
     __shared__ __attribute__((aligned(16))) float Vt[DVS * VP];  // V'^T: [column][token]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int fr = lane & 15, fg = lane >> 4;
-    const int h = blockIdx.x, sl = blockIdx.y, H = gridDim.x;
+    const int h = blockIdx.x, sl = blockIdx.y, H = gridDim.x, q = blockIdx.z;
+    if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
     const int c0 = sl * DVS;
     const bool load = lu ? lu[3] != 0u : load_default != 0;
     float* Sg = state + (size_t)h * DK * DV;
@@ -441,15 +448,17 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         const int k = e / DVS, cc = e % DVS;
         St[cc * SP + k] = load ? Sg[k * DV + c0 + cc] : 0.f;
     }
-    const int nch = (L + CH - 1) / CH;
-    for (int c = 0; c < nch; c++) {
+    const int cfirst = seqt ? (int)(seqt[q] & 0xFFFFu) : 0;
+    const int cend = seqt ? cfirst + (int)(seqt[q] >> 16) : (L + CH - 1) / CH;
+    for (int c = cfirst; c < cend; c++) {
         const size_t slot = (size_t)c * H + h;
         const f16* Wf = ws.wf + slot * WF_H;
         const f16* Qgf = ws.qgf + slot * QGF_H;
         const f16* Qkf = ws.qkf + slot * QKF_H;
         const f16* Kgf = ws.kgf + slot * KGF_H;
         const float* U = ws.u + slot * U_F;
-        const int Lc = min(CH, L - c * CH);
+        const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
+        const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - c * CH);
         f16x8 wh[4], wl[4], qh[4], ql[4];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -494,7 +503,7 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int i = wv * 16 + fg * 4 + r;
-            if (i < Lc) o[(size_t)(c * CH + i) * sh.H * DV + h * DV + c0 + fr] = ao[r];
+            if (i < Lc) o[(size_t)(t0 + i) * sh.H * DV + h * DV + c0 + fr] = ao[r];
         }
         // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
         const float gl = ws.gl[slot];
@@ -515,6 +524,7 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
             }
         }
     }
+    if (seqt) return;  // several sequences: their final states are not kept
     __syncthreads();
     for (int e = tid; e < DK * DVS; e += 256) {
         const int k = e / DVS, cc = e % DVS;
@@ -544,13 +554,14 @@ __global__ __launch_bounds__(256) void k_gnorm(const float* __restrict__ o, cons
 
 }  // namespace
 
+// Room for the chunks of `cap` rows split into up to SD_MAX_SEQS sequences.
 size_t gdn_ws_bytes(int cap, const GdnShape& s) {
-    const size_t slots = (size_t)((cap + CH - 1) / CH) * s.H;
+    const size_t slots = (size_t)((cap + CH - 1) / CH + SD_MAX_SEQS) * s.H;
     return slots * ((WF_H + QGF_H + QKF_H + KGF_H) * 2 + (U_F + 1) * 4) + 1024;
 }
 
 void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws) {
-    const size_t slots = (size_t)((cap + CH - 1) / CH) * s.H;
+    const size_t slots = (size_t)((cap + CH - 1) / CH + SD_MAX_SEQS) * s.H;
     f16* p = static_cast<f16*>(base);
     ws.wf = p;
     ws.qgf = ws.wf + slots * WF_H;
@@ -560,23 +571,28 @@ void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws) {
     ws.gl = ws.u + slots * U_F;
 }
 
-void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out, hipStream_t st) {
-    hipLaunchKernelGGL(k_conv, dim3((C + 255) / 256, L), dim3(256), 0, st, big, stride, L, C, w, hist, out);
+void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out, const Segs& sg,
+               hipStream_t st) {
+    hipLaunchKernelGGL(k_conv, dim3((C + 255) / 256, L), dim3(256), 0, st, big, stride, L, C, w, hist, out, sg.row);
     launched("conv");
 }
 
 void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
-              const GdnWs& ws, f16* hist, hipStream_t st) {
+              const GdnWs& ws, f16* hist, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
-    const int nch = (L + CH - 1) / CH;
-    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H), dim3(256), 0, st, qkvc, big, s, negA, dtb, L, ws, hist);
+    SD_CHECK(!sg.chunk || (lu && !hist), "gdn_prep: several sequences need lu and keep no conv history");
+    if (!sg.chunk) nch = (L + CH - 1) / CH;
+    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H), dim3(256), 0, st, qkvc, big, s, negA, dtb, L, ws, hist, sg.chunk, lu);
     launched("gdn_prep");
 }
 
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
-              hipStream_t st) {
+              const Segs& sg, int nseq, hipStream_t st) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
-    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS), dim3(256), 0, st, s, L, ws, state, lu, load_default, o);
+    SD_CHECK(!sg.seq || (lu && sg.chunk), "gdn_scan: several sequences need lu and the chunk table");
+    if (!sg.seq) nseq = 1;
+    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(256), 0, st, s, L, ws, state, lu, load_default, o,
+                       sg.chunk, sg.seq);
     launched("gdn_scan");
 }
 

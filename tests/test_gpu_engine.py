@@ -98,3 +98,69 @@ def test_profile_labels(tiny):
     assert {"embed", "norm", "in_proj", "conv", "gdn", "gnorm", "out_proj", "qkv", "qk_prep", "attn", "o_proj",
             "gate_up", "silu", "down"} <= labels
     assert all(ms >= 0 for _, ms in prof)
+
+
+@pytest.mark.parametrize("lens", [(40, 25, 70, 64, 129), (5, 12, 20), (33,)])
+def test_forward_batch_matches_separate_forwards(tiny, lens):
+    """Independent sequences in one forward == each sequence's own forward from the snapshot
+    (conv history, GDN state, RoPE positions and attention masks per sequence)."""
+    eng, head, om = tiny
+    state = ids_for(20, 150)
+    seqs = [ids_for(30 + i, n) for i, n in enumerate(lens)]
+    rows = [sorted({0, n // 3, n - 1}) for n in lens]
+    prefix = eng.forward(state, [], keep=True).snapshot
+    got, _ = eng.forward_batch(seqs, rows, cache=prefix)
+    for q, r, g in zip(seqs, rows, got):
+        want = eng.forward(q, r, cache=prefix).hidden
+        err = np.abs(g - want).max()
+        assert err < HIDDEN_TOL, f"lens {lens}: max |dh| {err} vs the separate forward"
+    # and against the oracle's continuation, for the longest sequence
+    _, osnap = om.forward(state, [], keep=True)
+    k = int(np.argmax(lens))
+    owant, _ = om.forward(seqs[k], rows[k], cache=osnap)
+    assert np.abs(got[k] - owant).max() < HIDDEN_TOL
+    # the prefix is intact afterwards: a plain continuation still matches
+    again = eng.forward(seqs[0], rows[0], cache=prefix).hidden
+    assert np.abs(again - got[0]).max() < HIDDEN_TOL
+    prefix.free()
+
+
+def test_forward_batch_without_prefix(tiny):
+    eng, head, om = tiny
+    seqs = [ids_for(40, 50), ids_for(41, 90)]
+    rows = [[0, 49], [10, 89]]
+    got, _ = eng.forward_batch(seqs, rows)
+    for q, r, g in zip(seqs, rows, got):
+        want, _ = om.forward(q, r)
+        assert np.abs(g - want).max() < HIDDEN_TOL
+
+
+def test_forward_batch_errors(tiny, sdamd):
+    eng, head, om = tiny
+    with pytest.raises(sdamd.EngineError, match="mixes sequences"):
+        eng.forward_batch([ids_for(50, 10), ids_for(51, 30)], [[0], [0]])
+    with pytest.raises(sdamd.EngineError, match="1 to 32 sequences"):
+        eng.forward_batch([ids_for(52 + i, 30) for i in range(33)], [[0]] * 33)
+    with pytest.raises(sdamd.EngineError, match="has no tokens"):
+        eng.forward_batch([ids_for(53, 30), np.zeros(0, np.uint32)], [[0], []])
+    snap = eng.forward(ids_for(54, 4000), [], keep=True).snapshot
+    with pytest.raises(sdamd.EngineError, match="at most 4096"):
+        eng.forward_batch([ids_for(55, 60), ids_for(56, 60)], [[0], [0]], cache=snap)
+    snap.free()
+    h = eng.forward(ids_for(57, 10), [9]).hidden
+    assert np.isfinite(h).all()
+
+
+def test_ask_ids_mixed_lengths(tiny, sdamd):
+    """Questions of <= 20 tokens and longer ones go to separate batches; every answer matches the
+    oracle's own forward of that question from the prefix."""
+    eng, head, om = tiny
+    state = ids_for(60, 90)
+    qs = [ids_for(61, 10), ids_for(62, 45), ids_for(63, 18), ids_for(64, 70)]
+    options = [[1, 4], [2, 9, 30], [0, 5, 11], [3, 50]]
+    temps = [1.0, 1.0, 0.5, 2.0]
+    got = sdamd.ask_ids(eng, head, state, qs, options, temps)
+    _, snap = om.forward(state, [], keep=True)
+    for q, o, t, g in zip(qs, options, temps, got):
+        h, _ = om.forward(q, list(o) + [len(q) - 1], cache=snap)
+        assert np.abs(g - om.probs(h, t)).max() < PROB_TOL
