@@ -149,6 +149,69 @@ def traffic_summary(fetch_dir, write_dir, cfg, state_len):
     print(f"traffic_bytes_per_launch: {traffic:.0f}")
 
 
+def trace_summary(trace_dir):
+    """Per-kernel totals of a `rocprofv3 --kernel-trace` run of this script, then the kernels of the
+    last state prefill and of the last batched question forward.  Each forward starts with one
+    k_embed launch; without --roofline/--profile the forwards of a step alternate prefill, questions."""
+    import csv
+    import glob
+    rows = []
+    for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    if not rows:
+        raise SystemExit(f"no kernel_trace.csv under {trace_dir}")
+    rows.sort()
+
+    import re
+
+    def short(name):
+        """k_gemm_w4<4,3,false,false> from the (demangled or mangled) kernel name."""
+        m = re.match(r"_ZN2sd12_GLOBAL__N_1(\d+)", name)
+        if m:  # mangled: length-prefixed name, then I<template args>E of integer/bool literals
+            n = int(m.group(1))
+            base = name[m.end():m.end() + n]
+            rest = name[m.end() + n:]
+            if rest.startswith("I"):
+                args = re.findall(r"L([ib])(\d+)E", rest[:rest.find("EE") + 2])
+                base += "<" + ",".join(v if t == "i" else ("true" if v == "1" else "false") for t, v in args) + ">"
+            return base
+        name = name.replace("void ", "").replace("sd::(anonymous namespace)::", "")
+        return name.split("(")[0]
+
+    def table(rs, title):
+        agg = {}
+        for s, e, k in rs:
+            a = agg.setdefault(short(k), [0, 0.0])
+            a[0] += 1
+            a[1] += (e - s) / 1e3
+        busy = sum(v[1] for v in agg.values())
+        print(title)
+        print(f"  {'kernel':44s} {'calls':>6s} {'total us':>10s} {'avg us':>8s} {'%':>6s}")
+        for k, (n, us) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+            print(f"  {k:44s} {n:6d} {us:10.1f} {us / n:8.2f} {100 * us / busy:6.2f}")
+        return busy
+
+    table(rows, "# per-kernel totals over the whole run")
+    starts = [i for i, r in enumerate(rows) if "k_embed" in r[2]]
+    fwd = [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
+    # the trailing forward ends at the last kernel before any non-engine work (none in this run)
+    for kind, idx in (("state prefill", range(0, len(fwd), 2)), ("batched question forward", range(1, len(fwd), 2))):
+        idx = list(idx)
+        if not idx:
+            continue
+        f = fwd[idx[-1]]
+        print()
+        span = (f[-1][1] - f[0][0]) / 1e3
+        busy = table(f, f"# one {kind} (last of {len(idx)}): {len(f)} kernels, first start to last end "
+                        f"{span:.1f} us")
+        print(f"  kernel busy {busy:.1f} us, gaps {span - busy:.1f} us")
+        g = [(e - s) / 1e3 for s, e, k in f if "k_gemm_w4" in k]
+        if g:
+            print(f"  k_gemm_w4 launches in this forward: {len(g)}, average duration {sum(g) / len(g):.2f} us")
+
+
 def cpu_baseline(model_dir, vocab, n_tokens=STATE_LEN):
     """The C oracle (a CPU port of the reference kernels) on the host cores: one prefill of
     n_tokens random ids (the 512-token state of the workload; about 15-20 s on 16 cores)."""
@@ -178,7 +241,12 @@ def main():
                     help="run only the workload of the rocprofv3 counter runs (copy kernel + one prefill)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic summary from two rocprofv3 --pmc output folders (no GPU)")
+    ap.add_argument("--trace-summary", metavar="TRACE_DIR",
+                    help="print the kernel summary of a rocprofv3 --kernel-trace output folder (no GPU)")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.traffic_summary:
         import __graft_entry__ as entry
         entry._import_pkg()
