@@ -43,6 +43,8 @@ struct OpWs {
     size_t part_floats = 0;
     void* gdn = nullptr;
     size_t gdn_bytes = 0;
+    uint32_t* wpack = nullptr;  // the weights of sd_op_matmul in the engine nibble order
+    size_t wpack_words = 0;
 };
 OpWs& op_ws() {
     static OpWs w;
@@ -221,7 +223,17 @@ int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, 
         const size_t cap = size_t(64) << 20;
         const int ks = sd::gemm_w4_split(M, N, K, c, 256, cap);
         const auto* a = static_cast<const sd::f16*>(A);
-        const auto* wq = static_cast<const uint32_t*>(Wq);
+        // The kernels read the engine nibble order: repack a copy of the caller's weights.
+        const size_t words = (size_t)N * K / 8;
+        if (w.wpack_words < words) {
+            if (w.wpack) SD_HIP(hipFree(w.wpack));
+            w.wpack = nullptr;
+            SD_HIP(hipMalloc(&w.wpack, words * 4));
+            w.wpack_words = words;
+        }
+        SD_HIP(hipMemcpyAsync(w.wpack, Wq, words * 4, hipMemcpyDeviceToDevice, st));
+        sd::repack_w4(w.wpack, words, st);
+        const uint32_t* wq = w.wpack;
         const auto* sc = static_cast<const sd::f16*>(Sc);
         if (ks == 1) {
             sd::gemm_w4(a, wq, sc, static_cast<sd::f16*>(Y), nullptr, M, N, K, exact != 0, 1, st, c);

@@ -42,8 +42,8 @@ void launched(const char* what);
 
 // ---- quantized matmul (gemm.hip) -----------------------------------------------------------
 // Y[M,N] f16 = A[M,K] f16 . deq(W[N,K])^T with W int4 group-32 symmetric in the reference's
-// layout ([N][K/32] blocks of 4 u32, element e in word e/8 at bits 4(e%8), value (q-8)*scale,
-// scales [N][K/32] f16).  `exact` selects the f32-dequant arithmetic of the reference's GEMV
+// block layout ([N][K/32] blocks of 4 u32, k = 8w + e of a block in word w, value (q-8)*scale,
+// scales [N][K/32] f16) with the nibbles of each word in the engine order of repack_w4.  `exact` selects the f32-dequant arithmetic of the reference's GEMV
 // path (used for M <= 20), otherwise the f16 dequant of its tiled path.  With `part` non-null the
 // k range is split over ks workgroups that write f32 partials part[ks][M][N] instead of Y (ks = 1
 // allowed); the consumer sums them in slot order (add_norm, or reduce_partials).  cfg < 0 picks
@@ -61,6 +61,9 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
 // Split count that brings the grid to about target_groups workgroups (power of 2, <= 8).
 int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_part_elems);
 void reduce_partials(const float* part, int ks, size_t n, f16* Y, hipStream_t st);
+// Rewrites `words` int4 weight words in place from the reference's nibble order (the model file's)
+// to the one every gemm_w4 kernel reads; run once per weight matrix.
+void repack_w4(uint32_t* W, size_t words, hipStream_t st);
 
 // ---- elementwise / norms (elem.hip) ----------------------------------------------------------
 void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f16* Bi, int d, int bits,

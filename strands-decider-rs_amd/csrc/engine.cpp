@@ -284,6 +284,20 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         layers.push_back(L);
     }
     final_norm = f32("final_norm", cfg.d);
+    // Matmul weights into the engine nibble order, each matrix once.
+    {
+        std::vector<const Mat*> all;
+        for (const LayerW& L : layers)
+            for (const Mat* m : {&L.in_proj, &L.out_proj, &L.qkv, &L.o_proj, &L.gate_up, &L.down, &L.proj})
+                if (m->q) all.push_back(m);
+        std::vector<const uint32_t*> done;
+        for (const Mat* m : all) {
+            if (std::find(done.begin(), done.end(), m->q) != done.end()) continue;
+            done.push_back(m->q);
+            repack_w4(const_cast<uint32_t*>(m->q), (size_t)m->N * m->K / 8, st);
+        }
+        SD_HIP(hipStreamSynchronize(st));
+    }
 
     // RoPE table, angles in f64 (src/engine.rs:259-267).
     {

@@ -10,12 +10,13 @@
 //    quant block (32 k values) of column j at block kb0+g, i.e. one macro step covers 128 k and
 //    feeds 4 v_mfma_f32_16x16x32_f16; step s uses word s of the block;
 //  * a word's 8 nibbles become 4 f16 pairs with the 0x6400 exponent trick:
-//      (w & 0x000F000F) | 0x64006400 = (1024 + q0, 1024 + q4), minus 1032 (exact) gives q - 8;
-//      (w & 0x00F000F0) | 0x64006400 = (1024 + 16 q1, 1024 + 16 q5), times 1/16 minus 72 (one
-//      exact fma) gives q - 8; the same on w >> 8 gives q2/q6 and q3/q7.  Times the f16 scale
-//    rounds once: exactly the reference's f16 dequant (f16(q) - 8) * sc.  The pairs come out in
-//    k order [0,4,1,5,2,6,3,7]; the A tile is stored to LDS in the same order, so the dot
-//    products see matching k;
+//      (w & 0x000F000F) | 0x64006400 = (1024 + q, 1024 + q'), minus 1032 (exact) gives q - 8;
+//      (w & 0x00F000F0) | 0x64006400 = (1024 + 16 q, 1024 + 16 q'), times 1/16 minus 72 (one
+//      exact fma) gives q - 8; the same on w >> 8 gives the other two pairs.  Times the f16 scale
+//    rounds once: exactly the reference's f16 dequant (f16(q) - 8) * sc.  The engine stores the
+//    words in its own nibble order (k_repack_w4, run once at load), in which the four pairs are
+//    (k0,k1), (k2,k3), (k4,k5), (k6,k7): the B fragments come out in natural k order and the A
+//    tile needs no permutation;
 //  * `EXACT` reproduces the reference GEMV's f32 dequant (q-8)*sc: the value is split into
 //    hi = f16((q-8)*sc) and lo = fma_f16(q-8, sc, -hi) (exact: the residual is a multiple of
 //    2^-24 with at most 5 significant bits), and both are fed to the MFMA;
@@ -37,9 +38,10 @@ constexpr int KSTEP = 128;      // k per macro step: 4 quant blocks
 #endif
 constexpr int LDA = KSTEP + SD_LDA_PAD;  // LDS row stride in halves
 
-// The 8 nibbles of a weight word as 4 f16 pairs q - 8 (exact), k order [0,4],[1,5],[2,6],[3,7]:
-// the low nibble of each byte lands in the f16 mantissa as 1024 + q, the high nibble as
-// 1024 + 16 q, so two masks per 8-bit shift give all four pairs.
+// The 8 nibbles of a weight word in the engine nibble order (see k_repack_w4) as 4 f16 pairs q - 8
+// (exact) for k = (0,1), (2,3), (4,5), (6,7): the nibble at bits 4p lands in the f16 mantissa as
+// 1024 + q for p = 0, 2 (and 4, 6 in the high half), as 1024 + 16 q for the others, so two masks per
+// 8-bit shift give all four pairs.
 // (a & m) | c in one v_and_or_b32 (the compiler otherwise emits separate and/or here).
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
     uint32_t r;
@@ -60,18 +62,49 @@ __device__ __forceinline__ void nib_pairs(uint32_t w, f16x2& p0, f16x2& p1, f16x
     p3 = __builtin_elementwise_fma(x3, c16, c72);
 }
 
-__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
-    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+// Raw buffer access (MUBUF): a 128-bit resource of base address and byte size, per-lane 32-bit
+// offsets (VGPR) plus a uniform one (SGPR); an offset at or past the size reads zeros and touches no
+// memory.  The host pass of hipcc does not see the builtins.
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+// 16 bytes per lane straight into LDS at lds + 16 lane (lds wave-uniform).
+__device__ __forceinline__ void buf_lds16(Rsrc r, uint32_t voff, uint32_t soff, void* lds) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ u32x4 buf_b128(Rsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t buf_b16(Rsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+#else
+struct Rsrc {};
+__device__ inline Rsrc make_rsrc(const void*, uint32_t) { return {}; }
+__device__ inline void buf_lds16(Rsrc, uint32_t, uint32_t, void*) {}
+__device__ inline u32x4 buf_b128(Rsrc, uint32_t, uint32_t) { return u32x4{}; }
+__device__ inline uint32_t buf_b16(Rsrc, uint32_t, uint32_t) { return 0; }
+#endif
+
+// s_waitcnt with a vmcnt that counts this thread's loads in issue order: scheduling barriers on
+// both sides keep the compiler from moving loads across it, which would change what it counts.
+template <int IMM>
+__device__ __forceinline__ void wait_loads() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(IMM);
+    __builtin_amdgcn_sched_barrier(0);
 }
 
-// Permute 8 halves [a0..a7] (as 4 words) to [a0,a4,a1,a5,a2,a6,a3,a7].
-__device__ __forceinline__ u32x4 perm_a(u32x4 d) {
-    u32x4 o;  // v_perm_b32: selector bytes 0-3 pick from the second source, 4-7 from the first
-    o[0] = __builtin_amdgcn_perm(d[2], d[0], 0x05040100u);
-    o[1] = __builtin_amdgcn_perm(d[2], d[0], 0x07060302u);
-    o[2] = __builtin_amdgcn_perm(d[3], d[1], 0x05040100u);
-    o[3] = __builtin_amdgcn_perm(d[3], d[1], 0x07060302u);
-    return o;
+// Workgroup barrier without the release fence of __syncthreads, whose wait for every outstanding
+// vector-memory load would drain the loads issued for later steps.  The caller waits (vmcnt) for
+// the loads the other waves need; the "memory" clobber keeps the compiler from moving LDS
+// accesses across.
+__device__ __forceinline__ void bar_noflush() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
+    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
 template <int MT, int NT, bool EXACT, bool PARTIAL>
@@ -150,7 +183,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 #pragma unroll
         for (int c = 0; c < ACH; c++) {
             const int idx = tid + 256 * c;
-            *reinterpret_cast<u32x4*>(&dst[(idx >> 4) * LDA + (idx & 15) * 8]) = perm_a(areg[c]);
+            *reinterpret_cast<u32x4*>(&dst[(idx >> 4) * LDA + (idx & 15) * 8]) = areg[c];
         }
     };
     auto frags = [&](const f16* Acur, int s, f16x8* af) {
@@ -246,25 +279,42 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
             }
 }
 
-// The same product on v_mfma_f32_32x32x16_f16, which on MI355X runs at twice the rate of the
-// 16x16x32 form (measured: about 2.1 vs 1.2 PFLOP/s).  Prefill only (f16 dequant).
-//  * a wave owns MT2 32-row tiles x NT2 32-column tiles; 4 waves side by side along N;
-//  * lane (r = l%32, g = l/32) holds column r of a column tile and dequantizes quant blocks 2g and
-//    2g+1 of each 128-wide k step; MFMA k-slice s (16 k) takes word s%4 of block 2g + s/4 in lane
-//    group g, so the A fragment of lane (r, g) is the 8 halves of row r at
-//    k = 64g + 32(s/4) + 8(s%4) (the A tile sits in LDS in the nibble pair order, as above);
+// The same product on v_mfma_f32_32x32x16_f16 (measured on MI355X: 2.2 PFLOP/s with 4 independent
+// accumulators per wave; the 16x16x32 form needs 16 to get close).  Prefill and batched questions
+// (f16 dequant).
+//  * a wave owns MT2 32-row tiles x NT2 32-column tiles; 4 waves side by side along N, so every
+//    dequantized weight feeds MT2 MFMAs (at MT2 = 4: 3 VALU per MFMA, which the MFMA pipe hides);
+//  * k advances in steps of 64 through a ring of 4 LDS stages, loads issued 3 steps ahead (the
+//    first touch of a weight block or an A row comes from HBM, a few microseconds under load);
+//    one barrier per step;
+//  * the A tile of a step (BM rows x 128 B) is fetched straight into LDS (buffer_load_dwordx4 lds):
+//    16-byte chunk q of the stage (q = (i * 4 + wave) * 64 + lane for the thread's i-th load) holds
+//    row q / 8, k-chunk (q % 8) ^ ((row / 2) % 8).  A wave instruction fills 1 KiB (8 whole rows),
+//    and the fragment reads (16 rows at one k-chunk per 16 lanes) cover all 64 banks;
+//  * lane (r = l % 32, g = l / 32) holds column r of its column tiles and loads quant block g of the
+//    step (16 bytes) and its scale, up to 3 steps ahead in registers; MFMA k-slice s (16 k) takes
+//    word s of that block, which is k-chunk 4g + s of the step, so the A fragment of lane (r, g) is
+//    the 8 halves of row r at that k-chunk (the engine nibble order makes them natural);
 //  * D of the 32x32 tile: register i of lane l is row 8(i/4) + 4(l/32) + i%4, column l%32.
 template <int MT2, int NT2, bool PARTIAL>
-__global__ __launch_bounds__(256) void k_gemm_w4x(const f16* __restrict__ A, const uint32_t* __restrict__ W,
-                                                  const f16* __restrict__ S, f16* __restrict__ Y,
-                                                  float* __restrict__ part, int M, int N, int K, int ksplit) {
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2))) void k_gemm_w4m(
+    const f16* __restrict__ A, const uint32_t* __restrict__ W, const f16* __restrict__ S, f16* __restrict__ Y,
+    float* __restrict__ part, int M, int N, int K, int ksplit) {
+    constexpr int KS = 64;                   // k per step
     constexpr int BM = MT2 * 32;
-    constexpr int BN = 4 * NT2 * 32;
-    constexpr int ACH = BM * 16 / 256;  // 16-byte A chunks per thread per k step
-    __shared__ __attribute__((aligned(16))) f16 As0[BM * LDA];
-    __shared__ __attribute__((aligned(16))) f16 As1[BM * LDA];
+    constexpr int STAGE = BM * KS * 2;       // bytes of one A stage
+    constexpr int NLD = BM / 32;             // direct-to-LDS loads per thread per step
+    constexpr int PER_STEP = NLD + 2 * NT2;  // vector-memory loads a thread issues per step
+    constexpr int WAIT2 = 0x0F70 | ((2 * PER_STEP) & 15) | (((2 * PER_STEP) >> 4) << 14);  // vmcnt(2 steps)
+    // One array per stage, so the compiler can see that the loads into one stage never alias the
+    // fragment reads of another.
+    __shared__ __attribute__((aligned(1024))) uint8_t As0[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As1[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As2[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As3[STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 31, g = lane >> 5;
     // XCD-aware tile order, as in k_gemm_w4
     const int gy = gridDim.y, gyz = gridDim.y * gridDim.z;
@@ -273,26 +323,38 @@ __global__ __launch_bounds__(256) void k_gemm_w4x(const f16* __restrict__ A, con
     const int q8 = G >> 3;
     const int tile = b < 8 * q8 ? (b & 7) * q8 + (b >> 3) : b;
     const int bx = tile / gyz, by = (tile % gyz) % gy, bz = (tile % gyz) / gy;
-    const int m0 = by * BM, n0 = bx * BN;
+    const int m0 = by * BM, n0 = bx * (4 * NT2 * 32);
     const int KB = K >> 5;
-    const int steps = (K / KSTEP) / ksplit;
+    const int steps = (K / KS) / ksplit;  // a multiple of 4 (checked by the launcher)
     const int step0 = bz * steps;
 
+    // Loads go through buffer resources: per-lane offsets fixed for the whole k loop, the step in the
+    // uniform offset.  A step past this workgroup's range gets an offset past the buffer (no memory
+    // access), so every step issues the same loads and the wait counts below are exact.
+    const Rsrc ra = make_rsrc(A, (uint32_t)M * K * 2), rw = make_rsrc(W, (uint32_t)N * K / 2),
+               rs = make_rsrc(S, (uint32_t)N * KB * 2);
+    // A: this thread's chunks of a step (rows past M read the last row; their outputs are never
+    // stored).
+    uint32_t aoff[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; i++) {
+        const int q = (i * 4 + wave) * 64 + lane;
+        const int row = q >> 3, c = (q & 7) ^ ((row >> 1) & 7);
+        aoff[i] = (uint32_t)(min(m0 + row, M - 1) * K + c * 8) * 2u;
+    }
+    // Fragment reads: LDS byte offset of row r, k-chunk 4g + s (tile a adds a * 4 KiB).
+    uint32_t foff[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) foff[s] = r * 128 + (((4 * g + s) ^ ((r >> 1) & 7)) << 4);
+
     int ncol[NT2];
-    const u32x4* wrow[NT2];
-    const f16* srow[NT2];
+    uint32_t woff[NT2], soff[NT2];
 #pragma unroll
     for (int t = 0; t < NT2; t++) {
         ncol[t] = n0 + (wave * NT2 + t) * 32 + r;
-        const size_t n = (size_t)min(ncol[t], N - 1);
-        wrow[t] = reinterpret_cast<const u32x4*>(W) + n * KB + 2 * g;
-        srow[t] = S + n * KB + 2 * g;
-    }
-    const f16* arow[ACH];
-#pragma unroll
-    for (int c = 0; c < ACH; c++) {
-        const int idx = tid + 256 * c;
-        arow[c] = A + (size_t)min(m0 + (idx >> 4), M - 1) * K + (idx & 15) * 8;
+        const uint32_t n = (uint32_t)min(ncol[t], N - 1);
+        woff[t] = (n * KB + g) * 16u;
+        soff[t] = (n * KB + g) * 2u;
     }
 
     f32x16 acc[MT2][NT2];
@@ -303,94 +365,98 @@ __global__ __launch_bounds__(256) void k_gemm_w4x(const f16* __restrict__ A, con
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[a][t][i] = 0.f;
 
-    u32x4 areg[ACH], bcur[NT2][2], bnext[NT2][2];
-    f16 scur[NT2][2], snext[NT2][2];
-    auto load_a = [&](int step) {
+    // Weight blocks and scales of the 4 steps in flight (ring index = step % 4).  A scale is kept in
+    // a register of its own: packing two per register would wait for the load at once.
+    u32x4 bw[4][NT2];
+    uint32_t bs[4][NT2];
+    auto issue = [&](int it, uint8_t* dst, u32x4* bwd, uint32_t* bsd) {
+        const bool in = it < steps;
+        const uint32_t ka = in ? (uint32_t)(step0 + it) * KS * 2 : 0x80000000u;
+        const uint32_t kw = in ? (uint32_t)(step0 + it) * 32 : 0x80000000u;
+        const uint32_t ks_ = in ? (uint32_t)(step0 + it) * 4 : 0x80000000u;
 #pragma unroll
-        for (int c = 0; c < ACH; c++) areg[c] = *reinterpret_cast<const u32x4*>(arow[c] + step * KSTEP);
-    };
-    auto load_b = [&](int step) {
-#pragma unroll
-        for (int t = 0; t < NT2; t++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                bnext[t][h] = wrow[t][step * 4 + h];
-                snext[t][h] = srow[t][step * 4 + h];
-            }
-    };
-    auto store_a = [&](f16* dst) {
-#pragma unroll
-        for (int c = 0; c < ACH; c++) {
-            const int idx = tid + 256 * c;
-            *reinterpret_cast<u32x4*>(&dst[(idx >> 4) * LDA + (idx & 15) * 8]) = perm_a(areg[c]);
-        }
-    };
-    auto frags = [&](const f16* Acur, int s, f16x8* af) {
-#pragma unroll
-        for (int a = 0; a < MT2; a++)
-            af[a] = __builtin_bit_cast(
-                f16x8, *reinterpret_cast<const u32x4*>(&Acur[(a * 32 + r) * LDA + 64 * g + 32 * (s >> 2) + 8 * (s & 3)]));
-    };
-    auto dequant = [&](int s, f16x8* bf) {
+        for (int i = 0; i < NLD; i++) buf_lds16(ra, aoff[i], ka, dst + (i * 4 + wave) * 1024);
 #pragma unroll
         for (int t = 0; t < NT2; t++) {
-            const f16 sc = scur[t][s >> 2];
-            const f16x2 sc2 = f16x2{sc, sc};
+            bwd[t] = buf_b128(rw, woff[t], kw);
+            bsd[t] = buf_b16(rs, soff[t], ks_);
+        }
+        // each step's loads stay together and in step order, also in the prologue
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto frag = [&](const uint8_t* cur, int s, f16x8* af) {
+#pragma unroll
+        for (int a = 0; a < MT2; a++)
+            af[a] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(cur + a * 4096 + foff[s]));
+    };
+    auto deq = [&](const u32x4* bwc, const uint32_t* bsc, int s, f16x8* bf) {
+#pragma unroll
+        for (int t = 0; t < NT2; t++) {
+            const f16 scv = __builtin_bit_cast(f16, (uint16_t)bsc[t]);
+            const f16x2 sc2 = f16x2{scv, scv};
             f16x2 p0, p1, p2, p3;
-            nib_pairs(bcur[t][s >> 2][s & 3], p0, p1, p2, p3);
+            nib_pairs(bwc[t][s], p0, p1, p2, p3);
             bf[t] = cat4(p0 * sc2, p1 * sc2, p2 * sc2, p3 * sc2);
         }
     };
-    // One k step = 8 MFMA k-slices; slice s+1's fragments and dequant are issued before slice s's
-    // MFMAs, the next tile's A store and loads first.
-    auto step = [&](const f16* Acur, f16* Anext, int it) {
+    // Step it reads stage `cur` and refills stage `fill` (the one read at it - 1) for step it + 3.
+    // Software pipeline: the A fragments and dequantized weights of k-slice s + 1 are produced while
+    // the MFMAs of slice s run (the last slice dequantizes the next step's first one into bf0), with
+    // the issue order pinned: per MFMA a share of the dequant VALU work and one fragment read.
+    // Before the barrier every thread waits for its loads of step it + 1.
+    constexpr int NMF = MT2 * NT2;                  // MFMAs per k-slice
+    constexpr int VPER = (13 * NT2 + NMF - 1) / NMF;  // dequant VALU instructions per MFMA
+    auto step = [&](const uint8_t* cur, uint8_t* fill, const u32x4* bwc, const uint32_t* bsc, const u32x4* bwn,
+                    const uint32_t* bsn, u32x4* bwf, uint32_t* bsf, f16x8* bf0, int it) {
+        issue(it + 3, fill, bwf, bsf);
         f16x8 af[2][MT2], bf[2][NT2];
-        frags(Acur, 0, af[0]);
-        dequant(0, bf[0]);
-        if (it + 1 < steps) {
-            store_a(Anext);
-            load_b(step0 + it + 1);
-            if (it + 2 < steps) load_a(step0 + it + 2);
-        }
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
+        for (int t = 0; t < NT2; t++) bf[0][t] = bf0[t];
+        frag(cur, 0, af[0]);
+        __builtin_amdgcn_sched_group_barrier(0x100, MT2, 0);  // the first slice's fragment reads
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
             const int cu = s & 1, nx = cu ^ 1;
-            if (s < 7) {
-                frags(Acur, s + 1, af[nx]);
-                dequant(s + 1, bf[nx]);
+            if (s < 3) {
+                frag(cur, s + 1, af[nx]);
+                deq(bwc, bsc, s + 1, bf[nx]);
+            } else {
+                deq(bwn, bsn, 0, bf0);
             }
 #pragma unroll
             for (int a = 0; a < MT2; a++)
 #pragma unroll
                 for (int t = 0; t < NT2; t++)
                     acc[a][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cu][a], bf[cu][t], acc[a][t], 0, 0, 0);
-        }
 #pragma unroll
-        for (int t = 0; t < NT2; t++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                bcur[t][h] = bnext[t][h];
-                scur[t][h] = snext[t][h];
+            for (int j = 0; j < NMF; j++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, VPER, 0);  // VALU
+                if (s < 3 && j < MT2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a fragment read
             }
-        __syncthreads();
+        }
+        wait_loads<WAIT2>();  // the loads of steps it + 2, it + 3 may still be in flight
+        bar_noflush();
     };
 
-    load_a(step0);
-    load_b(step0);
-#pragma unroll
-    for (int t = 0; t < NT2; t++)
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            bcur[t][h] = bnext[t][h];
-            scur[t][h] = snext[t][h];
-        }
-    store_a(As0);
-    if (steps > 1) load_a(step0 + 1);
-    __syncthreads();
-    for (int it = 0; it < steps; it += 2) {
-        step(As0, As1, it);
-        if (it + 1 < steps) step(As1, As0, it + 1);
-    }
+    issue(0, As0, bw[0], bs[0]);
+    issue(1, As1, bw[1], bs[1]);
+    issue(2, As2, bw[2], bs[2]);
+    wait_loads<WAIT2>();
+    bar_noflush();
+    f16x8 bf0[NT2];
+    deq(bw[0], bs[0], 0, bf0);
+    // steps >= 4: no zero-trip branch, which would let the compiler sink the prologue's weight loads
+    // past the first wait (and so change what it counts).
+    int it = 0;
+    do {
+        step(As0, As3, bw[0], bs[0], bw[1], bs[1], bw[3], bs[3], bf0, it);
+        step(As1, As0, bw[1], bs[1], bw[2], bs[2], bw[0], bs[0], bf0, it + 1);
+        step(As2, As1, bw[2], bs[2], bw[3], bs[3], bw[1], bs[1], bf0, it + 2);
+        step(As3, As2, bw[3], bs[3], bw[0], bs[0], bw[2], bs[2], bf0, it + 3);
+        it += 4;
+    } while (it < steps);
+    wait_loads<0x0F70>();  // the trailing out-of-range loads, before the LDS is released
 
     float* mine = PARTIAL ? part + (size_t)bz * M * N : nullptr;
 #pragma unroll
@@ -406,6 +472,22 @@ __global__ __launch_bounds__(256) void k_gemm_w4x(const f16* __restrict__ A, con
                 else Y[(size_t)m * N + ncol[t]] = (f16)acc[a][t][i];
             }
         }
+}
+
+// In-place rewrite of int4 weight words from the reference's nibble order (k = 8w + e of a quant
+// block at bits 4e of word w) to the engine's: nibble position p holds e = [0,2,4,6,1,3,5,7][p],
+// so that nib_pairs yields the pairs (k0,k1), (k2,k3), (k4,k5), (k6,k7) in natural k order.
+__global__ void k_repack_w4(uint32_t* __restrict__ W, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t o = W[i];
+    uint32_t w = 0;
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+        const int e = p < 4 ? 2 * p : 2 * (p - 4) + 1;
+        w |= ((o >> (4 * e)) & 15u) << (4 * p);
+    }
+    W[i] = w;
 }
 
 // Y[i] = f16(sum_z part[z][i]) in slot order.
@@ -433,10 +515,11 @@ struct Cfg {
     int mt, nt;
     bool exact;
     GemmFn f16_out, part_out;
+    bool wide;  // k_gemm_w4m (k steps of 64 in a ring of 4)
 };
 
-#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX, false>, k_gemm_w4<MT, NT, EX, true>}
-#define SD_CFGX(MT2, NT2) Cfg{2 * MT2, 2 * NT2, false, k_gemm_w4x<MT2, NT2, false>, k_gemm_w4x<MT2, NT2, true>}
+#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX, false>, k_gemm_w4<MT, NT, EX, true>, false}
+#define SD_CFGM(MT2, NT2) Cfg{2 * MT2, 2 * NT2, false, k_gemm_w4m<MT2, NT2, false>, k_gemm_w4m<MT2, NT2, true>, true}
 const Cfg kCfgs[] = {
     SD_CFG(1, 1, true), SD_CFG(2, 1, true),                                           // M <= 20: f32 dequant
     SD_CFG(1, 1, false), SD_CFG(2, 1, false), SD_CFG(3, 1, false), SD_CFG(4, 1, false),  // skinny
@@ -444,10 +527,10 @@ const Cfg kCfgs[] = {
     SD_CFG(4, 4, false), SD_CFG(6, 2, false), SD_CFG(3, 2, false), SD_CFG(2, 2, false),
     SD_CFG(4, 3, false), SD_CFG(3, 3, false), SD_CFG(2, 3, false), SD_CFG(5, 2, false),
     // 32x32x16 MFMA tiles (MT2 x 32 rows, 4 x NT2 x 32 columns), listed in 16-row / 64-column units
-    SD_CFGX(2, 1), SD_CFGX(2, 2), SD_CFGX(4, 1), SD_CFGX(3, 1), SD_CFGX(1, 1), SD_CFGX(1, 2),
+    SD_CFGM(2, 1), SD_CFGM(2, 2), SD_CFGM(4, 1), SD_CFGM(3, 1), SD_CFGM(1, 1), SD_CFGM(4, 2),
 };
 #undef SD_CFG
-#undef SD_CFGX
+#undef SD_CFGM
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 int pick_cfg(int M, bool exact) {
@@ -467,26 +550,39 @@ int gemm_w4_cfg(int M, bool exact) { return pick_cfg(M, exact); }
 
 GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t max_part_elems) {
     GemmPlan p{pick_cfg(M, exact), 1};
-    if (!exact && M >= 256 && M <= 1024) {
-        // Prefill-sized M.  From a sweep of the 2B's shapes at M = 512 on MI355X (256 CUs, two
-        // 256-thread workgroups each): filling whole rounds of workgroup slots matters more than a
-        // tile's own speed, so the tile follows N.
-        if (N >= 10000) p.cfg = 14;      // (4,3): N = 12288 -> 64 column blocks x 8 row blocks = 512
-        else if (N >= 7000) p.cfg = 17;  // (5,2): N = 8256 -> 65 x 7 = 455
-        else if (N >= 4000) p.cfg = 21;  // 32x32 (3,1): N = 5120 -> 40 x 6 = 240
-        else if (partial_ok) {           // N = 2048: split K so that the grid covers the chip
-            p.cfg = 18;                  // 32x32 (2,1): 16 x 8 tiles, x 4 splits (K = 6144) or x 2
-            p.ks = K > 3000 ? 4 : 2;
-        }
+    // Configuration indices into kCfgs: the 64-wide-step 32x32 MFMA tiles (need K a multiple of 256).
+    constexpr int W21 = 18, W41 = 20, W31 = 21;
+    constexpr int T41 = 5;  // 16x16 (4,1)
+    const bool wide_ok = K % 256 == 0;
+    auto fit = [&](GemmPlan q) {  // largest usable split <= q.ks
         const int steps = K / KSTEP;
-        while (p.ks > 1 && (steps % p.ks || (size_t)p.ks * M * N > max_part_elems)) p.ks /= 2;
-        return p;
+        while (q.ks > 1 && (steps % q.ks || (size_t)q.ks * M * N > max_part_elems ||
+                            (kCfgs[q.cfg].wide && (K / 64 / q.ks) % 4)))
+            q.ks /= 2;
+        return q;
+    };
+    if (!exact && wide_ok && M >= 256 && M <= 1024) {
+        // Prefill-sized M; from a sweep of the 2B's shapes at M = 512 on MI355X (random data):
+        // N = 12288: (4,1) 37 us; N = 8256: (3,1) 32 us; N = 5120: (3,1) 19 us; N = 2048: (2,1) with
+        // 2 splits 10.6 us (K = 2048), (4,1) with 4 splits 22 us (K = 6144).
+        if (N >= 10000) p.cfg = W41;
+        else if (N >= 4000) p.cfg = W31;
+        else if (partial_ok && K > 3000) p = GemmPlan{W41, 4};
+        else if (partial_ok) p = GemmPlan{W21, 2};
+        else p.cfg = W21;
+        return fit(p);
     }
-    if (!exact && M > 64 && M < 256) {
-        // Batched questions and short prefills: 16-column tiles per wave stream the weights with
-        // more workgroups in flight ((4,1) with split K where partials are allowed, else (3,1)).
-        p.cfg = partial_ok ? 5 : 4;
+    if (!exact && wide_ok && M > 64 && M < 256) {
+        // Batched questions (M = 120 in the sweep): in_proj (N = 8256, f16 out) (2,1) 14.6 us; qkv
+        // (N = 5120, f16 out) 16x16 (4,1) 12.2 us; gate_up (4,1) with 2 splits 14.4 us; down (K =
+        // 6144) (2,1) with 8 splits 9.1 us; out_proj / o_proj 16x16 (4,1) with 4 splits 5.6 us.
+        if (!partial_ok) p.cfg = N >= 7000 ? W21 : T41;
+        else if (N >= 10000) p = GemmPlan{W41, 2};
+        else if (K > 3000) p = GemmPlan{W21, 8};
+        else p = GemmPlan{T41, 4};
+        return fit(p);
     }
+    if (!exact && M > 64 && M < 256) p.cfg = partial_ok ? T41 : 4;
     if (partial_ok) p.ks = gemm_w4_split(M, N, K, p.cfg, 512, max_part_elems);
     return p;
 }
@@ -498,7 +594,7 @@ int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_pa
     const int steps = K / KSTEP;
     int ks = 1;
     while (groups * ks < target_groups && ks < 8 && steps % (ks * 2) == 0 && steps / (ks * 2) >= 2 &&
-           (size_t)(ks * 2) * M * N <= max_part_elems)
+           (!c.wide || (steps / (ks * 2)) % 2 == 0) && (size_t)(ks * 2) * M * N <= max_part_elems)
         ks *= 2;
     return ks;
 }
@@ -512,10 +608,17 @@ void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part,
     SD_CHECK(c.exact == exact, "gemm_w4: configuration does not match the dequant mode");
     SD_CHECK(ks >= 1 && (K / KSTEP) % ks == 0, "gemm_w4: split count must divide the k steps");
     SD_CHECK(part || (Y && ks == 1), "gemm_w4: split-K writes partials and needs a partial buffer");
+    SD_CHECK(!c.wide || (K / 64 / ks) % 4 == 0, "gemm_w4: this configuration needs K / ks a multiple of 256");
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
     dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, ks);
     hipLaunchKernelGGL(part ? c.part_out : c.f16_out, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks);
     launched("gemm_w4");
+}
+
+void repack_w4(uint32_t* W, size_t words, hipStream_t st) {
+    if (!words) return;
+    hipLaunchKernelGGL(k_repack_w4, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, W, words);
+    launched("repack_w4");
 }
 
 void reduce_partials(const float* part, int ks, size_t n, f16* Y, hipStream_t st) {

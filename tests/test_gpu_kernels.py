@@ -72,7 +72,9 @@ def test_gemm_every_config(sdamd, synth, oracle):
                     if "no configuration" in str(e):
                         assert cfg >= 2 and ran > 0
                         return
-                    assert "does not match" in str(e)
+                    # f16-dequant configuration asked for f32 dequant (or the reverse), or a
+                    # 64-wide-step configuration given K / ks not a multiple of 256
+                    assert "does not match" in str(e) or "multiple of 256" in str(e)
                     continue
                 check_gemm(oracle, A, W, S, Y, N, K, exact)
                 ran += 1
