@@ -6,11 +6,12 @@ weights, random init, vocab 151936) encodes a 512-token state of uniform-random 
 (Engine::forward with keep), then answers 3 questions of 40 random tokens each from the state's
 snapshot (2, 3 and 5 option rows + the last row), the pointer head scoring each.  That is the
 reference's Decider::ask_all (src/lib.rs:183-199) on token ids; the three question forwards run as
-independent sequences of one batched forward (the same results as three forwards).
+independent sequences of one batched forward (the same results as three forwards), and the head
+(src/head.rs:55-77, f64) runs on the device after it.
 
 Reported: `value` = prefill tokens/s (512-token state forwards), `ms_per_step` = ask_all latency
 (state prefill + 3 questions + head), plus the per-phase times (questions_ms: the batched question
-forward and the head), the roofline of the dominant kernel
+forward with the pointer head on the device), the roofline of the dominant kernel
 class (the prefill int4 GEMM, timed live with HIP events on the stream it runs on) and the CPU
 baseline (the C oracle on the host cores, a bounded prefill sample of the same model).
 """
@@ -286,23 +287,21 @@ def main():
         out = eng.forward(state, [], keep=True, timed=True)
         t1 = time.perf_counter()
         snap = out.snapshot
-        # the questions continue from the snapshot as independent sequences of one forward
-        hid, qgpu = eng.forward_batch(questions, [opts + [Q_LEN - 1] for opts in OPTIONS], cache=snap, timed=True)
-        th = time.perf_counter()
-        probs = [head.probs(h, d, temp) for h in hid]
+        # the questions continue from the snapshot as independent sequences of one batched forward,
+        # the pointer head runs on the device behind it
+        probs, qgpu = eng.ask_batch(head, questions, OPTIONS, [temp] * N_QUESTIONS, cache=snap, timed=True)
         t2 = time.perf_counter()
         snap.free()
-        return t1 - t0, t2 - t1, out.gpu_ms, [qgpu], probs, t2 - th
+        return t1 - t0, t2 - t1, out.gpu_ms, [qgpu], probs
 
     for i in range(args.warmup):
         step()
         log(f"warmup {i + 1}/{args.warmup} done")
     torch.cuda.synchronize()
-    pre, qs, pre_gpu, q_gpu, head_s = [], [], [], [], []
+    pre, qs, pre_gpu, q_gpu = [], [], [], []
     t_start = time.perf_counter()
     for i in range(args.steps):
-        a, b, g, qg, probs, hs = step()
-        head_s.append(hs)
+        a, b, g, qg, probs = step()
         pre.append(a)
         qs.append(b)
         pre_gpu.append(g)
@@ -334,7 +333,6 @@ def main():
         "prefill_gpu_ms": round(statistics.mean(pre_gpu), 3),
         "questions_ms": round(1e3 * statistics.mean(qs), 3),
         "questions_gpu_ms": round(statistics.mean(q_gpu), 3),
-        "head_ms": round(1e3 * statistics.mean(head_s), 3),
         "probs_last_step": [[round(float(x), 5) for x in p] for p in probs],
     }
     if args.profile:

@@ -101,6 +101,19 @@ int sd_engine_forward_batch(sd_engine* e, const uint32_t* ids, const size_t* len
                             size_t n_rows, const sd_snapshot* cache, int timed, float* hidden_out, double* gpu_ms,
                             char* err, size_t errlen);
 
+/* No counterpart in the reference's `Engine`: the question half of `Decider::ask_all`
+ * (src/lib.rs:192-198: every question forwarded from the prefix snapshot, then `Head::probs`,
+ * src/head.rs:66-77) with the pointer head evaluated on the device in f64.  Question i is
+ * q_ids[i][0..q_lens[i]); its option rows options[i][0..n_options[i]) index into it and its answer
+ * row is its last token.  probs_out receives sum(n_options) probabilities, question by question.
+ * Questions of one matmul class (<= 20 tokens, or longer) run as independent sequences of batched
+ * forwards (at most 32 each).  gpu_ms (nullable) receives the device time of all batches when
+ * `timed`, NaN otherwise.  cache is the prefix snapshot (nullable: no prefix). */
+int sd_engine_ask_batch(sd_engine* e, const sd_head* h, const sd_snapshot* cache, size_t n_questions,
+                        const uint32_t* const* q_ids, const size_t* q_lens, const size_t* const* options,
+                        const size_t* n_options, const double* temperatures, int timed, double* probs_out,
+                        double* gpu_ms, char* err, size_t errlen);
+
 /* `Snapshot::len` (src/engine.rs:82): prefix + forwarded tokens. */
 size_t sd_snapshot_len(const sd_snapshot* s);
 
@@ -124,8 +137,9 @@ int sd_head_probs(const sd_head* h, const float* hidden, size_t n_rows, size_t d
 
 /* The engine half of `Decider::run` (src/lib.rs:183-199) on token ids: one question is a single
  * forward of state ++ question; several share one forward of the state (keep = true) and continue
- * from its snapshot.  options[i][0..n_options[i]) are option token indices into question i;
- * probs_out receives sum(n_options) probabilities, question by question. */
+ * from its snapshot (as sd_engine_ask_batch).  options[i][0..n_options[i]) are option token
+ * indices into question i; probs_out receives sum(n_options) probabilities, question by question.
+ * The head runs on the device (f64). */
 int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_state, size_t n_questions,
                const uint32_t* const* q_ids, const size_t* q_lens, const size_t* const* options,
                const size_t* n_options, const double* temperatures, double* probs_out, char* err, size_t errlen);

@@ -26,7 +26,7 @@ CONTEXT = 4096
 SYMBOLS = [
     "sd_engine_load", "sd_engine_free", "sd_engine_hidden_size", "sd_engine_adapter", "sd_engine_forward",
     "sd_snapshot_len", "sd_snapshot_free", "sd_engine_profile", "sd_head_load", "sd_head_free", "sd_head_probs",
-    "sd_ask_ids", "sd_op_matmul", "sd_op_gdn", "sd_engine_forward_batch",
+    "sd_ask_ids", "sd_op_matmul", "sd_op_gdn", "sd_engine_forward_batch", "sd_engine_ask_batch",
 ]
 
 
@@ -81,6 +81,8 @@ def lib():
         L.sd_engine_forward.argtypes = [vp, vp, sz, vp, sz, vp, i32, i32, vp, C.POINTER(C.c_double), C.POINTER(vp),
                                         err, sz]
         L.sd_engine_forward_batch.argtypes = [vp, vp, vp, sz, vp, sz, vp, i32, vp, C.POINTER(C.c_double), err, sz]
+        L.sd_engine_ask_batch.argtypes = [vp, vp, vp, sz, C.POINTER(vp), vp, C.POINTER(vp), vp, vp, i32, vp,
+                                          C.POINTER(C.c_double), err, sz]
         L.sd_snapshot_len.argtypes = [vp]
         L.sd_snapshot_len.restype = sz
         L.sd_snapshot_free.argtypes = [vp]
@@ -237,6 +239,29 @@ class Engine:
         _call(lib().sd_engine_forward_batch, self._h, _ptr(ids), _ptr(lens), len(lens), _ptr(rows_a), len(rows_a),
               cache._h if cache is not None else None, int(timed), _ptr(hidden), C.byref(ms))
         return [hidden[a:a + n] for a, n in spans], (ms.value if timed else None)
+
+    def ask_batch(self, head: "Head", questions, options, temperatures, cache: Snapshot | None = None,
+                  timed: bool = False):
+        """The question half of Decider::ask_all (src/lib.rs:192-198) with the pointer head on the
+        device: question i continues from `cache`; options[i] index its option rows (its last token
+        is the answer row).  Returns ([option probabilities of question i], gpu_ms)."""
+        qs = [np.ascontiguousarray(q, dtype=np.uint32) for q in questions]
+        ops = [np.ascontiguousarray(o, dtype=np.uintp) for o in options]
+        nq = len(qs)
+        qptr = (C.c_void_p * nq)(*[q.ctypes.data for q in qs])
+        qlen = np.array([len(q) for q in qs], np.uintp)
+        optr = (C.c_void_p * nq)(*[o.ctypes.data for o in ops])
+        nopt = np.array([len(o) for o in ops], np.uintp)
+        temps = np.ascontiguousarray(temperatures, dtype=np.float64)
+        out = np.empty(int(nopt.sum()), np.float64)
+        ms = C.c_double(math.nan)
+        _call(lib().sd_engine_ask_batch, self._h, head._h, cache._h if cache is not None else None, nq, qptr,
+              _ptr(qlen), optr, _ptr(nopt), _ptr(temps), int(timed), _ptr(out), C.byref(ms))
+        res, o = [], 0
+        for n in nopt:
+            res.append(out[o:o + n])
+            o += n
+        return res, (ms.value if timed else None)
 
     def profile(self, ids):
         """src/engine.rs:668-711: [(label, ms)], slowest first."""

@@ -131,22 +131,102 @@ int sd_head_probs(const sd_head* h, const float* hidden, size_t n_rows, size_t d
     });
 }
 
+namespace {
+
+// The questions of an ask_all, each continuing from `prefix` (src/lib.rs:192-198), with the pointer
+// head on the device.  They run as independent sequences of batched forwards (the same results as
+// one forward each; the weights stream once per batch).  A batch holds questions of one matmul
+// class (<= 20 tokens or longer, src/engine.rs:419) and fits the context after the prefix.
+void ask_from(sd::Engine* eng, const sd::Head& head, const sd::Snapshot* prefix, size_t n_questions,
+              const uint32_t* const* q_ids, const size_t* q_lens, const size_t* const* options, const size_t* n_options,
+              const double* temperatures, bool timed, double* probs_out, double* gpu_ms) {
+    const size_t P = prefix ? prefix->len : 0;
+    std::vector<std::vector<size_t>> batches;
+    for (int cls = 0; cls < 2; cls++) {
+        std::vector<size_t> cur;
+        size_t tokens = 0;
+        for (size_t i = 0; i < n_questions; i++) {
+            if ((q_lens[i] <= 20) != (cls == 0)) continue;
+            if (!cur.empty() && (cur.size() == (size_t)sd::SD_MAX_SEQS || P + tokens + q_lens[i] > SD_CONTEXT)) {
+                batches.push_back(cur);
+                cur.clear();
+                tokens = 0;
+            }
+            cur.push_back(i);
+            tokens += q_lens[i];
+        }
+        if (!cur.empty()) batches.push_back(cur);
+    }
+    std::vector<size_t> out_at(n_questions);  // where question i's probabilities go
+    for (size_t i = 0, o = 0; i < n_questions; i++) {
+        out_at[i] = o;
+        o += n_options[i];
+    }
+    double total_ms = 0.0;
+    for (const auto& b : batches) {
+        std::vector<uint32_t> ids;
+        std::vector<size_t> lens, rows, nopt;
+        std::vector<double> temps;
+        size_t np = 0;
+        for (size_t i : b) {
+            const size_t base = ids.size();
+            for (size_t k = 0; k < n_options[i]; k++) rows.push_back(base + options[i][k]);
+            rows.push_back(base + q_lens[i] - 1);
+            ids.insert(ids.end(), q_ids[i], q_ids[i] + q_lens[i]);
+            lens.push_back(q_lens[i]);
+            nopt.push_back(n_options[i]);
+            temps.push_back(temperatures[i]);
+            np += n_options[i];
+        }
+        std::vector<double> p(np);
+        double ms = 0.0;
+        eng->ask_batch(head, ids.data(), lens.data(), lens.size(), rows.data(), nopt.data(), temps.data(), prefix,
+                       timed, p.data(), &ms);
+        total_ms += ms;
+        size_t o = 0;
+        for (size_t i : b) {
+            std::memcpy(probs_out + out_at[i], p.data() + o, n_options[i] * sizeof(double));
+            o += n_options[i];
+        }
+    }
+    if (gpu_ms) *gpu_ms = timed ? total_ms : NAN;
+}
+
+void check_questions(size_t n_questions, const uint32_t* const* q_ids, const size_t* q_lens,
+                     const size_t* const* options, const size_t* n_options, const double* temperatures) {
+    if (n_questions == 0) throw sd::Error("ask at least one question");
+    if (!q_ids || !q_lens || !options || !n_options || !temperatures) throw sd::Error("null question argument");
+    for (size_t i = 0; i < n_questions; i++) {
+        if (q_lens[i] == 0 || !q_ids[i]) throw sd::Error("question " + std::to_string(i) + " has no tokens");
+        if (n_options[i] == 0 || !options[i]) throw sd::Error("question " + std::to_string(i) + " has no options");
+        for (size_t k = 0; k < n_options[i]; k++)
+            if (options[i][k] >= q_lens[i])
+                throw sd::Error("question " + std::to_string(i) + ": option row " + std::to_string(options[i][k]) +
+                                " out of range for " + std::to_string(q_lens[i]) + " tokens");
+    }
+}
+
+}  // namespace
+
+int sd_engine_ask_batch(sd_engine* e, const sd_head* h, const sd_snapshot* cache, size_t n_questions,
+                        const uint32_t* const* q_ids, const size_t* q_lens, const size_t* const* options,
+                        const size_t* n_options, const double* temperatures, int timed, double* probs_out,
+                        double* gpu_ms, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!e || !h || !probs_out) throw sd::Error("sd_engine_ask_batch: null argument");
+        check_questions(n_questions, q_ids, q_lens, options, n_options, temperatures);
+        ask_from(E(e), *Hd(h), S(cache), n_questions, q_ids, q_lens, options, n_options, temperatures, timed != 0,
+                 probs_out, gpu_ms);
+    });
+}
+
 int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_state, size_t n_questions,
                const uint32_t* const* q_ids, const size_t* q_lens, const size_t* const* options,
                const size_t* n_options, const double* temperatures, double* probs_out, char* err, size_t errlen) {
     return guarded(err, errlen, [&] {
-        if (!e || !h || !probs_out) throw sd::Error("sd_ask_ids: null argument");
-        if (n_questions == 0) throw sd::Error("ask at least one question");
+        if (!e || !h || !probs_out || (!state && n_state)) throw sd::Error("sd_ask_ids: null argument");
+        check_questions(n_questions, q_ids, q_lens, options, n_options, temperatures);
         sd::Engine* eng = E(e);
-        const size_t d = eng->cfg.d;
-        size_t out_off = 0;
-        for (size_t i = 0; i < n_questions; i++)
-            if (q_lens[i] == 0) throw sd::Error("question " + std::to_string(i) + " has no tokens");
-        auto answer = [&](size_t i, const std::vector<size_t>& rows, const std::vector<float>& hidden) {
-            const auto p = Hd(h)->probs(hidden.data(), rows.size(), d, temperatures[i]);
-            std::memcpy(probs_out + out_off, p.data(), p.size() * sizeof(double));
-            out_off += p.size();
-        };
         if (n_questions == 1) {
             // src/lib.rs:185-190: one forward of state ++ question.
             std::vector<uint32_t> ids(state, state + n_state);
@@ -154,59 +234,18 @@ int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_s
             std::vector<size_t> rows;
             for (size_t k = 0; k < n_options[0]; k++) rows.push_back(n_state + options[0][k]);
             rows.push_back(ids.size() - 1);
-            std::vector<float> hidden(rows.size() * d);
-            eng->forward(ids.data(), ids.size(), rows.data(), rows.size(), nullptr, false, false, hidden.data(), nullptr, nullptr);
-            answer(0, rows, hidden);
+            const size_t len = ids.size();
+            eng->ask_batch(*Hd(h), ids.data(), &len, 1, rows.data(), n_options, temperatures, nullptr, false,
+                           probs_out, nullptr);
             return;
         }
-        // src/lib.rs:192-198: the state once, every question continuing from its snapshot.  The
-        // questions run as independent sequences of batched forwards (same results as one forward
-        // each; the weights stream once per batch).  A batch holds questions of one matmul class
-        // (<= 20 tokens or longer) and fits the context after the prefix.
+        // src/lib.rs:192-198: the state once, every question continuing from its snapshot.
+        if (n_state == 0) throw sd::Error("context of 0 tokens: must be 1 to " + std::to_string(SD_CONTEXT));
         sd::Snapshot* prefix = nullptr;
         eng->forward(state, n_state, nullptr, 0, nullptr, true, false, nullptr, nullptr, &prefix);
         std::unique_ptr<sd::Snapshot> hold(prefix);
-        std::vector<std::vector<size_t>> batches;
-        for (int cls = 0; cls < 2; cls++) {
-            std::vector<size_t> cur;
-            size_t tokens = 0;
-            for (size_t i = 0; i < n_questions; i++) {
-                if ((q_lens[i] <= 20) != (cls == 0)) continue;
-                if (!cur.empty() && (cur.size() == (size_t)sd::SD_MAX_SEQS || n_state + tokens + q_lens[i] > SD_CONTEXT)) {
-                    batches.push_back(cur);
-                    cur.clear();
-                    tokens = 0;
-                }
-                cur.push_back(i);
-                tokens += q_lens[i];
-            }
-            if (!cur.empty()) batches.push_back(cur);
-        }
-        std::vector<std::vector<double>> probs(n_questions);
-        for (const auto& b : batches) {
-            std::vector<uint32_t> ids;
-            std::vector<size_t> lens, rows;
-            std::vector<std::pair<size_t, size_t>> spans;  // (question, first hidden row)
-            for (size_t i : b) {
-                const size_t base = ids.size();
-                spans.emplace_back(i, rows.size());
-                for (size_t k = 0; k < n_options[i]; k++) rows.push_back(base + options[i][k]);
-                rows.push_back(base + q_lens[i] - 1);
-                ids.insert(ids.end(), q_ids[i], q_ids[i] + q_lens[i]);
-                lens.push_back(q_lens[i]);
-            }
-            std::vector<float> hidden(rows.size() * d);
-            eng->forward_batch(ids.data(), lens.data(), lens.size(), rows.data(), rows.size(), prefix, false,
-                               hidden.data(), nullptr);
-            for (const auto& sp : spans) {
-                const size_t i = sp.first, nr = n_options[i] + 1;
-                probs[i] = Hd(h)->probs(hidden.data() + sp.second * d, nr, d, temperatures[i]);
-            }
-        }
-        for (size_t i = 0; i < n_questions; i++) {
-            std::memcpy(probs_out + out_off, probs[i].data(), probs[i].size() * sizeof(double));
-            out_off += probs[i].size();
-        }
+        ask_from(eng, *Hd(h), prefix, n_questions, q_ids, q_lens, options, n_options, temperatures, false, probs_out,
+                 nullptr);
     });
 }
 

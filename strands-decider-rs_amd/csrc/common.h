@@ -128,6 +128,22 @@ void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uin
               const Segs& sg, int nseq, hipStream_t st);
 void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st);
 
+// ---- pointer head (head_gpu.hip) -------------------------------------------------------------
+// Device copies of head.safetensors (all f32): LayerNorm weight/bias [d], q and k [dim][d] + bias.
+struct HeadW {
+    const float *nw = nullptr, *nb = nullptr, *qw = nullptr, *qb = nullptr, *kw = nullptr, *kb = nullptr;
+    int dim = 0;
+};
+// proj[r][0..dim) = (answer row ? q : k) projection of LayerNorm(hidden[r]), f64.
+void head_rows(const float* hidden, int n_rows, int d, const HeadW& w, const uint8_t* is_answer, double* proj,
+               hipStream_t st);
+// Question q: option rows [first, first + n) and answer row first + n (qtab[q] = first | n << 16);
+// probs[ooff[q] + i] = softmax_i(k_i . q * scale[q]).
+void head_probs(const double* proj, int dim, const uint32_t* qtab, const double* scale, const uint32_t* ooff, int nq,
+                double* probs, hipStream_t st);
+// rows[r] <- unrotate * FWHT(rows[r]) (a rotated torso's output in the head's basis).
+void unrotate_rows(float* rows, int n_rows, int d, const double* unrot, hipStream_t st);
+
 // ---- attention (attn.hip) --------------------------------------------------------------------
 struct AttnShape {
     int HQ, HK, HD, RD, stride, ctx;

@@ -46,6 +46,9 @@ Engine::~Engine() {
     for (void* p : device_allocs) (void)hipFree(p);
     if (pool.base) (void)hipFree(pool.base);
     for (void* p : host_allocs) (void)hipHostFree(p);
+    if (head_dev) (void)hipFree(head_dev);
+    if (hb.dev) (void)hipFree(hb.dev);
+    if (hb.host) (void)hipHostFree(hb.host);
 }
 
 void Plan::destroy() {
@@ -555,7 +558,7 @@ void Engine::restore(const Snapshot* cache, size_t P) {
     }
 }
 
-void Engine::launch_and_read(Plan& pl, size_t n_rows, bool timed) {
+void Engine::launch_and_read(Plan& pl, size_t n_rows, bool timed, bool read) {
     if (timed) SD_HIP(hipEventRecord(ev0, st));
     if (pl.exec) {
         SD_HIP(hipGraphLaunch(pl.exec, st));
@@ -563,6 +566,7 @@ void Engine::launch_and_read(Plan& pl, size_t n_rows, bool timed) {
         for (auto& s : pl.steps) s.run(st);
     }
     if (n_rows) add_norm(pool.x, pl.last_y, final_norm, cfg.d, pool.rows, (int)n_rows, nullptr, pool.out, st);
+    if (!read) return;
     if (timed) SD_HIP(hipEventRecord(ev1, st));
     if (n_rows) SD_HIP(hipMemcpyAsync(out_h, pool.out, n_rows * cfg.d * 4, hipMemcpyDeviceToHost, st));
 }
@@ -599,7 +603,8 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
     for (uint32_t i = 0; i < n; i++)
         if (ids[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(ids[i]) + " out of range for vocab " + std::to_string(vocab));
     const int L = (int)n;
-    ensure_pool(L);
+    SD_CHECK(n_rows <= SD_CONTEXT, "at most 4096 hidden rows per forward");
+    ensure_pool(std::max(L, (int)n_rows));  // the row tables and outputs hold n_rows entries
     Plan& pl = plan(L);
     upload(ids, n, rows, n_rows, P, cache != nullptr, 0, 0);
     restore(cache, P);
@@ -639,8 +644,8 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
     else delete snap;
 }
 
-void Engine::forward_batch(const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows, size_t n_rows,
-                           const Snapshot* cache, bool timed, float* hidden, double* gpu_ms) {
+Plan& Engine::prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows, size_t n_rows,
+                            const Snapshot* cache) {
     if (nseq == 0 || nseq > (size_t)SD_MAX_SEQS)
         throw Error("a batch holds 1 to " + std::to_string(SD_MAX_SEQS) + " sequences");
     size_t n = 0;
@@ -662,7 +667,8 @@ void Engine::forward_batch(const uint32_t* ids, const size_t* lens, size_t nseq,
     for (size_t i = 0; i < n; i++)
         if (ids[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(ids[i]) + " out of range for vocab " + std::to_string(vocab));
     const int L = (int)n;
-    ensure_pool(L);
+    SD_CHECK(n_rows <= SD_CONTEXT, "at most 4096 hidden rows per forward");
+    ensure_pool(std::max(L, (int)n_rows));  // the row tables and outputs hold n_rows entries
     Plan& pl = plan(L, (int)nseq, any_short);
     // sequence tables (see Segs): rows, chunks of <= 64 rows inside each sequence, sequences
     uint32_t* rowt = seg_h;
@@ -686,12 +692,118 @@ void Engine::forward_batch(const uint32_t* ids, const size_t* lens, size_t nseq,
     SD_HIP(hipMemcpyAsync(pool.seg_seq, seqh, nseq * 4, hipMemcpyHostToDevice, st));
     upload(ids, n, rows, n_rows, P, cache != nullptr, nch, (uint32_t)nseq);
     restore(cache, P);
+    return pl;
+}
+
+void Engine::forward_batch(const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows, size_t n_rows,
+                           const Snapshot* cache, bool timed, float* hidden, double* gpu_ms) {
+    Plan& pl = prepare_batch(ids, lens, nseq, rows, n_rows, cache);
     launch_and_read(pl, n_rows, timed);
     // The live K/V prefix rows are untouched (rows >= P only); the GDN state and history are not
     // meaningful after several sequences, and the next forward restores or clears them.
     const hipError_t se = hipStreamSynchronize(st);
     if (se != hipSuccess) throw Error(std::string("GPU: ") + hipGetErrorString(se));
     finish(n_rows, hidden, timed, gpu_ms);
+}
+
+void Engine::attach_head(const Head& head) {
+    if (head_id == head.id) return;
+    const size_t d = (size_t)cfg.d, dim = head.dim;
+    if (head.t.at("norm.weight").size() != d || head.t.at("q.weight").size() != dim * d ||
+        head.t.at("k.weight").size() != dim * d || head.t.at("q.bias").size() != dim || head.t.at("k.bias").size() != dim ||
+        head.t.at("norm.bias").size() != d)
+        throw Error("head: tensor shapes do not match hidden size " + std::to_string(d));
+    if (head_dev) SD_HIP(hipFree(head_dev));
+    head_dev = nullptr;
+    head_id = 0;
+    const char* names[6] = {"norm.weight", "norm.bias", "q.weight", "q.bias", "k.weight", "k.bias"};
+    size_t off[7] = {0};
+    for (int i = 0; i < 6; i++) off[i + 1] = off[i] + align256(head.t.at(names[i]).size() * 4);
+    SD_HIP(hipMalloc(&head_dev, off[6]));
+    const float* p[6];
+    for (int i = 0; i < 6; i++) {
+        const auto& v = head.t.at(names[i]);
+        p[i] = reinterpret_cast<const float*>(static_cast<uint8_t*>(head_dev) + off[i]);
+        SD_HIP(hipMemcpy(const_cast<float*>(p[i]), v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    }
+    headw = HeadW{p[0], p[1], p[2], p[3], p[4], p[5], (int)dim};
+    if (!unrotate.empty() && !unrot_dev) {
+        unrot_dev = static_cast<double*>(dalloc(unrotate.size() * 8));
+        SD_HIP(hipMemcpy(unrot_dev, unrotate.data(), unrotate.size() * 8, hipMemcpyHostToDevice));
+    }
+    head_id = head.id;
+}
+
+void Engine::ensure_head_bufs(size_t rows, size_t nq) {
+    if (hb.rows >= rows && hb.nq >= nq && hb.dim == (size_t)headw.dim) return;
+    rows = std::max(rows, std::max<size_t>(hb.rows, 64));
+    nq = std::max(nq, std::max<size_t>(hb.nq, 32));
+    if (hb.dev) SD_HIP(hipFree(hb.dev));
+    if (hb.host) SD_HIP(hipHostFree(hb.host));
+    hb = HeadBufs{};
+    const size_t dim = (size_t)std::max(headw.dim, 1);
+    // device: proj [rows][dim] | scale [nq] | probs [rows] | qtab [nq] | ooff [nq] | is_answer [rows]
+    const size_t o1 = align256(rows * dim * 8), o2 = o1 + align256(nq * 8), o3 = o2 + align256(rows * 8),
+                 o4 = o3 + align256(nq * 4), o5 = o4 + align256(nq * 4), o6 = o5 + align256(rows);
+    SD_HIP(hipMalloc(&hb.dev, o6));
+    uint8_t* d = static_cast<uint8_t*>(hb.dev);
+    hb.proj = reinterpret_cast<double*>(d);
+    hb.scale = reinterpret_cast<double*>(d + o1);
+    hb.probs = reinterpret_cast<double*>(d + o2);
+    hb.qtab = reinterpret_cast<uint32_t*>(d + o3);
+    hb.ooff = reinterpret_cast<uint32_t*>(d + o4);
+    hb.is_answer = d + o5;
+    // host: scale | probs | qtab | ooff | is_answer (the same order as on the device, from scale)
+    const size_t hbytes = o6 - o1;
+    SD_HIP(hipHostMalloc(&hb.host, hbytes, hipHostMallocDefault));
+    uint8_t* h = static_cast<uint8_t*>(hb.host);
+    hb.scale_h = reinterpret_cast<double*>(h);
+    hb.probs_h = reinterpret_cast<double*>(h + (o2 - o1));
+    hb.qtab_h = reinterpret_cast<uint32_t*>(h + (o3 - o1));
+    hb.ooff_h = reinterpret_cast<uint32_t*>(h + (o4 - o1));
+    hb.is_answer_h = h + (o5 - o1);
+    hb.rows = rows;
+    hb.nq = nq;
+    hb.dim = dim;
+}
+
+void Engine::ask_batch(const Head& head, const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows,
+                       const size_t* n_opts, const double* temps, const Snapshot* cache, bool timed, double* probs,
+                       double* gpu_ms) {
+    size_t n_rows = 0, n_prob = 0;
+    for (size_t q = 0; q < nseq; q++) {
+        if (n_opts[q] == 0) throw Error("question " + std::to_string(q) + " has no options");
+        n_rows += n_opts[q] + 1;
+        n_prob += n_opts[q];
+    }
+    SD_CHECK(n_rows < 65536, "ask_batch: too many rows");
+    attach_head(head);
+    Plan& pl = prepare_batch(ids, lens, nseq, rows, n_rows, cache);
+    ensure_head_bufs(n_rows, nseq);
+    size_t r = 0, o = 0;
+    for (size_t q = 0; q < nseq; q++) {
+        hb.qtab_h[q] = (uint32_t)r | (uint32_t)(n_opts[q] << 16);
+        hb.ooff_h[q] = (uint32_t)o;
+        hb.scale_h[q] = std::pow((double)headw.dim, -0.5) / std::max(temps[q], 1e-6);
+        for (size_t k = 0; k < n_opts[q]; k++) hb.is_answer_h[r + k] = 0;
+        hb.is_answer_h[r + n_opts[q]] = 1;
+        r += n_opts[q] + 1;
+        o += n_opts[q];
+    }
+    // the tables: scale .. is_answer are one contiguous span on both sides
+    const size_t span = static_cast<size_t>(reinterpret_cast<uint8_t*>(hb.is_answer) + n_rows -
+                                            reinterpret_cast<uint8_t*>(hb.scale));
+    SD_HIP(hipMemcpyAsync(hb.scale, hb.scale_h, span, hipMemcpyHostToDevice, st));
+    launch_and_read(pl, n_rows, timed, false);
+    if (!unrotate.empty()) unrotate_rows(pool.out, (int)n_rows, cfg.d, unrot_dev, st);
+    head_rows(pool.out, (int)n_rows, cfg.d, headw, hb.is_answer, hb.proj, st);
+    head_probs(hb.proj, headw.dim, hb.qtab, hb.scale, hb.ooff, (int)nseq, hb.probs, st);
+    if (timed) SD_HIP(hipEventRecord(ev1, st));
+    SD_HIP(hipMemcpyAsync(hb.probs_h, hb.probs, n_prob * 8, hipMemcpyDeviceToHost, st));
+    const hipError_t se = hipStreamSynchronize(st);
+    if (se != hipSuccess) throw Error(std::string("GPU: ") + hipGetErrorString(se));
+    std::memcpy(probs, hb.probs_h, n_prob * 8);
+    finish(0, nullptr, timed, gpu_ms);
 }
 
 std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids, size_t n) {

@@ -11,6 +11,7 @@
 
 #include "../../include/sdhip.h"
 #include "common.h"
+#include "head.h"
 
 namespace sd {
 
@@ -136,6 +137,24 @@ struct Engine {
     float* out_h = nullptr;
     int ids_h_cap = 0;
     std::vector<void*> device_allocs, host_allocs;
+    // Device copy of the last head used by ask_batch, and the head's per-call buffers.
+    HeadW headw;
+    uint64_t head_id = 0;
+    void* head_dev = nullptr;     // the head's weights
+    double* unrot_dev = nullptr;  // `unrotate` on the device (rotated torsos only)
+    // Per-call buffers of ask_batch for up to `rows` rows / `nq` questions: device [proj | scale |
+    // probs | qtab | ooff | is_answer], pinned host [scale | probs | qtab | ooff | is_answer].
+    struct HeadBufs {
+        size_t rows = 0, nq = 0, dim = 0;
+        void *dev = nullptr, *host = nullptr;
+        double *proj = nullptr, *scale = nullptr, *probs = nullptr;
+        uint32_t *qtab = nullptr, *ooff = nullptr;
+        uint8_t* is_answer = nullptr;
+        double *scale_h = nullptr, *probs_h = nullptr;
+        uint32_t *qtab_h = nullptr, *ooff_h = nullptr;
+        uint8_t* is_answer_h = nullptr;
+    } hb;
+    void ensure_head_bufs(size_t rows, size_t nq);
 
     ~Engine();
     void load(const sd_config* c, const sd_tensor* ts, size_t nt, const char* const* shard_paths,
@@ -148,6 +167,12 @@ struct Engine {
     // reference's matmul choice depends on the length).
     void forward_batch(const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows, size_t n_rows,
                        const Snapshot* cache, bool timed, float* hidden, double* gpu_ms);
+    // forward_batch followed by the pointer head on the device: sequence q's rows are n_opts[q]
+    // option rows then its answer row (rows lists them sequence by sequence); probs receives
+    // sum(n_opts) option probabilities, sequence by sequence.  gpu_ms covers torso and head.
+    void ask_batch(const Head& head, const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows,
+                   const size_t* n_opts, const double* temps, const Snapshot* cache, bool timed, double* probs,
+                   double* gpu_ms);
     std::vector<std::pair<const char*, double>> profile(const uint32_t* ids, size_t n);
 
    private:
@@ -164,7 +189,11 @@ struct Engine {
     void upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
                 uint32_t chunks, uint32_t nseq);
     void restore(const Snapshot* cache, size_t P);
-    void launch_and_read(Plan& pl, size_t n_rows, bool timed);
+    void launch_and_read(Plan& pl, size_t n_rows, bool timed, bool read = true);
+    // Validation, sequence tables, upload and restore of a batched forward; returns its plan.
+    Plan& prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows, size_t n_rows,
+                        const Snapshot* cache);
+    void attach_head(const Head& head);
     void finish(size_t n_rows, float* hidden, bool timed, double* gpu_ms);
     void mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L, bool short_rows);
     YIn mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L, bool short_rows);

@@ -3,6 +3,7 @@
 // from head.safetensors (8-byte header length, JSON header, raw little-endian F32 data).
 #include "head.h"
 
+#include <atomic>
 #include <cmath>
 #include <cstring>
 
@@ -150,6 +151,8 @@ struct JParser {
 }  // namespace
 
 void Head::load(const uint8_t* bytes, size_t len) {
+    static std::atomic<uint64_t> ids{0};
+    id = ++ids;
     if (len < 8) throw Error("head.safetensors: malformed");
     uint64_t n = 0;
     std::memcpy(&n, bytes, 8);

@@ -164,3 +164,58 @@ def test_ask_ids_mixed_lengths(tiny, sdamd):
     for q, o, t, g in zip(qs, options, temps, got):
         h, _ = om.forward(q, list(o) + [len(q) - 1], cache=snap)
         assert np.abs(g - om.probs(h, t)).max() < PROB_TOL
+
+
+def test_ask_batch_device_head_matches_host_head(tiny, sdamd):
+    """The pointer head on the device (f64) against Head::probs on the host (src/head.rs:66-77) on the
+    same hidden rows: the torso is deterministic, so only the f64 summation order differs."""
+    eng, head, om = tiny
+    state = ids_for(70, 100)
+    qs = [ids_for(71, 33), ids_for(72, 47), ids_for(73, 25)]
+    options = [[1, 5, 20], [2, 40], [0, 3, 7, 11, 24]]
+    temps = [1.0, 0.8, 1e-9]  # the last one exercises the max(T, 1e-6) floor
+    prefix = eng.forward(state, [], keep=True).snapshot
+    got, ms = eng.ask_batch(head, qs, options, temps, cache=prefix, timed=True)
+    assert ms is not None and ms > 0
+    hid, _ = eng.forward_batch(qs, [list(o) + [len(q) - 1] for q, o in zip(qs, options)], cache=prefix)
+    for g, h, t in zip(got, hid, temps):
+        want = head.probs(h, h.shape[1], t)
+        assert g.shape == want.shape
+        assert np.abs(g - want).max() < 1e-9
+        assert abs(g.sum() - 1.0) < 1e-12
+    # without a prefix: each question is a whole sequence
+    got0, _ = eng.ask_batch(head, qs[:2], options[:2], temps[:2])
+    hid0, _ = eng.forward_batch(qs[:2], [list(o) + [len(q) - 1] for q, o in zip(qs[:2], options[:2])])
+    for g, h, t in zip(got0, hid0, temps):
+        assert np.abs(g - head.probs(h, h.shape[1], t)).max() < 1e-9
+    with pytest.raises(sdamd.EngineError, match="out of range"):
+        eng.ask_batch(head, qs[:1], [[33]], [1.0], cache=prefix)
+    with pytest.raises(sdamd.EngineError, match="no options"):
+        eng.ask_batch(head, qs[:1], [[]], [1.0], cache=prefix)
+    prefix.free()
+
+
+def test_rotated_torso_unrotate_on_device(sdamd, synth, oracle, tmp_path_factory):
+    """A rotated torso (src/engine.rs:652-660): hidden rows are unrotate * FWHT(row).  forward applies
+    it on the host, ask_ids on the device before the head; both match the oracle."""
+    cfg = dict(synth.CONFIG_TINY)
+    d = cfg["hidden_size"]
+    cfg["unrotate"] = [float(x) for x in np.random.default_rng(9).choice([-1.0, 1.0], d) / np.sqrt(d)]
+    path = synth.write_model(str(tmp_path_factory.mktemp("rot")), cfg, vocab=4096, seed=1)
+    eng, head, _ = sdamd.load_decider(path)
+    om = oracle.OracleModel(path)
+    try:
+        state, q = ids_for(80, 60), ids_for(81, 30)
+        rows = [4, 12, 29]
+        got = eng.forward(np.concatenate([state, q]), [60 + r for r in rows]).hidden
+        want, _ = om.forward(np.concatenate([state, q]), [60 + r for r in rows])
+        assert np.abs(got - want).max() < HIDDEN_TOL
+        qs = [q, ids_for(82, 26)]
+        options = [[4, 12], [3, 9, 20]]
+        probs = sdamd.ask_ids(eng, head, state, qs, options, [1.0, 1.0])
+        _, snap = om.forward(state, [], keep=True)
+        for qq, o, g in zip(qs, options, probs):
+            h, _ = om.forward(qq, list(o) + [len(qq) - 1], cache=snap)
+            assert np.abs(g - om.probs(h, 1.0)).max() < PROB_TOL
+    finally:
+        eng.free()
