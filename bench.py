@@ -213,6 +213,143 @@ def trace_summary(trace_dir):
             print(f"  k_gemm_w4 launches in this forward: {len(g)}, average duration {sum(g) / len(g):.2f} us")
 
 
+def _dev(a):
+    """numpy array -> device bytes (torch is only the allocator)."""
+    import numpy as np
+    import torch
+    a = np.ascontiguousarray(a)
+    return torch.from_numpy(a.view(np.uint8).reshape(-1).copy()).cuda()
+
+
+def _timed(fn, reps):
+    """Average device ms of fn() over reps calls on torch's current stream (after one warm-up)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def kernel_bench(pkg, reps=50):
+    """BASELINE configs[0..2] as kernel-level measurements (parity for them is in tests/): the int4
+    GEMM on one linear layer, the GEMM set of one decoder layer at M = 512 and M = 8, and one gated
+    delta net layer.  Weights are repacked once (sd_op_repack_w4), as the engine does at load."""
+    import numpy as np
+    import torch
+    import sdamd.synth as synth
+    stream = torch.cuda.current_stream().cuda_stream
+    rng = np.random.default_rng(0)
+    out = {"metric": "kernel-level configs[0..2] (int4 GEMM, layer GEMM set, gated delta net layer), 1 GPU",
+           "unit": "us", "data": "synthetic (BASELINE configs distributions, seed 0)"}
+
+    def gemm(M, N, K):
+        A = rng.standard_normal((M, K)).astype(np.float16)
+        W = synth.pack_nibbles(rng.integers(0, 16, size=(N, K), dtype=np.uint32))
+        S = rng.uniform(0.005, 0.02, size=(N, K // 32)).astype(np.float16)
+        dA, dW, dS = _dev(A), _dev(W), _dev(S)
+        dY = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
+        pkg.op_repack_w4(dW.data_ptr(), N, K, stream)
+        exact = M <= 20
+        ms = _timed(lambda: pkg.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, exact,
+                                          -1, True, stream), reps)
+        wbytes = N * K // 2 + N * K // 16
+        io = 2 * M * K + 2 * M * N
+        return {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                "tflops": round(2.0 * M * N * K / ms / 1e9, 1),
+                "mfma_frac": round(2.0 * M * N * K / ms / 1e9 / PEAK_MFMA_F16, 4),
+                "gbps": round((wbytes + io) / ms / 1e6, 1),
+                "hbm_frac": round((wbytes + io) / ms / 1e6 / PEAK_HBM, 4)}
+
+    out["cfg0_linear"] = gemm(128, 6144, 2048)
+    layer = [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048), ("gate", 6144, 2048),
+             ("up", 6144, 2048), ("down", 2048, 6144)]
+    fused = [("qkv", 5120, 2048), ("in_proj", 8256, 2048), ("gate_up", 12288, 2048), ("o", 2048, 2048),
+             ("down", 2048, 6144)]
+    for M in (512, 8):
+        rs = {name: gemm(M, N, K) for name, N, K in layer}
+        tot_us = sum(r["us"] for r in rs.values())
+        flops = sum(2.0 * M * N * K for _, N, K in layer)
+        wbytes = sum(N * K // 2 + N * K // 16 for _, N, K in layer)
+        out[f"cfg1_layer_M{M}"] = {"shapes": rs, "total_us": round(tot_us, 2),
+                                   "tflops": round(flops / tot_us / 1e6, 1),
+                                   "mfma_frac": round(flops / tot_us / 1e6 / PEAK_MFMA_F16, 4),
+                                   "weight_gbps": round(wbytes / tot_us / 1e3, 1),
+                                   "hbm_frac": round(wbytes / tot_us / 1e3 / PEAK_HBM, 4)}
+        if M == 512:
+            out["cfg1_fused_M512"] = {name: gemm(M, N, K) for name, N, K in fused}
+    # configs[2]: one gated delta net layer (prep + scan), T = 512, 16 heads, dk = dv = 128
+    T, H, dk, dv = 512, 16, 128, 128
+    C = 2 * H * dk + H * dv
+    qkv = rng.standard_normal((T, C)).astype(np.float32)
+    for j in range(2 * H):  # q and k rows L2-normalized per head (the kernel normalizes again)
+        blk = qkv[:, j * dk:(j + 1) * dk]
+        blk /= np.linalg.norm(blk, axis=1, keepdims=True)
+    big = np.zeros((T, 2 * H), np.float16)
+    big[:, :H] = rng.standard_normal((T, H)).astype(np.float16)   # a: g = -softplus(a)
+    big[:, H:] = rng.standard_normal((T, H)).astype(np.float16)   # b: beta = sigmoid(b)
+    d_qkv, d_big = _dev(qkv), _dev(big)
+    d_nA, d_dtb = _dev(np.full(H, -1.0, np.float32)), _dev(np.zeros(H, np.float32))
+    d_state = torch.zeros(H * dk * dv, dtype=torch.float32, device="cuda")
+    d_o = torch.empty(T * H * dv, dtype=torch.float32, device="cuda")
+    ms = _timed(lambda: pkg.op_gdn(d_qkv.data_ptr(), d_big.data_ptr(), 2 * H, 0, H, d_nA.data_ptr(), d_dtb.data_ptr(),
+                                   T, H, dk, dv, d_state.data_ptr(), 0, d_o.data_ptr(), stream), reps)
+    alg = 4 * T * H * (2 * dk + dv) + 8 * T * H + 4 * T * H * dv + 4 * H * dk * dv
+    out["cfg2_gdn_layer"] = {"T": T, "H": H, "us": round(ms * 1e3, 2), "algorithmic_bytes": alg,
+                             "gbps": round(alg / ms / 1e6, 1), "hbm_frac": round(alg / ms / 1e6 / PEAK_HBM, 4),
+                             "recurrent_equiv_tflops": round(7.0 * T * H * dk * dv / ms / 1e9, 2)}
+    return out
+
+
+def sweep_bench(eng, head, temp, n_states=64, n_q=8, seed=4):
+    """64 independent states of U[128, 2048] random tokens, each encoded once
+    (forward with keep), then 8 questions of U[24, 64] tokens answered from its snapshot as one
+    batched forward with the device head.  Aggregate prefill tokens/s; per-question latency = the
+    wall time of the batch that answers it.  A first pass over the same inputs builds the per-length
+    plans (captured graphs) and is reported separately as the cold pass."""
+    import numpy as np
+    import sdamd.synth as synth
+    rng = np.random.default_rng(seed)
+    work = []
+    for _ in range(n_states):
+        L = int(rng.integers(128, 2049))
+        state = rng.integers(0, synth.VOCAB_2B, L).astype(np.uint32)
+        qs = [rng.integers(0, synth.VOCAB_2B, int(rng.integers(24, 65))).astype(np.uint32) for _ in range(n_q)]
+        opts = [sorted(rng.choice(len(q) - 1, int(rng.integers(2, 6)), replace=False).tolist()) for q in qs]
+        work.append((state, qs, opts))
+
+    def run_pass():
+        pre_tok, pre_s, q_lat = 0, 0.0, []
+        for state, qs, opts in work:
+            t0 = time.perf_counter()
+            snap = eng.forward(state, [], keep=True).snapshot
+            t1 = time.perf_counter()
+            eng.ask_batch(head, qs, opts, [temp] * n_q, cache=snap)
+            t2 = time.perf_counter()
+            snap.free()
+            pre_tok += len(state)
+            pre_s += t1 - t0
+            q_lat.extend([t2 - t1] * n_q)
+        q_lat.sort()
+        return pre_tok / pre_s, q_lat
+
+    t = time.perf_counter()
+    cold_rate, _ = run_pass()
+    log(f"sweep cold pass (plans built) in {time.perf_counter() - t:.1f} s")
+    rate, q_lat = run_pass()
+    return {"metric": "configs[4] sweep: aggregate prefill tokens/s, per-question latency p50/p99 (ms)",
+            "prefill_tokens_per_s": round(rate, 1), "cold_pass_prefill_tokens_per_s": round(cold_rate, 1),
+            "states": n_states, "questions_per_state": n_q,
+            "question_p50_ms": round(1e3 * q_lat[len(q_lat) // 2], 3),
+            "question_p99_ms": round(1e3 * q_lat[min(len(q_lat) - 1, int(0.99 * len(q_lat)))], 3),
+            "data": "synthetic: random-init 2B, uniform-random ids; lengths U[128, 2048], questions U[24, 64], "
+                    "2-5 options each"}
+
+
 def cpu_baseline(model_dir, vocab, n_tokens=STATE_LEN):
     """The C oracle (a CPU port of the reference kernels) on the host cores: one prefill of
     n_tokens random ids (the 512-token state of the workload; about 15-20 s on 16 cores)."""
@@ -244,6 +381,10 @@ def main():
                     help="print the HBM traffic summary from two rocprofv3 --pmc output folders (no GPU)")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
                     help="print the kernel summary of a rocprofv3 --kernel-trace output folder (no GPU)")
+    ap.add_argument("--kernels", action="store_true",
+                    help="kernel-level BASELINE configs[0..2] instead of the ask_all workload (one JSON line)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="BASELINE configs[4] (64 states, 8 questions each) instead of the ask_all workload")
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary)
@@ -266,6 +407,9 @@ def main():
     pkg = entry._import_pkg()
     pkg.lib()
     import sdamd.synth as synth
+    if args.kernels:
+        print(json.dumps(kernel_bench(pkg)), flush=True)
+        return
 
     t = time.perf_counter()
     model_dir = synth.write_model(args.model_dir, synth.CONFIG_2B, vocab=synth.VOCAB_2B, seed=0)
@@ -280,6 +424,9 @@ def main():
     temp = float(dcfg["temperature"])
     if args.pmc_workload:
         pmc_workload(eng, state)
+        return
+    if args.sweep:
+        print(json.dumps(sweep_bench(eng, head, temp)), flush=True)
         return
 
     def step():

@@ -27,6 +27,7 @@ SYMBOLS = [
     "sd_engine_load", "sd_engine_free", "sd_engine_hidden_size", "sd_engine_adapter", "sd_engine_forward",
     "sd_snapshot_len", "sd_snapshot_free", "sd_engine_profile", "sd_head_load", "sd_head_free", "sd_head_probs",
     "sd_ask_ids", "sd_op_matmul", "sd_op_gdn", "sd_engine_forward_batch", "sd_engine_ask_batch",
+    "sd_op_repack_w4",
 ]
 
 
@@ -92,7 +93,8 @@ def lib():
         L.sd_head_free.argtypes = [vp]
         L.sd_head_probs.argtypes = [vp, vp, sz, sz, C.c_double, vp, err, sz]
         L.sd_ask_ids.argtypes = [vp, vp, vp, sz, sz, C.POINTER(vp), vp, C.POINTER(vp), vp, vp, vp, err, sz]
-        L.sd_op_matmul.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, err, sz]
+        L.sd_op_matmul.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, err, sz]
+        L.sd_op_repack_w4.argtypes = [vp, i32, i32, vp, err, sz]
         L.sd_op_gdn.argtypes = [vp, vp, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, err, sz]
         for name in SYMBOLS:
             if name not in ("sd_engine_free", "sd_snapshot_free", "sd_head_free", "sd_engine_hidden_size",
@@ -353,9 +355,15 @@ def load_decider(model_dir: str):
 
 # ---- kernel-level entry points (device pointers as ints; stream handle as int or None) ----------
 
-def op_matmul(A, Wq, Sc, Y, M, N, K, exact=False, cfg=-1, stream=None):
+def op_matmul(A, Wq, Sc, Y, M, N, K, exact=False, cfg=-1, packed=False, stream=None):
+    """sd_op_matmul on device pointers; packed: Wq already went through op_repack_w4."""
     _call(lib().sd_op_matmul, C.c_void_p(A), C.c_void_p(Wq), C.c_void_p(Sc), C.c_void_p(Y), M, N, K, int(exact), cfg,
-          C.c_void_p(stream) if stream else None)
+          int(packed), C.c_void_p(stream) if stream else None)
+
+
+def op_repack_w4(Wq, N, K, stream=None):
+    """sd_op_repack_w4: rewrites N*K/8 weight words in place into the GEMM kernels' nibble order."""
+    _call(lib().sd_op_repack_w4, C.c_void_p(Wq), N, K, C.c_void_p(stream) if stream else None)
 
 
 def op_gdn(qkv, big, stride, a_off, b_off, negA, dtb, L, H, dk, dv, state, load_state, o, stream=None):

@@ -249,8 +249,16 @@ int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_s
     });
 }
 
+int sd_op_repack_w4(void* Wq, int N, int K, void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!Wq) throw sd::Error("sd_op_repack_w4: null argument");
+        if (N < 1 || K < 32 || K % 32) throw sd::Error("sd_op_repack_w4: need N >= 1 and K a multiple of 32");
+        sd::repack_w4(static_cast<uint32_t*>(Wq), (size_t)N * K / 8, static_cast<hipStream_t>(stream));
+    });
+}
+
 int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, int N, int K, int exact, int cfg,
-                 void* stream, char* err, size_t errlen) {
+                 int packed, void* stream, char* err, size_t errlen) {
     return guarded(err, errlen, [&] {
         if (!A || !Wq || !Sc || !Y) throw sd::Error("sd_op_matmul: null argument");
         if (cfg >= sd::gemm_w4_configs()) throw sd::Error("sd_op_matmul: no configuration " + std::to_string(cfg));
@@ -258,21 +266,33 @@ int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, 
         OpWs& w = op_ws();
         std::lock_guard<std::mutex> lock(w.mu);
         const hipStream_t st = static_cast<hipStream_t>(stream);
-        const int c = cfg >= 0 ? cfg : sd::gemm_w4_cfg(M, exact != 0);
+        // cfg < 0: the engine's own choice for this shape (tile and split-K, the split summed by
+        // reduce_partials here); cfg >= 0: that configuration, split until the grid covers the chip.
         const size_t cap = size_t(64) << 20;
-        const int ks = sd::gemm_w4_split(M, N, K, c, 256, cap);
-        const auto* a = static_cast<const sd::f16*>(A);
-        // The kernels read the engine nibble order: repack a copy of the caller's weights.
-        const size_t words = (size_t)N * K / 8;
-        if (w.wpack_words < words) {
-            if (w.wpack) SD_HIP(hipFree(w.wpack));
-            w.wpack = nullptr;
-            SD_HIP(hipMalloc(&w.wpack, words * 4));
-            w.wpack_words = words;
+        int c = cfg, ks = 1;
+        if (cfg < 0) {
+            const sd::GemmPlan p = sd::gemm_w4_plan(M, N, K, exact != 0, true, cap);
+            c = p.cfg;
+            ks = p.ks;
+        } else {
+            ks = sd::gemm_w4_split(M, N, K, c, 256, cap);
         }
-        SD_HIP(hipMemcpyAsync(w.wpack, Wq, words * 4, hipMemcpyDeviceToDevice, st));
-        sd::repack_w4(w.wpack, words, st);
-        const uint32_t* wq = w.wpack;
+        const auto* a = static_cast<const sd::f16*>(A);
+        // The kernels read the engine nibble order: unless the caller repacked its weights already,
+        // repack a copy of them.
+        const uint32_t* wq = static_cast<const uint32_t*>(Wq);
+        if (!packed) {
+            const size_t words = (size_t)N * K / 8;
+            if (w.wpack_words < words) {
+                if (w.wpack) SD_HIP(hipFree(w.wpack));
+                w.wpack = nullptr;
+                SD_HIP(hipMalloc(&w.wpack, words * 4));
+                w.wpack_words = words;
+            }
+            SD_HIP(hipMemcpyAsync(w.wpack, Wq, words * 4, hipMemcpyDeviceToDevice, st));
+            sd::repack_w4(w.wpack, words, st);
+            wq = w.wpack;
+        }
         const auto* sc = static_cast<const sd::f16*>(Sc);
         if (ks == 1) {
             sd::gemm_w4(a, wq, sc, static_cast<sd::f16*>(Y), nullptr, M, N, K, exact != 0, 1, st, c);

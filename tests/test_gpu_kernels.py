@@ -138,3 +138,19 @@ def test_gdn_matches_sequential_oracle(sdamd, oracle, L, H, load, negA, a_scale)
     wo, wst = oracle_gdn(oracle, qkv, big, stride, nA, db, L, H, state0, load)
     np.testing.assert_allclose(o, wo, rtol=2e-4, atol=2e-4)
     np.testing.assert_allclose(st, wst, rtol=2e-4, atol=2e-4)
+
+
+def test_gemm_prepacked_weights(sdamd, synth):
+    """sd_op_repack_w4 once + sd_op_matmul(packed=1) gives the very same output as the per-call
+    repack of sd_op_matmul(packed=0)."""
+    rng = np.random.default_rng(11)
+    for (M, N, K, exact) in [(96, 640, 1024, False), (512, 256, 2048, False), (7, 320, 512, True)]:
+        A, W, S = gemm_case(synth, rng, M, N, K)
+        Y0 = run_gemm(sdamd, A, W, S, M, N, K, exact)
+        dA, dW, dS = dev(A), dev(W), dev(S)
+        sdamd.op_repack_w4(dW.data_ptr(), N, K)
+        dY = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
+        sdamd.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, exact, -1, True)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(dY, np.float16, (M, N)), Y0)
+        assert not np.array_equal(host(dW, np.uint32, W.shape), W)  # the words were rewritten
