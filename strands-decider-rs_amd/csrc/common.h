@@ -126,6 +126,12 @@ void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float*
 // back only for a single sequence (sg.seq null).  nseq = sequence grid size.
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
               const Segs& sg, int nseq, hipStream_t st);
+// The same recurrence token by token (the reference's own order), for short inputs: every
+// sequence starts from `state` (loaded when lu[3] / load_default); with one sequence the final
+// state is written back and hist (nullable) updated afterwards, as gdn_prep + gdn_scan do.
+void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
+               float* state, const uint32_t* lu, int load_default, float* o, f16* hist, const Segs& sg, int nseq,
+               hipStream_t st);
 void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st);
 
 // ---- pointer head (head_gpu.hip) -------------------------------------------------------------

@@ -439,6 +439,9 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
     Segs sg;
     if (nseq) sg = Segs{pool.seg_row, pool.seg_chunk, pool.seg_seq};
     const int nch = (L + 63) / 64 + (nseq ? nseq - 1 : 0);  // most chunks L rows can split into
+    // Short inputs (at most 64 tokens per sequence on average: a question, a batch of them) run the
+    // delta rule token by token; longer ones in chunks of 64 (prep + scan).
+    const bool recur = L <= 64 * std::max(nseq, 1);
     auto& steps = pl.steps;
     const Pool P = pool;
     const int d = cfg.d, I = cfg.inter;
@@ -466,10 +469,16 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
             mm(steps, "in_proj", P.h, W.in_proj, P.big, L, sr);
             steps.push_back({"conv", [=](hipStream_t s) { conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, sg, s); }});
             f16* hist_upd = nseq ? nullptr : W.hist;  // several sequences leave no history
-            steps.push_back({"gdn", [=](hipStream_t s) {
-                gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, hist_upd, sg, nch, luv, s);
-            }});
-            steps.push_back({"gdn", [=](hipStream_t s) { gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s); }});
+            if (recur) {
+                steps.push_back({"gdn", [=](hipStream_t s) {
+                    gdn_recur(P.qkvc, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, hist_upd, sg, nseq, s);
+                }});
+            } else {
+                steps.push_back({"gdn", [=](hipStream_t s) {
+                    gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, hist_upd, sg, nch, luv, s);
+                }});
+                steps.push_back({"gdn", [=](hipStream_t s) { gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s); }});
+            }
             steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
             y = mm_y(steps, "out_proj", P.o, W.out_proj, L, sr);
         } else {

@@ -427,6 +427,142 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     }
 }
 
+// Sum over the 16 lanes of this lane's DPP row, the same bits in every lane: partners by mirror,
+// half mirror, then quad xor 2 and xor 1, so each lane adds the same pairs in the same grouping.
+__device__ __forceinline__ float dpp_f(float x, int ctrl) {
+    switch (ctrl) {  // the control is an immediate of the instruction
+        case 0x140: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x140, 0xF, 0xF, false));
+        case 0x141: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+        case 0x4E: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));
+        default: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+    }
+}
+__device__ __forceinline__ float row_allsum16(float x) {
+    x += dpp_f(x, 0x140);  // row_mirror: lane i and 15 - i
+    x += dpp_f(x, 0x141);  // row_half_mirror: i and 7 - i within each half
+    x += dpp_f(x, 0x4E);   // quad_perm [2,3,0,1]
+    x += dpp_f(x, 0xB1);   // quad_perm [1,0,3,2]
+    return x;
+}
+
+// The reference's own token-by-token delta rule (src/kernels.rs:280-297) for short inputs (the
+// questions of an ask_all): the chunked form's fixed cost per 64-token chunk outweighs a few dozen
+// sequential steps.  Per token t and head h: qn = q rsqrt(q.q + 1e-6) / sqrt(dk), kn = k rsqrt(k.k
+// + 1e-6), beta = sigmoid(b), decay = exp(negA softplus(a + dt_bias)); per value column:
+// S *= decay; delta = (v - S^T kn) beta; S += kn delta; o = S^T qn.
+// Workgroup (head, 16 value columns, sequence): wave w owns columns 16 y + 4 w + l / 16 and lane l
+// state rows 8 (l % 16) .. + 7, so every reduction over a column's 128 rows is one DPP row.  The
+// state stays in registers.  The inputs of up to 64 tokens are staged in LDS by the whole
+// workgroup with wide loads (their latency is paid once per block, not per token).
+constexpr int RTB = 64;  // tokens per LDS block
+__global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkvc, const f16* __restrict__ big,
+                                                   GdnShape sh, const float* __restrict__ negA,
+                                                   const float* __restrict__ dtb, float* __restrict__ state,
+                                                   const uint32_t* __restrict__ lu, int load_default,
+                                                   float* __restrict__ o, const uint32_t* __restrict__ chunkt,
+                                                   const uint32_t* __restrict__ seqt, int L, f16* hist) {
+    constexpr int DK = 128, DV = 128;
+    __shared__ float4 Qs[RTB][DK / 4], Ks[RTB][DK / 4];
+    __shared__ float Vs[RTB][16];
+    __shared__ float Bt[RTB], Dc[RTB];  // beta and decay per token
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int h = blockIdx.x, H = gridDim.x, q = blockIdx.z;
+    if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
+    const int cb = blockIdx.y * 16, cl = wv * 4 + (lane >> 4), col = cb + cl, r0 = 8 * (lane & 15);
+    int t0 = 0, t1 = L;
+    if (seqt) {
+        const int f = (int)(seqt[q] & 0xFFFFu), n = (int)(seqt[q] >> 16);
+        const uint32_t last = chunkt[f + n - 1];
+        t0 = (int)(chunkt[f] & 0xFFFFu);
+        t1 = (int)(last & 0xFFFFu) + (int)(last >> 16);
+    }
+    const bool load = lu ? lu[3] != 0u : load_default != 0;
+    float* Sg = state + (size_t)h * DK * DV;
+    float S[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) S[i] = load ? Sg[(size_t)(r0 + i) * DV + col] : 0.f;
+    const int C = sh.C;
+    const float na = negA[h], db = dtb[h], qs = 1.0f / sqrtf((float)DK);
+    for (int tb = t0; tb < t1; tb += RTB) {
+        const int nt = min(RTB, t1 - tb);
+        __syncthreads();  // the previous block is consumed
+        // q and k of a token: 32 lanes x 4 values, normalised on the way into LDS (the sums of
+        // squares over the 32 lanes: a DPP row, then the other row of the 32)
+        for (int e0 = 0; e0 < nt * (DK / 4); e0 += 256) {
+            const int e = e0 + tid, tt = e / (DK / 4), j = e % (DK / 4);
+            const bool ok = e < nt * (DK / 4);
+            float4 q4 = {0.f, 0.f, 0.f, 0.f}, k4 = q4;
+            if (ok) {
+                const float* row = qkvc + (size_t)(tb + tt) * C;
+                q4 = *reinterpret_cast<const float4*>(row + h * DK + 4 * j);
+                k4 = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + 4 * j);
+            }
+            float sq = row_allsum16(q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w);
+            float sk = row_allsum16(k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w);
+            sq += __shfl_xor(sq, 16);
+            sk += __shfl_xor(sk, 16);
+            const float rq = 1.0f / sqrtf(sq + 1e-6f), rk = 1.0f / sqrtf(sk + 1e-6f);
+            if (ok) {
+                Qs[tt][j] = float4{q4.x * rq * qs, q4.y * rq * qs, q4.z * rq * qs, q4.w * rq * qs};
+                Ks[tt][j] = float4{k4.x * rk, k4.y * rk, k4.z * rk, k4.w * rk};
+            }
+        }
+        for (int e = tid; e < nt * 16; e += 256) {
+            const int tt = e >> 4, j = e & 15;
+            Vs[tt][j] = qkvc[(size_t)(tb + tt) * C + 2 * sh.H * DK + h * DV + cb + j];
+        }
+        if (tid < nt) {
+            const float a = (float)big[(size_t)(tb + tid) * sh.stride + sh.a_off + h];
+            const float b = (float)big[(size_t)(tb + tid) * sh.stride + sh.b_off + h];
+            Bt[tid] = 1.0f / (1.0f + expf(-b));
+            const float x = a + db;
+            const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
+            Dc[tid] = expf(na * sp);
+        }
+        __syncthreads();
+        for (int tt = 0; tt < nt; tt++) {
+            const float4 qa = Qs[tt][r0 / 4], qb = Qs[tt][r0 / 4 + 1];
+            const float4 ka = Ks[tt][r0 / 4], kb = Ks[tt][r0 / 4 + 1];
+            const float qn[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            const float kn[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+            const float dc = Dc[tt];
+            float kv = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                S[i] *= dc;
+                kv += S[i] * kn[i];
+            }
+            const float delta = (Vs[tt][cl] - row_allsum16(kv)) * Bt[tt];
+            float oc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                S[i] += kn[i] * delta;
+                oc += S[i] * qn[i];
+            }
+            oc = row_allsum16(oc);
+            if ((lane & 15) == 0) o[(size_t)(tb + tt) * sh.H * DV + h * DV + col] = oc;
+        }
+    }
+    if (seqt) return;  // several sequences: their final states are not kept
+#pragma unroll
+    for (int i = 0; i < 8; i++) Sg[(size_t)(r0 + i) * DV + col] = S[i];
+    // the reference's hist_update (src/kernels.rs:173-190), each workgroup on a slice of the channels
+    if (hist) {
+        const int nb = gridDim.x * gridDim.y, per = (C + nb - 1) / nb, bi = blockIdx.y * H + h;
+        const int lo = bi * per, hi = min(C, lo + per);
+        for (int ch = lo + tid; ch < hi; ch += 256) {
+            f16 hv[3];
+#pragma unroll
+            for (int r = 0; r < 3; r++) {
+                const int src = L - 3 + r;
+                hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : hist[(size_t)(src + 3) * C + ch];
+            }
+#pragma unroll
+            for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = hv[r];
+        }
+    }
+}
+
 // Sequential over chunks for one head and 16 value columns; wave w owns rows 16w..16w+15 of the
 // chunk (and state rows 32w..32w+31 for the update).
 __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, float* __restrict__ state,
@@ -594,6 +730,17 @@ void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uin
     hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(256), 0, st, s, L, ws, state, lu, load_default, o,
                        sg.chunk, sg.seq);
     launched("gdn_scan");
+}
+
+void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
+               float* state, const uint32_t* lu, int load_default, float* o, f16* hist, const Segs& sg, int nseq,
+               hipStream_t st) {
+    SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
+    SD_CHECK(!sg.seq || (lu && sg.chunk && !hist), "gdn_recur: several sequences need lu and keep no history");
+    if (!sg.seq) nseq = 1;
+    hipLaunchKernelGGL(k_gdn_recur, dim3(s.H, s.DV / 16, nseq), dim3(256), 0, st, qkvc, big, s, negA, dtb, state, lu,
+                       load_default, o, sg.chunk, sg.seq, L, hist);
+    launched("gdn_recur");
 }
 
 void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st) {
