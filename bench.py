@@ -70,8 +70,9 @@ def read_traffic():
 
 def gemm_roofline(eng, state, cfg, reps=5):
     """The prefill int4 GEMM (k_gemm_w4, M = 512) inside the engine's own 512-token forward: each
-    GEMM is one launch, bracketed by HIP events on the engine's stream (Engine.profile).  achieved =
-    algorithmic flops per launch / average launch duration."""
+    GEMM is one launch whose own start and end HIP records into a pair of events on the engine's
+    stream (hipExtLaunchKernel, Engine.profile).  achieved = algorithmic flops per launch / average
+    launch duration."""
     shapes = gemm_shapes(cfg)
     M = len(state)
     total_ms = []
@@ -152,8 +153,9 @@ def traffic_summary(fetch_dir, write_dir, cfg, state_len):
 
 def trace_summary(trace_dir):
     """Per-kernel totals of a `rocprofv3 --kernel-trace` run of this script, then the kernels of the
-    last state prefill and of the last batched question forward.  Each forward starts with one
-    k_embed launch; without --roofline/--profile the forwards of a step alternate prefill, questions."""
+    last state prefill and of the last batched question forward, then the GEMM launches of the
+    roofline's eager forwards.  Each forward starts with one k_embed launch; the forwards of a step
+    alternate prefill, questions; the roofline's forwards follow a marker kernel of torch's."""
     import csv
     import glob
     rows = []
@@ -195,9 +197,14 @@ def trace_summary(trace_dir):
         return busy
 
     table(rows, "# per-kernel totals over the whole run")
-    starts = [i for i, r in enumerate(rows) if "k_embed" in r[2]]
-    fwd = [rows[a:b] for a, b in zip(starts, starts[1:] + [len(rows)])]
-    # the trailing forward ends at the last kernel before any non-engine work (none in this run)
+
+    def is_marker(name):
+        return "at::native" in name or name.startswith("_ZN2at6native")
+
+    mark = next((i for i, r in enumerate(rows) if is_marker(r[2])), len(rows))
+    steps_rows, roof_rows = rows[:mark], [r for r in rows[mark:] if not is_marker(r[2])]
+    starts = [i for i, r in enumerate(steps_rows) if "k_embed" in r[2]]
+    fwd = [steps_rows[a:b] for a, b in zip(starts, starts[1:] + [len(steps_rows)])]
     for kind, idx in (("state prefill", range(0, len(fwd), 2)), ("batched question forward", range(1, len(fwd), 2))):
         idx = list(idx)
         if not idx:
@@ -211,6 +218,12 @@ def trace_summary(trace_dir):
         g = [(e - s) / 1e3 for s, e, k in f if "k_gemm_w4" in k]
         if g:
             print(f"  k_gemm_w4 launches in this forward: {len(g)}, average duration {sum(g) / len(g):.2f} us")
+    g = [(e - s) / 1e3 for s, e, k in roof_rows if "k_gemm_w4" in k]
+    if g:
+        n_fwd = sum(1 for r in roof_rows if "k_embed" in r[2])
+        print()
+        print(f"# roofline: the GEMM launches of its {n_fwd} eager {STATE_LEN}-token forwards (Engine.profile)")
+        print(f"  k_gemm_w4 launches: {len(g)}, average duration {sum(g) / len(g):.2f} us")
 
 
 def _dev(a):
@@ -488,6 +501,10 @@ def main():
         prof_q = eng.profile(questions[0])
         res["profile_question_ms"] = {k: round(v, 4) for k, v in prof_q}
     if not args.no_roofline:
+        # a marker kernel of torch's separates the timed steps from the roofline's forwards in a
+        # kernel trace of this script (see trace_summary)
+        torch.ones(1, device="cuda")
+        torch.cuda.synchronize()
         res["roofline"] = gemm_roofline(eng, state, synth.CONFIG_2B)
     if not args.no_cpu_baseline:
         eng.free()

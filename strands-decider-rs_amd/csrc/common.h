@@ -40,6 +40,15 @@ struct Error : std::runtime_error {
 // so a failed launch is reported at its call site.
 void launched(const char* what);
 
+// Kernel-own timing for Engine::profile: while a step runs with this slot set, the first GEMM it
+// launches goes through hipExtLaunchKernel, which records the kernel's own start and end in
+// `start` / `stop` (the event pair around a step would add the dispatch of the launch).
+struct KernelEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+    int launches = 0;
+};
+KernelEvents*& kernel_events();
+
 // ---- quantized matmul (gemm.hip) -----------------------------------------------------------
 // Y[M,N] f16 = A[M,K] f16 . deq(W[N,K])^T with W int4 group-32 symmetric in the reference's
 // block layout ([N][K/32] blocks of 4 u32, k = 8w + e of a block in word w, value (q-8)*scale,

@@ -16,6 +16,11 @@ void launched(const char* what) {
     if (e != hipSuccess) throw Error(std::string("launching ") + what + ": " + hipGetErrorString(e));
 }
 
+KernelEvents*& kernel_events() {
+    thread_local KernelEvents* k = nullptr;
+    return k;
+}
+
 namespace {
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
@@ -824,23 +829,37 @@ std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids,
     Plan& pl = plan(L);
     upload(ids, n, nullptr, 0, 0, false, 0, 0);
     restore(nullptr, 0);
-    std::vector<hipEvent_t> evs(pl.steps.size() + 1);
+    // A step that launched a GEMM is timed by the kernel's own start and end; any other step by
+    // the events recorded between steps.
+    const size_t ns = pl.steps.size();
+    std::vector<hipEvent_t> evs(ns + 1), kev(2 * ns);
+    std::vector<int> own(ns, 0);
     for (auto& e : evs) SD_HIP(hipEventCreate(&e));
+    for (auto& e : kev) SD_HIP(hipEventCreate(&e));
+    struct Reset {
+        ~Reset() { kernel_events() = nullptr; }
+    } reset;
     SD_HIP(hipEventRecord(evs[0], st));
-    for (size_t i = 0; i < pl.steps.size(); i++) {
+    for (size_t i = 0; i < ns; i++) {
+        KernelEvents ke{kev[2 * i], kev[2 * i + 1], 0};
+        kernel_events() = &ke;
         pl.steps[i].run(st);
+        kernel_events() = nullptr;
+        own[i] = ke.launches;
         SD_HIP(hipEventRecord(evs[i + 1], st));
     }
     SD_HIP(hipStreamSynchronize(st));
     std::vector<std::pair<const char*, double>> by;
-    for (size_t i = 0; i < pl.steps.size(); i++) {
+    for (size_t i = 0; i < ns; i++) {
         float ms = 0.f;
-        SD_HIP(hipEventElapsedTime(&ms, evs[i], evs[i + 1]));
+        if (own[i]) SD_HIP(hipEventElapsedTime(&ms, kev[2 * i], kev[2 * i + 1]));
+        else SD_HIP(hipEventElapsedTime(&ms, evs[i], evs[i + 1]));
         auto f = std::find_if(by.begin(), by.end(), [&](auto& p) { return std::strcmp(p.first, pl.steps[i].label) == 0; });
         if (f == by.end()) by.emplace_back(pl.steps[i].label, ms);
         else f->second += ms;
     }
     for (auto& e : evs) (void)hipEventDestroy(e);
+    for (auto& e : kev) (void)hipEventDestroy(e);
     std::sort(by.begin(), by.end(), [](auto& a, auto& b) { return a.second > b.second; });
     return by;
 }

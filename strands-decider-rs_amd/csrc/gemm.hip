@@ -27,6 +27,8 @@
 //    workgroup synchronisation (on MI355X a device-scope fence writes back the whole XCD L2); the
 //    consumer sums the ks slots in a fixed order: the residual add + RMSNorm does it for the
 //    projections that feed it, `reduce_partials` for everything else.
+#include <hip/hip_ext.h>
+
 #include "common.h"
 
 namespace sd {
@@ -611,7 +613,14 @@ void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part,
     SD_CHECK(!c.wide || (K / 64 / ks) % 4 == 0, "gemm_w4: this configuration needs K / ks a multiple of 256");
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
     dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, ks);
-    hipLaunchKernelGGL(part ? c.part_out : c.f16_out, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks);
+    const auto kern = part ? c.part_out : c.f16_out;
+    KernelEvents* ke = kernel_events();
+    if (ke && ke->launches == 0) {
+        hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, ks);
+        ke->launches++;
+    } else {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks);
+    }
     launched("gemm_w4");
 }
 
