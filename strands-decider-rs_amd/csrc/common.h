@@ -73,6 +73,14 @@ void reduce_partials(const float* part, int ks, size_t n, f16* Y, hipStream_t st
 // Rewrites `words` int4 weight words in place from the reference's nibble order (the model file's)
 // to the one every gemm_w4 kernel reads; run once per weight matrix.
 void repack_w4(uint32_t* W, size_t words, hipStream_t st);
+// gate_up [2I][K] (weights and scales) rewritten in place with its rows interleaved in groups of
+// 16: rows 32p .. 32p + 15 = gate rows 16p .., rows 32p + 16 .. = the matching up rows.  tmp holds
+// N*K/2 + N*K/16 bytes.
+void interleave_gate_up(uint32_t* W, f16* S, int N, int K, void* tmp, hipStream_t st);
+// mid[M][N/2] f16 = silu(g) * u of the unsplit gate_up product A . deq(W)^T, W interleaved as above
+// (f16 dequant, a 32x32-tile configuration of gemm_w4_plan); N a multiple of 32, K of 256.
+void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M, int N, int K, hipStream_t st,
+                  int cfg);
 
 // ---- elementwise / norms (elem.hip) ----------------------------------------------------------
 void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f16* Bi, int d, int bits,
@@ -88,8 +96,9 @@ struct YIn {
 // x[rows[r]] += y, h[r] = rmsnorm(x[rows[r]]) * w -> f16 (h16) or f32 (h32); rows null = identity.
 void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* rows, int nrows, f16* h16, float* h32,
               hipStream_t st);
-// gate_up output in big (f16, [L][2I]) or as ks f32 split-K slots in part.
-void silu_mul(const f16* big, const float* part, int ks, int L, int I, f16* mid, hipStream_t st);
+// gate_up output in big (f16, [L][2I]) or as ks f32 split-K slots in part; `il`: gate and up
+// columns interleaved in groups of 16 (the layout interleave_gate_up gives the weights).
+void silu_mul(const f16* big, const float* part, int ks, int L, int I, bool il, f16* mid, hipStream_t st);
 void add_bias(f16* y, int L, int N, const float* c, hipStream_t st);
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);
 

@@ -96,17 +96,20 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
 
 // mid[t, j] = f16(silu(g) * u), big[t] = [g | u] (src/kernels.rs:123-135).  8 values per thread.
 // With KS > 0 the gate_up output arrives as KS f32 split-K slots of [L][2I]; their slot-order
-// sum rounded to f16 is the f16 value the reference stores in `big`.
+// sum rounded to f16 is the f16 value the reference stores in `big`.  `il`: the engine's gate_up
+// weights have their rows interleaved in groups of 16 (interleave_gate_up), so gate j sits at
+// column 32 (j / 16) + j % 16 and up j 16 columns further.
 template <int KS>
-__global__ void k_silu_mul(const f16* __restrict__ big, const float* __restrict__ part, int L, int I,
+__global__ void k_silu_mul(const f16* __restrict__ big, const float* __restrict__ part, int L, int I, int il,
                            f16* __restrict__ mid) {
     const size_t i8 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
     if (i8 >= (size_t)L * I) return;
     const size_t t = i8 / I, j = i8 % I;
+    const size_t gc = il ? (j >> 4) * 32 + (j & 15) : j, uc = il ? gc + 16 : I + j;
     float gv[8], uv[8];
     if constexpr (KS == 0) {
-        const f16x8 g8 = *reinterpret_cast<const f16x8*>(big + t * 2 * I + j);
-        const f16x8 u8 = *reinterpret_cast<const f16x8*>(big + t * 2 * I + I + j);
+        const f16x8 g8 = *reinterpret_cast<const f16x8*>(big + t * 2 * I + gc);
+        const f16x8 u8 = *reinterpret_cast<const f16x8*>(big + t * 2 * I + uc);
 #pragma unroll
         for (int e = 0; e < 8; e++) gv[e] = (float)g8[e], uv[e] = (float)u8[e];
     } else {
@@ -116,8 +119,8 @@ __global__ void k_silu_mul(const f16* __restrict__ big, const float* __restrict_
         for (int z = 0; z < KS; z++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                g4[z][h] = *reinterpret_cast<const float4*>(part + z * slot + t * 2 * I + j + 4 * h);
-                u4[z][h] = *reinterpret_cast<const float4*>(part + z * slot + t * 2 * I + I + j + 4 * h);
+                g4[z][h] = *reinterpret_cast<const float4*>(part + z * slot + t * 2 * I + gc + 4 * h);
+                u4[z][h] = *reinterpret_cast<const float4*>(part + z * slot + t * 2 * I + uc + 4 * h);
             }
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -179,17 +182,18 @@ void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* row
     launched("add_norm");
 }
 
-void silu_mul(const f16* big, const float* part, int ks, int L, int I, f16* mid, hipStream_t st) {
+void silu_mul(const f16* big, const float* part, int ks, int L, int I, bool il, f16* mid, hipStream_t st) {
     SD_CHECK(I % 8 == 0, "silu_mul: intermediate size must be a multiple of 8");
+    SD_CHECK(!il || I % 16 == 0, "silu_mul: interleaved gate/up needs I a multiple of 16");
     const size_t n8 = (size_t)L * I / 8;
     const dim3 grid((n8 + 255) / 256);
     const int k = part ? ks : 0;
     switch (k) {
-        case 0: hipLaunchKernelGGL(k_silu_mul<0>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
-        case 1: hipLaunchKernelGGL(k_silu_mul<1>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
-        case 2: hipLaunchKernelGGL(k_silu_mul<2>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
-        case 4: hipLaunchKernelGGL(k_silu_mul<4>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
-        case 8: hipLaunchKernelGGL(k_silu_mul<8>, grid, dim3(256), 0, st, big, part, L, I, mid); break;
+        case 0: hipLaunchKernelGGL(k_silu_mul<0>, grid, dim3(256), 0, st, big, part, L, I, il, mid); break;
+        case 1: hipLaunchKernelGGL(k_silu_mul<1>, grid, dim3(256), 0, st, big, part, L, I, il, mid); break;
+        case 2: hipLaunchKernelGGL(k_silu_mul<2>, grid, dim3(256), 0, st, big, part, L, I, il, mid); break;
+        case 4: hipLaunchKernelGGL(k_silu_mul<4>, grid, dim3(256), 0, st, big, part, L, I, il, mid); break;
+        case 8: hipLaunchKernelGGL(k_silu_mul<8>, grid, dim3(256), 0, st, big, part, L, I, il, mid); break;
         default: throw Error("silu_mul: unsupported partial count");
     }
     launched("silu_mul");

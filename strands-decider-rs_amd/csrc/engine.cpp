@@ -304,6 +304,35 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
             done.push_back(m->q);
             repack_w4(const_cast<uint32_t*>(m->q), (size_t)m->N * m->K / 8, st);
         }
+        // gate_up rows interleaved in groups of 16, so the GEMM's epilogue can apply silu * mul
+        // (possible when no other matrix shares a gate_up's memory)
+        std::vector<const Mat*> gus;
+        for (const LayerW& L : layers)
+            if (L.kind != SD_ADAPTER && L.gate_up.q) gus.push_back(&L.gate_up);
+        gu_il = !gus.empty() && cfg.inter % 16 == 0;
+        for (const Mat* g : gus)
+            for (const Mat* m : all)
+                if (m->q == g->q && m != g && std::find(gus.begin(), gus.end(), m) == gus.end()) gu_il = false;
+        if (gu_il) {
+            size_t tmp_bytes = 0;
+            for (const Mat* g : gus) tmp_bytes = std::max(tmp_bytes, (size_t)g->N * g->K / 2 + (size_t)g->N * g->K / 16);
+            void* tmp = nullptr;  // load-time scratch, freed below
+            SD_HIP(hipMalloc(&tmp, tmp_bytes));
+            std::vector<const uint32_t*> il_done;
+            try {
+                for (const Mat* g : gus) {
+                    if (std::find(il_done.begin(), il_done.end(), g->q) != il_done.end()) continue;
+                    il_done.push_back(g->q);
+                    interleave_gate_up(const_cast<uint32_t*>(g->q), const_cast<f16*>(g->s), g->N, g->K, tmp, st);
+                }
+                SD_HIP(hipStreamSynchronize(st));
+            } catch (...) {
+                (void)hipStreamSynchronize(st);
+                (void)hipFree(tmp);
+                throw;
+            }
+            SD_HIP(hipFree(tmp));
+        }
         SD_HIP(hipStreamSynchronize(st));
     }
 
@@ -507,16 +536,23 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
             steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.post_norm, d, nullptr, L, P.h, nullptr, s); }});
         }
         {
-            // gate_up only feeds silu * mul, which sums split-K partials itself
+            // gate_up only feeds silu * mul: prefill-sized inputs run it unsplit with silu * mul in
+            // the GEMM's epilogue; otherwise silu_mul sums the split-K partials itself
             const bool exact = sr || W.gate_up.N % 64 != 0;
-            const GemmPlan plan_ = gemm_w4_plan(L, W.gate_up.N, W.gate_up.K, exact, true, P.gpart_elems);
-            const int cg = plan_.cfg, ks = plan_.ks;
             const Mat m = W.gate_up;
-            float* gp = ks > 1 ? P.gpart : nullptr;  // unsplit: f16 straight into big
-            steps.push_back({"gate_up", [=](hipStream_t s) {
-                gemm_w4(P.h, m.q, m.s, P.big, gp, L, m.N, m.K, exact, ks, s, cg);
-            }});
-            steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, gp, ks, L, I, P.mid, s); }});
+            const bool il = gu_il;
+            if (il && !exact && m.K % 256 == 0 && L >= 256 && L <= 1024) {
+                const int cg = gemm_w4_plan(L, m.N, m.K, false, false, 0).cfg;
+                steps.push_back({"gate_up", [=](hipStream_t s) { gemm_w4_silu(P.h, m.q, m.s, P.mid, L, m.N, m.K, s, cg); }});
+            } else {
+                const GemmPlan plan_ = gemm_w4_plan(L, m.N, m.K, exact, true, P.gpart_elems);
+                const int cg = plan_.cfg, ks = plan_.ks;
+                float* gp = ks > 1 ? P.gpart : nullptr;  // unsplit: f16 straight into big
+                steps.push_back({"gate_up", [=](hipStream_t s) {
+                    gemm_w4(P.h, m.q, m.s, P.big, gp, L, m.N, m.K, exact, ks, s, cg);
+                }});
+                steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, gp, ks, L, I, il, P.mid, s); }});
+            }
         }
         y = mm_y(steps, "down", P.mid, W.down, L, sr);
     }

@@ -131,6 +131,7 @@ struct Engine {
     int max_n = 0;
     uint64_t snapshot_ids = 0, kv_owner = 0;
     bool use_graphs = true;
+    bool gu_il = false;  // gate_up weights interleaved in groups of 16 rows (interleave_gate_up)
     Pool pool;
     std::map<int, Plan> plans;
     uint32_t *ids_h = nullptr, *rows_h = nullptr, *seg_h = nullptr;

@@ -51,6 +51,13 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
     return r;
 }
 
+// mask bit of the lane set ? b : a, as one v_cndmask_b32.
+__device__ __forceinline__ float sel_lanes(uint64_t mask, float a, float b) {
+    float r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+    return r;
+}
+
 __device__ __forceinline__ void nib_pairs(uint32_t w, f16x2& p0, f16x2& p1, f16x2& p2, f16x2& p3) {
     const uint32_t w8 = w >> 8;
     const f16x2 x0 = __builtin_bit_cast(f16x2, and_or(w, 0x000F000Fu, 0x64006400u));
@@ -297,8 +304,13 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 //    step (16 bytes) and its scale, up to 3 steps ahead in registers; MFMA k-slice s (16 k) takes
 //    word s of that block, which is k-chunk 4g + s of the step, so the A fragment of lane (r, g) is
 //    the 8 halves of row r at that k-chunk (the engine nibble order makes them natural);
-//  * D of the 32x32 tile: register i of lane l is row 8(i/4) + 4(l/32) + i%4, column l%32.
-template <int MT2, int NT2, bool PARTIAL>
+//  * D of the 32x32 tile: register i of lane l is row 8(i/4) + 4(l/32) + i%4, column l%32;
+//  * SILU (gate_up, unsplit): W holds gate_up with its rows interleaved in groups of 16 (rows
+//    32p .. 32p + 15 are gate rows 16p .., the next 16 the matching up rows, interleave_gate_up),
+//    so lanes l and l ^ 16 hold gate and up of one (row, j); they swap halves of their registers
+//    and each writes 8 values of Y = mid[M][N / 2] = f16(silu(g) * u), g and u rounded to f16 first
+//    as the reference stores them.
+template <int MT2, int NT2, bool PARTIAL, bool SILU = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2))) void k_gemm_w4m(
     const f16* __restrict__ A, const uint32_t* __restrict__ W, const f16* __restrict__ S, f16* __restrict__ Y,
     float* __restrict__ part, int M, int N, int K, int ksplit) {
@@ -460,6 +472,45 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     } while (it < steps);
     wait_loads<0x0F70>();  // the trailing out-of-range loads, before the LDS is released
 
+    if constexpr (SILU) {
+        // N % 32 == 0 (checked by the launcher): a tile's columns are all in range or all out
+        const bool up = r >= 16;
+        const uint64_t upm = __ballot(up);  // lanes 16..31 and 48..63
+        const int half = N >> 1;
+#pragma unroll
+        for (int a = 0; a < MT2; a++)
+#pragma unroll
+            for (int t = 0; t < NT2; t++) {
+                if (ncol[t] >= N) continue;
+                const int j = ((ncol[t] >> 5) << 4) + (r & 15);
+                const int mb = m0 + a * 32 + (up ? 16 : 0) + 4 * g;
+                const bool full = m0 + a * 32 + 32 <= M;
+                // the gate lane keeps registers 0..7 and receives the up lane's, and the other way
+                // round for 8..15 (one v_cndmask each: a plain ?: on the two registers becomes a
+                // variable index into the accumulator); all 8 swaps are issued before any use
+                float keep[8], got[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    keep[k] = sel_lanes(upm, acc[a][t][k], acc[a][t][8 + k]);
+                    const float send = sel_lanes(upm, acc[a][t][8 + k], acc[a][t][k]);
+                    got[k] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x401F));  // lane ^ 16
+                }
+                f16 out[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float gv = (float)(f16)sel_lanes(upm, keep[k], got[k]);
+                    const float uv = (float)(f16)sel_lanes(upm, got[k], keep[k]);
+                    out[k] = (f16)(gv / (1.0f + expf(-gv)) * uv);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int m = mb + 8 * (k >> 2) + (k & 3);
+                    if (full || m < M) Y[(size_t)m * half + j] = out[k];
+                }
+            }
+        return;
+    }
     float* mine = PARTIAL ? part + (size_t)bz * M * N : nullptr;
 #pragma unroll
     for (int a = 0; a < MT2; a++)
@@ -492,6 +543,21 @@ __global__ void k_repack_w4(uint32_t* __restrict__ W, size_t n) {
     W[i] = w;
 }
 
+// dst row n of a [N][K] int4 matrix (16-byte blocks and f16 scales) = src row gate_up_row(n): groups
+// of 32 rows alternate 16 gate rows and the 16 matching up rows (N = 2I).
+__device__ __forceinline__ int gate_up_row(int n, int N) {
+    const int p = n >> 5, w = n & 31;
+    return w < 16 ? 16 * p + w : (N >> 1) + 16 * p + (w - 16);
+}
+__global__ void k_interleave_gate_up(const u32x4* __restrict__ sw, const f16* __restrict__ ss, u32x4* __restrict__ dw,
+                                     f16* __restrict__ ds, int N, int KB) {
+    const int n = blockIdx.x, src = gate_up_row(n, N);
+    for (int b = threadIdx.x; b < KB; b += blockDim.x) {
+        dw[(size_t)n * KB + b] = sw[(size_t)src * KB + b];
+        ds[(size_t)n * KB + b] = ss[(size_t)src * KB + b];
+    }
+}
+
 // Y[i] = f16(sum_z part[z][i]) in slot order.
 __global__ void k_reduce_partials(const float* __restrict__ part, int ks, size_t n, f16* __restrict__ Y) {
     const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
@@ -518,10 +584,13 @@ struct Cfg {
     bool exact;
     GemmFn f16_out, part_out;
     bool wide;  // k_gemm_w4m (k steps of 64 in a ring of 4)
+    GemmFn silu_out;  // k_gemm_w4m with the SiLU * mul epilogue (wide configurations only)
 };
 
-#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX, false>, k_gemm_w4<MT, NT, EX, true>, false}
-#define SD_CFGM(MT2, NT2) Cfg{2 * MT2, 2 * NT2, false, k_gemm_w4m<MT2, NT2, false>, k_gemm_w4m<MT2, NT2, true>, true}
+#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX, false>, k_gemm_w4<MT, NT, EX, true>, false, nullptr}
+#define SD_CFGM(MT2, NT2)                                                                                        \
+    Cfg{2 * MT2, 2 * NT2, false, k_gemm_w4m<MT2, NT2, false>, k_gemm_w4m<MT2, NT2, true>, true,                  \
+        k_gemm_w4m<MT2, NT2, false, true>}
 const Cfg kCfgs[] = {
     SD_CFG(1, 1, true), SD_CFG(2, 1, true),                                           // M <= 20: f32 dequant
     SD_CFG(1, 1, false), SD_CFG(2, 1, false), SD_CFG(3, 1, false), SD_CFG(4, 1, false),  // skinny
@@ -601,6 +670,21 @@ int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_pa
     return ks;
 }
 
+namespace {
+// A GEMM launch; while Engine::profile times a step, the step's first GEMM records its own start
+// and end (see KernelEvents).
+void launch_gemm(GemmFn kern, dim3 grid, hipStream_t st, const f16* A, const uint32_t* W, const f16* S, f16* Y,
+                 float* part, int M, int N, int K, int ks) {
+    KernelEvents* ke = kernel_events();
+    if (ke && ke->launches == 0) {
+        hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, ks);
+        ke->launches++;
+    } else {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks);
+    }
+}
+}  // namespace
+
 void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part, int M, int N, int K, bool exact,
              int ks, hipStream_t st, int cfg) {
     SD_CHECK(M >= 1 && N >= 1 && K >= KSTEP && K % KSTEP == 0, "gemm_w4: need M, N >= 1 and K a multiple of 128");
@@ -613,15 +697,31 @@ void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part,
     SD_CHECK(!c.wide || (K / 64 / ks) % 4 == 0, "gemm_w4: this configuration needs K / ks a multiple of 256");
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
     dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, ks);
-    const auto kern = part ? c.part_out : c.f16_out;
-    KernelEvents* ke = kernel_events();
-    if (ke && ke->launches == 0) {
-        hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, ks);
-        ke->launches++;
-    } else {
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks);
-    }
+    launch_gemm(part ? c.part_out : c.f16_out, grid, st, A, W, S, Y, part, M, N, K, ks);
     launched("gemm_w4");
+}
+
+void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M, int N, int K, hipStream_t st,
+                  int cfg) {
+    SD_CHECK(M >= 1 && N >= 32 && N % 32 == 0 && K % 256 == 0, "gemm_w4_silu: need N a multiple of 32, K of 256");
+    SD_CHECK(cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg].silu_out, "gemm_w4_silu: not a 32x32-tile configuration");
+    const Cfg& c = kCfgs[cfg];
+    const int bm = c.mt * 16, bn = 4 * c.nt * 16;
+    dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, 1);
+    launch_gemm(c.silu_out, grid, st, A, W, S, mid, (float*)nullptr, M, N, K, 1);
+    launched("gemm_w4_silu");
+}
+
+void interleave_gate_up(uint32_t* W, f16* S, int N, int K, void* tmp, hipStream_t st) {
+    SD_CHECK(N % 32 == 0 && K % 32 == 0, "interleave_gate_up: need N a multiple of 32");
+    const int KB = K / 32;
+    u32x4* tw = static_cast<u32x4*>(tmp);
+    f16* ts = reinterpret_cast<f16*>(tw + (size_t)N * KB);
+    hipLaunchKernelGGL(k_interleave_gate_up, dim3(N), dim3(256), 0, st, reinterpret_cast<const u32x4*>(W), S, tw, ts,
+                       N, KB);
+    launched("interleave_gate_up");
+    SD_HIP(hipMemcpyAsync(W, tw, (size_t)N * KB * 16, hipMemcpyDeviceToDevice, st));
+    SD_HIP(hipMemcpyAsync(S, ts, (size_t)N * KB * 2, hipMemcpyDeviceToDevice, st));
 }
 
 void repack_w4(uint32_t* W, size_t words, hipStream_t st) {
