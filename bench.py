@@ -266,7 +266,7 @@ def kernel_bench(pkg, reps=50):
         S = rng.uniform(0.005, 0.02, size=(N, K // 32)).astype(np.float16)
         dA, dW, dS = _dev(A), _dev(W), _dev(S)
         dY = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
-        pkg.op_repack_w4(dW.data_ptr(), N, K, stream)
+        pkg.op_repack_w4(dW.data_ptr(), dS.data_ptr(), N, K, stream)
         exact = M <= 20
         ms = _timed(lambda: pkg.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, exact,
                                           -1, True, stream), reps)

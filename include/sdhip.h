@@ -149,15 +149,18 @@ int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_s
 /* Y[M,N] f16 = A[M,K] f16 . deq(W)^T, W int4 group-32 symmetric in the model layout
  * ([N][K/32] blocks of 4 u32, scales [N][K/32] f16): the reference's matmul_gemv/matmul_tiled
  * (src/kernels.rs:590-709).  exact = 1 selects the GEMV's f32 dequant, 0 the tiled f16 dequant;
- * cfg < 0 takes the engine's choice for the shape (tile and split-K).  packed = 0: Wq is in the model's nibble order and
- * is repacked into a library workspace on every call; packed = 1: Wq was already rewritten by
- * sd_op_repack_w4 (what the engine does to its weights once at load). */
+ * cfg < 0 takes the engine's choice for the shape (tile and split-K).  packed = 0: Wq and Sc are
+ * in the model's order and layout and are rewritten into a library workspace on every call;
+ * packed = 1: they were already rewritten by sd_op_repack_w4 (what the engine does to its weights
+ * once at load). */
 int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, int N, int K, int exact, int cfg,
                  int packed, void* stream, char* err, size_t errlen);
 
-/* No counterpart in the reference: rewrites N*K/8 int4 weight words in place from the model's
- * nibble order into the one the GEMM kernels read (sd_op_matmul with packed = 1). */
-int sd_op_repack_w4(void* Wq, int N, int K, void* stream, char* err, size_t errlen);
+/* No counterpart in the reference: rewrites an N x K int4 matrix in place into what the GEMM
+ * kernels read (sd_op_matmul with packed = 1): the N*K/8 words into the engine nibble order and,
+ * when N is a multiple of 32 and K of 64, words and scales into 32-column x 64-k tiles (each tile's
+ * blocks contiguous, column by column). */
+int sd_op_repack_w4(void* Wq, void* Sc, int N, int K, void* stream, char* err, size_t errlen);
 
 /* One gated-delta-net recurrence, the reference's Gdn kernel (src/kernels.rs:257-372), on device
  * buffers: qkv [L][2*H*dk + H*dv] f32, a/b gates f16 in big [L][stride] at a_off + h / b_off + h,

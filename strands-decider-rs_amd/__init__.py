@@ -94,7 +94,7 @@ def lib():
         L.sd_head_probs.argtypes = [vp, vp, sz, sz, C.c_double, vp, err, sz]
         L.sd_ask_ids.argtypes = [vp, vp, vp, sz, sz, C.POINTER(vp), vp, C.POINTER(vp), vp, vp, vp, err, sz]
         L.sd_op_matmul.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, err, sz]
-        L.sd_op_repack_w4.argtypes = [vp, i32, i32, vp, err, sz]
+        L.sd_op_repack_w4.argtypes = [vp, vp, i32, i32, vp, err, sz]
         L.sd_op_gdn.argtypes = [vp, vp, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, err, sz]
         for name in SYMBOLS:
             if name not in ("sd_engine_free", "sd_snapshot_free", "sd_head_free", "sd_engine_hidden_size",
@@ -356,14 +356,15 @@ def load_decider(model_dir: str):
 # ---- kernel-level entry points (device pointers as ints; stream handle as int or None) ----------
 
 def op_matmul(A, Wq, Sc, Y, M, N, K, exact=False, cfg=-1, packed=False, stream=None):
-    """sd_op_matmul on device pointers; packed: Wq already went through op_repack_w4."""
+    """sd_op_matmul on device pointers; packed: Wq and Sc already went through op_repack_w4."""
     _call(lib().sd_op_matmul, C.c_void_p(A), C.c_void_p(Wq), C.c_void_p(Sc), C.c_void_p(Y), M, N, K, int(exact), cfg,
           int(packed), C.c_void_p(stream) if stream else None)
 
 
-def op_repack_w4(Wq, N, K, stream=None):
-    """sd_op_repack_w4: rewrites N*K/8 weight words in place into the GEMM kernels' nibble order."""
-    _call(lib().sd_op_repack_w4, C.c_void_p(Wq), N, K, C.c_void_p(stream) if stream else None)
+def op_repack_w4(Wq, Sc, N, K, stream=None):
+    """sd_op_repack_w4: rewrites an N x K matrix's words and scales in place into what the GEMM
+    kernels read (the engine nibble order, and 32-column x 64-k tiles where the shape allows)."""
+    _call(lib().sd_op_repack_w4, C.c_void_p(Wq), C.c_void_p(Sc), N, K, C.c_void_p(stream) if stream else None)
 
 
 def op_gdn(qkv, big, stride, a_off, b_off, negA, dtb, L, H, dk, dv, state, load_state, o, stream=None):

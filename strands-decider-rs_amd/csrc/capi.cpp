@@ -43,9 +43,21 @@ struct OpWs {
     size_t part_floats = 0;
     void* gdn = nullptr;
     size_t gdn_bytes = 0;
-    uint32_t* wpack = nullptr;  // the weights of sd_op_matmul in the engine nibble order
-    size_t wpack_words = 0;
+    // the weights and scales of sd_op_matmul in the engine's order and layout, and the scratch of
+    // the tiled-layout rewrite
+    void* wpack = nullptr;
+    size_t wpack_bytes = 0;
+    void* wtmp = nullptr;
+    size_t wtmp_bytes = 0;
 };
+void grow(void*& p, size_t& have, size_t need) {
+    if (have >= need) return;
+    if (p) SD_HIP(hipFree(p));
+    p = nullptr;
+    have = 0;
+    SD_HIP(hipMalloc(&p, need));
+    have = need;
+}
 OpWs& op_ws() {
     static OpWs w;
     return w;
@@ -249,11 +261,18 @@ int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_s
     });
 }
 
-int sd_op_repack_w4(void* Wq, int N, int K, void* stream, char* err, size_t errlen) {
+int sd_op_repack_w4(void* Wq, void* Sc, int N, int K, void* stream, char* err, size_t errlen) {
     return guarded(err, errlen, [&] {
-        if (!Wq) throw sd::Error("sd_op_repack_w4: null argument");
+        if (!Wq || !Sc) throw sd::Error("sd_op_repack_w4: null argument");
         if (N < 1 || K < 32 || K % 32) throw sd::Error("sd_op_repack_w4: need N >= 1 and K a multiple of 32");
-        sd::repack_w4(static_cast<uint32_t*>(Wq), (size_t)N * K / 8, static_cast<hipStream_t>(stream));
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        sd::repack_w4(static_cast<uint32_t*>(Wq), (size_t)N * K / 8, st);
+        if (sd::w4_tileable(N, K)) {
+            OpWs& w = op_ws();
+            std::lock_guard<std::mutex> lock(w.mu);
+            grow(w.wtmp, w.wtmp_bytes, (size_t)N * K / 2 + (size_t)N * K / 16);
+            sd::tile_w4(static_cast<uint32_t*>(Wq), static_cast<sd::f16*>(Sc), N, K, w.wtmp, st);
+        }
     });
 }
 
@@ -278,24 +297,28 @@ int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, 
             ks = sd::gemm_w4_split(M, N, K, c, 256, cap);
         }
         const auto* a = static_cast<const sd::f16*>(A);
-        // The kernels read the engine nibble order: unless the caller repacked its weights already,
-        // repack a copy of them.
+        // The kernels read the engine nibble order and, where the shape has one, the tiled layout:
+        // unless the caller rewrote its weights already (sd_op_repack_w4), rewrite a copy of them.
+        const bool tiled = sd::w4_tileable(N, K);
         const uint32_t* wq = static_cast<const uint32_t*>(Wq);
-        if (!packed) {
-            const size_t words = (size_t)N * K / 8;
-            if (w.wpack_words < words) {
-                if (w.wpack) SD_HIP(hipFree(w.wpack));
-                w.wpack = nullptr;
-                SD_HIP(hipMalloc(&w.wpack, words * 4));
-                w.wpack_words = words;
-            }
-            SD_HIP(hipMemcpyAsync(w.wpack, Wq, words * 4, hipMemcpyDeviceToDevice, st));
-            sd::repack_w4(w.wpack, words, st);
-            wq = w.wpack;
-        }
         const auto* sc = static_cast<const sd::f16*>(Sc);
+        if (!packed) {
+            const size_t words = (size_t)N * K / 8, scales = (size_t)N * K / 32;
+            grow(w.wpack, w.wpack_bytes, words * 4 + scales * 2);
+            auto* pw = static_cast<uint32_t*>(w.wpack);
+            auto* ps = reinterpret_cast<sd::f16*>(pw + words);
+            SD_HIP(hipMemcpyAsync(pw, Wq, words * 4, hipMemcpyDeviceToDevice, st));
+            SD_HIP(hipMemcpyAsync(ps, Sc, scales * 2, hipMemcpyDeviceToDevice, st));
+            sd::repack_w4(pw, words, st);
+            if (tiled) {
+                grow(w.wtmp, w.wtmp_bytes, words * 4 + scales * 2);
+                sd::tile_w4(pw, ps, N, K, w.wtmp, st);
+            }
+            wq = pw;
+            sc = ps;
+        }
         if (ks == 1) {
-            sd::gemm_w4(a, wq, sc, static_cast<sd::f16*>(Y), nullptr, M, N, K, exact != 0, 1, st, c);
+            sd::gemm_w4(a, wq, sc, static_cast<sd::f16*>(Y), nullptr, M, N, K, exact != 0, 1, st, c, tiled);
             return;
         }
         if (w.part_floats < (size_t)ks * M * N) {
@@ -304,7 +327,7 @@ int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, 
             SD_HIP(hipMalloc(&w.part, cap * 4));
             w.part_floats = cap;
         }
-        sd::gemm_w4(a, wq, sc, nullptr, w.part, M, N, K, exact != 0, ks, st, c);
+        sd::gemm_w4(a, wq, sc, nullptr, w.part, M, N, K, exact != 0, ks, st, c, tiled);
         sd::reduce_partials(w.part, ks, (size_t)M * N, static_cast<sd::f16*>(Y), st);
     });
 }

@@ -57,8 +57,16 @@ KernelEvents*& kernel_events();
 // k range is split over ks workgroups that write f32 partials part[ks][M][N] instead of Y (ks = 1
 // allowed); the consumer sums them in slot order (add_norm, or reduce_partials).  cfg < 0 picks
 // the tile shape by M.
+// `tiled`: W and S are in the tiled layout of tile_w4.
 void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part, int M, int N, int K, bool exact,
-             int ks, hipStream_t st, int cfg = -1);
+             int ks, hipStream_t st, int cfg = -1, bool tiled = false);
+// Whether tile_w4 takes an N x K matrix (N a multiple of 32, K of 64).
+bool w4_tileable(int N, int K);
+// Rewrites a matrix's words (already in the engine nibble order) and scales in place into the tiled
+// layout: each tile of 32 columns x 64 k (2 blocks per column) becomes one contiguous KiB of words,
+// block (n, b) at 16-byte index ((n / 32) * (K / 64) + b / 2) * 64 + (n % 32) * 2 + b % 2, its
+// scale at the same f16 index.  tmp holds N*K/2 + N*K/16 bytes.
+void tile_w4(uint32_t* W, f16* S, int N, int K, void* tmp, hipStream_t st);
 int gemm_w4_configs();
 int gemm_w4_cfg(int M, bool exact);
 // Kernel configuration and split-K count for an M x N x K product.  partial_ok: the consumer can
@@ -80,7 +88,7 @@ void interleave_gate_up(uint32_t* W, f16* S, int N, int K, void* tmp, hipStream_
 // mid[M][N/2] f16 = silu(g) * u of the unsplit gate_up product A . deq(W)^T, W interleaved as above
 // (f16 dequant, a 32x32-tile configuration of gemm_w4_plan); N a multiple of 32, K of 256.
 void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M, int N, int K, hipStream_t st,
-                  int cfg);
+                  int cfg, bool tiled);
 
 // ---- elementwise / norms (elem.hip) ----------------------------------------------------------
 void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f16* Bi, int d, int bits,

@@ -292,14 +292,17 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         layers.push_back(L);
     }
     final_norm = f32("final_norm", cfg.d);
-    // Matmul weights into the engine nibble order, each matrix once.
+    // Matmul weights into the engine nibble order, gate_up rows interleaved, then the tiled layout,
+    // each matrix once (matrices are told apart by their memory).
     {
-        std::vector<const Mat*> all;
-        for (const LayerW& L : layers)
-            for (const Mat* m : {&L.in_proj, &L.out_proj, &L.qkv, &L.o_proj, &L.gate_up, &L.down, &L.proj})
+        std::vector<Mat*> all;
+        for (LayerW& L : layers)
+            for (Mat* m : {&L.in_proj, &L.out_proj, &L.qkv, &L.o_proj, &L.gate_up, &L.down, &L.proj})
                 if (m->q) all.push_back(m);
         std::vector<const uint32_t*> done;
+        size_t tmp_bytes = 0;
         for (const Mat* m : all) {
+            tmp_bytes = std::max(tmp_bytes, (size_t)m->N * m->K / 2 + (size_t)m->N * m->K / 16);
             if (std::find(done.begin(), done.end(), m->q) != done.end()) continue;
             done.push_back(m->q);
             repack_w4(const_cast<uint32_t*>(m->q), (size_t)m->N * m->K / 8, st);
@@ -313,27 +316,31 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         for (const Mat* g : gus)
             for (const Mat* m : all)
                 if (m->q == g->q && m != g && std::find(gus.begin(), gus.end(), m) == gus.end()) gu_il = false;
-        if (gu_il) {
-            size_t tmp_bytes = 0;
-            for (const Mat* g : gus) tmp_bytes = std::max(tmp_bytes, (size_t)g->N * g->K / 2 + (size_t)g->N * g->K / 16);
-            void* tmp = nullptr;  // load-time scratch, freed below
-            SD_HIP(hipMalloc(&tmp, tmp_bytes));
+        void* tmp = nullptr;  // load-time scratch, freed below
+        SD_HIP(hipMalloc(&tmp, std::max<size_t>(tmp_bytes, 256)));
+        try {
             std::vector<const uint32_t*> il_done;
-            try {
-                for (const Mat* g : gus) {
-                    if (std::find(il_done.begin(), il_done.end(), g->q) != il_done.end()) continue;
-                    il_done.push_back(g->q);
-                    interleave_gate_up(const_cast<uint32_t*>(g->q), const_cast<f16*>(g->s), g->N, g->K, tmp, st);
-                }
-                SD_HIP(hipStreamSynchronize(st));
-            } catch (...) {
-                (void)hipStreamSynchronize(st);
-                (void)hipFree(tmp);
-                throw;
+            for (const Mat* g : gus) {
+                if (!gu_il || std::find(il_done.begin(), il_done.end(), g->q) != il_done.end()) continue;
+                il_done.push_back(g->q);
+                interleave_gate_up(const_cast<uint32_t*>(g->q), const_cast<f16*>(g->s), g->N, g->K, tmp, st);
             }
-            SD_HIP(hipFree(tmp));
+            // the tiled layout for every matrix that has one (each matrix sharing memory with a
+            // tiled one is tiled with it)
+            std::vector<const uint32_t*> tiled_done;
+            for (Mat* m : all) {
+                m->tiled = w4_tileable(m->N, m->K);
+                if (!m->tiled || std::find(tiled_done.begin(), tiled_done.end(), m->q) != tiled_done.end()) continue;
+                tiled_done.push_back(m->q);
+                tile_w4(const_cast<uint32_t*>(m->q), const_cast<f16*>(m->s), m->N, m->K, tmp, st);
+            }
+            SD_HIP(hipStreamSynchronize(st));
+        } catch (...) {
+            (void)hipStreamSynchronize(st);
+            (void)hipFree(tmp);
+            throw;
         }
-        SD_HIP(hipStreamSynchronize(st));
+        SD_HIP(hipFree(tmp));
     }
 
     // RoPE table, angles in f64 (src/engine.rs:259-267).
@@ -445,7 +452,7 @@ void Engine::mm(std::vector<Step>& steps, const char* label, const f16* A, const
     // The reference's GEMV (f32 dequant) serves M <= 20 and N % 64 != 0 (src/engine.rs:419-442).
     const bool exact = short_rows || m.N % 64 != 0;
     const int cfg_ = gemm_w4_plan(L, m.N, m.K, exact, false, 0).cfg;
-    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, nullptr, L, m.N, m.K, exact, 1, s, cfg_); }});
+    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, nullptr, L, m.N, m.K, exact, 1, s, cfg_, m.tiled); }});
 }
 
 YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L, bool short_rows) {
@@ -455,7 +462,9 @@ YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, cons
     const GemmPlan gp = gemm_w4_plan(L, m.N, m.K, exact, true, pool.ypart_elems);
     const int cfg_ = gp.cfg, ks = gp.ks;
     float* part = pool.ypart;
-    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, nullptr, part, L, m.N, m.K, exact, ks, s, cfg_); }});
+    steps.push_back({label, [=](hipStream_t s) {
+        gemm_w4(A, m.q, m.s, nullptr, part, L, m.N, m.K, exact, ks, s, cfg_, m.tiled);
+    }});
     YIn y;
     y.yp = part;
     y.ks = ks;
@@ -543,13 +552,15 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
             const bool il = gu_il;
             if (il && !exact && m.K % 256 == 0 && L >= 256 && L <= 1024) {
                 const int cg = gemm_w4_plan(L, m.N, m.K, false, false, 0).cfg;
-                steps.push_back({"gate_up", [=](hipStream_t s) { gemm_w4_silu(P.h, m.q, m.s, P.mid, L, m.N, m.K, s, cg); }});
+                steps.push_back({"gate_up", [=](hipStream_t s) {
+                    gemm_w4_silu(P.h, m.q, m.s, P.mid, L, m.N, m.K, s, cg, m.tiled);
+                }});
             } else {
                 const GemmPlan plan_ = gemm_w4_plan(L, m.N, m.K, exact, true, P.gpart_elems);
                 const int cg = plan_.cfg, ks = plan_.ks;
                 float* gp = ks > 1 ? P.gpart : nullptr;  // unsplit: f16 straight into big
                 steps.push_back({"gate_up", [=](hipStream_t s) {
-                    gemm_w4(P.h, m.q, m.s, P.big, gp, L, m.N, m.K, exact, ks, s, cg);
+                    gemm_w4(P.h, m.q, m.s, P.big, gp, L, m.N, m.K, exact, ks, s, cg, m.tiled);
                 }});
                 steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, gp, ks, L, I, il, P.mid, s); }});
             }

@@ -30,6 +30,7 @@ struct Mat {
     const uint32_t* q = nullptr;
     const f16* s = nullptr;
     int N = 0, K = 0;
+    bool tiled = false;  // words and scales in the tiled layout (tile_w4)
 };
 
 struct EmbedW {

@@ -27,6 +27,13 @@
 //    workgroup synchronisation (on MI355X a device-scope fence writes back the whole XCD L2); the
 //    consumer sums the ks slots in a fixed order: the residual add + RMSNorm does it for the
 //    projections that feed it, `reduce_partials` for everything else.
+//
+// Weight layouts (both in the engine nibble order): `plain` is the model file's [N][K/32] blocks of
+// 16 bytes with scales [N][K/32]; `tiled` (N % 32 == 0, K % 64 == 0, tile_w4 at load) stores each
+// tile of 32 columns x 64 k (2 blocks per column) as one contiguous KiB, column-major inside:
+// block (n, b) at 16-byte index ((n / 32) * (K / 64) + b / 2) * 64 + (n % 32) * 2 + b % 2, its scale
+// at the same f16 index.  A wave's weights for one k step are then one KiB of whole cache lines
+// (and 128 bytes of scales) instead of 16 or 2 bytes out of every column's lines.
 #include <hip/hip_ext.h>
 
 #include "common.h"
@@ -119,7 +126,8 @@ __device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
 template <int MT, int NT, bool EXACT, bool PARTIAL>
 __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, const uint32_t* __restrict__ W,
                                                  const f16* __restrict__ S, f16* __restrict__ Y,
-                                                 float* __restrict__ part, int M, int N, int K, int ksplit) {
+                                                 float* __restrict__ part, int M, int N, int K, int ksplit,
+                                                 int tiled) {
     constexpr int BM = MT * 16;
     constexpr int BN = 4 * NT * 16;
     constexpr int ACH = BM * 16 / 256;  // 16-byte A chunks per thread per macro step (== MT)
@@ -154,13 +162,17 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
     }
     // Loads are branch-free: rows past M and columns past N read the last valid row/column, and
     // the outputs they feed are never stored.
+    // block kb0 + g of column n: plain n * KB + kb0 + g; tiled (kb0 a multiple of 4) the tile
+    // step (kb0 + g) / 2 of column tile n / 32
     const u32x4* wrow[NT];
     const f16* srow[NT];
+    const int wst = tiled ? 128 : 4;  // 16-byte blocks (and scales) per macro step of 128 k
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const size_t n = (size_t)min(ncol[t], N - 1);
-        wrow[t] = reinterpret_cast<const u32x4*>(W) + n * KB + g;
-        srow[t] = S + n * KB + g;
+        const size_t i0 = tiled ? ((n >> 5) * (size_t)(KB >> 1) + (g >> 1)) * 64 + (n & 31) * 2 + (g & 1) : n * KB + g;
+        wrow[t] = reinterpret_cast<const u32x4*>(W) + i0;
+        srow[t] = S + i0;
     }
     const f16* arow[ACH];
 #pragma unroll
@@ -184,8 +196,8 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
     auto load_b = [&](int step) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            bnext[t] = wrow[t][step * 4];
-            snext[t] = srow[t][step * 4];
+            bnext[t] = wrow[t][step * wst];
+            snext[t] = srow[t][step * wst];
         }
     };
     auto store_a = [&](f16* dst) {
@@ -313,7 +325,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 template <int MT2, int NT2, bool PARTIAL, bool SILU = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2))) void k_gemm_w4m(
     const f16* __restrict__ A, const uint32_t* __restrict__ W, const f16* __restrict__ S, f16* __restrict__ Y,
-    float* __restrict__ part, int M, int N, int K, int ksplit) {
+    float* __restrict__ part, int M, int N, int K, int ksplit, int tiled) {
     constexpr int KS = 64;                   // k per step
     constexpr int BM = MT2 * 32;
     constexpr int STAGE = BM * KS * 2;       // bytes of one A stage
@@ -361,15 +373,19 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 #pragma unroll
     for (int s = 0; s < 4; s++) foff[s] = r * 128 + (((4 * g + s) ^ ((r >> 1) & 7)) << 4);
 
+    // Block g of step 0 of column n (plain: n * KB + g; tiled: inside column tile n / 32), and the
+    // bytes one step advances the weight and scale offsets.
     int ncol[NT2];
     uint32_t woff[NT2], soff[NT2];
 #pragma unroll
     for (int t = 0; t < NT2; t++) {
         ncol[t] = n0 + (wave * NT2 + t) * 32 + r;
         const uint32_t n = (uint32_t)min(ncol[t], N - 1);
-        woff[t] = (n * KB + g) * 16u;
-        soff[t] = (n * KB + g) * 2u;
+        const uint32_t i0 = tiled ? (n >> 5) * (uint32_t)(KB >> 1) * 64 + (n & 31) * 2 + g : n * KB + g;
+        woff[t] = i0 * 16u;
+        soff[t] = i0 * 2u;
     }
+    const uint32_t wstep = tiled ? 1024u : 32u, sstep = tiled ? 128u : 4u;
 
     f32x16 acc[MT2][NT2];
 #pragma unroll
@@ -386,8 +402,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     auto issue = [&](int it, uint8_t* dst, u32x4* bwd, uint32_t* bsd) {
         const bool in = it < steps;
         const uint32_t ka = in ? (uint32_t)(step0 + it) * KS * 2 : 0x80000000u;
-        const uint32_t kw = in ? (uint32_t)(step0 + it) * 32 : 0x80000000u;
-        const uint32_t ks_ = in ? (uint32_t)(step0 + it) * 4 : 0x80000000u;
+        const uint32_t kw = in ? (uint32_t)(step0 + it) * wstep : 0x80000000u;
+        const uint32_t ks_ = in ? (uint32_t)(step0 + it) * sstep : 0x80000000u;
 #pragma unroll
         for (int i = 0; i < NLD; i++) buf_lds16(ra, aoff[i], ka, dst + (i * 4 + wave) * 1024);
 #pragma unroll
@@ -549,6 +565,17 @@ __device__ __forceinline__ int gate_up_row(int n, int N) {
     const int p = n >> 5, w = n & 31;
     return w < 16 ? 16 * p + w : (N >> 1) + 16 * p + (w - 16);
 }
+// dst = src in the tiled layout (one thread per 16-byte block and its scale)
+__global__ void k_tile_w4(const u32x4* __restrict__ sw, const f16* __restrict__ ss, u32x4* __restrict__ dw,
+                          f16* __restrict__ ds, int N, int KB) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)N * KB) return;
+    const size_t n = i / KB, b = i % KB;
+    const size_t o = ((n >> 5) * (size_t)(KB >> 1) + (b >> 1)) * 64 + (n & 31) * 2 + (b & 1);
+    dw[o] = sw[i];
+    ds[o] = ss[i];
+}
+
 __global__ void k_interleave_gate_up(const u32x4* __restrict__ sw, const f16* __restrict__ ss, u32x4* __restrict__ dw,
                                      f16* __restrict__ ds, int N, int KB) {
     const int n = blockIdx.x, src = gate_up_row(n, N);
@@ -578,7 +605,7 @@ __global__ void k_reduce_partials(const float* __restrict__ part, int ks, size_t
     }
 }
 
-typedef void (*GemmFn)(const f16*, const uint32_t*, const f16*, f16*, float*, int, int, int, int);
+typedef void (*GemmFn)(const f16*, const uint32_t*, const f16*, f16*, float*, int, int, int, int, int);
 struct Cfg {
     int mt, nt;
     bool exact;
@@ -674,20 +701,24 @@ namespace {
 // A GEMM launch; while Engine::profile times a step, the step's first GEMM records its own start
 // and end (see KernelEvents).
 void launch_gemm(GemmFn kern, dim3 grid, hipStream_t st, const f16* A, const uint32_t* W, const f16* S, f16* Y,
-                 float* part, int M, int N, int K, int ks) {
+                 float* part, int M, int N, int K, int ks, bool tiled) {
+    const int tl = tiled ? 1 : 0;
     KernelEvents* ke = kernel_events();
     if (ke && ke->launches == 0) {
-        hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, ks);
+        hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, ks, tl);
         ke->launches++;
     } else {
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks);
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks, tl);
     }
 }
 }  // namespace
 
+bool w4_tileable(int N, int K) { return N >= 32 && N % 32 == 0 && K >= 64 && K % 64 == 0; }
+
 void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part, int M, int N, int K, bool exact,
-             int ks, hipStream_t st, int cfg) {
+             int ks, hipStream_t st, int cfg, bool tiled) {
     SD_CHECK(M >= 1 && N >= 1 && K >= KSTEP && K % KSTEP == 0, "gemm_w4: need M, N >= 1 and K a multiple of 128");
+    SD_CHECK(!tiled || w4_tileable(N, K), "gemm_w4: the tiled layout needs N a multiple of 32");
     const int ci = cfg >= 0 ? cfg : pick_cfg(M, exact);
     SD_CHECK(ci < kNumCfgs, "gemm_w4: bad configuration index");
     const Cfg& c = kCfgs[ci];
@@ -697,19 +728,32 @@ void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part,
     SD_CHECK(!c.wide || (K / 64 / ks) % 4 == 0, "gemm_w4: this configuration needs K / ks a multiple of 256");
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
     dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, ks);
-    launch_gemm(part ? c.part_out : c.f16_out, grid, st, A, W, S, Y, part, M, N, K, ks);
+    launch_gemm(part ? c.part_out : c.f16_out, grid, st, A, W, S, Y, part, M, N, K, ks, tiled);
     launched("gemm_w4");
 }
 
 void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M, int N, int K, hipStream_t st,
-                  int cfg) {
+                  int cfg, bool tiled) {
     SD_CHECK(M >= 1 && N >= 32 && N % 32 == 0 && K % 256 == 0, "gemm_w4_silu: need N a multiple of 32, K of 256");
     SD_CHECK(cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg].silu_out, "gemm_w4_silu: not a 32x32-tile configuration");
     const Cfg& c = kCfgs[cfg];
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
     dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, 1);
-    launch_gemm(c.silu_out, grid, st, A, W, S, mid, (float*)nullptr, M, N, K, 1);
+    launch_gemm(c.silu_out, grid, st, A, W, S, mid, (float*)nullptr, M, N, K, 1, tiled);
     launched("gemm_w4_silu");
+}
+
+void tile_w4(uint32_t* W, f16* S, int N, int K, void* tmp, hipStream_t st) {
+    SD_CHECK(w4_tileable(N, K), "tile_w4: need N a multiple of 32 and K of 64");
+    const int KB = K / 32;
+    const size_t blocks = (size_t)N * KB;
+    u32x4* tw = static_cast<u32x4*>(tmp);
+    f16* ts = reinterpret_cast<f16*>(tw + blocks);
+    hipLaunchKernelGGL(k_tile_w4, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const u32x4*>(W), S, tw, ts, N, KB);
+    launched("tile_w4");
+    SD_HIP(hipMemcpyAsync(W, tw, blocks * 16, hipMemcpyDeviceToDevice, st));
+    SD_HIP(hipMemcpyAsync(S, ts, blocks * 2, hipMemcpyDeviceToDevice, st));
 }
 
 void interleave_gate_up(uint32_t* W, f16* S, int N, int K, void* tmp, hipStream_t st) {

@@ -59,11 +59,12 @@ def test_gemm_matches_oracle(sdamd, synth, oracle, M, N, K):
 
 
 def test_gemm_every_config(sdamd, synth, oracle):
-    """Each kernel configuration (tile shape, dequant mode) on ragged shapes."""
+    """Each kernel configuration (tile shape, dequant mode) on ragged shapes, in the plain weight
+    layout (N not a multiple of 32) and the tiled one (N = 352, 96: column tiles past N)."""
     rng = np.random.default_rng(5)
     cfg, ran = 0, 0
     while True:
-        for (M, N, K) in [(3, 100, 256), (37, 330, 640), (130, 72, 1024)]:
+        for (M, N, K) in [(3, 100, 256), (37, 330, 640), (130, 72, 1024), (37, 352, 640), (130, 96, 1024)]:
             A, W, S = gemm_case(synth, rng, M, N, K)
             for exact in (False, True):
                 try:
@@ -142,15 +143,19 @@ def test_gdn_matches_sequential_oracle(sdamd, oracle, L, H, load, negA, a_scale)
 
 def test_gemm_prepacked_weights(sdamd, synth):
     """sd_op_repack_w4 once + sd_op_matmul(packed=1) gives the very same output as the per-call
-    repack of sd_op_matmul(packed=0)."""
+    rewrite of sd_op_matmul(packed=0), for shapes with the tiled layout (N a multiple of 32) and
+    without it (N = 336 + 8)."""
     rng = np.random.default_rng(11)
-    for (M, N, K, exact) in [(96, 640, 1024, False), (512, 256, 2048, False), (7, 320, 512, True)]:
+    for (M, N, K, exact) in [(96, 640, 1024, False), (512, 256, 2048, False), (7, 320, 512, True),
+                             (40, 344, 512, False), (5, 344, 256, True)]:
         A, W, S = gemm_case(synth, rng, M, N, K)
         Y0 = run_gemm(sdamd, A, W, S, M, N, K, exact)
         dA, dW, dS = dev(A), dev(W), dev(S)
-        sdamd.op_repack_w4(dW.data_ptr(), N, K)
+        sdamd.op_repack_w4(dW.data_ptr(), dS.data_ptr(), N, K)
         dY = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
         sdamd.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, exact, -1, True)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(host(dY, np.float16, (M, N)), Y0)
         assert not np.array_equal(host(dW, np.uint32, W.shape), W)  # the words were rewritten
+        if N % 32 == 0:  # tiled: the scales moved too
+            assert not np.array_equal(host(dS, np.float16, S.shape), S)
