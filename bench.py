@@ -295,6 +295,13 @@ def kernel_bench(pkg, reps=50):
                                    "hbm_frac": round(wbytes / tot_us / 1e3 / PEAK_HBM, 4)}
         if M == 512:
             out["cfg1_fused_M512"] = {name: gemm(M, N, K) for name, N, K in fused}
+            # the vendor library's f16 GEMM (torch.matmul -> hipBLASLt) on the same shapes, with f16
+            # weights (4x the weight bytes, no dequant): what the hardware gives a plain GEMM here
+            for name, N, K in fused:
+                a16 = torch.randn(M, K, dtype=torch.float16, device="cuda")
+                b16 = torch.randn(N, K, dtype=torch.float16, device="cuda")
+                ms = _timed(lambda: torch.matmul(a16, b16.t()), reps)
+                out["cfg1_fused_M512"][name]["hipblaslt_f16_us"] = round(ms * 1e3, 2)
     # one gated delta net layer (prep + scan), T = 512, 16 heads, dk = dv = 128
     T, H, dk, dv = 512, 16, 128, 128
     C = 2 * H * dk + H * dv

@@ -47,6 +47,10 @@ __device__ __forceinline__ void split8(const float* v, f16x8& hi, f16x8& lo) {
     }
 }
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations but not for its global
+// loads in flight (__syncthreads waits for those too, which undoes a prefetch).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ f32x4 mma3(const f16x8& ah, const f16x8& al, const f16x8& bh, const f16x8& bl, f32x4 acc) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
@@ -586,25 +590,41 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
     }
     const int cfirst = seqt ? (int)(seqt[q] & 0xFFFFu) : 0;
     const int cend = seqt ? cfirst + (int)(seqt[q] >> 16) : (L + CH - 1) / CH;
-    for (int c = cfirst; c < cend; c++) {
-        const size_t slot = (size_t)c * H + h;
-        const f16* Wf = ws.wf + slot * WF_H;
-        const f16* Qgf = ws.qgf + slot * QGF_H;
-        const f16* Qkf = ws.qkf + slot * QKF_H;
-        const f16* Kgf = ws.kgf + slot * KGF_H;
-        const float* U = ws.u + slot * U_F;
-        const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
-        const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - c * CH);
+    // A chunk's operands (prep's output, not written here) are loaded ahead of their use: W, Qg and
+    // U of chunk c + 1 into a second register set when chunk c starts, its Qk and Kg once chunk c
+    // has used its own, so the load latency overlaps a chunk's MFMA work instead of following it.
+    struct WQ {
         f16x8 wh[4], wl[4], qh[4], ql[4];
+        float ur[4];
+    };
+    WQ set0, set1;
+    f16x8 kh[2][2], kl[2][2], qkh[2], qkl[2];
+    float gl = 0.f;
+    auto load_wq = [&](WQ& d, int c) {
+        const size_t slot = (size_t)c * H + h;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            get_frag(Wf, 4, wv, s, lane, wh[s], wl[s]);
-            get_frag(Qgf, 4, wv, s, lane, qh[s], ql[s]);
+            get_frag(ws.wf + slot * WF_H, 4, wv, s, lane, d.wh[s], d.wl[s]);
+            get_frag(ws.qgf + slot * QGF_H, 4, wv, s, lane, d.qh[s], d.ql[s]);
         }
-        float ur[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) ur[r] = U[(wv * 16 + fg * 4 + r) * DV + c0 + fr];
-        __syncthreads();  // St holds this chunk's starting state; Vt is free
+        for (int r = 0; r < 4; r++) d.ur[r] = ws.u[slot * U_F + (wv * 16 + fg * 4 + r) * DV + c0 + fr];
+    };
+    auto load_qk = [&](int c) {
+        const size_t slot = (size_t)c * H + h;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            get_frag(ws.qkf + slot * QKF_H, 2, wv, s, lane, qkh[s], qkl[s]);
+#pragma unroll
+            for (int q2 = 0; q2 < 2; q2++) get_frag(ws.kgf + slot * KGF_H, 2, wv * 2 + q2, s, lane, kh[q2][s], kl[q2][s]);
+        }
+        gl = ws.gl[slot];
+    };
+    auto chunk = [&](int c, const WQ& cur, WQ& nxt) {
+        if (c + 1 < cend) load_wq(nxt, c + 1);
+        const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
+        const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - c * CH);
+        lds_barrier();  // St holds this chunk's starting state; Vt is free
         f32x4 av = {0.f, 0.f, 0.f, 0.f}, ao = av;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
@@ -614,12 +634,12 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
             for (int u = 0; u < 8; u++) s8[u] = sp[u];
             f16x8 sh8, sl8;
             split8(s8, sh8, sl8);
-            av = mma3(wh[s], wl[s], sh8, sl8, av);
-            ao = mma3(qh[s], ql[s], sh8, sl8, ao);
+            av = mma3(cur.wh[s], cur.wl[s], sh8, sl8, av);
+            ao = mma3(cur.qh[s], cur.ql[s], sh8, sl8, ao);
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) Vt[fr * VP + wv * 16 + fg * 4 + r] = ur[r] - av[r];
-        __syncthreads();
+        for (int r = 0; r < 4; r++) Vt[fr * VP + wv * 16 + fg * 4 + r] = cur.ur[r] - av[r];
+        lds_barrier();
         // V'^T fragments (B operand), used by Qk V' and by the state update
         f16x8 vh[2], vl[2];
 #pragma unroll
@@ -631,34 +651,37 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
             split8(v8, vh[s], vl[s]);
         }
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            f16x8 ah, al;
-            get_frag(Qkf, 2, wv, s, lane, ah, al);
-            ao = mma3(ah, al, vh[s], vl[s], ao);
-        }
+        for (int s = 0; s < 2; s++) ao = mma3(qkh[s], qkl[s], vh[s], vl[s], ao);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int i = wv * 16 + fg * 4 + r;
             if (i < Lc) o[(size_t)(t0 + i) * sh.H * DV + h * DV + c0 + fr] = ao[r];
         }
         // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
-        const float gl = ws.gl[slot];
+        f32x4 as[2];
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int kt = wv * 2 + q;
-            f32x4 as = {0.f, 0.f, 0.f, 0.f};
+        for (int q2 = 0; q2 < 2; q2++) {
+            as[q2] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 2; s++) {
-                f16x8 ah, al;
-                get_frag(Kgf, 2, kt, s, lane, ah, al);
-                as = mma3(ah, al, vh[s], vl[s], as);
-            }
+            for (int s = 0; s < 2; s++) as[q2] = mma3(kh[q2][s], kl[q2][s], vh[s], vl[s], as[q2]);
+        }
+        const float g_c = gl;
+        if (c + 1 < cend) load_qk(c + 1);  // Qk, Kg, gl are consumed
+#pragma unroll
+        for (int q2 = 0; q2 < 2; q2++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int k = kt * 16 + fg * 4 + r;
-                St[fr * SP + k] = gl * St[fr * SP + k] + as[r];
+                const int k = (wv * 2 + q2) * 16 + fg * 4 + r;
+                St[fr * SP + k] = g_c * St[fr * SP + k] + as[q2][r];
             }
-        }
+    };
+    if (cfirst < cend) {
+        load_wq(set0, cfirst);
+        load_qk(cfirst);
+    }
+    for (int c = cfirst; c < cend; c += 2) {
+        chunk(c, set0, set1);
+        if (c + 1 < cend) chunk(c + 1, set1, set0);
     }
     if (seqt) return;  // several sequences: their final states are not kept
     __syncthreads();
