@@ -89,6 +89,8 @@ void interleave_gate_up(uint32_t* W, f16* S, int N, int K, void* tmp, hipStream_
 // (f16 dequant, a 32x32-tile configuration of gemm_w4_plan); N a multiple of 32, K of 256.
 void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M, int N, int K, hipStream_t st,
                   int cfg, bool tiled);
+// Whether configuration cfg has the SiLU * mul epilogue of gemm_w4_silu.
+bool gemm_w4_has_silu(int cfg);
 
 // ---- elementwise / norms (elem.hip) ----------------------------------------------------------
 void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f16* Bi, int d, int bits,

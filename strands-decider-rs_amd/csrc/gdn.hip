@@ -453,7 +453,8 @@ __device__ __forceinline__ float row_allsum16(float x) {
 // questions of an ask_all): the chunked form's fixed cost per 64-token chunk outweighs a few dozen
 // sequential steps.  Per token t and head h: qn = q rsqrt(q.q + 1e-6) / sqrt(dk), kn = k rsqrt(k.k
 // + 1e-6), beta = sigmoid(b), decay = exp(negA softplus(a + dt_bias)); per value column:
-// S *= decay; delta = (v - S^T kn) beta; S += kn delta; o = S^T qn.
+// S *= decay; delta = (v - S^T kn) beta; S += kn delta; o = S^T qn (evaluated as below, with both
+// column sums taken from the previous state).
 // Workgroup (head, 16 value columns, sequence): wave w owns columns 16 y + 4 w + l / 16 and lane l
 // state rows 8 (l % 16) .. + 7, so every reduction over a column's 128 rows is one DPP row.  The
 // state stays in registers.  The inputs of up to 64 tokens are staged in LDS by the whole
@@ -468,7 +469,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     constexpr int DK = 128, DV = 128;
     __shared__ float4 Qs[RTB][DK / 4], Ks[RTB][DK / 4];
     __shared__ float Vs[RTB][16];
-    __shared__ float Bt[RTB], Dc[RTB];  // beta and decay per token
+    __shared__ float Bt[RTB], Dc[RTB], KQ[RTB];  // beta, decay and kn . qn per token
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int h = blockIdx.x, H = gridDim.x, q = blockIdx.z;
     if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
@@ -490,60 +491,93 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     for (int tb = t0; tb < t1; tb += RTB) {
         const int nt = min(RTB, t1 - tb);
         __syncthreads();  // the previous block is consumed
-        // q and k of a token: 32 lanes x 4 values, normalised on the way into LDS (the sums of
-        // squares over the 32 lanes: a DPP row, then the other row of the 32)
-        for (int e0 = 0; e0 < nt * (DK / 4); e0 += 256) {
-            const int e = e0 + tid, tt = e / (DK / 4), j = e % (DK / 4);
-            const bool ok = e < nt * (DK / 4);
-            float4 q4 = {0.f, 0.f, 0.f, 0.f}, k4 = q4;
-            if (ok) {
+        // q and k of a token: one DPP row of 16 lanes x 8 values, normalised on the way into LDS
+        // (the sums over the row are one row_allsum16).  Every load of the block is issued before
+        // the first is used.
+        constexpr int NIT = RTB * 16 / 256;  // tokens per wave-pass: 16 per workgroup
+        float4 qr[NIT][2], kr[NIT][2];
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int e = it * 256 + tid, tt = e >> 4, j = e & 15;
+#pragma unroll
+            for (int u = 0; u < 2; u++) qr[it][u] = kr[it][u] = float4{0.f, 0.f, 0.f, 0.f};
+            if (tt < nt) {
                 const float* row = qkvc + (size_t)(tb + tt) * C;
-                q4 = *reinterpret_cast<const float4*>(row + h * DK + 4 * j);
-                k4 = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + 4 * j);
-            }
-            float sq = row_allsum16(q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w);
-            float sk = row_allsum16(k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w);
-            sq += __shfl_xor(sq, 16);
-            sk += __shfl_xor(sk, 16);
-            const float rq = 1.0f / sqrtf(sq + 1e-6f), rk = 1.0f / sqrtf(sk + 1e-6f);
-            if (ok) {
-                Qs[tt][j] = float4{q4.x * rq * qs, q4.y * rq * qs, q4.z * rq * qs, q4.w * rq * qs};
-                Ks[tt][j] = float4{k4.x * rk, k4.y * rk, k4.z * rk, k4.w * rk};
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    qr[it][u] = *reinterpret_cast<const float4*>(row + h * DK + 8 * j + 4 * u);
+                    kr[it][u] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + 8 * j + 4 * u);
+                }
             }
         }
-        for (int e = tid; e < nt * 16; e += 256) {
-            const int tt = e >> 4, j = e & 15;
-            Vs[tt][j] = qkvc[(size_t)(tb + tt) * C + 2 * sh.H * DK + h * DV + cb + j];
+        float vr[RTB * 16 / 256];
+#pragma unroll
+        for (int it = 0; it < RTB * 16 / 256; it++) {
+            const int e = it * 256 + tid, tt = e >> 4, j = e & 15;
+            vr[it] = tt < nt ? qkvc[(size_t)(tb + tt) * C + 2 * sh.H * DK + h * DV + cb + j] : 0.f;
+        }
+        float ga = 0.f, gb = 0.f;
+        if (tid < nt) {
+            ga = (float)big[(size_t)(tb + tid) * sh.stride + sh.a_off + h];
+            gb = (float)big[(size_t)(tb + tid) * sh.stride + sh.b_off + h];
+        }
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int e = it * 256 + tid, tt = e >> 4, j = e & 15;
+            float sq = 0.f, sk = 0.f, kq = 0.f;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float4 q4 = qr[it][u], k4 = kr[it][u];
+                sq += q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w;
+                sk += k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w;
+                kq += q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+            }
+            sq = row_allsum16(sq);
+            sk = row_allsum16(sk);
+            kq = row_allsum16(kq);
+            const float rq = 1.0f / sqrtf(sq + 1e-6f), rk = 1.0f / sqrtf(sk + 1e-6f);
+            if (tt < nt) {
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const float4 q4 = qr[it][u], k4 = kr[it][u];
+                    Qs[tt][2 * j + u] = float4{q4.x * rq * qs, q4.y * rq * qs, q4.z * rq * qs, q4.w * rq * qs};
+                    Ks[tt][2 * j + u] = float4{k4.x * rk, k4.y * rk, k4.z * rk, k4.w * rk};
+                }
+                if (j == 0) KQ[tt] = kq * rq * qs * rk;
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < RTB * 16 / 256; it++) {
+            const int e = it * 256 + tid;
+            if ((e >> 4) < nt) Vs[e >> 4][e & 15] = vr[it];
         }
         if (tid < nt) {
-            const float a = (float)big[(size_t)(tb + tid) * sh.stride + sh.a_off + h];
-            const float b = (float)big[(size_t)(tb + tid) * sh.stride + sh.b_off + h];
-            Bt[tid] = 1.0f / (1.0f + expf(-b));
-            const float x = a + db;
+            Bt[tid] = 1.0f / (1.0f + expf(-gb));
+            const float x = ga + db;
             const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
             Dc[tid] = expf(na * sp);
         }
         __syncthreads();
+        // Both column sums come from the previous state, so they are independent:
+        //   S_t = dc S + kn delta^T, delta = beta (v - dc S^T kn), o = S_t^T qn = dc S^T qn + (kn . qn) delta
         for (int tt = 0; tt < nt; tt++) {
             const float4 qa = Qs[tt][r0 / 4], qb = Qs[tt][r0 / 4 + 1];
             const float4 ka = Ks[tt][r0 / 4], kb = Ks[tt][r0 / 4 + 1];
             const float qn[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
             const float kn[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
             const float dc = Dc[tt];
-            float kv = 0.f;
+            float sk = 0.f, sq = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                S[i] *= dc;
-                kv += S[i] * kn[i];
+                sk += S[i] * kn[i];
+                sq += S[i] * qn[i];
             }
-            const float delta = (Vs[tt][cl] - row_allsum16(kv)) * Bt[tt];
-            float oc = 0.f;
+            sk = row_allsum16(sk);
+            sq = row_allsum16(sq);
+            const float delta = (Vs[tt][cl] - dc * sk) * Bt[tt];
+            const float oc = dc * sq + KQ[tt] * delta;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                S[i] += kn[i] * delta;
-                oc += S[i] * qn[i];
-            }
-            oc = row_allsum16(oc);
+            for (int i = 0; i < 8; i++) S[i] = dc * S[i] + kn[i] * delta;
             if ((lane & 15) == 0) o[(size_t)(tb + tt) * sh.H * DV + h * DV + col] = oc;
         }
     }

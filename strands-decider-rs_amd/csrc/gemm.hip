@@ -732,6 +732,8 @@ void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part,
     launched("gemm_w4");
 }
 
+bool gemm_w4_has_silu(int cfg) { return cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg].silu_out != nullptr; }
+
 void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M, int N, int K, hipStream_t st,
                   int cfg, bool tiled) {
     SD_CHECK(M >= 1 && N >= 32 && N % 32 == 0 && K % 256 == 0, "gemm_w4_silu: need N a multiple of 32, K of 256");
