@@ -71,7 +71,7 @@ __device__ __forceinline__ float wave_sum16(float v) {
 // v_mfma_f32_16x16x32_f16 over the 256 dims), the online softmax per query (column), then
 // O^T += V^T P^T (256 dims x 16 queries); with S^T in the MFMA output layout, P^T is already in
 // the B-operand layout (lane = query, 8 keys), and the V cache is stored transposed so V^T
-// fragments are contiguous.  P is split into f16 hi + lo (two MFMAs) so that the product keeps the
+// fragments are contiguous (the keys of a block are permuted so that they are 8 consecutive).  P is split into f16 hi + lo (two MFMAs) so that the product keeps the
 // reference's f32 P.V to about 22 bits.  With ks > 1 the workgroups along z also split the keys
 // and write unnormalised (acc, max, sum) for k_attn_combine.
 template <int HD>
@@ -113,6 +113,11 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
             for (int e = 0; e < 8; e++) qf[st][e] = (f16)((float)v[e] * scale);
         }
     }
+    // the output gates of this block's queries (dimension tid), loaded while the keys are processed
+    float gq[16];
+#pragma unroll
+    for (int q = 0; q < 16; q++)
+        gq[q] = ks == 1 && q < nq ? (float)big[(size_t)(t0 + q) * s.stride + h * 2 * HD + HD + tid] : 0.f;
     f32x4 acc[ND];
 #pragma unroll
     for (int dt = 0; dt < ND; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -121,18 +126,27 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     const f16* Vb = Vt + (size_t)kh * HD * s.ctx;
 
     for (int j0 = kbeg + wv * KB; j0 < kend; j0 += 4 * KB) {
-        // S^T for keys j0 .. j0+31: two 16-key tiles; lane (query fq) holds keys j0 + 16tt + 4fg + r
+        // Keys are ordered inside the 32-key block so that lane (query fq, group fg) ends up with the
+        // probabilities of keys j0 + 8fg .. +7: row i of S^T tile tt is key j0 + 8(i/4) + 4tt + i%4.
+        // Then the V^T fragment of lane (dim fq, group fg) is those 8 keys, one 16-byte load.  The
+        // V loads are issued with the K loads, ahead of the S MFMAs and the softmax.
+        f16x8 kf[2][NS], vf[ND];
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const int key = min(j0 + 8 * (fq >> 2) + 4 * tt + (fq & 3), kend - 1);
+            const f16* krow = Kb + (size_t)key * HD + fg * 8;
+#pragma unroll
+            for (int st = 0; st < NS; st++) kf[tt][st] = *reinterpret_cast<const f16x8*>(krow + st * 32);
+        }
+#pragma unroll
+        for (int dt = 0; dt < ND; dt++)
+            vf[dt] = *reinterpret_cast<const f16x8*>(Vb + (size_t)(dt * 16 + fq) * s.ctx + j0 + fg * 8);
         f32x4 st2[2];
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
-            const int key = min(j0 + tt * 16 + fq, kend - 1);
-            const f16* krow = Kb + (size_t)key * HD + fg * 8;
-            f16x8 kf[NS];
-#pragma unroll
-            for (int st = 0; st < NS; st++) kf[st] = *reinterpret_cast<const f16x8*>(krow + st * 32);
             f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int st = 0; st < NS; st++) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[st], qf[st], a, 0, 0, 0);
+            for (int st = 0; st < NS; st++) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][st], qf[st], a, 0, 0, 0);
             st2[tt] = a;
         }
         float sv[8];
@@ -141,7 +155,7 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         for (int tt = 0; tt < 2; tt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int j = j0 + tt * 16 + fg * 4 + r;
+                const int j = j0 + 8 * fg + 4 * tt + r;
                 const float v = (qok && j < kend && j <= qpos && (j < P || j >= qlo)) ? st2[tt][r] : -INFINITY;
                 sv[tt * 4 + r] = v;
                 tmax = fmaxf(tmax, v);
@@ -161,17 +175,13 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         }
         l_run = l_run * alpha + wave_sum16(psum);
         m_run = m_new;
-        // O^T += V^T P^T; A operand lane (dim 16dt + fq, group fg): keys j0 + 4fg .. +3, j0 + 16 + 4fg .. +3
+        // O^T += V^T P^T
 #pragma unroll
         for (int dt = 0; dt < ND; dt++) {
-            const f16* vrow = Vb + (size_t)(dt * 16 + fq) * s.ctx + j0 + fg * 4;
-            const f16x4 v0 = *reinterpret_cast<const f16x4*>(vrow);
-            const f16x4 v1 = *reinterpret_cast<const f16x4*>(vrow + 16);
-            const f16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
             f32x4 a = acc[dt];
             a[0] *= alpha, a[1] *= alpha, a[2] *= alpha, a[3] *= alpha;
-            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, a, 0, 0, 0);
-            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], ph, a, 0, 0, 0);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pl, a, 0, 0, 0);
         }
     }
     // merge the 4 waves: acc[dt][r] is O[query fq][dim 16dt + 4fg + r]
@@ -184,30 +194,50 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         Lm[wv][fq] = l_run;
     }
     __syncthreads();
-    const int d = tid;  // one output dimension per thread, all 16 queries
-    for (int q = 0; q < nq; q++) {
+    // per query (thread q): the merged max, the weight of each wave's state, the merged sum
+    __shared__ float Fw[16][4], Ml[16][2];
+    if (tid < nq) {
+        const int q = tid;
         float m = -INFINITY;
 #pragma unroll
         for (int w = 0; w < 4; w++)
             if (Lm[w][q] > 0.f) m = fmaxf(m, Mm[w][q]);
-        float l = 0.f, a = 0.f;
+        float l = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; w++)
-            if (Lm[w][q] > 0.f) {
-                const float f = expf(Mm[w][q] - m);
-                l += Lm[w][q] * f;
-                a += Om[w][q][d] * f;
-            }
+        for (int w = 0; w < 4; w++) {
+            const float f = Lm[w][q] > 0.f ? expf(Mm[w][q] - m) : 0.f;
+            l += Lm[w][q] * f;
+            Fw[q][w] = f;
+        }
+        Ml[q][0] = m;
+        Ml[q][1] = l;
+    }
+    __syncthreads();
+    const int d = tid;  // one output dimension per thread, all 16 queries
+    // every LDS read first, then the stores (a store through a generic pointer keeps the compiler
+    // from moving LDS reads past it)
+    float av[16], ml[16][2];
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        float a = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) a += Om[w][q][d] * Fw[q][w];
+        av[q] = a;
+        ml[q][0] = Ml[q][0];
+        ml[q][1] = Ml[q][1];
+    }
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        if (q >= nq) continue;
         const int t = t0 + q;
         if (ks == 1) {
-            const float g = (float)big[(size_t)t * s.stride + h * 2 * HD + HD + d];
-            out[(size_t)t * s.HQ * HD + h * HD + d] = (f16)(a / l / (1.0f + expf(-g)));
+            out[(size_t)t * s.HQ * HD + h * HD + d] = (f16)(av[q] / ml[q][1] / (1.0f + expf(-gq[q])));
         } else {
             const size_t r = ((size_t)z * L + t) * s.HQ + h;
-            pacc[r * HD + d] = a;
+            pacc[r * HD + d] = av[q];
             if (d == 0) {
-                pml[r * 2] = m;
-                pml[r * 2 + 1] = l;
+                pml[r * 2] = ml[q][0];
+                pml[r * 2 + 1] = ml[q][1];
             }
         }
     }
