@@ -43,41 +43,71 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
                                                   const float* __restrict__ w, const uint32_t* __restrict__ rows,
                                                   f16* __restrict__ h16, float* __restrict__ h32) {
     constexpr int d = D * 256;
+    // D % 4 == 0: thread t takes the D consecutive elements [D t, D t + D) with 16-byte accesses;
+    // otherwise element c = t + 256 i
+    constexpr bool VEC = D % 4 == 0;
     __shared__ float red[4];
     const int r = blockIdx.x;
     const size_t row = rows ? rows[r] : (size_t)r;
     float* xr = x + row * d;
+    auto col = [&](int i) { return VEC ? (int)threadIdx.x * D + i : (int)threadIdx.x + 256 * i; };
     float v[D];
     float part[D][KS > 0 ? KS : 1];
     // issue every load of the row before using any
+    if constexpr (VEC) {
 #pragma unroll
-    for (int i = 0; i < D; i++) {
-        const int c = threadIdx.x + 256 * i;
-        v[i] = xr[c];
-        if constexpr (KS > 0) {
+        for (int i = 0; i < D; i += 4) {
+            const int c = col(i);
+            const float4 x4 = *reinterpret_cast<const float4*>(xr + c);
+            v[i] = x4.x, v[i + 1] = x4.y, v[i + 2] = x4.z, v[i + 3] = x4.w;
+            if constexpr (KS > 0) {
 #pragma unroll
-            for (int z = 0; z < KS; z++) part[i][z] = yp[z * slot + row * d + c];
-        } else {
-            part[i][0] = y ? (float)y[row * d + c] : 0.f;
+                for (int z = 0; z < KS; z++) {
+                    const float4 p4 = *reinterpret_cast<const float4*>(yp + z * slot + row * d + c);
+                    part[i][z] = p4.x, part[i + 1][z] = p4.y, part[i + 2][z] = p4.z, part[i + 3][z] = p4.w;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; u++) part[i + u][0] = y ? (float)y[row * d + c + u] : 0.f;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            const int c = col(i);
+            v[i] = xr[c];
+            if constexpr (KS > 0) {
+#pragma unroll
+                for (int z = 0; z < KS; z++) part[i][z] = yp[z * slot + row * d + c];
+            } else {
+                part[i][0] = y ? (float)y[row * d + c] : 0.f;
+            }
         }
     }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < D; i++) {
-        const int c = threadIdx.x + 256 * i;
         float a = v[i];
         if constexpr (KS > 0) {
             float s = part[i][0];
 #pragma unroll
             for (int z = 1; z < KS; z++) s += part[i][z];
             a += (float)(f16)s;
-            xr[c] = a;
         } else if (y) {
             a += part[i][0];
-            xr[c] = a;
         }
         v[i] = a;
         ss += a * a;
+    }
+    if (KS > 0 || y) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < D; i += 4)
+                *reinterpret_cast<float4*>(xr + col(i)) = float4{v[i], v[i + 1], v[i + 2], v[i + 3]};
+        } else {
+#pragma unroll
+            for (int i = 0; i < D; i++) xr[col(i)] = v[i];
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
@@ -85,12 +115,28 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
     __syncthreads();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / sqrtf(tot / (float)d + 1e-6f);
+    if constexpr (VEC) {
 #pragma unroll
-    for (int i = 0; i < D; i++) {
-        const int c = threadIdx.x + 256 * i;
-        const float o = v[i] * inv * w[c];
-        if (h16) h16[(size_t)r * d + c] = (f16)o;
-        else h32[(size_t)r * d + c] = o;
+        for (int i = 0; i < D; i += 4) {
+            const int c = col(i);
+            const float4 w4 = *reinterpret_cast<const float4*>(w + c);
+            const float o0 = v[i] * inv * w4.x, o1 = v[i + 1] * inv * w4.y, o2 = v[i + 2] * inv * w4.z,
+                        o3 = v[i + 3] * inv * w4.w;
+            if (h16) {
+                const f16x4 o4 = {(f16)o0, (f16)o1, (f16)o2, (f16)o3};
+                *reinterpret_cast<f16x4*>(h16 + (size_t)r * d + c) = o4;
+            } else {
+                *reinterpret_cast<float4*>(h32 + (size_t)r * d + c) = float4{o0, o1, o2, o3};
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            const int c = col(i);
+            const float o = v[i] * inv * w[c];
+            if (h16) h16[(size_t)r * d + c] = (f16)o;
+            else h32[(size_t)r * d + c] = o;
+        }
     }
 }
 
