@@ -114,7 +114,10 @@ const float* Engine::f32(const std::string& name, size_t count) const {
     const TensorRef& t = tensor(name);
     SD_CHECK(t.bytes >= count * 4, name + ": expected at least " + std::to_string(count) + " f32 values");
     const void* p = dptr(name);
-    SD_CHECK(reinterpret_cast<uintptr_t>(p) % 4 == 0, name + " is not 4-byte aligned");
+    // the kernels read f32 vectors 16 bytes at a time; the model format places every tensor at a
+    // multiple of 256 bytes (the reference binds each one as a storage-buffer slice,
+    // src/engine.rs:325-357, whose offsets must be 256-aligned)
+    SD_CHECK(reinterpret_cast<uintptr_t>(p) % 16 == 0, name + " is not 16-byte aligned");
     return static_cast<const float*>(p);
 }
 

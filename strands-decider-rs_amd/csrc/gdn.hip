@@ -77,20 +77,33 @@ __device__ __forceinline__ void get_frag(const f16* base, int KS, int rt, int s,
 // With several sequences, row t is index i of the sequence starting at row s0.
 __global__ void k_conv(const f16* __restrict__ big, int stride, int L, int C, const float* __restrict__ w,
                        const f16* __restrict__ hist, float* __restrict__ out, const uint32_t* __restrict__ rowt) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    // 4 consecutive channels per thread (C % 4 == 0, checked by the launcher): 8-byte row loads,
+    // 16-byte weight loads and stores
+    const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
     const int t = blockIdx.y;
     if (c >= C || t >= L) return;
     const int i = rowt ? (int)(rowt[t] & 0xFFFFu) : t;
     const int s0 = rowt ? (int)(rowt[t] >> 16) : 0;
-    const float kk[4] = {w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
-    float s = 0.f;
+    float4 kk[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) kk[u] = *reinterpret_cast<const float4*>(w + 4 * (c + u));
+    f16x4 xs[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int tt = i + j - 3;
-        const float x = tt >= 0 ? (float)big[(size_t)(s0 + tt) * stride + c] : (float)hist[(size_t)(tt + 3) * C + c];
-        s += kk[j] * x;
+        xs[j] = tt >= 0 ? *reinterpret_cast<const f16x4*>(big + (size_t)(s0 + tt) * stride + c)
+                        : *reinterpret_cast<const f16x4*>(hist + (size_t)(tt + 3) * C + c);
     }
-    out[(size_t)t * C + c] = s / (1.0f + expf(-s));
+    float r[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const float kj[4] = {kk[u].x, kk[u].y, kk[u].z, kk[u].w};
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) s += kj[j] * (float)xs[j][u];
+        r[u] = s / (1.0f + expf(-s));
+    }
+    *reinterpret_cast<float4*>(out + (size_t)t * C + c) = float4{r[0], r[1], r[2], r[3]};
 }
 
 // Workspace slot sizes (halves / floats) per (chunk, head).
@@ -733,16 +746,18 @@ __global__ __launch_bounds__(256) void k_gnorm(const float* __restrict__ o, cons
     const int lane = threadIdx.x & 63;
     if (row >= L * sh.H) return;
     const int t = row / sh.H, h = row % sh.H;
-    const size_t b = (size_t)t * sh.H * sh.DV + h * sh.DV;
-    const float v0 = o[b + lane], v1 = o[b + 64 + lane];
-    float ss = v0 * v0 + v1 * v1;
+    // lane: the two consecutive values 2 lane, 2 lane + 1 (8- and 4-byte accesses)
+    const size_t b = (size_t)t * sh.H * sh.DV + h * sh.DV + 2 * lane;
+    const float2 v = *reinterpret_cast<const float2*>(o + b);
+    float ss = v.x * v.x + v.y * v.y;
 #pragma unroll
     for (int s = 32; s > 0; s >>= 1) ss += __shfl_xor(ss, s);
     const float inv = 1.0f / sqrtf(ss / (float)sh.DV + 1e-6f);
-    const f16* zr = big + (size_t)t * sh.stride + sh.z_off + h * sh.DV;
-    const float z0 = (float)zr[lane], z1 = (float)zr[64 + lane];
-    out[b + lane] = (f16)(w[lane] * v0 * inv * z0 / (1.0f + expf(-z0)));
-    out[b + 64 + lane] = (f16)(w[64 + lane] * v1 * inv * z1 / (1.0f + expf(-z1)));
+    const f16x2 z = *reinterpret_cast<const f16x2*>(big + (size_t)t * sh.stride + sh.z_off + h * sh.DV + 2 * lane);
+    const float2 w2 = *reinterpret_cast<const float2*>(w + 2 * lane);
+    const float z0 = (float)z[0], z1 = (float)z[1];
+    const f16x2 r = {(f16)(w2.x * v.x * inv * z0 / (1.0f + expf(-z0))), (f16)(w2.y * v.y * inv * z1 / (1.0f + expf(-z1)))};
+    *reinterpret_cast<f16x2*>(out + b) = r;
 }
 
 }  // namespace
@@ -766,7 +781,8 @@ void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws) {
 
 void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out, const Segs& sg,
                hipStream_t st) {
-    hipLaunchKernelGGL(k_conv, dim3((C + 255) / 256, L), dim3(256), 0, st, big, stride, L, C, w, hist, out, sg.row);
+    SD_CHECK(C % 4 == 0 && stride % 4 == 0, "conv: channels and row stride must be multiples of 4");
+    hipLaunchKernelGGL(k_conv, dim3((C / 4 + 255) / 256, L), dim3(256), 0, st, big, stride, L, C, w, hist, out, sg.row);
     launched("conv");
 }
 
@@ -802,6 +818,7 @@ void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float
 
 void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st) {
     SD_CHECK(s.DV == 128, "gnorm: only 128-wide value heads are supported");
+    SD_CHECK(s.stride % 2 == 0 && s.z_off % 2 == 0, "gnorm: gate row stride and offset must be even");
     const int rows = L * s.H;
     hipLaunchKernelGGL(k_gnorm, dim3((rows + 3) / 4), dim3(256), 0, st, o, big, s, w, L, out);
     launched("gnorm");
