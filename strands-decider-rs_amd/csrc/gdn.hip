@@ -127,7 +127,8 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     __shared__ __attribute__((aligned(16))) uint8_t R2[2 * DK * TP * 2];
     __shared__ __attribute__((aligned(16))) f16 KT[2][DK * TP];
     __shared__ __attribute__((aligned(16))) float Ts[CH * FP];
-    __shared__ float Xs[4][16][17], Ys[4][16][17];
+    __shared__ float Xs[4][16][17];
+    __shared__ float Nb[6][16][17];  // the off-diagonal 16 x 16 blocks of A, (p, r) at p (p - 1) / 2 + r
     __shared__ float beta[CH], G[CH], eG[CH], eL[CH];
     f16* Kh = reinterpret_cast<f16*>(R1);
     f16* Kl = Kh + CH * RP;
@@ -308,67 +309,58 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
         }
     }
 
-    // ---- phase 2: T = (I - A)^-1 in place (Ts holds I + A, A strictly lower).
-    // Diagonal blocks: wave w turns block w (I + N) into (I+N)(I+N^2)(I+N^4)(I+N^8).
+    // ---- phase 2: T = (I - A)^-1 in place (Ts holds I + A, A strictly lower), in 16 x 16 blocks.
+    // Diagonal block b (wave b): forward substitution, lane j < 16 holding column j of
+    // T_bb = (I - A_bb)^-1 in registers: T[i][j] = delta_ij + sum_{k<i} A[i][k] T[k][j].
+    // The off-diagonal blocks of A are copied aside first, since T_pq overwrites A_pq.
     {
-        float(&Mb)[16][17] = Xs[wv];
-        float(&Pb)[16][17] = Ys[wv];
         const int base = wv * 16;
-        for (int e = lane; e < 256; e += 64) {
-            const int a = e >> 4, b = e & 15;
-            Mb[a][b] = a > b ? Ts[(base + a) * FP + base + b] : 0.f;
-            Pb[a][b] = Ts[(base + a) * FP + base + b];
+        for (int e = tid; e < 6 * 256; e += 256) {
+            const int blk = e >> 8, a = (e >> 4) & 15, b = e & 15;
+            const int p = blk == 0 ? 1 : (blk < 3 ? 2 : 3), r = blk - p * (p - 1) / 2;
+            Nb[blk][a][b] = Ts[(16 * p + a) * FP + 16 * r + b];
         }
-        __syncthreads();
-        const int a = lane >> 2, b0 = (lane & 3) * 4;
-        for (int step = 0; step < 3; step++) {
-            float m2[4] = {0.f, 0.f, 0.f, 0.f};
+        if (lane < 16) {
+            float x[16];
 #pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float x = Mb[a][k];
+            for (int i = 0; i < 16; i++) {
+                float acc = i == lane ? 1.f : 0.f;
 #pragma unroll
-                for (int u = 0; u < 4; u++) m2[u] += x * Mb[k][b0 + u];
+                for (int k = 0; k < i; k++) acc += Ts[(base + i) * FP + base + k] * x[k];
+                x[i] = acc;
             }
-            __syncthreads();
 #pragma unroll
-            for (int u = 0; u < 4; u++) Mb[a][b0 + u] = m2[u];
-            __syncthreads();
-            float pn[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) pn[u] = Pb[a][b0 + u];
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float x = Pb[a][k];
-#pragma unroll
-                for (int u = 0; u < 4; u++) pn[u] += x * Mb[k][b0 + u];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int u = 0; u < 4; u++) Pb[a][b0 + u] = pn[u];
-            __syncthreads();
+            for (int i = 0; i < 16; i++) Ts[(base + i) * FP + base + lane] = x[i];
         }
-        for (int e = lane; e < 256; e += 64) Ts[(base + (e >> 4)) * FP + base + (e & 15)] = Pb[e >> 4][e & 15];
         __syncthreads();
     }
-    // Block rows p = 1..3: X_q = sum_{r=q}^{p-1} A_pr T_rq for every q < p at once, then
-    // T_pq = T_pp X_q (A_pq is overwritten only after every X of the row is formed).
-    for (int p = 1; p < 4; p++) {
-        const int nq = p;  // blocks q = 0..p-1
-        for (int e = tid; e < nq * 256; e += 256) {
-            const int q = e >> 8, a = (e >> 4) & 15, b = e & 15;
-            float x = 0.f;
-            for (int r = q; r < p; r++)
+    // Off-diagonal blocks: column block q by wave q, block rows p = q+1..3 in order (no workgroup
+    // barrier: a wave reads only the final diagonal blocks, the copied A blocks and its own column):
+    // T_pq = T_pp X, X = sum_{r=q}^{p-1} A_pr T_rq, each 16 x 16 x 16 product as 4 f32 MFMAs
+    // (v_mfma_f32_16x16x4_f32: lane l holds A[l % 16][k0 + l / 16], B[k0 + l / 16][l % 16] and
+    // D[4 (l / 16) + r][l % 16]).  X passes through the wave's own LDS block to become an operand.
+    {
+        const int q = wv, lr = lane & 15, lg = lane >> 4;
+        float(&Xw)[16][17] = Xs[wv];
+        for (int p = q + 1; p < 4; p++) {
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            for (int r = q; r < p; r++) {
+                const int blk = p * (p - 1) / 2 + r;
 #pragma unroll
-                for (int k = 0; k < 16; k++) x += Ts[(16 * p + a) * FP + 16 * r + k] * Ts[(16 * r + k) * FP + 16 * q + b];
-            Xs[q][a][b] = x;
-        }
-        __syncthreads();
-        for (int e = tid; e < nq * 256; e += 256) {
-            const int q = e >> 8, a = (e >> 4) & 15, b = e & 15;
-            float y = 0.f;
+                for (int k0 = 0; k0 < 16; k0 += 4)
+                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(Nb[blk][lr][k0 + lg], Ts[(16 * r + k0 + lg) * FP + 16 * q + lr],
+                                                             x, 0, 0, 0);
+            }
 #pragma unroll
-            for (int k = 0; k < 16; k++) y += Ts[(16 * p + a) * FP + 16 * p + k] * Xs[q][k][b];
-            Ts[(16 * p + a) * FP + 16 * q + b] = y;
+            for (int rr = 0; rr < 4; rr++) Xw[4 * lg + rr][lr] = x[rr];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's writes land before its reads
+            f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k0 = 0; k0 < 16; k0 += 4)
+                y = __builtin_amdgcn_mfma_f32_16x16x4f32(Ts[(16 * p + lr) * FP + 16 * p + k0 + lg], Xw[k0 + lg][lr], y, 0, 0, 0);
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) Ts[(16 * p + 4 * lg + rr) * FP + 16 * q + lr] = y[rr];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // X is read before the next p writes it
         }
         __syncthreads();
     }
