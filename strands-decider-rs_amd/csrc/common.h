@@ -111,6 +111,14 @@ void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* row
 void silu_mul(const f16* big, const float* part, int ks, int L, int I, bool il, f16* mid, hipStream_t st);
 void add_bias(f16* y, int L, int N, const float* c, hipStream_t st);
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);
+// Several strided device copies in one launch: rows x row_bytes from src (rows src_pitch apart) to
+// dst (rows dst_pitch apart).  Pointers, pitches and row_bytes must be multiples of 16 bytes.
+struct CopyDesc {
+    const uint8_t* src;
+    uint8_t* dst;
+    uint64_t rows, row_bytes, src_pitch, dst_pitch;
+};
+void copy_batch(const CopyDesc* d, size_t n, hipStream_t st);
 
 // ---- gated delta net (gdn.hip) ---------------------------------------------------------------
 // Several independent token sequences in one forward (the questions of an ask_all, each continuing

@@ -1,5 +1,7 @@
 // Row-wise and elementwise kernels: embedding gather, residual add + RMSNorm, SiLU gate,
 // adapter bias, and a fill used instead of hipMemsetAsync (safe inside captured graphs).
+#include <algorithm>
+
 #include "common.h"
 
 namespace sd {
@@ -249,6 +251,42 @@ void add_bias(f16* y, int L, int N, const float* c, hipStream_t st) {
     const size_t n = (size_t)L * N;
     hipLaunchKernelGGL(k_add_bias, dim3((n + 255) / 256), dim3(256), 0, st, y, n, N, c);
     launched("add_bias");
+}
+
+namespace {
+constexpr int kCopyBatch = 32;
+struct CopyArgs {
+    CopyDesc d[kCopyBatch];
+};
+// Descriptor blockIdx.y; the workgroups along x stride over its 16-byte chunks.
+__global__ __launch_bounds__(256) void k_copy_batch(CopyArgs a) {
+    const CopyDesc& d = a.d[blockIdx.y];
+    const uint32_t per_row = (uint32_t)(d.row_bytes / 16);
+    const uint64_t total = d.rows * per_row;
+    for (uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (uint64_t)gridDim.x * 256) {
+        const uint64_t r = c / per_row, o = (c % per_row) * 16;
+        *reinterpret_cast<uint4*>(d.dst + r * d.dst_pitch + o) = *reinterpret_cast<const uint4*>(d.src + r * d.src_pitch + o);
+    }
+}
+}  // namespace
+
+void copy_batch(const CopyDesc* d, size_t n, hipStream_t st) {
+    for (size_t i0 = 0; i0 < n; i0 += kCopyBatch) {
+        const size_t m = std::min<size_t>(kCopyBatch, n - i0);
+        CopyArgs a{};
+        uint64_t most = 0;
+        for (size_t i = 0; i < m; i++) {
+            const CopyDesc& c = d[i0 + i];
+            SD_CHECK(((uintptr_t)c.src | (uintptr_t)c.dst | c.row_bytes | c.src_pitch | c.dst_pitch) % 16 == 0,
+                     "copy_batch: addresses, pitches and row sizes must be multiples of 16 bytes");
+            a.d[i] = c;
+            most = std::max(most, c.rows * c.row_bytes / 16);
+        }
+        if (most == 0) continue;
+        const unsigned gx = (unsigned)std::min<uint64_t>((most + 255) / 256, 512);
+        hipLaunchKernelGGL(k_copy_batch, dim3(gx, (unsigned)m), dim3(256), 0, st, a);
+        launched("copy_batch");
+    }
 }
 
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st) {

@@ -54,6 +54,36 @@ Engine::~Engine() {
     if (head_dev) (void)hipFree(head_dev);
     if (hb.dev) (void)hipFree(hb.dev);
     if (hb.host) (void)hipHostFree(hb.host);
+    for (auto& b : snap_pool) (void)hipFree(b.first);
+}
+
+void* Engine::snap_alloc(size_t bytes) {
+    {
+        std::lock_guard<std::mutex> lock(snap_mu);
+        size_t best = snap_pool.size();
+        for (size_t i = 0; i < snap_pool.size(); i++)
+            if (snap_pool[i].second >= bytes && snap_pool[i].second <= 2 * bytes &&
+                (best == snap_pool.size() || snap_pool[i].second < snap_pool[best].second))
+                best = i;
+        if (best < snap_pool.size()) {
+            void* p = snap_pool[best].first;
+            snap_pool.erase(snap_pool.begin() + best);
+            return p;
+        }
+    }
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) throw Error(std::string("snapshot allocation: ") + hipGetErrorString(e));
+    return p;
+}
+
+void Engine::snap_release(void* p, size_t bytes) const {
+    std::lock_guard<std::mutex> lock(snap_mu);
+    if (snap_pool.size() < 4) {
+        snap_pool.emplace_back(p, bytes);
+        return;
+    }
+    (void)hipFree(p);
 }
 
 void Plan::destroy() {
@@ -605,19 +635,23 @@ void Engine::upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_
 // only, so after one restore the prefix stays valid for every later question).
 void Engine::restore(const Snapshot* cache, size_t P) {
     if (cache) {
-        SD_HIP(hipMemcpyAsync(arena, cache->arena, arena_bytes, hipMemcpyDeviceToDevice, st));
+        std::vector<CopyDesc> cp;
+        cp.push_back(CopyDesc{static_cast<const uint8_t*>(cache->arena), arena, 1, arena_bytes, arena_bytes, arena_bytes});
         if (kv_owner != cache->id) {
-            // K rows [hk][t][hd]; V transposed [hk][hd][t] (the attention kernel's layout)
-            const size_t row = (size_t)cfg.hd * 2;
+            // K rows [hk][t][hd]; V transposed [hk][hd][t] (the attention kernel's layout).  The V
+            // rows carry P8 keys: the live rows P..P8-1 are rewritten by the forward before any
+            // read (a forward writes rows >= P of its own ids first)
+            const size_t row = (size_t)cfg.hd * 2, P8 = (P + 7) & ~size_t(7);
             for (size_t a = 0; a < attn_layers.size(); a++) {
                 const LayerW& W = layers[attn_layers[a]];
-                const uint8_t* ks = cache->kv(a, 0), *vs = cache->kv(a, 1);
-                SD_HIP(hipMemcpy2DAsync(W.kc, SD_CONTEXT * row, ks, P * row, P * row, cfg.hk, hipMemcpyDeviceToDevice, st));
-                SD_HIP(hipMemcpy2DAsync(W.vc, SD_CONTEXT * 2, vs, P * 2, P * 2, (size_t)cfg.hk * cfg.hd,
-                                        hipMemcpyDeviceToDevice, st));
+                cp.push_back(CopyDesc{cache->kv(a, 0), reinterpret_cast<uint8_t*>(W.kc), (uint64_t)cfg.hk, P * row, P * row,
+                                      SD_CONTEXT * row});
+                cp.push_back(CopyDesc{cache->kv(a, 1), reinterpret_cast<uint8_t*>(W.vc), (uint64_t)cfg.hk * cfg.hd, P8 * 2,
+                                      P8 * 2, SD_CONTEXT * 2});
             }
             kv_owner = cache->id;
         }
+        copy_batch(cp.data(), cp.size(), st);
     } else {
         fill_u32(reinterpret_cast<uint32_t*>(arena + arena_state_bytes), (arena_bytes - arena_state_bytes) / 4, 0u, st);
         kv_owner = 0;
@@ -682,22 +716,29 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
         snap->engine = this;
         snap->len = T;
         snap->id = ++snapshot_ids;
-        snap->kv_stride = (size_t)cfg.hk * T * cfg.hd * 2;
+        const size_t T8 = (T + 7) & ~size_t(7);
+        snap->kv_stride = (size_t)cfg.hk * T8 * cfg.hd * 2;
         snap->arena_bytes = arena_bytes;
-        const size_t bytes = arena_bytes + attn_layers.size() * 2 * snap->kv_stride;
-        const hipError_t e = hipMalloc(&snap->arena, bytes);
-        if (e != hipSuccess) {
+        snap->alloc_bytes = arena_bytes + attn_layers.size() * 2 * snap->kv_stride;
+        try {
+            snap->arena = snap_alloc(snap->alloc_bytes);
+        } catch (...) {
             delete snap;
-            throw Error(std::string("snapshot allocation: ") + hipGetErrorString(e));
+            throw;
         }
-        SD_HIP(hipMemcpyAsync(snap->arena, arena, arena_bytes, hipMemcpyDeviceToDevice, st));
+        // the arena image, then K rows [hk][T][hd] and V [hk][hd][T8] (V rows rounded up to 8 keys so
+        // that every copy moves whole 16-byte chunks; the keys past T are not read back)
+        std::vector<CopyDesc> cp;
+        cp.push_back(CopyDesc{arena, static_cast<uint8_t*>(snap->arena), 1, arena_bytes, arena_bytes, arena_bytes});
         const size_t row = (size_t)cfg.hd * 2;
         for (size_t a = 0; a < attn_layers.size(); a++) {
             const LayerW& W = layers[attn_layers[a]];
-            SD_HIP(hipMemcpy2DAsync(snap->kv(a, 0), T * row, W.kc, SD_CONTEXT * row, T * row, cfg.hk, hipMemcpyDeviceToDevice, st));
-            SD_HIP(hipMemcpy2DAsync(snap->kv(a, 1), T * 2, W.vc, SD_CONTEXT * 2, T * 2, (size_t)cfg.hk * cfg.hd,
-                                    hipMemcpyDeviceToDevice, st));
+            cp.push_back(CopyDesc{reinterpret_cast<const uint8_t*>(W.kc), snap->kv(a, 0), (uint64_t)cfg.hk, T * row,
+                                  SD_CONTEXT * row, T * row});
+            cp.push_back(CopyDesc{reinterpret_cast<const uint8_t*>(W.vc), snap->kv(a, 1), (uint64_t)cfg.hk * cfg.hd, T8 * 2,
+                                  SD_CONTEXT * 2, T8 * 2});
         }
+        copy_batch(cp.data(), cp.size(), st);
         kv_owner = snap->id;
     }
     const hipError_t se = hipStreamSynchronize(st);
@@ -917,7 +958,9 @@ std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids,
 }
 
 Snapshot::~Snapshot() {
-    if (arena) (void)hipFree(arena);
+    if (!arena) return;
+    if (engine) engine->snap_release(arena, alloc_bytes);
+    else (void)hipFree(arena);
 }
 
 }  // namespace sd

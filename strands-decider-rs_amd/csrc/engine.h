@@ -4,6 +4,7 @@
 
 #include <functional>
 #include <map>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <utility>
@@ -100,8 +101,9 @@ struct Snapshot {
     const Engine* engine = nullptr;
     size_t len = 0;
     uint64_t id = 0;
-    void* arena = nullptr;
-    size_t arena_bytes = 0, kv_stride = 0;
+    void* arena = nullptr;  // [arena image | per attention layer: K [hk][len][hd], V [hk][hd][len8]]
+    size_t alloc_bytes = 0;
+    size_t arena_bytes = 0, kv_stride = 0;  // kv_stride: hk * len8 * hd * 2, len8 = len rounded up to 8
     uint8_t* kv(size_t attn_index, int which) const {
         return static_cast<uint8_t*>(arena) + arena_bytes + (attn_index * 2 + which) * kv_stride;
     }
@@ -131,6 +133,12 @@ struct Engine {
     int n_linear = 0;
     int max_n = 0;
     uint64_t snapshot_ids = 0, kv_owner = 0;
+    // Freed snapshot buffers kept for reuse (a snapshot is made by every keep-forward; hipMalloc and
+    // hipFree would each cost more than its copies).  A snapshot may be freed from another thread.
+    mutable std::mutex snap_mu;
+    mutable std::vector<std::pair<void*, size_t>> snap_pool;
+    void* snap_alloc(size_t bytes);
+    void snap_release(void* p, size_t bytes) const;
     bool use_graphs = true;
     bool gu_il = false;  // gate_up weights interleaved in groups of 16 rows (interleave_gate_up)
     Pool pool;
