@@ -388,8 +388,6 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         rope = static_cast<float*>(dalloc(table.size() * 4));
         SD_HIP(hipMemcpy(rope, table.data(), table.size() * 4, hipMemcpyHostToDevice));
     }
-    lu = static_cast<uint32_t*>(dalloc(32));
-    lu_h = static_cast<uint32_t*>(halloc(32));
     use_graphs = !env_off("SD_GRAPHS");
     for (const LayerW& L : layers) {
         if (L.kind == SD_LINEAR_ATTENTION) max_n = std::max(max_n, L.in_proj.N);
@@ -414,9 +412,16 @@ void Engine::ensure_pool(int l) {
     const size_t ypart = (size_t)8 * cap * cfg.d;
     // gate_up partials: 8 slots for short inputs, fewer for long ones (whose grids need no split)
     const size_t gpart = (size_t)(cap <= 256 ? 8 : 1) * cap * 2 * cfg.inter;
+    // the upload block: lu, ids, rows, Segs row / chunk / sequence tables
+    Pool up;
+    up.off_ids = 256;
+    up.off_rows = up.off_ids + align256((size_t)cap * 4);
+    up.off_seg_row = up.off_rows + align256((size_t)cap * 4);
+    up.off_seg_chunk = up.off_seg_row + align256((size_t)cap * 4);
+    up.off_seg_seq = up.off_seg_chunk + align256((size_t)(cap / 64 + SD_MAX_SEQS) * 4);
+    up.up_bytes = up.off_seg_seq + align256((size_t)SD_MAX_SEQS * 4);
     const size_t sizes[] = {
-        (size_t)cap * 4,                               // ids
-        (size_t)cap * 4,                               // rows
+        up.up_bytes,                                   // upload block
         (size_t)cap * cfg.d * 4,                       // x
         (size_t)cap * cfg.d * 2,                       // h
         (size_t)cap * max_n * 2,                       // big
@@ -431,9 +436,6 @@ void Engine::ensure_pool(int l) {
         attn_ws_floats(std::min(cap, 256), as) * 4,    // attention key-split workspace
         ypart * 4,                                     // split-K partials of y
         gpart * 4,                                     // split-K partials of gate_up
-        (size_t)cap * 4,                               // Segs: row table
-        (size_t)(cap / 64 + SD_MAX_SEQS) * 4,          // Segs: chunk table
-        (size_t)SD_MAX_SEQS * 4,                       // Segs: sequence table
     };
     size_t total = 0;
     for (size_t s : sizes) total += align256(s);
@@ -447,36 +449,47 @@ void Engine::ensure_pool(int l) {
         ptrs[i] = p;
         p += align256(sizes[i]);
     }
-    pool.ids = (uint32_t*)ptrs[0];
-    pool.rows = (uint32_t*)ptrs[1];
-    pool.x = (float*)ptrs[2];
-    pool.h = (f16*)ptrs[3];
-    pool.big = (f16*)ptrs[4];
-    pool.mid = (f16*)ptrs[5];
-    pool.qkvc = (float*)ptrs[6];
-    pool.of = (float*)ptrs[7];
-    pool.o = (f16*)ptrs[8];
-    pool.y = (f16*)ptrs[9];
-    pool.q = (f16*)ptrs[10];
-    pool.out = (float*)ptrs[11];
-    gdn_ws_carve(ptrs[12], cap, gs, pool.gdn);
-    pool.attn_ws = (float*)ptrs[13];
-    pool.attn_rows = std::min(cap, 256);
-    pool.ypart = (float*)ptrs[14];
-    pool.ypart_elems = ypart;
-    pool.gpart = (float*)ptrs[15];
-    pool.gpart_elems = gpart;
-    pool.seg_row = (uint32_t*)ptrs[16];
-    pool.seg_chunk = (uint32_t*)ptrs[17];
-    pool.seg_seq = (uint32_t*)ptrs[18];
+    uint8_t* upb = static_cast<uint8_t*>(ptrs[0]);
+    pool.up_bytes = up.up_bytes;
+    pool.off_ids = up.off_ids;
+    pool.off_rows = up.off_rows;
+    pool.off_seg_row = up.off_seg_row;
+    pool.off_seg_chunk = up.off_seg_chunk;
+    pool.off_seg_seq = up.off_seg_seq;
+    lu = reinterpret_cast<uint32_t*>(upb);
+    pool.ids = reinterpret_cast<uint32_t*>(upb + up.off_ids);
+    pool.rows = reinterpret_cast<uint32_t*>(upb + up.off_rows);
+    pool.seg_row = reinterpret_cast<uint32_t*>(upb + up.off_seg_row);
+    pool.seg_chunk = reinterpret_cast<uint32_t*>(upb + up.off_seg_chunk);
+    pool.seg_seq = reinterpret_cast<uint32_t*>(upb + up.off_seg_seq);
     pool.seg_chunk_cap = cap / 64 + SD_MAX_SEQS;
+    pool.x = (float*)ptrs[1];
+    pool.h = (f16*)ptrs[2];
+    pool.big = (f16*)ptrs[3];
+    pool.mid = (f16*)ptrs[4];
+    pool.qkvc = (float*)ptrs[5];
+    pool.of = (float*)ptrs[6];
+    pool.o = (f16*)ptrs[7];
+    pool.y = (f16*)ptrs[8];
+    pool.q = (f16*)ptrs[9];
+    pool.out = (float*)ptrs[10];
+    gdn_ws_carve(ptrs[11], cap, gs, pool.gdn);
+    pool.attn_ws = (float*)ptrs[12];
+    pool.attn_rows = std::min(cap, 256);
+    pool.ypart = (float*)ptrs[13];
+    pool.ypart_elems = ypart;
+    pool.gpart = (float*)ptrs[14];
+    pool.gpart_elems = gpart;
     SD_HIP(hipMemset(pool.x, 0, (size_t)cap * cfg.d * 4));
-    if (ids_h_cap < cap) {
-        ids_h = static_cast<uint32_t*>(halloc((size_t)cap * 4));
-        rows_h = static_cast<uint32_t*>(halloc((size_t)cap * 4));
+    SD_HIP(hipMemset(upb, 0, up.up_bytes));
+    if (up_h_bytes < up.up_bytes) {
+        up_h = static_cast<uint8_t*>(halloc(up.up_bytes));
+        up_h_bytes = up.up_bytes;
+    }
+    up_dirty = 0;
+    if (out_h_cap < cap) {
         out_h = static_cast<float*>(halloc((size_t)cap * cfg.d * 4));
-        seg_h = static_cast<uint32_t*>(halloc((size_t)(cap + cap / 64 + 2 * SD_MAX_SEQS) * 4));
-        ids_h_cap = cap;
+        out_h_cap = cap;
     }
 }
 
@@ -621,13 +634,15 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
 
 void Engine::upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
                     uint32_t chunks, uint32_t nseq) {
-    std::memcpy(ids_h, ids, n * 4);
-    SD_HIP(hipMemcpyAsync(pool.ids, ids_h, n * 4, hipMemcpyHostToDevice, st));
-    for (size_t r = 0; r < n_rows; r++) rows_h[r] = (uint32_t)rows[r];
-    if (n_rows) SD_HIP(hipMemcpyAsync(pool.rows, rows_h, n_rows * 4, hipMemcpyHostToDevice, st));
+    // lu, ids and rows (and the Segs tables a batch wrote before) in one host-to-device copy
     const uint32_t v[8] = {(uint32_t)n, (uint32_t)P, SD_CONTEXT, has_cache ? 1u : 0u, chunks, nseq, 0u, 0u};
-    std::memcpy(lu_h, v, sizeof(v));
-    SD_HIP(hipMemcpyAsync(lu, lu_h, sizeof(v), hipMemcpyHostToDevice, st));
+    std::memcpy(up_h, v, sizeof(v));
+    std::memcpy(up_h + pool.off_ids, ids, n * 4);
+    uint32_t* rows_h = reinterpret_cast<uint32_t*>(up_h + pool.off_rows);
+    for (size_t r = 0; r < n_rows; r++) rows_h[r] = (uint32_t)rows[r];
+    const size_t end = std::max(up_dirty, n_rows ? pool.off_rows + n_rows * 4 : pool.off_ids + n * 4);
+    SD_HIP(hipMemcpyAsync(lu, up_h, end, hipMemcpyHostToDevice, st));
+    up_dirty = 0;
 }
 
 // Restore (src/engine.rs:552-571): GDN state + conv history in one copy; K/V prefix rows only when
@@ -778,8 +793,8 @@ Plan& Engine::prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq
     ensure_pool(std::max(L, (int)n_rows));  // the row tables and outputs hold n_rows entries
     Plan& pl = plan(L, (int)nseq, any_short);
     // sequence tables (see Segs): rows, chunks of <= 64 rows inside each sequence, sequences
-    uint32_t* rowt = seg_h;
-    uint32_t* chunkt = seg_h + n;
+    uint32_t* rowt = reinterpret_cast<uint32_t*>(up_h + pool.off_seg_row);
+    uint32_t* chunkt = reinterpret_cast<uint32_t*>(up_h + pool.off_seg_chunk);
     uint32_t nch = 0;
     size_t s0 = 0;
     std::vector<uint32_t> seqt(nseq);
@@ -792,11 +807,8 @@ Plan& Engine::prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq
         s0 += lens[q];
     }
     SD_CHECK((int)nch <= pool.seg_chunk_cap, "forward_batch: chunk table overflow");
-    uint32_t* seqh = chunkt + nch;
-    std::memcpy(seqh, seqt.data(), nseq * 4);
-    SD_HIP(hipMemcpyAsync(pool.seg_row, rowt, n * 4, hipMemcpyHostToDevice, st));
-    SD_HIP(hipMemcpyAsync(pool.seg_chunk, chunkt, nch * 4, hipMemcpyHostToDevice, st));
-    SD_HIP(hipMemcpyAsync(pool.seg_seq, seqh, nseq * 4, hipMemcpyHostToDevice, st));
+    std::memcpy(up_h + pool.off_seg_seq, seqt.data(), nseq * 4);
+    up_dirty = pool.off_seg_seq + nseq * 4;  // sent with the ids by upload()
     upload(ids, n, rows, n_rows, P, cache != nullptr, nch, (uint32_t)nseq);
     restore(cache, P);
     return pl;

@@ -64,6 +64,9 @@ struct Cfg {
 struct Pool {
     int cap = 0;
     void* base = nullptr;
+    // Everything the host sends before a forward sits in one block at the start of the pool (the
+    // lu block, ids, rows, the Segs tables), mirrored by a pinned host block: one copy per forward.
+    size_t up_bytes = 0, off_ids = 0, off_rows = 0, off_seg_row = 0, off_seg_chunk = 0, off_seg_seq = 0;
     uint32_t *ids = nullptr, *rows = nullptr;
     float *x = nullptr, *qkvc = nullptr, *of = nullptr, *out = nullptr;
     f16 *h = nullptr, *big = nullptr, *mid = nullptr, *o = nullptr, *y = nullptr, *q = nullptr;
@@ -126,8 +129,9 @@ struct Engine {
     std::vector<int> attn_layers;
     const float* final_norm = nullptr;
     float* rope = nullptr;
-    uint32_t* lu = nullptr;  // device [L, P, CONTEXT, has_cache, chunks, sequences, 0, 0]
-    uint32_t* lu_h = nullptr;
+    uint32_t* lu = nullptr;  // device [L, P, CONTEXT, has_cache, chunks, sequences, 0, 0] (start of the pool)
+    uint8_t* up_h = nullptr;  // host mirror of the pool's upload block
+    size_t up_h_bytes = 0, up_dirty = 0;
     uint8_t* arena = nullptr;  // [GDN states | conv histories]
     size_t arena_bytes = 0, arena_state_bytes = 0;
     int n_linear = 0;
@@ -143,9 +147,8 @@ struct Engine {
     bool gu_il = false;  // gate_up weights interleaved in groups of 16 rows (interleave_gate_up)
     Pool pool;
     std::map<int, Plan> plans;
-    uint32_t *ids_h = nullptr, *rows_h = nullptr, *seg_h = nullptr;
     float* out_h = nullptr;
-    int ids_h_cap = 0;
+    int out_h_cap = 0;
     std::vector<void*> device_allocs, host_allocs;
     // Device copy of the last head used by ask_batch, and the head's per-call buffers.
     HeadW headw;
