@@ -75,35 +75,39 @@ __device__ __forceinline__ void get_frag(const f16* base, int KS, int rt, int s,
 
 // qkvc[t, c] = silu(sum_j w[c][j] x[t + j - 3, c]), rows before 0 from hist (src/kernels.rs:152-170).
 // With several sequences, row t is index i of the sequence starting at row s0.
-__global__ void k_conv(const f16* __restrict__ big, int stride, int L, int C, const float* __restrict__ w,
-                       const f16* __restrict__ hist, float* __restrict__ out, const uint32_t* __restrict__ rowt) {
+__global__ __launch_bounds__(256) void k_conv(const f16* __restrict__ big, int stride, int L, int C,
+                                              const float* __restrict__ w, const f16* __restrict__ hist,
+                                              float* __restrict__ out, const uint32_t* __restrict__ rowt, int R) {
     // 4 consecutive channels per thread (C % 4 == 0, checked by the launcher): 8-byte row loads,
-    // 16-byte weight loads and stores
+    // 16-byte weight loads and stores; R consecutive rows per workgroup, so the weights are read
+    // once per R rows and the rows a window shares come from L1
     const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
-    const int t = blockIdx.y;
-    if (c >= C || t >= L) return;
-    const int i = rowt ? (int)(rowt[t] & 0xFFFFu) : t;
-    const int s0 = rowt ? (int)(rowt[t] >> 16) : 0;
+    if (c >= C) return;
     float4 kk[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) kk[u] = *reinterpret_cast<const float4*>(w + 4 * (c + u));
-    f16x4 xs[4];
+    const int tend = min(L, (int)(blockIdx.y + 1) * R);
+    for (int t = blockIdx.y * R; t < tend; t++) {
+        const int i = rowt ? (int)(rowt[t] & 0xFFFFu) : t;
+        const int s0 = rowt ? (int)(rowt[t] >> 16) : 0;
+        f16x4 xs[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int tt = i + j - 3;
-        xs[j] = tt >= 0 ? *reinterpret_cast<const f16x4*>(big + (size_t)(s0 + tt) * stride + c)
-                        : *reinterpret_cast<const f16x4*>(hist + (size_t)(tt + 3) * C + c);
+        for (int j = 0; j < 4; j++) {
+            const int tt = i + j - 3;
+            xs[j] = tt >= 0 ? *reinterpret_cast<const f16x4*>(big + (size_t)(s0 + tt) * stride + c)
+                            : *reinterpret_cast<const f16x4*>(hist + (size_t)(tt + 3) * C + c);
+        }
+        float r[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float kj[4] = {kk[u].x, kk[u].y, kk[u].z, kk[u].w};
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) s += kj[j] * (float)xs[j][u];
+            r[u] = s / (1.0f + expf(-s));
+        }
+        *reinterpret_cast<float4*>(out + (size_t)t * C + c) = float4{r[0], r[1], r[2], r[3]};
     }
-    float r[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const float kj[4] = {kk[u].x, kk[u].y, kk[u].z, kk[u].w};
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) s += kj[j] * (float)xs[j][u];
-        r[u] = s / (1.0f + expf(-s));
-    }
-    *reinterpret_cast<float4*>(out + (size_t)t * C + c) = float4{r[0], r[1], r[2], r[3]};
 }
 
 // Workspace slot sizes (halves / floats) per (chunk, head).
@@ -774,7 +778,11 @@ void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws) {
 void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out, const Segs& sg,
                hipStream_t st) {
     SD_CHECK(C % 4 == 0 && stride % 4 == 0, "conv: channels and row stride must be multiples of 4");
-    hipLaunchKernelGGL(k_conv, dim3((C / 4 + 255) / 256, L), dim3(256), 0, st, big, stride, L, C, w, hist, out, sg.row);
+    // rows per workgroup: enough workgroups to fill the chip, at most 8 rows each
+    const int cb = (C / 4 + 255) / 256;
+    int R = 1;
+    while (R < 8 && (size_t)cb * ((L + 2 * R - 1) / (2 * R)) >= 512) R *= 2;
+    hipLaunchKernelGGL(k_conv, dim3(cb, (L + R - 1) / R), dim3(256), 0, st, big, stride, L, C, w, hist, out, sg.row, R);
     launched("conv");
 }
 
