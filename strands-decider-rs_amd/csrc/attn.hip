@@ -17,43 +17,73 @@ namespace {
 constexpr int BQ = 16;  // queries per workgroup
 
 template <int HD>
-__global__ __launch_bounds__(HD) void k_qk_prep(const f16* __restrict__ big, AttnShape s, const float* __restrict__ qw,
-                                                const float* __restrict__ kw, const float* __restrict__ rope, int L,
-                                                const uint32_t* __restrict__ lu, const uint32_t* __restrict__ rowt,
-                                                f16* __restrict__ Q, f16* __restrict__ Kc, f16* __restrict__ Vc) {
-    __shared__ float red[HD / 64];
-    __shared__ float nv[HD];
-    const int t = blockIdx.x, slot = blockIdx.y, d = threadIdx.x;
-    const int pos = (int)lu[1] + t;                                        // cache row
-    const int rpos = (int)lu[1] + (rowt ? (int)(rowt[t] & 0xFFFFu) : t);  // RoPE position
+__global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, AttnShape s, const float* __restrict__ qw,
+                                                 const float* __restrict__ kw, const float* __restrict__ rope, int L,
+                                                 const uint32_t* __restrict__ lu, const uint32_t* __restrict__ rowt,
+                                                 f16* __restrict__ Q, f16* __restrict__ Kc, f16* __restrict__ Vc) {
+    // Workgroup (4 rows, one q or kv head): wave w takes row w, lane l the 4 dimensions 4l..4l+3
+    // (8-byte loads and stores, the norm a wave reduction).  A kv head also writes the 4 rows of
+    // V^T, dimension by dimension: 8 contiguous bytes per dimension.
+    static_assert(HD == 256, "qk_prep is written for 256-wide heads");
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int t0 = blockIdx.x * 4, slot = blockIdx.y;
+    const int P = (int)lu[1];
     const bool isq = slot < s.HQ;
     const int k_off = 2 * s.HQ * HD, v_off = k_off + s.HK * HD;
-    const f16* row = big + (size_t)t * s.stride;
-    if (!isq) {  // V cache is stored transposed, [hk][hd][ctx]
-        const int kh = slot - s.HQ;
-        Vc[((size_t)kh * HD + d) * s.ctx + pos] = row[v_off + kh * HD + d];
+    const int nt = min(4, L - t0);
+    if (!isq) {  // V cache is stored transposed, [hk][hd][ctx]: thread d writes rows t0 .. t0+3
+        const int kh = slot - s.HQ, d = tid;
+        f16 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = i < nt ? big[(size_t)(t0 + i) * s.stride + v_off + kh * HD + d] : (f16)0.f;
+        f16* dst = Vc + ((size_t)kh * HD + d) * s.ctx + P + t0;
+        if (nt == 4 && ((P + t0) & 3) == 0) {
+            *reinterpret_cast<f16x4*>(dst) = f16x4{v[0], v[1], v[2], v[3]};
+        } else {
+            for (int i = 0; i < nt; i++) dst[i] = v[i];
+        }
     }
-    const float v = (float)row[isq ? slot * 2 * HD + d : k_off + (slot - s.HQ) * HD + d];
-    float ss = v * v;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if ((d & 63) == 0) red[d >> 6] = ss;
-    __syncthreads();
-    float tot = 0.f;
-#pragma unroll
-    for (int i = 0; i < HD / 64; i++) tot += red[i];
-    const float n = v * (1.0f / sqrtf(tot / (float)HD + 1e-6f)) * (isq ? qw[d] : kw[d]);
-    nv[d] = n;
-    __syncthreads();
-    float r = n;
+    const float* nw = isq ? qw : kw;
+    const float4 w4 = *reinterpret_cast<const float4*>(nw + 4 * lane);
     const int rd2 = s.RD / 2;
-    if (d < s.RD) {
-        const int i = d % rd2;
-        const float c = rope[((size_t)rpos * rd2 + i) * 2], sn = rope[((size_t)rpos * rd2 + i) * 2 + 1];
-        r = d < rd2 ? n * c - nv[d + rd2] * sn : n * c + nv[d - rd2] * sn;
+    if (wv < nt) {
+        const int t = t0 + wv;
+        const int pos = P + t;                                        // cache row
+        const int rpos = P + (rowt ? (int)(rowt[t] & 0xFFFFu) : t);  // RoPE position
+        const f16* src = big + (size_t)t * s.stride + (isq ? slot * 2 * HD : k_off + (slot - s.HQ) * HD) + 4 * lane;
+        const f16x4 x4 = *reinterpret_cast<const f16x4*>(src);
+        float x[4] = {(float)x4[0], (float)x4[1], (float)x4[2], (float)x4[3]};
+        float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
+        const float wv4[4] = {w4.x, w4.y, w4.z, w4.w};
+        float n[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) n[u] = x[u] * inv * wv4[u];
+        // rotate-half RoPE on dims < RD: the partner of dim d is d +- RD/2, in lane l +- RD/8
+        float pn[4];
+        const int sh = rd2 / 4;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float up = __shfl(n[u], (lane + sh) & 63), dn = __shfl(n[u], (lane - sh) & 63);
+            pn[u] = 4 * lane < rd2 ? up : dn;
+        }
+        f16x4 r4;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int d = 4 * lane + u;
+            float r = n[u];
+            if (d < s.RD) {
+                const int j = d % rd2;
+                const float c = rope[((size_t)rpos * rd2 + j) * 2], sn = rope[((size_t)rpos * rd2 + j) * 2 + 1];
+                r = d < rd2 ? n[u] * c - pn[u] * sn : n[u] * c + pn[u] * sn;
+            }
+            r4[u] = (f16)r;
+        }
+        if (isq) *reinterpret_cast<f16x4*>(Q + ((size_t)slot * L + t) * HD + 4 * lane) = r4;
+        else *reinterpret_cast<f16x4*>(Kc + ((size_t)(slot - s.HQ) * s.ctx + pos) * HD + 4 * lane) = r4;
     }
-    if (isq) Q[((size_t)slot * L + t) * HD + d] = (f16)r;
-    else Kc[((size_t)(slot - s.HQ) * s.ctx + pos) * HD + d] = (f16)r;
 }
 
 __device__ __forceinline__ float wave_max16(float v) {  // max over lanes {l, l^16, l^32, l^48}
@@ -273,8 +303,9 @@ void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* k
              const uint32_t* lu, const Segs& sg, f16* Q, f16* Kc, f16* Vc, hipStream_t st) {
     SD_CHECK(s.HD == 256, "attention: only head_dim 256 is supported");
     SD_CHECK(s.RD % 2 == 0 && s.RD <= s.HD, "attention: bad rotary_dim");
-    hipLaunchKernelGGL(k_qk_prep<256>, dim3(L, s.HQ + s.HK), dim3(256), 0, st, big, s, qw, kw, rope, L, lu, sg.row, Q,
-                       Kc, Vc);
+    SD_CHECK(s.RD % 8 == 0 && s.stride % 4 == 0, "attention: rotary_dim must be a multiple of 8, the row stride of 4");
+    hipLaunchKernelGGL(k_qk_prep<256>, dim3((L + 3) / 4, s.HQ + s.HK), dim3(256), 0, st, big, s, qw, kw, rope, L, lu,
+                       sg.row, Q, Kc, Vc);
     launched("qk_prep");
 }
 
