@@ -650,7 +650,7 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
     GemmPlan p{pick_cfg(M, exact), 1};
     // Configuration indices into kCfgs: the 64-wide-step 32x32 MFMA tiles (need K a multiple of 256).
     constexpr int W21 = 18, W41 = 20, W31 = 21;
-    constexpr int T41 = 5;  // 16x16 (4,1)
+    constexpr int T21 = 3, T31 = 4, T41 = 5;  // 16x16 (2,1), (3,1), (4,1)
     const bool wide_ok = K % 256 == 0;
     auto fit = [&](GemmPlan q) {  // largest usable split <= q.ks
         const int steps = K / KSTEP;
@@ -671,13 +671,14 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
         return fit(p);
     }
     if (!exact && wide_ok && M > 64 && M < 256) {
-        // Batched questions (M = 120 in the sweep): in_proj (N = 8256, f16 out) (2,1) 14.6 us; qkv
-        // (N = 5120, f16 out) 16x16 (4,1) 12.2 us; gate_up (4,1) with 2 splits 14.4 us; down (K =
-        // 6144) (2,1) with 8 splits 9.1 us; out_proj / o_proj 16x16 (4,1) with 4 splits 5.6 us.
-        if (!partial_ok) p.cfg = N >= 7000 ? W21 : T41;
+        // Batched questions (M = 120 in a sweep of the tiled weights): in_proj (N = 8256, f16 out)
+        // (2,1) 14.1 us; qkv (N = 5120, f16 out) 16x16 (3,1) 10.5 us; gate_up split (4,1) with 2
+        // splits 14.1 us; down (K = 6144) (2,1) with 8 splits 8.6 us; out_proj / o_proj 16x16 (2,1)
+        // with 4 splits 5.1 us.
+        if (!partial_ok) p.cfg = N >= 7000 ? W21 : T31;
         else if (N >= 10000) p = GemmPlan{W41, 2};
         else if (K > 3000) p = GemmPlan{W21, 8};
-        else p = GemmPlan{T41, 4};
+        else p = GemmPlan{T21, 4};
         return fit(p);
     }
     if (!exact && M > 64 && M < 256) p.cfg = partial_ok ? T41 : 4;
