@@ -58,12 +58,6 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
     return r;
 }
 
-// mask bit of the lane set ? b : a, as one v_cndmask_b32.
-__device__ __forceinline__ float sel_lanes(uint64_t mask, float a, float b) {
-    float r;
-    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
-    return r;
-}
 
 __device__ __forceinline__ void nib_pairs(uint32_t w, f16x2& p0, f16x2& p1, f16x2& p2, f16x2& p3) {
     const uint32_t w8 = w >> 8;
@@ -118,6 +112,10 @@ __device__ __forceinline__ void wait_loads() {
 // the loads the other waves need; the "memory" clobber keeps the compiler from moving LDS
 // accesses across.
 __device__ __forceinline__ void bar_noflush() { asm volatile("s_barrier" ::: "memory"); }
+
+// Workgroup barrier after this wave's LDS accesses have completed (outstanding global stores are
+// not waited for, unlike __syncthreads).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
     return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
@@ -316,11 +314,19 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 //    step (16 bytes) and its scale, up to 3 steps ahead in registers; MFMA k-slice s (16 k) takes
 //    word s of that block, which is k-chunk 4g + s of the step, so the A fragment of lane (r, g) is
 //    the 8 halves of row r at that k-chunk (the engine nibble order makes them natural);
-//  * D of the 32x32 tile: register i of lane l is row 8(i/4) + 4(l/32) + i%4, column l%32;
+//  * D of the 32x32 tile: register i of lane l is D row 8(i/4) + 4(l/32) + i%4, D column l%32.
+//    Split-K partials (PARTIAL) take A as the row operand: lane l holds output column l%32 of 16
+//    rows, stored as single floats (a store instruction covers 32 columns of 2 rows).  f16 outputs
+//    take the weights as the row operand (the same fragments, swapped): lane (r, g) holds output
+//    row r and the columns 8j + 4g .. 8j + 4g + 3 of its tile in registers 4j .. 4j + 3;
+//  * the end of a kernel writes the dirty L2 lines back (the next kernel may run on another XCD),
+//    and every workgroup finishes at about the same time, so the output is written in one burst
+//    after the last MFMA.  f16 outputs go through the (then free) LDS ring as f32 and leave as
+//    whole-row 16-byte non-temporal stores; partials are stored non-temporally;
 //  * SILU (gate_up, unsplit): W holds gate_up with its rows interleaved in groups of 16 (rows
 //    32p .. 32p + 15 are gate rows 16p .., the next 16 the matching up rows, interleave_gate_up),
-//    so lanes l and l ^ 16 hold gate and up of one (row, j); they swap halves of their registers
-//    and each writes 8 values of Y = mid[M][N / 2] = f16(silu(g) * u), g and u rounded to f16 first
+//    so registers k and 8 + k of a lane hold gate and up of one output element (row r, mid column
+//    16p + 8(k/4) + 4g + k%4); Y = mid[M][N / 2] = f16(silu(g) * u), g and u rounded to f16 first
 //    as the reference stores them.
 template <int MT2, int NT2, bool PARTIAL, bool SILU = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2))) void k_gemm_w4m(
@@ -457,7 +463,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
             for (int a = 0; a < MT2; a++)
 #pragma unroll
                 for (int t = 0; t < NT2; t++)
-                    acc[a][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cu][a], bf[cu][t], acc[a][t], 0, 0, 0);
+                    acc[a][t] = PARTIAL ? __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cu][a], bf[cu][t], acc[a][t], 0, 0, 0)
+                                        : __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cu][t], af[cu][a], acc[a][t], 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < NMF; j++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // one MFMA
@@ -488,59 +495,104 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     } while (it < steps);
     wait_loads<0x0F70>();  // the trailing out-of-range loads, before the LDS is released
 
-    if constexpr (SILU) {
-        // N % 32 == 0 (checked by the launcher): a tile's columns are all in range or all out
-        const bool up = r >= 16;
-        const uint64_t upm = __ballot(up);  // lanes 16..31 and 48..63
-        const int half = N >> 1;
+    if constexpr (PARTIAL) {
+        float* mine = part + (size_t)bz * M * N;
 #pragma unroll
         for (int a = 0; a < MT2; a++)
 #pragma unroll
             for (int t = 0; t < NT2; t++) {
                 if (ncol[t] >= N) continue;
-                const int j = ((ncol[t] >> 5) << 4) + (r & 15);
-                const int mb = m0 + a * 32 + (up ? 16 : 0) + 4 * g;
-                const bool full = m0 + a * 32 + 32 <= M;
-                // the gate lane keeps registers 0..7 and receives the up lane's, and the other way
-                // round for 8..15 (one v_cndmask each: a plain ?: on the two registers becomes a
-                // variable index into the accumulator); all 8 swaps are issued before any use
-                float keep[8], got[8];
 #pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    keep[k] = sel_lanes(upm, acc[a][t][k], acc[a][t][8 + k]);
-                    const float send = sel_lanes(upm, acc[a][t][8 + k], acc[a][t][k]);
-                    got[k] = __builtin_bit_cast(
-                        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x401F));  // lane ^ 16
-                }
-                f16 out[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const float gv = (float)(f16)sel_lanes(upm, keep[k], got[k]);
-                    const float uv = (float)(f16)sel_lanes(upm, got[k], keep[k]);
-                    out[k] = (f16)(gv / (1.0f + expf(-gv)) * uv);
-                }
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const int m = mb + 8 * (k >> 2) + (k & 3);
-                    if (full || m < M) Y[(size_t)m * half + j] = out[k];
+                for (int i = 0; i < 16; i++) {
+                    const int m = m0 + a * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                    if (m < M) __builtin_nontemporal_store(acc[a][t][i], mine + (size_t)m * N + ncol[t]);
                 }
             }
         return;
     }
-    float* mine = PARTIAL ? part + (size_t)bz * M * N : nullptr;
+    // f16 outputs: row m0 + 32a + r, columns cb + 8j + 4g + e of column tile cb.  Staged through
+    // LDS when every row of the output is 16-byte aligned; otherwise stored element by element.
+    const int ow = SILU ? N >> 1 : N;  // output row width
+    const bool staged = ow % 8 == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+    if (!staged) {
 #pragma unroll
-    for (int a = 0; a < MT2; a++)
+        for (int a = 0; a < MT2; a++)
 #pragma unroll
-        for (int t = 0; t < NT2; t++) {
-            if (ncol[t] >= N) continue;
+            for (int t = 0; t < NT2; t++) {
+                const int cb = n0 + (wave * NT2 + t) * 32, m = m0 + a * 32 + r;
+                if (cb >= N || m >= M) continue;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int m = m0 + a * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-                if (m >= M) continue;
-                if constexpr (PARTIAL) mine[(size_t)m * N + ncol[t]] = acc[a][t][i];
-                else Y[(size_t)m * N + ncol[t]] = (f16)acc[a][t][i];
+                for (int i = 0; i < 16; i++) {
+                    if constexpr (SILU) {
+                        if (i >= 8) continue;  // N % 32 == 0: the tile is whole
+                        const float gv = (float)(f16)acc[a][t][i], uv = (float)(f16)acc[a][t][8 + i];
+                        const int j = (cb >> 1) + 8 * (i >> 2) + 4 * g + (i & 3);
+                        Y[(size_t)m * ow + j] = (f16)(gv / (1.0f + expf(-gv)) * uv);
+                    } else {
+                        const int n = cb + 8 * (i >> 2) + 4 * g + (i & 3);
+                        if (n < N) Y[(size_t)m * N + n] = (f16)acc[a][t][i];
+                    }
+                }
+            }
+        return;
+    }
+    // One pass per column tile t of the waves.  Wave w writes its 32 columns of the pass into stage
+    // w: f32 rows of 128 B, 16-byte chunk q of row rho at (q ^ (rho / 2) % 8) (conflict-free
+    // ds_write_b128 over 16 lanes); SILU writes its 16 f16 outputs, rows of 32 B.  Then each thread
+    // reads 8 consecutive outputs of one row and stores them with one 16-byte store.
+    uint8_t* const wst = wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? As2 : As3;
+#pragma unroll
+    for (int t = 0; t < NT2; t++) {
+        lds_barrier();  // the ring (or the previous pass) is free: every wave's loads have landed
+#pragma unroll
+        for (int a = 0; a < MT2; a++) {
+            const int rho = 32 * a + r;
+            if constexpr (SILU) {
+                f16 o[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float gv = (float)(f16)acc[a][t][k], uv = (float)(f16)acc[a][t][8 + k];
+                    o[k] = (f16)(gv / (1.0f + expf(-gv)) * uv);
+                }
+                *reinterpret_cast<f16x4*>(wst + rho * 32 + 8 * g) = f16x4{o[0], o[1], o[2], o[3]};
+                *reinterpret_cast<f16x4*>(wst + rho * 32 + 16 + 8 * g) = f16x4{o[4], o[5], o[6], o[7]};
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int q = (2 * j + g) ^ ((rho >> 1) & 7);
+                    *reinterpret_cast<f32x4*>(wst + rho * 128 + q * 16) =
+                        f32x4{acc[a][t][4 * j], acc[a][t][4 * j + 1], acc[a][t][4 * j + 2], acc[a][t][4 * j + 3]};
+                }
             }
         }
+        lds_barrier();
+        if constexpr (SILU) {
+            // a mid row of the pass: 4 waves x 16 outputs = 8 chunks
+            const int c = tid & 7, w = c >> 1;
+            const uint8_t* src = w == 0 ? As0 : w == 1 ? As1 : w == 2 ? As2 : As3;
+            const int cb = n0 + (w * NT2 + t) * 32, j = (cb >> 1) + 8 * (c & 1);
+#pragma unroll
+            for (int it = 0; it < MT2; it++) {
+                const int rho = it * 32 + (tid >> 3), m = m0 + rho;
+                const f16x8 v = *reinterpret_cast<const f16x8*>(src + rho * 32 + 16 * (c & 1));
+                if (m < M && cb < N) __builtin_nontemporal_store(v, reinterpret_cast<f16x8*>(Y + (size_t)m * ow + j));
+            }
+        } else {
+            // an output row of the pass: 4 waves x 32 columns = 16 groups of 8
+            const int cp = tid & 15, w = cp >> 2, q = 2 * (cp & 3);
+            const uint8_t* src = w == 0 ? As0 : w == 1 ? As1 : w == 2 ? As2 : As3;
+            const int n = n0 + (w * NT2 + t) * 32 + 8 * (cp & 3);
+#pragma unroll
+            for (int it = 0; it < MT2 * 2; it++) {
+                const int rho = it * 16 + (tid >> 4), m = m0 + rho, sw = (rho >> 1) & 7;
+                const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + rho * 128 + ((q ^ sw) * 16));
+                const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + rho * 128 + (((q + 1) ^ sw) * 16));
+                const f16x8 h = f16x8{(f16)v0[0], (f16)v0[1], (f16)v0[2], (f16)v0[3],
+                                      (f16)v1[0], (f16)v1[1], (f16)v1[2], (f16)v1[3]};
+                if (m < M && n < N) __builtin_nontemporal_store(h, reinterpret_cast<f16x8*>(Y + (size_t)m * N + n));
+            }
+        }
+    }
 }
 
 // In-place rewrite of int4 weight words from the reference's nibble order (k = 8w + e of a quant
