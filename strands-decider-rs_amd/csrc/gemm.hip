@@ -323,13 +323,17 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 //    and every workgroup finishes at about the same time, so the output is written in one burst
 //    after the last MFMA.  f16 outputs go through the (then free) LDS ring as f32 and leave as
 //    whole-row 16-byte non-temporal stores; partials are stored non-temporally;
+//  * KH = 2 (NT2 = 1): 8 waves, two halves of 4 that take the first and the second half of the
+//    workgroup's k steps, each with its own ring; at the end the second half hands its
+//    accumulators to the first through LDS.  The k chain per wave halves and every SIMD holds two
+//    waves, for grids of about one workgroup per CU (batched questions, split-K prefill shapes);
 //  * SILU (gate_up, unsplit): W holds gate_up with its rows interleaved in groups of 16 (rows
 //    32p .. 32p + 15 are gate rows 16p .., the next 16 the matching up rows, interleave_gate_up),
 //    so registers k and 8 + k of a lane hold gate and up of one output element (row r, mid column
 //    16p + 8(k/4) + 4g + k%4); Y = mid[M][N / 2] = f16(silu(g) * u), g and u rounded to f16 first
 //    as the reference stores them.
-template <int MT2, int NT2, bool PARTIAL, bool SILU = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2))) void k_gemm_w4m(
+template <int MT2, int NT2, bool PARTIAL, bool SILU = false, int KH = 1>
+__global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgpu_waves_per_eu(2))) void k_gemm_w4m(
     const f16* __restrict__ A, const uint32_t* __restrict__ W, const f16* __restrict__ S, f16* __restrict__ Y,
     float* __restrict__ part, int M, int N, int K, int ksplit, int tiled) {
     constexpr int KS = 64;                   // k per step
@@ -340,14 +344,21 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     constexpr int WAIT2 = 0x0F70 | ((2 * PER_STEP) & 15) | (((2 * PER_STEP) >> 4) << 14);  // vmcnt(2 steps)
     // One array per stage, so the compiler can see that the loads into one stage never alias the
     // fragment reads of another.
-    __shared__ __attribute__((aligned(1024))) uint8_t As0[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t As1[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t As2[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t As3[STAGE];
+    static_assert(KH == 1 || (KH == 2 && NT2 == 1), "k halves: one column tile per wave");
+    __shared__ __attribute__((aligned(1024))) uint8_t As0[KH * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As1[KH * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As2[KH * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As3[KH * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wall = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = wall >> 2, wave = wall & 3;  // k half, wave within the half
     const int r = lane & 31, g = lane >> 5;
+    // this half's ring: stage i at Asi + kh * STAGE
+    uint8_t* const R0 = As0 + kh * STAGE;
+    uint8_t* const R1 = As1 + kh * STAGE;
+    uint8_t* const R2 = As2 + kh * STAGE;
+    uint8_t* const R3 = As3 + kh * STAGE;
     // XCD-aware tile order, as in k_gemm_w4
     const int gy = gridDim.y, gyz = gridDim.y * gridDim.z;
     const int G = gridDim.x * gyz;
@@ -357,8 +368,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     const int bx = tile / gyz, by = (tile % gyz) % gy, bz = (tile % gyz) / gy;
     const int m0 = by * BM, n0 = bx * (4 * NT2 * 32);
     const int KB = K >> 5;
-    const int steps = (K / KS) / ksplit;  // a multiple of 4 (checked by the launcher)
-    const int step0 = bz * steps;
+    const int steps = (K / KS) / ksplit / KH;  // a multiple of 4 (checked by the launcher)
+    const int step0 = (bz * KH + kh) * steps;
 
     // Loads go through buffer resources: per-lane offsets fixed for the whole k loop, the step in the
     // uniform offset.  A step past this workgroup's range gets an offset past the buffer (no memory
@@ -476,9 +487,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
         bar_noflush();
     };
 
-    issue(0, As0, bw[0], bs[0]);
-    issue(1, As1, bw[1], bs[1]);
-    issue(2, As2, bw[2], bs[2]);
+    issue(0, R0, bw[0], bs[0]);
+    issue(1, R1, bw[1], bs[1]);
+    issue(2, R2, bw[2], bs[2]);
     wait_loads<WAIT2>();
     bar_noflush();
     f16x8 bf0[NT2];
@@ -487,15 +498,45 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
     // past the first wait (and so change what it counts).
     int it = 0;
     do {
-        step(As0, As3, bw[0], bs[0], bw[1], bs[1], bw[3], bs[3], bf0, it);
-        step(As1, As0, bw[1], bs[1], bw[2], bs[2], bw[0], bs[0], bf0, it + 1);
-        step(As2, As1, bw[2], bs[2], bw[3], bs[3], bw[1], bs[1], bf0, it + 2);
-        step(As3, As2, bw[3], bs[3], bw[0], bs[0], bw[2], bs[2], bf0, it + 3);
+        step(R0, R3, bw[0], bs[0], bw[1], bs[1], bw[3], bs[3], bf0, it);
+        step(R1, R0, bw[1], bs[1], bw[2], bs[2], bw[0], bs[0], bf0, it + 1);
+        step(R2, R1, bw[2], bs[2], bw[3], bs[3], bw[1], bs[1], bf0, it + 2);
+        step(R3, R2, bw[3], bs[3], bw[0], bs[0], bw[2], bs[2], bf0, it + 3);
         it += 4;
     } while (it < steps);
     wait_loads<0x0F70>();  // the trailing out-of-range loads, before the LDS is released
 
+    if constexpr (KH == 2) {
+        // The second half's accumulators go to the first half's wave of the same columns through the
+        // second half of that wave's ring array (lane-major 16-byte chunks, conflict-free).
+        uint8_t* const xr = (wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? As2 : As3) + STAGE;
+        lds_barrier();  // every wave's loads have landed: the rings are free
+        if (kh == 1) {
+#pragma unroll
+            for (int a = 0; a < MT2; a++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    *reinterpret_cast<f32x4*>(xr + ((a * 4 + q) * 64 + lane) * 16) =
+                        f32x4{acc[a][0][4 * q], acc[a][0][4 * q + 1], acc[a][0][4 * q + 2], acc[a][0][4 * q + 3]};
+        }
+        lds_barrier();
+        if (kh == 0) {
+#pragma unroll
+            for (int a = 0; a < MT2; a++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(xr + ((a * 4 + q) * 64 + lane) * 16);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[a][0][4 * q + e] += v[e];
+                }
+        }
+    }
+    // From here on the first half (threads 0 .. 255) stores; the second half only joins the
+    // barriers of the staged path.
+    const bool act = kh == 0;
+
     if constexpr (PARTIAL) {
+        if (!act) return;
         float* mine = part + (size_t)bz * M * N;
 #pragma unroll
         for (int a = 0; a < MT2; a++)
@@ -510,17 +551,58 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
             }
         return;
     }
-    // f16 outputs: row m0 + 32a + r, columns cb + 8j + 4g + e of column tile cb.  Staged through
-    // LDS when every row of the output is 16-byte aligned; otherwise stored element by element.
+    // f16 outputs: row m0 + 32a + r, columns cb + 8j + 4g + e of column tile cb.  With every output
+    // row 16-byte aligned they leave as 16-byte stores: staged through LDS for prefill-sized M, else
+    // straight from registers after v_permlane32_swap has given lane (r, 0) the 8 columns 16h .. 16h
+    // + 7 and lane (r, 1) the next 8 (h = 0, 1; the swap exchanges the upper 32 lanes of its first
+    // operand with the lower 32 lanes of its second).  Otherwise element by element.
     const int ow = SILU ? N >> 1 : N;  // output row width
-    const bool staged = ow % 8 == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+    const bool vec = ow % 8 == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+    const bool staged = vec && M >= 256;  // measured: direct stores win for a lone workgroup per CU
     if (!staged) {
+        if (!act) return;
 #pragma unroll
         for (int a = 0; a < MT2; a++)
 #pragma unroll
             for (int t = 0; t < NT2; t++) {
                 const int cb = n0 + (wave * NT2 + t) * 32, m = m0 + a * 32 + r;
-                if (cb >= N || m >= M) continue;
+                if (cb >= N) continue;  // wave-uniform
+                if (vec) {
+                    // P[2j + e/2] packs columns 8j + 4g + e, e + 1 (SILU: the 8 outputs, 2 per register)
+                    uint32_t P[8];
+                    if constexpr (SILU) {
+#pragma unroll
+                        for (int k = 0; k < 8; k += 2) {
+                            f16 o[2];
+#pragma unroll
+                            for (int u = 0; u < 2; u++) {
+                                const float gv = (float)(f16)acc[a][t][k + u], uv = (float)(f16)acc[a][t][8 + k + u];
+                                o[u] = (f16)(gv / (1.0f + expf(-gv)) * uv);
+                            }
+                            P[k / 2] = __builtin_bit_cast(uint32_t, f16x2{o[0], o[1]});
+                        }
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 16; k += 2)
+                            P[k / 2] = __builtin_bit_cast(uint32_t, f16x2{(f16)acc[a][t][k], (f16)acc[a][t][k + 1]});
+                    }
+                    constexpr int NH = SILU ? 1 : 2;  // 16-column halves of the tile's outputs
+#pragma unroll
+                    for (int h = 0; h < NH; h++) {
+#pragma unroll
+                        for (int e = 0; e < 2; e++) {
+                            const auto sw = __builtin_amdgcn_permlane32_swap(P[4 * h + e], P[4 * h + 2 + e], false, false);
+                            P[4 * h + e] = sw[0];
+                            P[4 * h + 2 + e] = sw[1];
+                        }
+                        const int n = (SILU ? cb >> 1 : cb) + 16 * h + 8 * g;
+                        if (m < M && n < ow)
+                            __builtin_nontemporal_store(u32x4{P[4 * h], P[4 * h + 1], P[4 * h + 2], P[4 * h + 3]},
+                                                        reinterpret_cast<u32x4*>(Y + (size_t)m * ow + n));
+                    }
+                    continue;
+                }
+                if (m >= M) continue;
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     if constexpr (SILU) {
@@ -546,6 +628,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
         lds_barrier();  // the ring (or the previous pass) is free: every wave's loads have landed
 #pragma unroll
         for (int a = 0; a < MT2; a++) {
+            if (!act) break;
             const int rho = 32 * a + r;
             if constexpr (SILU) {
                 f16 o[8];
@@ -566,6 +649,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
             }
         }
         lds_barrier();
+        if (!act) continue;
         if constexpr (SILU) {
             // a mid row of the pass: 4 waves x 16 outputs = 8 chunks
             const int c = tid & 7, w = c >> 1;
@@ -664,12 +748,16 @@ struct Cfg {
     GemmFn f16_out, part_out;
     bool wide;  // k_gemm_w4m (k steps of 64 in a ring of 4)
     GemmFn silu_out;  // k_gemm_w4m with the SiLU * mul epilogue (wide configurations only)
+    int kh;           // k halves per workgroup (256 threads each)
 };
 
-#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX, false>, k_gemm_w4<MT, NT, EX, true>, false, nullptr}
+#define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX, false>, k_gemm_w4<MT, NT, EX, true>, false, nullptr, 1}
 #define SD_CFGM(MT2, NT2)                                                                                        \
     Cfg{2 * MT2, 2 * NT2, false, k_gemm_w4m<MT2, NT2, false>, k_gemm_w4m<MT2, NT2, true>, true,                  \
-        k_gemm_w4m<MT2, NT2, false, true>}
+        k_gemm_w4m<MT2, NT2, false, true>, 1}
+#define SD_CFGMH(MT2)                                                                                            \
+    Cfg{2 * MT2, 2, false, k_gemm_w4m<MT2, 1, false, false, 2>, k_gemm_w4m<MT2, 1, true, false, 2>, true,        \
+        k_gemm_w4m<MT2, 1, false, true, 2>, 2}
 const Cfg kCfgs[] = {
     SD_CFG(1, 1, true), SD_CFG(2, 1, true),                                           // M <= 20: f32 dequant
     SD_CFG(1, 1, false), SD_CFG(2, 1, false), SD_CFG(3, 1, false), SD_CFG(4, 1, false),  // skinny
@@ -678,9 +766,12 @@ const Cfg kCfgs[] = {
     SD_CFG(4, 3, false), SD_CFG(3, 3, false), SD_CFG(2, 3, false), SD_CFG(5, 2, false),
     // 32x32x16 MFMA tiles (MT2 x 32 rows, 4 x NT2 x 32 columns), listed in 16-row / 64-column units
     SD_CFGM(2, 1), SD_CFGM(2, 2), SD_CFGM(4, 1), SD_CFGM(3, 1), SD_CFGM(1, 1), SD_CFGM(4, 2),
+    // the same with two k halves per workgroup (512 threads): (2,1), (4,1), (3,1)
+    SD_CFGMH(2), SD_CFGMH(4), SD_CFGMH(3),
 };
 #undef SD_CFG
 #undef SD_CFGM
+#undef SD_CFGMH
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 int pick_cfg(int M, bool exact) {
@@ -700,34 +791,36 @@ int gemm_w4_cfg(int M, bool exact) { return pick_cfg(M, exact); }
 
 GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t max_part_elems) {
     GemmPlan p{pick_cfg(M, exact), 1};
-    // Configuration indices into kCfgs: the 64-wide-step 32x32 MFMA tiles (need K a multiple of 256).
-    constexpr int W21 = 18, W41 = 20, W31 = 21;
+    // Configuration indices into kCfgs: the 64-wide-step 32x32 MFMA tiles (need K a multiple of
+    // 256), the same with two k halves per workgroup (K a multiple of 512), and 16x16 tiles.
+    constexpr int W21 = 18, W41 = 20, W31 = 21, W21h = 24, W31h = 26;
     constexpr int T21 = 3, T31 = 4, T41 = 5;  // 16x16 (2,1), (3,1), (4,1)
-    const bool wide_ok = K % 256 == 0;
+    const bool wide_ok = K % 256 == 0, halves_ok = K % 512 == 0;
     auto fit = [&](GemmPlan q) {  // largest usable split <= q.ks
         const int steps = K / KSTEP;
         while (q.ks > 1 && (steps % q.ks || (size_t)q.ks * M * N > max_part_elems ||
-                            (kCfgs[q.cfg].wide && (K / 64 / q.ks) % 4)))
+                            (kCfgs[q.cfg].wide && (K / 64 / q.ks) % (4 * kCfgs[q.cfg].kh))))
             q.ks /= 2;
         return q;
     };
     if (!exact && wide_ok && M >= 256 && M <= 1024) {
-        // Prefill-sized M; from a sweep of the 2B's shapes at M = 512 on MI355X (random data):
-        // N = 12288: (4,1) 37 us; N = 8256: (3,1) 32 us; N = 5120: (3,1) 19 us; N = 2048: (2,1) with
-        // 2 splits 10.6 us (K = 2048), (4,1) with 4 splits 22 us (K = 6144).
+        // Prefill-sized M; from a sweep of the 2B's shapes at M = 512 on MI355X (random data, tiled
+        // weights): N = 12288: (4,1) 31.5 us; N = 8256: (3,1) 24.8 us; N = 5120: (3,1) with k halves
+        // 16.8 us; N = 2048: (2,1) with 2 splits 9.8 us (K = 2048), (4,1) with 4 splits 18.8 us
+        // (K = 6144; (2,1) is 18.2 us alone but 22.5 us inside the forward).
         if (N >= 10000) p.cfg = W41;
-        else if (N >= 4000) p.cfg = W31;
+        else if (N >= 7000 || (N >= 4000 && !halves_ok)) p.cfg = W31;
+        else if (N >= 4000) p.cfg = W31h;
         else if (partial_ok && K > 3000) p = GemmPlan{W41, 4};
         else if (partial_ok) p = GemmPlan{W21, 2};
         else p.cfg = W21;
         return fit(p);
     }
     if (!exact && wide_ok && M > 64 && M < 256) {
-        // Batched questions (M = 120 in a sweep of the tiled weights): in_proj (N = 8256, f16 out)
-        // (2,1) 14.1 us; qkv (N = 5120, f16 out) 16x16 (3,1) 10.5 us; gate_up split (4,1) with 2
-        // splits 14.1 us; down (K = 6144) (2,1) with 8 splits 8.6 us; out_proj / o_proj 16x16 (2,1)
-        // with 4 splits 5.1 us.
-        if (!partial_ok) p.cfg = N >= 7000 ? W21 : T31;
+        // Batched questions (M = 120): in_proj (N = 8256, f16 out) (2,1) with k halves 13.0 us;
+        // gate_up (N = 12288) the same 13.9 us; qkv (N = 5120, f16 out) 16x16 (3,1) 10.7 us; down
+        // (K = 6144) (2,1) with 8 splits 8.3 us; out_proj / o_proj 16x16 (2,1) with 4 splits 5.2 us.
+        if (!partial_ok) p.cfg = N >= 7000 ? (halves_ok ? W21h : W21) : T31;
         else if (N >= 10000) p = GemmPlan{W41, 2};
         else if (K > 3000) p = GemmPlan{W21, 8};
         else p = GemmPlan{T21, 4};
@@ -745,7 +838,7 @@ int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_pa
     const int steps = K / KSTEP;
     int ks = 1;
     while (groups * ks < target_groups && ks < 8 && steps % (ks * 2) == 0 && steps / (ks * 2) >= 2 &&
-           (!c.wide || (steps / (ks * 2)) % 2 == 0) && (size_t)(ks * 2) * M * N <= max_part_elems)
+           (!c.wide || (steps / (ks * 2)) % (2 * c.kh) == 0) && (size_t)(ks * 2) * M * N <= max_part_elems)
         ks *= 2;
     return ks;
 }
@@ -753,15 +846,16 @@ int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_pa
 namespace {
 // A GEMM launch; while Engine::profile times a step, the step's first GEMM records its own start
 // and end (see KernelEvents).
-void launch_gemm(GemmFn kern, dim3 grid, hipStream_t st, const f16* A, const uint32_t* W, const f16* S, f16* Y,
-                 float* part, int M, int N, int K, int ks, bool tiled) {
+void launch_gemm(GemmFn kern, dim3 grid, int threads, hipStream_t st, const f16* A, const uint32_t* W, const f16* S,
+                 f16* Y, float* part, int M, int N, int K, int ks, bool tiled) {
     const int tl = tiled ? 1 : 0;
     KernelEvents* ke = kernel_events();
     if (ke && ke->launches == 0) {
-        hipExtLaunchKernelGGL(kern, grid, dim3(256), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, ks, tl);
+        hipExtLaunchKernelGGL(kern, grid, dim3(threads), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, ks,
+                              tl);
         ke->launches++;
     } else {
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, A, W, S, Y, part, M, N, K, ks, tl);
+        hipLaunchKernelGGL(kern, grid, dim3(threads), 0, st, A, W, S, Y, part, M, N, K, ks, tl);
     }
 }
 }  // namespace
@@ -778,10 +872,12 @@ void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part,
     SD_CHECK(c.exact == exact, "gemm_w4: configuration does not match the dequant mode");
     SD_CHECK(ks >= 1 && (K / KSTEP) % ks == 0, "gemm_w4: split count must divide the k steps");
     SD_CHECK(part || (Y && ks == 1), "gemm_w4: split-K writes partials and needs a partial buffer");
-    SD_CHECK(!c.wide || (K / 64 / ks) % 4 == 0, "gemm_w4: this configuration needs K / ks a multiple of 256");
+    SD_CHECK(!c.wide || (K / 64 / ks) % (4 * c.kh) == 0,
+             c.kh == 1 ? "gemm_w4: this configuration needs K / ks a multiple of 256"
+                       : "gemm_w4: this configuration needs K / ks a multiple of 256 per k half");
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
     dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, ks);
-    launch_gemm(part ? c.part_out : c.f16_out, grid, st, A, W, S, Y, part, M, N, K, ks, tiled);
+    launch_gemm(part ? c.part_out : c.f16_out, grid, 256 * c.kh, st, A, W, S, Y, part, M, N, K, ks, tiled);
     launched("gemm_w4");
 }
 
@@ -789,12 +885,13 @@ bool gemm_w4_has_silu(int cfg) { return cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg]
 
 void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M, int N, int K, hipStream_t st,
                   int cfg, bool tiled) {
-    SD_CHECK(M >= 1 && N >= 32 && N % 32 == 0 && K % 256 == 0, "gemm_w4_silu: need N a multiple of 32, K of 256");
     SD_CHECK(cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg].silu_out, "gemm_w4_silu: not a 32x32-tile configuration");
     const Cfg& c = kCfgs[cfg];
+    SD_CHECK(M >= 1 && N >= 32 && N % 32 == 0 && K % (256 * c.kh) == 0,
+             "gemm_w4_silu: need N a multiple of 32 and K of 256 per k half");
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
     dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, 1);
-    launch_gemm(c.silu_out, grid, st, A, W, S, mid, (float*)nullptr, M, N, K, 1, tiled);
+    launch_gemm(c.silu_out, grid, 256 * c.kh, st, A, W, S, mid, (float*)nullptr, M, N, K, 1, tiled);
     launched("gemm_w4_silu");
 }
 
