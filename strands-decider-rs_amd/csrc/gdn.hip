@@ -569,12 +569,20 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
         __syncthreads();
         // Both column sums come from the previous state, so they are independent:
         //   S_t = dc S + kn delta^T, delta = beta (v - dc S^T kn), o = S_t^T qn = dc S^T qn + (kn . qn) delta
-        for (int tt = 0; tt < nt; tt++) {
-            const float4 qa = Qs[tt][r0 / 4], qb = Qs[tt][r0 / 4 + 1];
-            const float4 ka = Ks[tt][r0 / 4], kb = Ks[tt][r0 / 4 + 1];
-            const float qn[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-            const float kn[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
-            const float dc = Dc[tt];
+        // A token's operands do not depend on the state: those of token tt + 1 are read from LDS
+        // while token tt runs (the chain per token is then FMAs and DPP sums only).
+        struct Tok {
+            float4 qa, qb, ka, kb;
+            float dc, bt, v, kq;
+        };
+        auto tok = [&](int tt) {
+            return Tok{Qs[tt][r0 / 4], Qs[tt][r0 / 4 + 1], Ks[tt][r0 / 4], Ks[tt][r0 / 4 + 1],
+                       Dc[tt],         Bt[tt],             Vs[tt][cl],     KQ[tt]};
+        };
+        auto run = [&](const Tok& x, int tt) {
+            const float qn[8] = {x.qa.x, x.qa.y, x.qa.z, x.qa.w, x.qb.x, x.qb.y, x.qb.z, x.qb.w};
+            const float kn[8] = {x.ka.x, x.ka.y, x.ka.z, x.ka.w, x.kb.x, x.kb.y, x.kb.z, x.kb.w};
+            const float dc = x.dc;
             float sk = 0.f, sq = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -583,12 +591,22 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
             }
             sk = row_allsum16(sk);
             sq = row_allsum16(sq);
-            const float delta = (Vs[tt][cl] - dc * sk) * Bt[tt];
-            const float oc = dc * sq + KQ[tt] * delta;
+            const float delta = (x.v - dc * sk) * x.bt;
+            const float oc = dc * sq + x.kq * delta;
 #pragma unroll
             for (int i = 0; i < 8; i++) S[i] = dc * S[i] + kn[i] * delta;
             if ((lane & 15) == 0) o[(size_t)(tb + tt) * sh.H * DV + h * DV + col] = oc;
+        };
+        // two tokens per iteration, their operand sets alternating (no register copies)
+        Tok ta = tok(0);
+        int tt = 0;
+        for (; tt + 1 < nt; tt += 2) {
+            const Tok tb2 = tok(tt + 1);
+            run(ta, tt);
+            ta = tok(min(tt + 2, nt - 1));
+            run(tb2, tt + 1);
         }
+        if (tt < nt) run(ta, tt);
     }
     if (seqt) return;  // several sequences: their final states are not kept
 #pragma unroll
