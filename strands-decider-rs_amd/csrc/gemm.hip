@@ -808,13 +808,26 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
         // weights): N = 12288: (4,1) 31.5 us; N = 8256: (3,1) 24.8 us; N = 5120: (3,1) with k halves
         // 16.8 us; N = 2048: (2,1) with 2 splits 9.8 us (K = 2048), (4,1) with 4 splits 18.8 us
         // (K = 6144; (2,1) is 18.2 us alone but 22.5 us inside the forward).
+        // (3,1) with k halves holds one 512-thread workgroup per CU: only for grids of one round
+        const bool one_round = (size_t)((N + 127) / 128) * ((M + 95) / 96) <= 256;
         if (N >= 10000) p.cfg = W41;
-        else if (N >= 7000 || (N >= 4000 && !halves_ok)) p.cfg = W31;
-        else if (N >= 4000) p.cfg = W31h;
+        else if (N >= 4000) p.cfg = halves_ok && one_round ? W31h : W31;
         else if (partial_ok && K > 3000) p = GemmPlan{W41, 4};
         else if (partial_ok) p = GemmPlan{W21, 2};
         else p.cfg = W21;
         return fit(p);
+    }
+    if (!exact && wide_ok && M > 1024) {
+        // Long prefill, no K split (sweep at M = 1536 and 2048): gate_up (4,1) 106.9 us at 2048, (3,1)
+        // 80.1 us at 1536; in_proj (3,1) 77.2 / 61.2 us; qkv (4,1) 51.9 / 35.3 us; N = 2048 (3,1)
+        // with k halves where its grid is one round (43.2 us down, 17.6 us o at 1536), else (4,1)
+        // (57.9 / 22.3 us at 2048).  The 16x16 (4,2) tiles take 26-50% longer at these sizes.
+        const bool one_round = (size_t)((N + 127) / 128) * ((M + 95) / 96) <= 256;
+        if (N >= 10000) p.cfg = M >= 1792 ? W41 : W31;
+        else if (N >= 7000) p.cfg = W31;
+        else if (N >= 4000) p.cfg = W41;
+        else p.cfg = halves_ok && one_round ? W31h : W41;
+        return p;
     }
     if (!exact && wide_ok && M > 64 && M < 256) {
         // Batched questions (M = 120): in_proj (N = 8256, f16 out) (2,1) with k halves 13.0 us;

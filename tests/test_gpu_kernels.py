@@ -49,6 +49,7 @@ def check_gemm(oracle, A, W, S, Y, N, K, exact):
     (128, 6144, 2048),
     (1, 64, 128), (5, 320, 256), (17, 200, 384), (40, 2048, 2048), (64, 8256, 2048),
     (100, 1000, 512), (512, 2048, 6144), (300, 5120, 2048),
+    (1100, 640, 512), (2100, 384, 256),  # long prefill: (3,1) with k halves, (4,1)
 ])
 def test_gemm_matches_oracle(sdamd, synth, oracle, M, N, K):
     rng = np.random.default_rng(M * 7919 + N * 31 + K)
