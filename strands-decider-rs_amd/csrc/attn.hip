@@ -86,6 +86,12 @@ __global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, At
     }
 }
 
+// The online softmax runs in base 2: scores are scaled by log2(e) and exponentiated with
+// v_exp_f32, exp(s - m) = 2^(s log2 e - m log2 e); max and sum states (also those the combine kernel
+// merges) are in these units.
+constexpr float LOG2E = 1.4426950408889634f;
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ float wave_max16(float v) {  // max over lanes {l, l^16, l^32, l^48}
     v = fmaxf(v, __shfl_xor(v, 16));
     return fmaxf(v, __shfl_xor(v, 32));
@@ -181,23 +187,28 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         }
         float sv[8];
         float tmax = -INFINITY;
+        // a block before every query of the workgroup (and, with several sequences, inside the
+        // shared prefix) needs no mask; the rows of queries past nq are computed but never stored
+        const bool open = j0 + KB <= kend && j0 + KB <= P + t0 + 1 && (!rowt || j0 + KB <= P);
 #pragma unroll
         for (int tt = 0; tt < 2; tt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int j = j0 + 8 * fg + 4 * tt + r;
-                const float v = (qok && j < kend && j <= qpos && (j < P || j >= qlo)) ? st2[tt][r] : -INFINITY;
+                const float v = (open || (qok && j < kend && j <= qpos && (j < P || j >= qlo))) ? st2[tt][r] * LOG2E
+                                                                                                : -INFINITY;
                 sv[tt * 4 + r] = v;
                 tmax = fmaxf(tmax, v);
             }
         tmax = wave_max16(tmax);
         const float m_new = fmaxf(m_run, tmax);
-        const float alpha = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+        const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_run - m_new);
+        const float m_sub = m_new == -INFINITY ? 0.f : m_new;  // every key masked so far: p = 2^-inf = 0
         float psum = 0.f;
         f16x8 ph, pl;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const float pv = sv[e] == -INFINITY ? 0.f : expf(sv[e] - m_new);
+            const float pv = exp2_fast(sv[e] - m_sub);
             psum += pv;
             const f16 hi = (f16)pv;
             ph[e] = hi;
@@ -235,7 +246,7 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         float l = 0.f;
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            const float f = Lm[w][q] > 0.f ? expf(Mm[w][q] - m) : 0.f;
+            const float f = Lm[w][q] > 0.f ? exp2_fast(Mm[w][q] - m) : 0.f;
             l += Lm[w][q] * f;
             Fw[q][w] = f;
         }
@@ -288,7 +299,7 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ p
         const size_t r = ((size_t)z * L + t) * s.HQ + h;
         const float lz = pml[r * 2 + 1];
         if (lz > 0.f) {
-            const float f = expf(pml[r * 2] - m);
+            const float f = exp2_fast(pml[r * 2] - m);
             l += lz * f;
             a += pacc[r * HD + d] * f;
         }
