@@ -15,25 +15,30 @@ __device__ __forceinline__ uint32_t qcode(const uint32_t* __restrict__ Q, size_t
     return lo;
 }
 
-// x[t, :] = dequantized row ids[t] (src/kernels.rs:63-89).  One thread per 32-element block.
-__global__ void k_embed(const uint32_t* __restrict__ ids, int L, const uint32_t* __restrict__ Q,
-                        const f16* __restrict__ S, const f16* __restrict__ Bi, int d, int bits, int group, int asym,
-                        float* __restrict__ x) {
+// x[t, :] = dequantized row ids[t] (src/kernels.rs:63-89).  One thread per 8 consecutive elements
+// (a quarter of a 32-element block): two 16-byte stores, so that a wave writes 2 KiB of a row.
+__global__ __launch_bounds__(256) void k_embed(const uint32_t* __restrict__ ids, int L,
+                                               const uint32_t* __restrict__ Q, const f16* __restrict__ S,
+                                               const f16* __restrict__ Bi, int d, int bits, int group, int asym,
+                                               float* __restrict__ x) {
     const int t = blockIdx.y;
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    const int nb = d >> 5;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // 8-element part of the row
+    const int nb = d >> 5, b = i >> 2, e0 = 8 * (i & 3);
     if (t >= L || b >= nb) return;
     const size_t blk = (size_t)ids[t] * nb + b;
     const size_t gi = group == 32 ? blk : blk / (size_t)(group >> 5);
     const float sc = (float)S[gi];
     const float bi = asym ? (float)Bi[gi] : 0.f;
     const float off = (float)(1 << (bits - 1));
-    float* out = x + (size_t)t * d + b * 32;
-#pragma unroll 8
-    for (int e = 0; e < 32; e++) {
-        const float q = (float)qcode(Q, blk, e, bits);
-        out[e] = asym ? q * sc + bi : (q - off) * sc;
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const float q = (float)qcode(Q, blk, e0 + u, bits);
+        v[u] = asym ? q * sc + bi : (q - off) * sc;
     }
+    float4* out = reinterpret_cast<float4*>(x + (size_t)t * d + b * 32 + e0);
+    out[0] = float4{v[0], v[1], v[2], v[3]};
+    out[1] = float4{v[4], v[5], v[6], v[7]};
 }
 
 // One workgroup (256 threads) per output row; D = d / 256 values per thread.
@@ -204,8 +209,8 @@ void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f1
            bool asym, float* x, hipStream_t st) {
     SD_CHECK(d % 32 == 0 && (bits == 2 || bits == 3 || bits == 4) && group % 32 == 0 && group > 0,
              "embed: unsupported format");
-    const int nb = d / 32;
-    hipLaunchKernelGGL(k_embed, dim3((nb + 63) / 64, L), dim3(64), 0, st, ids, L, Q, S, Bi, d, bits, group,
+    const int parts = d / 8;  // 8-element parts per row
+    hipLaunchKernelGGL(k_embed, dim3((parts + 255) / 256, L), dim3(256), 0, st, ids, L, Q, S, Bi, d, bits, group,
                        (int)asym, x);
     launched("embed");
 }
