@@ -805,12 +805,14 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
     };
     if (!exact && wide_ok && M >= 256 && M <= 1024) {
         // Prefill-sized M; from a sweep of the 2B's shapes at M = 512 on MI355X (random data, tiled
-        // weights): N = 12288: (4,1) 31.5 us; N = 8256: (3,1) 24.8 us; N = 5120: (3,1) with k halves
-        // 16.8 us; N = 2048: (2,1) with 2 splits 9.8 us (K = 2048), (4,1) with 4 splits 18.8 us
-        // (K = 6144; (2,1) is 18.2 us alone but 22.5 us inside the forward).
+        // weights): N = 12288 with the SiLU epilogue: (2,1) 33.2 us, (4,1) 34.5 us (3 runs each on
+        // one box; 768 workgroups are 3 per CU where 384 are 1.5); N = 8256: (3,1) 24.8 us;
+        // N = 5120: (3,1) with k halves 16.8 us; N = 2048: (2,1) with 2 splits 9.8 us (K = 2048),
+        // (4,1) with 4 splits 18.8 us (K = 6144; (2,1) is 18.2 us alone but 22.5 us inside the
+        // forward).
         // (3,1) with k halves holds one 512-thread workgroup per CU: only for grids of one round
         const bool one_round = (size_t)((N + 127) / 128) * ((M + 95) / 96) <= 256;
-        if (N >= 10000) p.cfg = W41;
+        if (N >= 10000) p.cfg = W21;
         else if (N >= 4000) p.cfg = halves_ok && one_round ? W31h : W31;
         else if (partial_ok && K > 3000) p = GemmPlan{W41, 4};
         else if (partial_ok) p = GemmPlan{W21, 2};
