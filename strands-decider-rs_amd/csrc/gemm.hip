@@ -807,7 +807,8 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
         // Prefill-sized M; from a sweep of the 2B's shapes at M = 512 on MI355X (random data, tiled
         // weights): N = 12288 with the SiLU epilogue: (2,1) 33.2 us, (4,1) 34.5 us (3 runs each on
         // one box; 768 workgroups are 3 per CU where 384 are 1.5); N = 8256: (3,1) 24.8 us;
-        // N = 5120: (3,1) with k halves 16.8 us; N = 2048: (2,1) with 2 splits 9.8 us (K = 2048),
+        // N = 5120: (3,1) with k halves 16.8 us; N = 2048: (2,1) with k halves and 2 splits 9.0 us
+        // (K = 2048; 9.6 us without k halves, 3 runs each on one box),
         // (4,1) with 4 splits 18.8 us (K = 6144; (2,1) is 18.2 us alone but 22.5 us inside the
         // forward).
         // (3,1) with k halves holds one 512-thread workgroup per CU: only for grids of one round
@@ -815,7 +816,7 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
         if (N >= 10000) p.cfg = W21;
         else if (N >= 4000) p.cfg = halves_ok && one_round ? W31h : W31;
         else if (partial_ok && K > 3000) p = GemmPlan{W41, 4};
-        else if (partial_ok) p = GemmPlan{W21, 2};
+        else if (partial_ok) p = GemmPlan{halves_ok ? W21h : W21, 2};  // k halves: 9.04 vs 9.56 us
         else p.cfg = W21;
         return fit(p);
     }
