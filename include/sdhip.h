@@ -55,13 +55,18 @@ typedef struct {
     int32_t had; /* online Hadamard size, -1 when absent (rejected, as in src/engine.rs:248-250) */
 } sd_tensor;
 
-/* The embedding rows file, `model::Embed` (src/model.rs:92-103), rows already in GPU layout. */
+/* The embedding rows file, `model::Embed` (src/model.rs:92-103).  Rows are in token-id order, the
+ * parts of a row back to back.  With u8 = 1 a row stores its "embed.s" part as 8-bit scale codes (a
+ * 4-byte header and one code per scale, decoded at load as `embed_parts` does, src/model.rs:260-283)
+ * and is wire_row_bytes long; otherwise rows are row_bytes long (wire_row_bytes 0). */
 typedef struct {
     const char* rows_path;
     uint64_t vocab, row_bytes;
     size_t n_parts;
     const char* const* part_names; /* e.g. "embed.q", "embed.s" */
-    const uint64_t* part_bytes;    /* bytes per row of each part */
+    const uint64_t* part_bytes;    /* bytes per row of each part in GPU layout */
+    uint64_t wire_row_bytes;       /* bytes per stored row when they differ from row_bytes, else 0 */
+    int32_t u8;                    /* "embed.s" stored as 8-bit scale codes */
 } sd_embed;
 
 /* `Engine::load(dir, &Manifest)` (src/engine.rs:175-303): uploads the shards (shard i holds the
@@ -70,6 +75,12 @@ typedef struct {
 int sd_engine_load(const sd_config* cfg, const sd_tensor* tensors, size_t n_tensors, const char* const* shard_paths,
                    const uint64_t* shard_starts, const uint64_t* shard_bytes, size_t n_shards, const sd_embed* embed,
                    sd_engine** out, char* err, size_t errlen);
+
+/* `decode_scales` (src/model.rs:217-236), the load-time decode of 8-bit scale codes: n rows of g
+ * codes at src (first a 4-byte header per row: m as f16 bits and j as u16, little-endian; then the
+ * n*g codes, sign << 7 | k) into n*g f16 scales (bits) at dst: |scale| = f16(f32(m 2^(-k j / 4096))).
+ * Host only; no device is used. */
+void sd_decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst);
 
 /* Drop of `Engine`. */
 void sd_engine_free(sd_engine* e);
@@ -169,6 +180,71 @@ int sd_op_repack_w4(void* Wq, void* Sc, int N, int K, void* stream, char* err, s
 int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off, const void* negA, const void* dtb,
               int L, int H, int dk, int dv, void* state, int load_state, void* o, void* stream, char* err,
               size_t errlen);
+
+/* The reference's matmul_gemv(f) (src/kernels.rs:590-635, decode 550-576) for any of its weight
+ * formats, on device buffers in the model's layout: Y[M,N] f16 = A[M,K] f16 . deq(W)^T with W
+ * [N][K/32] blocks of 4*bits bytes (int2/int3/int4), scales [N][K/group] f16 and, when asym, biases
+ * Bi [N][K/group] f16; the weights are dequantized in f32 ((q - 2^(bits-1)) s, or fma(q, s, b)). */
+int sd_op_matmul_fmt(const void* A, const void* Wq, const void* Sc, const void* Bi, void* Y, int M, int N, int K,
+                     int bits, int group, int asym, void* stream, char* err, size_t errlen);
+
+/* No counterpart in the reference: the split-K form of sd_op_matmul that the engine uses for the
+ * projections feeding the residual add: part[z][M][N] f32 (z < ks) holds the partial product over
+ * the z-th k range, whose slot-order sum rounded to f16 is Y.  exact = 1: the f32-dequant GEMV (cfg
+ * ignored); else configuration cfg (0 <= cfg) with f16 dequant.  packed as in sd_op_matmul. */
+int sd_op_matmul_split(const void* A, const void* Wq, const void* Sc, void* part, int M, int N, int K, int exact,
+                       int cfg, int ks, int packed, void* stream, char* err, size_t errlen);
+
+/* gate_up followed by silu_mul (src/kernels.rs:123-135, 590-709) as the engine fuses them:
+ * mid[M][N/2] f16 = f16(silu(g) * u) with [g | u] = f16(A . deq(W)^T), W the model's gate_up ([gate
+ * (N/2) | up (N/2)] rows, int4 g32).  exact = 1: the GEMV's f32 dequant, else the tiled f16 dequant
+ * with configuration cfg (< 0: the engine's choice). */
+int sd_op_gate_up_silu(const void* A, const void* Wq, const void* Sc, void* mid, int M, int N, int K, int exact, int cfg,
+                       void* stream, char* err, size_t errlen);
+
+/* embed (src/kernels.rs:63-89): x[L][d] f32 = the dequantized table rows ids[0..L) (u32), table Q
+ * [vocab][d/32][bits] u32 words, scales S (and asym biases Bi) [vocab][d/group] f16. */
+int sd_op_embed(const void* ids, int L, const void* Q, const void* S, const void* Bi, int d, int bits, int group, int asym,
+                void* x, void* stream, char* err, size_t errlen);
+
+/* add_norm (src/kernels.rs:93-120): for r < nrows, row = rows[r] (u32; rows null: r): x[row] += y[row]
+ * (f16 [.][d], nullable: no add), then out[r] = x[row] rsqrt(mean(x[row]^2) + 1e-6) w as f16 (h16)
+ * or f32 (h32); exactly one of h16, h32. */
+int sd_op_add_norm(void* x, const void* y, const void* w, int d, const void* rows, int nrows, void* h16, void* h32,
+                   void* stream, char* err, size_t errlen);
+
+/* silu_mul (src/kernels.rs:123-135): mid[L][I] f16 = f16(silu(g) u), big[L] = [g (I) | u (I)] f16. */
+int sd_op_silu_mul(const void* big, int L, int I, void* mid, void* stream, char* err, size_t errlen);
+
+/* add_bias (src/kernels.rs:138-149): y[L][N] f16 += c[N] f32 (the adapter layers' bias). */
+int sd_op_add_bias(void* y, int L, int N, const void* c, void* stream, char* err, size_t errlen);
+
+/* conv (src/kernels.rs:152-170): out[t][c] f32 = silu(sum_j w[c][j] x[t + j - 3][c]) over channels
+ * c < C of big [L][stride] f16, rows before 0 from hist [3][C] f16; w [C][4] f32. */
+int sd_op_conv(const void* big, int stride, int L, int C, const void* w, const void* hist, void* out, void* stream,
+               char* err, size_t errlen);
+
+/* gnorm (src/kernels.rs:377-396): out[t][h*DV + c] f16 = f16(w[c] o rsqrt(mean_c(o^2) + 1e-6) silu(z)),
+ * o [L][H*DV] f32, z = big[t*stride + z_off + h*DV + c] f16, w [DV] f32 (DV = 128). */
+int sd_op_gnorm(const void* o, const void* big, int stride, int z_off, const void* w, int L, int H, int DV, void* out,
+                void* stream, char* err, size_t errlen);
+
+/* qk_prep then attn (src/kernels.rs:400-541) for one sequence at cache rows P .. P+L-1: Q [HQ][L][HD]
+ * f16 receives the normed, rotated queries; K cache Kc [HK][ctx][HD] and the transposed V cache Vt
+ * [HK][HD][ctx] (f16, the engine's layouts) receive rows P .. P+L-1, rows below P are the prefix; out
+ * [L][HQ*HD] f16 the gated attention output.  big [L][stride] holds [q | gate] per q head, then K,
+ * V heads; rope [ctx][RD/2][2] f32 (cos, sin).  head_dim 256 only. */
+int sd_op_attention(const void* big, int stride, const void* qw, const void* kw, const void* rope, int L, int P, int HQ,
+                    int HK, int HD, int RD, void* Q, void* Kc, void* Vt, int ctx, void* out, void* stream, char* err,
+                    size_t errlen);
+
+/* No counterpart in the reference (a test hook for per-layer parity): the forward of ids from cache
+ * (nullable) run step by step; after every residual add + RMSNorm of the layers (each layer's
+ * in_norm, then its post_norm) the residual x (f32) and the normalized h (f16 bits) of rows[0..n_rows)
+ * are copied to x_out / h_out + tap * n_rows * hidden.  At most cap taps are copied; *n_taps receives
+ * the number the forward has.  The live state afterwards is that of a forward without keep. */
+int sd_engine_trace(sd_engine* e, const uint32_t* ids, size_t n, const sd_snapshot* cache, const size_t* rows,
+                    size_t n_rows, float* x_out, uint16_t* h_out, size_t cap, size_t* n_taps, char* err, size_t errlen);
 
 #ifdef __cplusplus
 }

@@ -94,6 +94,45 @@ def add_norm(x, y16, w, rows=None, out_f32=False):
     return out
 
 
+def embed(ids, Q, S, d, bits=4, group=32, asym=False, Bi=None):
+    """x[L, d] f32 = the dequantized table rows ids (src/kernels.rs:63-89)."""
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    x = np.empty((len(ids), d), np.float32)
+    lib().or_embed(P(ids), I(len(ids)), P(np.ascontiguousarray(Q, dtype=np.uint32)),
+                   P(np.ascontiguousarray(S, dtype=np.uint16)),
+                   P(None if Bi is None else np.ascontiguousarray(Bi, dtype=np.uint16)), I(d), I(bits), I(group),
+                   I(int(asym)), P(x))
+    return x
+
+
+def add_bias(y16, c):
+    """y[t, j] = f16(f32(y) + c[j]) on f16 bits (src/kernels.rs:138-149)."""
+    y = np.ascontiguousarray(y16, dtype=np.uint16).copy()
+    L, N = y.shape
+    lib().or_add_bias(P(y), I(L), I(N), P(np.ascontiguousarray(c, dtype=np.float32)))
+    return y
+
+
+def decode_scale_codes(src, n, g):
+    """8-bit scale codes -> f16 bits [n, g] (src/model.rs:217-236): each of the n rows has a 4-byte
+    header (m as f16 bits, j as u16, little-endian), then the n*g codes follow, sign << 7 | k each;
+    |scale| = f16(f32(m * 2^(-k j / 4096))) with the power and product in f64, and the code's sign
+    bit becomes the f16 sign bit."""
+    src = np.frombuffer(bytes(src), np.uint8)
+    return decode_scale_rows(src[:4 * n].reshape(n, 4), src[4 * n:4 * n + n * g].reshape(n, g))
+
+
+def decode_scale_rows(head, codes):
+    """decode_scale_codes with the headers [n, 4] and codes [n, g] (u8) given apart."""
+    h = np.ascontiguousarray(head, dtype=np.uint8).view(np.uint16).reshape(-1, 2)
+    c = np.asarray(codes, dtype=np.uint16)
+    m = h[:, 0].view(np.float16).astype(np.float64)[:, None]
+    j = h[:, 1].astype(np.float64)[:, None]
+    k = (c & 127).astype(np.float64)
+    mag = (m * np.power(2.0, -(k * j) / 4096.0)).astype(np.float32).astype(np.float16).view(np.uint16)
+    return mag | ((c & 128) << 8).astype(np.uint16)
+
+
 def rope_table(rd, theta, ctx=CONTEXT):
     t = np.empty((ctx, rd), np.float32)
     lib().or_rope_table(I(ctx), I(rd), ctypes.c_double(theta), P(t))
@@ -127,11 +166,22 @@ class OracleModel:
             data = np.fromfile(os.path.join(model_dir, f"weights.{i}.bin"), dtype=np.uint8)
             self.shards.append((s["start"], s["bytes"], data))
         e = m["embed"]
-        rows = np.fromfile(os.path.join(model_dir, e["rows"]), dtype=np.uint8).reshape(e["vocab"], e["row_bytes"])
+        # embedding rows in token-id order, parts back to back; with `u8` the row stores the scale
+        # part as 8-bit codes (4-byte header + one code per scale) and is wire_row_bytes long
+        # (src/model.rs:260-283)
+        u8 = bool(e.get("u8", False))
+        rb = e.get("wire_row_bytes") or e["row_bytes"]
+        rows = np.fromfile(os.path.join(model_dir, e["rows"]), dtype=np.uint8).reshape(e["vocab"], rb)
         self.embed, off = {}, 0
         for name, b in e["parts"]:
-            self.embed[name] = np.ascontiguousarray(rows[:, off:off + b]).reshape(-1)
-            off += b
+            if u8 and name == "embed.s":
+                g = b // 2
+                part = decode_scale_rows(rows[:, off:off + 4], rows[:, off + 4:off + 4 + g])
+                self.embed[name] = np.ascontiguousarray(part).view(np.uint8).reshape(-1)
+                off += 4 + g
+            else:
+                self.embed[name] = np.ascontiguousarray(rows[:, off:off + b]).reshape(-1)
+                off += b
         self.d = c["hidden_size"]
         self.I = c["intermediate_size"]
         self.H, self.DK, self.DV = c["linear_num_key_heads"], c["linear_key_head_dim"], c["linear_value_head_dim"]
@@ -173,9 +223,13 @@ class OracleModel:
         return matmul(a16, self.raw(name + ".q", np.uint32), self.raw(name + ".s", np.uint16), N, K, f16_deq,
                       bits, group, asym, Bi)
 
-    def forward(self, ids, rows, cache=None, keep=False, trace=None):
+    def forward(self, ids, rows, cache=None, keep=False, trace=None, taps=None, tap_rows=None):
         """Hidden rows [len(rows), d] f32 (and a Snapshot when keep); src/engine.rs:529-662.
-        `trace`, when a list, receives (label, array) per sublayer output for per-layer checks."""
+        `trace`, when a list, receives (label, array) per sublayer output for per-layer checks.
+        `taps`, when a list, receives (x, h) after every residual add + RMSNorm of the layers (in
+        plan order: each layer's in_norm, then its post_norm): the residual stream x (f32) and the
+        normalized activations h (f16 bits) that feed the next sublayer, of the rows tap_rows (all
+        rows when None)."""
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         L = len(ids)
         Pn = cache.len if cache else 0
@@ -201,9 +255,16 @@ class OracleModel:
                    P(self.raw("embed.b", np.uint16) if ef.get("asym") else None), I(d), I(ef.get("bits", 4)),
                    I(ef.get("group", 32)), I(int(ef.get("asym", False))), P(x))
         y = None
+        sel = slice(None) if tap_rows is None else np.asarray(tap_rows)
+
+        def tap(h):
+            if taps is not None:
+                taps.append((x[sel].copy(), h[sel].copy()))
+            return h
+
         for i, kind in enumerate(self.kinds):
             p = f"layers.{i}."
-            h = add_norm(x, y if i > 0 else None, self.f32(p + "in_norm"))
+            h = tap(add_norm(x, y if i > 0 else None, self.f32(p + "in_norm")))
             if kind == "adapter":
                 y = self.mm(h, p + "proj", L)
                 o.or_add_bias(P(y), I(L), I(d), P(self.f32(p + "bias")))
@@ -239,7 +300,7 @@ class OracleModel:
                     trace.append((f"{i}.attn", att.copy()))
             if trace is not None:
                 trace.append((f"{i}.mixer", y.copy()))
-            h = add_norm(x, y, self.f32(p + "post_norm"))
+            h = tap(add_norm(x, y, self.f32(p + "post_norm")))
             big = self.mm(h, p + "gate_up", L)
             mid = np.empty((L, self.I), np.uint16)
             o.or_silu_mul(P(big), I(L), I(self.I), P(mid))

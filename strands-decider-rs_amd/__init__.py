@@ -27,8 +27,12 @@ SYMBOLS = [
     "sd_engine_load", "sd_engine_free", "sd_engine_hidden_size", "sd_engine_adapter", "sd_engine_forward",
     "sd_snapshot_len", "sd_snapshot_free", "sd_engine_profile", "sd_head_load", "sd_head_free", "sd_head_probs",
     "sd_ask_ids", "sd_op_matmul", "sd_op_gdn", "sd_engine_forward_batch", "sd_engine_ask_batch",
-    "sd_op_repack_w4",
+    "sd_op_repack_w4", "sd_decode_scale_codes", "sd_op_matmul_fmt", "sd_op_matmul_split", "sd_op_gate_up_silu",
+    "sd_op_embed", "sd_op_add_norm", "sd_op_silu_mul", "sd_op_add_bias", "sd_op_conv", "sd_op_gnorm",
+    "sd_op_attention", "sd_engine_trace",
 ]
+VOID_SYMBOLS = ("sd_engine_free", "sd_snapshot_free", "sd_head_free", "sd_engine_hidden_size", "sd_engine_adapter",
+                "sd_snapshot_len", "sd_decode_scale_codes")
 
 
 class EngineError(RuntimeError):
@@ -56,6 +60,7 @@ class sd_embed(C.Structure):
     _fields_ = [
         ("rows_path", C.c_char_p), ("vocab", C.c_uint64), ("row_bytes", C.c_uint64), ("n_parts", C.c_size_t),
         ("part_names", C.POINTER(C.c_char_p)), ("part_bytes", C.POINTER(C.c_uint64)),
+        ("wire_row_bytes", C.c_uint64), ("u8", C.c_int32),
     ]
 
 
@@ -96,9 +101,21 @@ def lib():
         L.sd_op_matmul.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, err, sz]
         L.sd_op_repack_w4.argtypes = [vp, vp, i32, i32, vp, err, sz]
         L.sd_op_gdn.argtypes = [vp, vp, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, err, sz]
+        L.sd_decode_scale_codes.argtypes = [vp, sz, sz, vp]
+        L.sd_decode_scale_codes.restype = None
+        L.sd_op_matmul_fmt.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, err, sz]
+        L.sd_op_matmul_split.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, err, sz]
+        L.sd_op_gate_up_silu.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, err, sz]
+        L.sd_op_embed.argtypes = [vp, i32, vp, vp, vp, i32, i32, i32, i32, vp, vp, err, sz]
+        L.sd_op_add_norm.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp, vp, err, sz]
+        L.sd_op_silu_mul.argtypes = [vp, i32, i32, vp, vp, err, sz]
+        L.sd_op_add_bias.argtypes = [vp, i32, i32, vp, vp, err, sz]
+        L.sd_op_conv.argtypes = [vp, i32, i32, i32, vp, vp, vp, vp, err, sz]
+        L.sd_op_gnorm.argtypes = [vp, vp, i32, i32, vp, i32, i32, i32, vp, vp, err, sz]
+        L.sd_op_attention.argtypes = [vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, err, sz]
+        L.sd_engine_trace.argtypes = [vp, vp, sz, vp, vp, sz, vp, vp, sz, C.POINTER(sz), err, sz]
         for name in SYMBOLS:
-            if name not in ("sd_engine_free", "sd_snapshot_free", "sd_head_free", "sd_engine_hidden_size",
-                            "sd_engine_adapter", "sd_snapshot_len"):
+            if name not in VOID_SYMBOLS:
                 getattr(L, name).restype = i32
         _lib = L
     return _lib
@@ -187,11 +204,10 @@ class Engine:
         e = m.embed
         if e is None:
             raise EngineError("manifest has no embedding")
-        if e.u8 or e.wire_row_bytes is not None:
-            raise EngineError("packed (wire) embedding rows are a download format; convert them first")
         pn = [p[0].encode() for p in e.parts]
         emb = sd_embed(os.path.join(model_dir, e.rows).encode(), e.vocab, e.row_bytes, len(pn),
-                       (C.c_char_p * len(pn))(*pn), (C.c_uint64 * len(pn))(*[p[1] for p in e.parts]))
+                       (C.c_char_p * len(pn))(*pn), (C.c_uint64 * len(pn))(*[p[1] for p in e.parts]),
+                       e.wire_row_bytes or 0, int(bool(e.u8)))
         h = C.c_void_p()
         _call(lib().sd_engine_load, C.byref(cfg), ts, len(names), cpaths, starts, sizes, len(m.shards),
               C.byref(emb), C.byref(h))
@@ -274,6 +290,21 @@ class Engine:
         n = C.c_size_t()
         _call(lib().sd_engine_profile, self._h, _ptr(ids), len(ids), labels, ms, cap, C.byref(n))
         return [(labels[i].decode(), ms[i]) for i in range(min(n.value, cap))]
+
+    def trace(self, ids, rows, cache: Snapshot | None = None, cap: int = 256):
+        """Per-layer activations (a test hook, no counterpart in the reference): after every residual
+        add + RMSNorm of the layers, the residual x [len(rows), d] f32 and the normalized h (f16) of
+        the given rows.  Returns [(x, h)] in plan order."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        rows_a = np.ascontiguousarray(rows, dtype=np.uintp)
+        d = self.hidden_size()
+        x = np.empty((cap, len(rows_a), d), np.float32)
+        h = np.empty((cap, len(rows_a), d), np.uint16)
+        n = C.c_size_t()
+        _call(lib().sd_engine_trace, self._h, _ptr(ids), len(ids), cache._h if cache is not None else None,
+              _ptr(rows_a), len(rows_a), _ptr(x), _ptr(h), cap, C.byref(n))
+        k = min(n.value, cap)
+        return [(x[i], h[i].view(np.float16).astype(np.float32)) for i in range(k)]
 
     def free(self):
         if self._h:
@@ -370,3 +401,64 @@ def op_repack_w4(Wq, Sc, N, K, stream=None):
 def op_gdn(qkv, big, stride, a_off, b_off, negA, dtb, L, H, dk, dv, state, load_state, o, stream=None):
     _call(lib().sd_op_gdn, C.c_void_p(qkv), C.c_void_p(big), stride, a_off, b_off, C.c_void_p(negA), C.c_void_p(dtb),
           L, H, dk, dv, C.c_void_p(state), int(load_state), C.c_void_p(o), C.c_void_p(stream) if stream else None)
+
+
+def decode_scale_codes(src: bytes, n: int, g: int) -> np.ndarray:
+    """sd_decode_scale_codes (src/model.rs:217-236): n rows of g 8-bit scale codes -> f16 bits [n, g]."""
+    buf = np.frombuffer(bytes(src), np.uint8).copy()
+    out = np.empty((n, g), np.uint16)
+    lib().sd_decode_scale_codes(_ptr(buf), n, g, _ptr(out))
+    return out
+
+
+def _sp(stream):
+    return C.c_void_p(stream) if stream else None
+
+
+def op_matmul_fmt(A, Wq, Sc, Bi, Y, M, N, K, bits, group, asym, stream=None):
+    """sd_op_matmul_fmt: the reference GEMV for any weight format (model layout, f32 dequant)."""
+    _call(lib().sd_op_matmul_fmt, C.c_void_p(A), C.c_void_p(Wq), C.c_void_p(Sc), C.c_void_p(Bi) if Bi else None,
+          C.c_void_p(Y), M, N, K, bits, group, int(asym), _sp(stream))
+
+
+def op_matmul_split(A, Wq, Sc, part, M, N, K, exact, cfg, ks, packed=False, stream=None):
+    _call(lib().sd_op_matmul_split, C.c_void_p(A), C.c_void_p(Wq), C.c_void_p(Sc), C.c_void_p(part), M, N, K,
+          int(exact), cfg, ks, int(packed), _sp(stream))
+
+
+def op_gate_up_silu(A, Wq, Sc, mid, M, N, K, exact, cfg=-1, stream=None):
+    _call(lib().sd_op_gate_up_silu, C.c_void_p(A), C.c_void_p(Wq), C.c_void_p(Sc), C.c_void_p(mid), M, N, K,
+          int(exact), cfg, _sp(stream))
+
+
+def op_embed(ids, L, Q, S, Bi, d, bits, group, asym, x, stream=None):
+    _call(lib().sd_op_embed, C.c_void_p(ids), L, C.c_void_p(Q), C.c_void_p(S), C.c_void_p(Bi) if Bi else None, d, bits,
+          group, int(asym), C.c_void_p(x), _sp(stream))
+
+
+def op_add_norm(x, y, w, d, rows, nrows, h16=None, h32=None, stream=None):
+    _call(lib().sd_op_add_norm, C.c_void_p(x), C.c_void_p(y) if y else None, C.c_void_p(w), d,
+          C.c_void_p(rows) if rows else None, nrows, C.c_void_p(h16) if h16 else None, C.c_void_p(h32) if h32 else None,
+          _sp(stream))
+
+
+def op_silu_mul(big, L, I_, mid, stream=None):
+    _call(lib().sd_op_silu_mul, C.c_void_p(big), L, I_, C.c_void_p(mid), _sp(stream))
+
+
+def op_add_bias(y, L, N, c, stream=None):
+    _call(lib().sd_op_add_bias, C.c_void_p(y), L, N, C.c_void_p(c), _sp(stream))
+
+
+def op_conv(big, stride, L, Cn, w, hist, out, stream=None):
+    _call(lib().sd_op_conv, C.c_void_p(big), stride, L, Cn, C.c_void_p(w), C.c_void_p(hist), C.c_void_p(out), _sp(stream))
+
+
+def op_gnorm(o, big, stride, z_off, w, L, H, DV, out, stream=None):
+    _call(lib().sd_op_gnorm, C.c_void_p(o), C.c_void_p(big), stride, z_off, C.c_void_p(w), L, H, DV, C.c_void_p(out),
+          _sp(stream))
+
+
+def op_attention(big, stride, qw, kw, rope, L, P, HQ, HK, HD, RD, Q, Kc, Vt, ctx, out, stream=None):
+    _call(lib().sd_op_attention, C.c_void_p(big), stride, C.c_void_p(qw), C.c_void_p(kw), C.c_void_p(rope), L, P, HQ, HK,
+          HD, RD, C.c_void_p(Q), C.c_void_p(Kc), C.c_void_p(Vt), ctx, C.c_void_p(out), _sp(stream))

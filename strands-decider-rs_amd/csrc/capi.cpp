@@ -49,6 +49,8 @@ struct OpWs {
     size_t wpack_bytes = 0;
     void* wtmp = nullptr;
     size_t wtmp_bytes = 0;
+    void* attn = nullptr;  // sd_op_attention: the lu block, then the key-split workspace
+    size_t attn_bytes = 0;
 };
 void grow(void*& p, size_t& have, size_t need) {
     if (have >= need) return;
@@ -61,6 +63,34 @@ void grow(void*& p, size_t& have, size_t need) {
 OpWs& op_ws() {
     static OpWs w;
     return w;
+}
+
+}  // namespace
+
+namespace {
+
+// The weights of an int4 g32 matrix in what the kernels read: the caller's own when already
+// rewritten by sd_op_repack_w4 (packed) or when the shape keeps the model's layout (the GEMV's),
+// else a rewritten copy in the workspace (engine nibble order, tiled).  `force_engine_order`: the
+// kernel wants the engine nibble order even where the shape is not tileable (the f16-dequant
+// configurations).
+std::pair<const uint32_t*, const sd::f16*> op_weights(OpWs& w, const void* Wq, const void* Sc, int N, int K, bool packed,
+                                                      bool force_engine_order, hipStream_t st) {
+    const bool tiled = sd::w4_tileable(N, K);
+    if ((packed && tiled) || (!tiled && !force_engine_order))
+        return {static_cast<const uint32_t*>(Wq), static_cast<const sd::f16*>(Sc)};
+    const size_t words = (size_t)N * K / 8, scales = (size_t)N * K / 32;
+    grow(w.wpack, w.wpack_bytes, words * 4 + scales * 2);
+    auto* pw = static_cast<uint32_t*>(w.wpack);
+    auto* ps = reinterpret_cast<sd::f16*>(pw + words);
+    SD_HIP(hipMemcpyAsync(pw, Wq, words * 4, hipMemcpyDeviceToDevice, st));
+    SD_HIP(hipMemcpyAsync(ps, Sc, scales * 2, hipMemcpyDeviceToDevice, st));
+    sd::repack_w4(pw, words, st);
+    if (tiled) {
+        grow(w.wtmp, w.wtmp_bytes, words * 4 + scales * 2);
+        sd::tile_w4(pw, ps, N, K, w.wtmp, st);
+    }
+    return {pw, ps};
 }
 
 }  // namespace
@@ -265,14 +295,14 @@ int sd_op_repack_w4(void* Wq, void* Sc, int N, int K, void* stream, char* err, s
     return guarded(err, errlen, [&] {
         if (!Wq || !Sc) throw sd::Error("sd_op_repack_w4: null argument");
         if (N < 1 || K < 32 || K % 32) throw sd::Error("sd_op_repack_w4: need N >= 1 and K a multiple of 32");
+        // other shapes keep the model's layout, which is what the GEMV reads for them
+        if (!sd::w4_tileable(N, K)) return;
         const hipStream_t st = static_cast<hipStream_t>(stream);
         sd::repack_w4(static_cast<uint32_t*>(Wq), (size_t)N * K / 8, st);
-        if (sd::w4_tileable(N, K)) {
-            OpWs& w = op_ws();
-            std::lock_guard<std::mutex> lock(w.mu);
-            grow(w.wtmp, w.wtmp_bytes, (size_t)N * K / 2 + (size_t)N * K / 16);
-            sd::tile_w4(static_cast<uint32_t*>(Wq), static_cast<sd::f16*>(Sc), N, K, w.wtmp, st);
-        }
+        OpWs& w = op_ws();
+        std::lock_guard<std::mutex> lock(w.mu);
+        grow(w.wtmp, w.wtmp_bytes, (size_t)N * K / 2 + (size_t)N * K / 16);
+        sd::tile_w4(static_cast<uint32_t*>(Wq), static_cast<sd::f16*>(Sc), N, K, w.wtmp, st);
     });
 }
 
@@ -285,6 +315,14 @@ int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, 
         OpWs& w = op_ws();
         std::lock_guard<std::mutex> lock(w.mu);
         const hipStream_t st = static_cast<hipStream_t>(stream);
+        if (exact && cfg < 0) {
+            // the engine's choice for the GEMV rows: the f32-dequant GEMV, tiled where the shape is
+            const auto wts = op_weights(w, Wq, Sc, N, K, packed != 0, false, st);
+            const bool tiled = sd::w4_tileable(N, K);
+            sd::gemv(static_cast<const sd::f16*>(A), wts.first, wts.second, nullptr, Y, 0, M, N, K, 4, 32, false, tiled,
+                     sd::gemv_plan(M, N, K, tiled, 0, 0), st);
+            return;
+        }
         // cfg < 0: the engine's own choice for this shape (tile and split-K, the split summed by
         // reduce_partials here); cfg >= 0: that configuration, split until the grid covers the chip.
         const size_t cap = size_t(64) << 20;
@@ -300,23 +338,9 @@ int sd_op_matmul(const void* A, const void* Wq, const void* Sc, void* Y, int M, 
         // The kernels read the engine nibble order and, where the shape has one, the tiled layout:
         // unless the caller rewrote its weights already (sd_op_repack_w4), rewrite a copy of them.
         const bool tiled = sd::w4_tileable(N, K);
-        const uint32_t* wq = static_cast<const uint32_t*>(Wq);
-        const auto* sc = static_cast<const sd::f16*>(Sc);
-        if (!packed) {
-            const size_t words = (size_t)N * K / 8, scales = (size_t)N * K / 32;
-            grow(w.wpack, w.wpack_bytes, words * 4 + scales * 2);
-            auto* pw = static_cast<uint32_t*>(w.wpack);
-            auto* ps = reinterpret_cast<sd::f16*>(pw + words);
-            SD_HIP(hipMemcpyAsync(pw, Wq, words * 4, hipMemcpyDeviceToDevice, st));
-            SD_HIP(hipMemcpyAsync(ps, Sc, scales * 2, hipMemcpyDeviceToDevice, st));
-            sd::repack_w4(pw, words, st);
-            if (tiled) {
-                grow(w.wtmp, w.wtmp_bytes, words * 4 + scales * 2);
-                sd::tile_w4(pw, ps, N, K, w.wtmp, st);
-            }
-            wq = pw;
-            sc = ps;
-        }
+        const auto wts = op_weights(w, Wq, Sc, N, K, packed != 0, true, st);
+        const uint32_t* wq = wts.first;
+        const sd::f16* sc = wts.second;
         if (ks == 1) {
             sd::gemm_w4(a, wq, sc, static_cast<sd::f16*>(Y), nullptr, M, N, K, exact != 0, 1, st, c, tiled);
             return;
@@ -355,6 +379,171 @@ int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off
         sd::gdn_prep(static_cast<const float*>(qkv), static_cast<const sd::f16*>(big), s, static_cast<const float*>(negA),
                      static_cast<const float*>(dtb), L, ws, nullptr, sd::Segs{}, 0, nullptr, st);
         sd::gdn_scan(s, L, ws, static_cast<float*>(state), nullptr, load_state, static_cast<float*>(o), sd::Segs{}, 1, st);
+    });
+}
+
+void sd_decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst) {
+    if (src && dst) sd::decode_scale_codes(src, n, g, dst);
+}
+
+int sd_op_matmul_fmt(const void* A, const void* Wq, const void* Sc, const void* Bi, void* Y, int M, int N, int K,
+                     int bits, int group, int asym, void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!A || !Wq || !Sc || !Y || (asym && !Bi)) throw sd::Error("sd_op_matmul_fmt: null argument");
+        sd::gemv(static_cast<const sd::f16*>(A), static_cast<const uint32_t*>(Wq), static_cast<const sd::f16*>(Sc),
+                 static_cast<const sd::f16*>(Bi), Y, 0, M, N, K, bits, group, asym != 0, false,
+                 sd::gemv_plan(M, N, K, false, 0, 0), static_cast<hipStream_t>(stream));
+    });
+}
+
+int sd_op_matmul_split(const void* A, const void* Wq, const void* Sc, void* part, int M, int N, int K, int exact,
+                       int cfg, int ks, int packed, void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!A || !Wq || !Sc || !part) throw sd::Error("sd_op_matmul_split: null argument");
+        if (M < 1 || N < 1 || K < 128 || K % 128) throw sd::Error("sd_op_matmul_split: need M, N >= 1 and K a multiple of 128");
+        if (ks < 1 || ks > 8) throw sd::Error("sd_op_matmul_split: ks must be 1 to 8");
+        OpWs& w = op_ws();
+        std::lock_guard<std::mutex> lock(w.mu);
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        const bool tiled = sd::w4_tileable(N, K);
+        const auto* a = static_cast<const sd::f16*>(A);
+        if (exact) {
+            const auto wts = op_weights(w, Wq, Sc, N, K, packed != 0, false, st);
+            sd::GemvPlan p = sd::gemv_plan(M, N, K, tiled, 1, (size_t)ks * M * N);
+            p.ks = ks;
+            sd::gemv(a, wts.first, wts.second, nullptr, part, 1, M, N, K, 4, 32, false, tiled, p, st);
+            return;
+        }
+        if (cfg < 0 || cfg >= sd::gemm_w4_configs()) throw sd::Error("sd_op_matmul_split: no configuration " + std::to_string(cfg));
+        const auto wts = op_weights(w, Wq, Sc, N, K, packed != 0, true, st);
+        sd::gemm_w4(a, wts.first, wts.second, nullptr, static_cast<float*>(part), M, N, K, false, ks, st, cfg, tiled);
+    });
+}
+
+int sd_op_gate_up_silu(const void* A, const void* Wq, const void* Sc, void* mid, int M, int N, int K, int exact, int cfg,
+                       void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!A || !Wq || !Sc || !mid) throw sd::Error("sd_op_gate_up_silu: null argument");
+        if (M < 1 || N < 32 || N % 32 || K < 256 || K % 256)
+            throw sd::Error("sd_op_gate_up_silu: need N a multiple of 32 and K of 256");
+        OpWs& w = op_ws();
+        std::lock_guard<std::mutex> lock(w.mu);
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        // the model's [gate | up] rows -> engine order, rows interleaved in groups of 16, tiled
+        const size_t words = (size_t)N * K / 8, scales = (size_t)N * K / 32;
+        grow(w.wpack, w.wpack_bytes, words * 4 + scales * 2);
+        grow(w.wtmp, w.wtmp_bytes, words * 4 + scales * 2);
+        auto* pw = static_cast<uint32_t*>(w.wpack);
+        auto* ps = reinterpret_cast<sd::f16*>(pw + words);
+        SD_HIP(hipMemcpyAsync(pw, Wq, words * 4, hipMemcpyDeviceToDevice, st));
+        SD_HIP(hipMemcpyAsync(ps, Sc, scales * 2, hipMemcpyDeviceToDevice, st));
+        sd::repack_w4(pw, words, st);
+        sd::interleave_gate_up(pw, ps, N, K, w.wtmp, st);
+        sd::tile_w4(pw, ps, N, K, w.wtmp, st);
+        const auto* a = static_cast<const sd::f16*>(A);
+        if (exact) {
+            sd::gemv(a, pw, ps, nullptr, mid, 2, M, N, K, 4, 32, false, true, sd::gemv_plan(M, N, K, true, 2, 0), st);
+            return;
+        }
+        const int c = cfg >= 0 ? cfg : sd::gemm_w4_plan(M, N, K, false, false, 0).cfg;
+        if (!sd::gemm_w4_has_silu(c)) throw sd::Error("sd_op_gate_up_silu: configuration " + std::to_string(c) + " has no SiLU epilogue");
+        sd::gemm_w4_silu(a, pw, ps, static_cast<sd::f16*>(mid), M, N, K, st, c, true);
+    });
+}
+
+int sd_op_embed(const void* ids, int L, const void* Q, const void* S, const void* Bi, int d, int bits, int group, int asym,
+                void* x, void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!ids || !Q || !S || !x || (asym && !Bi)) throw sd::Error("sd_op_embed: null argument");
+        if (L < 1) throw sd::Error("sd_op_embed: need at least one id");
+        sd::embed(static_cast<const uint32_t*>(ids), L, static_cast<const uint32_t*>(Q), static_cast<const sd::f16*>(S),
+                  static_cast<const sd::f16*>(Bi), d, bits, group, asym != 0, static_cast<float*>(x),
+                  static_cast<hipStream_t>(stream));
+    });
+}
+
+int sd_op_add_norm(void* x, const void* y, const void* w, int d, const void* rows, int nrows, void* h16, void* h32,
+                   void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!x || !w || (!h16 == !h32)) throw sd::Error("sd_op_add_norm: null argument (exactly one of h16, h32)");
+        sd::YIn yi;
+        yi.y16 = static_cast<const sd::f16*>(y);
+        sd::add_norm(static_cast<float*>(x), yi, static_cast<const float*>(w), d, static_cast<const uint32_t*>(rows), nrows,
+                     static_cast<sd::f16*>(h16), static_cast<float*>(h32), static_cast<hipStream_t>(stream));
+    });
+}
+
+int sd_op_silu_mul(const void* big, int L, int I, void* mid, void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!big || !mid) throw sd::Error("sd_op_silu_mul: null argument");
+        sd::silu_mul(static_cast<const sd::f16*>(big), nullptr, 0, L, I, false, static_cast<sd::f16*>(mid),
+                     static_cast<hipStream_t>(stream));
+    });
+}
+
+int sd_op_add_bias(void* y, int L, int N, const void* c, void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!y || !c) throw sd::Error("sd_op_add_bias: null argument");
+        sd::add_bias(static_cast<sd::f16*>(y), L, N, static_cast<const float*>(c), static_cast<hipStream_t>(stream));
+    });
+}
+
+int sd_op_conv(const void* big, int stride, int L, int C, const void* w, const void* hist, void* out, void* stream,
+               char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!big || !w || !hist || !out) throw sd::Error("sd_op_conv: null argument");
+        sd::conv_silu(static_cast<const sd::f16*>(big), stride, L, C, static_cast<const float*>(w),
+                      static_cast<const sd::f16*>(hist), static_cast<float*>(out), sd::Segs{},
+                      static_cast<hipStream_t>(stream));
+    });
+}
+
+int sd_op_gnorm(const void* o, const void* big, int stride, int z_off, const void* w, int L, int H, int DV, void* out,
+                void* stream, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!o || !big || !w || !out) throw sd::Error("sd_op_gnorm: null argument");
+        const sd::GdnShape s{H, 128, DV, stride, 0, 0, z_off, 0};
+        sd::gnorm(static_cast<const float*>(o), static_cast<const sd::f16*>(big), s, static_cast<const float*>(w), L,
+                  static_cast<sd::f16*>(out), static_cast<hipStream_t>(stream));
+    });
+}
+
+int sd_op_attention(const void* big, int stride, const void* qw, const void* kw, const void* rope, int L, int P, int HQ,
+                    int HK, int HD, int RD, void* Q, void* Kc, void* Vt, int ctx, void* out, void* stream, char* err,
+                    size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!big || !qw || !kw || !rope || !Q || !Kc || !Vt || !out) throw sd::Error("sd_op_attention: null argument");
+        if (L < 1 || P < 0 || P + L > ctx) throw sd::Error("sd_op_attention: need 1 <= L and P + L <= ctx");
+        if (HK < 1 || HQ % HK) throw sd::Error("sd_op_attention: q heads must be a multiple of kv heads");
+        const sd::AttnShape as{HQ, HK, HD, RD, stride, ctx};
+        // the engine's key split: query blocks of 16 that cannot fill the chip split the keys too
+        const int nb = (L + 15) / 16;
+        int ks = 1;
+        if (L <= 256)
+            while (ks < 8 && nb * HQ * ks < 256) ks *= 2;
+        OpWs& w = op_ws();
+        std::lock_guard<std::mutex> lock(w.mu);
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        grow(w.attn, w.attn_bytes, 256 + sd::attn_ws_floats(L, as) * 4);
+        auto* lu = static_cast<uint32_t*>(w.attn);
+        const uint32_t v[8] = {(uint32_t)L, (uint32_t)P, (uint32_t)ctx, P > 0 ? 1u : 0u, 0u, 0u, 0u, 0u};
+        sd::set_u32x8(lu, v, st);
+        sd::qk_prep(static_cast<const sd::f16*>(big), as, static_cast<const float*>(qw), static_cast<const float*>(kw),
+                    static_cast<const float*>(rope), L, lu, sd::Segs{}, static_cast<sd::f16*>(Q), static_cast<sd::f16*>(Kc),
+                    static_cast<sd::f16*>(Vt), st);
+        sd::attention_split(static_cast<const sd::f16*>(Q), static_cast<const sd::f16*>(Kc), static_cast<const sd::f16*>(Vt),
+                            static_cast<const sd::f16*>(big), as, L, lu, sd::Segs{}, ks,
+                            reinterpret_cast<float*>(static_cast<uint8_t*>(w.attn) + 256), static_cast<sd::f16*>(out), st);
+    });
+}
+
+int sd_engine_trace(sd_engine* e, const uint32_t* ids, size_t n, const sd_snapshot* cache, const size_t* rows,
+                    size_t n_rows, float* x_out, uint16_t* h_out, size_t cap, size_t* n_taps, char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!e || !ids || (!rows && n_rows) || (cap && n_rows && (!x_out || !h_out)))
+            throw sd::Error("sd_engine_trace: null argument");
+        const size_t t = E(e)->trace(ids, n, S(cache), rows, n_rows, x_out, h_out, cap);
+        if (n_taps) *n_taps = t;
     });
 }
 

@@ -18,6 +18,8 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct Error : std::runtime_error {
     using std::runtime_error::runtime_error;
@@ -48,6 +50,9 @@ struct KernelEvents {
     int launches = 0;
 };
 KernelEvents*& kernel_events();
+
+// 8-bit scale codes -> f16 bits (src/model.rs:217-236); host only (engine.cpp).
+void decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst);
 
 // ---- quantized matmul (gemm.hip) -----------------------------------------------------------
 // Y[M,N] f16 = A[M,K] f16 . deq(W[N,K])^T with W int4 group-32 symmetric in the reference's
@@ -92,6 +97,20 @@ void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M
 // Whether configuration cfg has the SiLU * mul epilogue of gemm_w4_silu.
 bool gemm_w4_has_silu(int cfg);
 
+// ---- quantized GEMV (gemv.hip) ---------------------------------------------------------------
+// Y = A[M,K] f16 . deq(W[N,K])^T with the reference GEMV's f32 dequant (src/kernels.rs:590-635) for
+// any of its formats (int2/3/4, group a multiple of 32, symmetric or asymmetric with biases Bi).
+// `tiled`: W and S in the engine's int4 g32 tiled layout (tile_w4, engine nibble order); else the
+// reference's plain layout and bit order.  out: 0 = f16 Y [M][N]; 1 = f32 partial slots Y [ks][M][N]
+// (summed in slot order by the consumer); 2 = f16 mid [M][N/2] = silu(gate) * up of a tiled gate_up
+// whose rows are interleaved in groups of 16 (interleave_gate_up).
+struct GemvPlan {
+    int nct = 1, mt = 1, ks = 1;  // column tiles of 16 per workgroup, row tiles of 16, k splits
+};
+GemvPlan gemv_plan(int M, int N, int K, bool tiled, int out, size_t max_part_elems);
+void gemv(const f16* A, const uint32_t* W, const f16* S, const f16* Bi, void* Y, int out, int M, int N, int K, int bits,
+          int group, bool asym, bool tiled, const GemvPlan& p, hipStream_t st);
+
 // ---- elementwise / norms (elem.hip) ----------------------------------------------------------
 void embed(const uint32_t* ids, int L, const uint32_t* Q, const f16* S, const f16* Bi, int d, int bits,
            int group, bool asym, float* x, hipStream_t st);
@@ -111,6 +130,8 @@ void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* row
 void silu_mul(const f16* big, const float* part, int ks, int L, int I, bool il, f16* mid, hipStream_t st);
 void add_bias(f16* y, int L, int N, const float* c, hipStream_t st);
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);
+// p[0..8) = v[0..8) by a kernel (a value carried in the launch, so the call may be captured)
+void set_u32x8(uint32_t* p, const uint32_t v[8], hipStream_t st);
 // Several strided device copies in one launch: rows x row_bytes from src (rows src_pitch apart) to
 // dst (rows dst_pitch apart).  Pointers, pitches and row_bytes must be multiples of 16 bytes.
 struct CopyDesc {

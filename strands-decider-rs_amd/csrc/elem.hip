@@ -198,6 +198,13 @@ __global__ void k_add_bias(f16* __restrict__ y, size_t n, int N, const float* __
     if (i < n) y[i] = (f16)((float)y[i] + c[i % N]);
 }
 
+struct U32x8 {
+    uint32_t v[8];
+};
+__global__ void k_set_u32x8(uint32_t* __restrict__ p, U32x8 a) {
+    if (threadIdx.x < 8) p[threadIdx.x] = a.v[threadIdx.x];
+}
+
 __global__ void k_fill_u32(uint32_t* __restrict__ p, size_t n, uint32_t v) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -292,6 +299,13 @@ void copy_batch(const CopyDesc* d, size_t n, hipStream_t st) {
         hipLaunchKernelGGL(k_copy_batch, dim3(gx, (unsigned)m), dim3(256), 0, st, a);
         launched("copy_batch");
     }
+}
+
+void set_u32x8(uint32_t* p, const uint32_t v[8], hipStream_t st) {
+    U32x8 a;
+    for (int i = 0; i < 8; i++) a.v[i] = v[i];
+    hipLaunchKernelGGL(k_set_u32x8, dim3(1), dim3(64), 0, st, p, a);
+    launched("set_u32x8");
 }
 
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st) {

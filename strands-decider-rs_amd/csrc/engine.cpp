@@ -43,6 +43,36 @@ void fwht(float* x, size_t n) {
 
 }  // namespace
 
+void decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst) {
+    // 2^(-i / 4096) for every exponent the rows use, in f64, kept across calls and grown on demand
+    // (the loader decodes one row at a time)
+    thread_local std::vector<double> pw;
+    size_t jmax = 0;
+    for (size_t r = 0; r < n; r++) jmax = std::max<size_t>(jmax, (size_t)src[4 * r + 2] | ((size_t)src[4 * r + 3] << 8));
+    if (pw.size() < 127 * jmax + 1) {
+        const size_t have = pw.size();
+        pw.resize(127 * jmax + 1);
+        for (size_t i = have; i < pw.size(); i++) pw[i] = std::pow(2.0, -(double)i / 4096.0);
+    }
+    const uint8_t* codes = src + 4 * n;
+    for (size_t r = 0; r < n; r++) {
+        const uint16_t mb = (uint16_t)(src[4 * r] | (src[4 * r + 1] << 8));
+        const size_t j = (size_t)src[4 * r + 2] | ((size_t)src[4 * r + 3] << 8);
+        const double m = (double)__builtin_bit_cast(f16, mb);
+        uint16_t mag[128];
+        bool have[128] = {};
+        for (size_t i = 0; i < g; i++) {
+            const uint8_t c = codes[r * g + i];
+            const int k = c & 127;
+            if (!have[k]) {
+                mag[k] = __builtin_bit_cast(uint16_t, (f16)(float)(m * pw[k * j]));
+                have[k] = true;
+            }
+            dst[r * g + i] = (uint16_t)(mag[k] | ((c & 128) << 8));
+        }
+    }
+}
+
 Engine::~Engine() {
     for (auto& kv : plans) kv.second.destroy();
     if (ev0) (void)hipEventDestroy(ev0);
@@ -127,18 +157,30 @@ const void* Engine::dptr(const std::string& name) const {
 
 Mat Engine::mat(const std::string& name) const {
     const TensorRef& t = tensor(name + ".q");
-    if (!(t.bits == 4 && t.group == 32 && !t.asym))
-        throw Error(name + ": matmul weights must be int4, group 32, symmetric (got " + std::to_string(t.bits) +
-                    " bits, group " + std::to_string(t.group) + (t.asym ? ", asymmetric)" : ")"));
-    SD_CHECK(t.K % 128 == 0, name + ": K must be a multiple of 128");
+    // the reference's formats (src/kernels.rs:550-576): int2/3/4, groups of a multiple of 32
+    if (!(t.bits >= 2 && t.bits <= 4 && t.group >= 32 && t.group % 32 == 0 && t.K % t.group == 0))
+        throw Error(name + ": unsupported weight format (" + std::to_string(t.bits) + " bits, group " +
+                    std::to_string(t.group) + ", K " + std::to_string(t.K) + ")");
     Mat m;
     m.q = static_cast<const uint32_t*>(dptr(name + ".q"));
     m.s = static_cast<const f16*>(dptr(name + ".s"));
+    if (t.asym) m.b = static_cast<const f16*>(dptr(name + ".b"));
     SD_CHECK(reinterpret_cast<uintptr_t>(m.q) % 16 == 0, name + ".q is not 16-byte aligned");
     m.N = (int)t.N;
     m.K = (int)t.K;
+    m.bits = (int)t.bits;
+    m.group = (int)t.group;
+    m.asym = t.asym;
+    SD_CHECK(tensor(name + ".s").bytes >= (uint64_t)m.N * (m.K / m.group) * 2, name + ".s: too few scales");
+    // the tiled f16-dequant kernels need K a multiple of 128; the reference uses them for the
+    // default format with N % 64 == 0 (src/engine.rs:434-442), the GEMV for everything else
+    SD_CHECK(!m.deflt() || m.N % 64 != 0 || m.K % 128 == 0, name + ": K must be a multiple of 128");
     return m;
 }
+
+// The reference's GEMV (f32 dequant) serves M <= 20 rows, non-default formats and N % 64 != 0
+// (src/engine.rs:419-442).
+static bool gemv_rows(const Mat& m, bool short_rows) { return short_rows || !m.deflt() || m.N % 64 != 0; }
 
 const float* Engine::f32(const std::string& name, size_t count) const {
     const TensorRef& t = tensor(name);
@@ -218,36 +260,50 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
     // Embedding parts: rows of [part0 | part1 | ...] split into one device array per part
     // (src/model.rs:260-283).
     {
-        uint64_t rb = 0;
-        for (size_t p = 0; p < em->n_parts; p++) rb += em->part_bytes[p];
-        SD_CHECK(rb == em->row_bytes, "embed: part sizes do not add up to row_bytes");
+        uint64_t gb = 0, wb = 0;  // bytes per row in GPU layout and as stored
+        std::vector<bool> coded(em->n_parts, false);
+        for (size_t p = 0; p < em->n_parts; p++) {
+            coded[p] = em->u8 && std::strcmp(em->part_names[p], "embed.s") == 0;
+            SD_CHECK(!coded[p] || em->part_bytes[p] % 2 == 0, "embed: the scale part must hold f16 values");
+            gb += em->part_bytes[p];
+            wb += coded[p] ? 4 + em->part_bytes[p] / 2 : em->part_bytes[p];
+        }
+        SD_CHECK(gb == em->row_bytes, "embed: part sizes do not add up to row_bytes");
+        const uint64_t rb = em->wire_row_bytes ? em->wire_row_bytes : em->row_bytes;
+        SD_CHECK(wb == rb, "embed: the stored parts do not add up to the stored row size");
         FILE* f = std::fopen(em->rows_path, "rb");
         if (!f) throw Error(std::string(em->rows_path) + ": cannot open");
         std::fseek(f, 0, SEEK_END);
         const long size = std::ftell(f);
         std::fseek(f, 0, SEEK_SET);
-        if ((uint64_t)size != em->vocab * em->row_bytes) {
+        if ((uint64_t)size != em->vocab * rb) {
             std::fclose(f);
             throw Error(std::string(em->rows_path) + ": " + std::to_string(size) + " bytes, expected " +
-                        std::to_string(em->vocab) + " rows of " + std::to_string(em->row_bytes));
+                        std::to_string(em->vocab) + " rows of " + std::to_string(rb));
         }
         std::vector<std::vector<uint8_t>> parts(em->n_parts);
         for (size_t p = 0; p < em->n_parts; p++) parts[p].resize(em->vocab * em->part_bytes[p]);
-        std::vector<uint8_t> row(em->row_bytes);
-        const size_t rows_per = std::max<size_t>(1, chunk / em->row_bytes);
-        std::vector<uint8_t> buf(rows_per * em->row_bytes);
+        const size_t rows_per = std::max<size_t>(1, chunk / rb);
+        std::vector<uint8_t> buf(rows_per * rb);
         for (uint64_t r0 = 0; r0 < em->vocab; r0 += rows_per) {
             const size_t nr = (size_t)std::min<uint64_t>(rows_per, em->vocab - r0);
-            if (std::fread(buf.data(), em->row_bytes, nr, f) != nr) {
+            if (std::fread(buf.data(), rb, nr, f) != nr) {
                 std::fclose(f);
                 throw Error(std::string(em->rows_path) + ": read failed");
             }
             for (size_t r = 0; r < nr; r++) {
                 size_t off = 0;
                 for (size_t p = 0; p < em->n_parts; p++) {
-                    std::memcpy(parts[p].data() + (r0 + r) * em->part_bytes[p], buf.data() + r * em->row_bytes + off,
-                                em->part_bytes[p]);
-                    off += em->part_bytes[p];
+                    uint8_t* dst = parts[p].data() + (r0 + r) * em->part_bytes[p];
+                    const uint8_t* src = buf.data() + r * rb + off;
+                    if (coded[p]) {
+                        const size_t g = em->part_bytes[p] / 2;
+                        decode_scale_codes(src, 1, g, reinterpret_cast<uint16_t*>(dst));
+                        off += 4 + g;
+                    } else {
+                        std::memcpy(dst, src, em->part_bytes[p]);
+                        off += em->part_bytes[p];
+                    }
                 }
             }
         }
@@ -332,9 +388,20 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         for (LayerW& L : layers)
             for (Mat* m : {&L.in_proj, &L.out_proj, &L.qkv, &L.o_proj, &L.gate_up, &L.down, &L.proj})
                 if (m->q) all.push_back(m);
+        // Only int4 g32 symmetric matrices of a tileable shape are rewritten (the kernels with f16
+        // dequant read nothing else); every other matrix keeps the reference's layout and bit order,
+        // which the GEMV reads.  A matrix sharing memory with another of a different format or
+        // shape is left as it is.
+        auto rewritable = [&](const Mat* m) {
+            if (!m->deflt() || !w4_tileable(m->N, m->K)) return false;
+            for (const Mat* o : all)
+                if (o->q == m->q && (o->N != m->N || o->K != m->K || !o->deflt())) return false;
+            return true;
+        };
         std::vector<const uint32_t*> done;
         size_t tmp_bytes = 0;
         for (const Mat* m : all) {
+            if (!rewritable(m)) continue;
             tmp_bytes = std::max(tmp_bytes, (size_t)m->N * m->K / 2 + (size_t)m->N * m->K / 16);
             if (std::find(done.begin(), done.end(), m->q) != done.end()) continue;
             done.push_back(m->q);
@@ -346,6 +413,8 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         for (const LayerW& L : layers)
             if (L.kind != SD_ADAPTER && L.gate_up.q) gus.push_back(&L.gate_up);
         gu_il = !gus.empty() && cfg.inter % 16 == 0;
+        for (const Mat* g : gus)
+            if (!rewritable(g)) gu_il = false;
         for (const Mat* g : gus)
             for (const Mat* m : all)
                 if (m->q == g->q && m != g && std::find(gus.begin(), gus.end(), m) == gus.end()) gu_il = false;
@@ -362,7 +431,7 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
             // tiled one is tiled with it)
             std::vector<const uint32_t*> tiled_done;
             for (Mat* m : all) {
-                m->tiled = w4_tileable(m->N, m->K);
+                m->tiled = rewritable(m);
                 if (!m->tiled || std::find(tiled_done.begin(), tiled_done.end(), m->q) != tiled_done.end()) continue;
                 tiled_done.push_back(m->q);
                 tile_w4(const_cast<uint32_t*>(m->q), const_cast<f16*>(m->s), m->N, m->K, tmp, st);
@@ -495,16 +564,33 @@ void Engine::ensure_pool(int l) {
 
 void Engine::mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L,
                 bool short_rows) {
-    // The reference's GEMV (f32 dequant) serves M <= 20 and N % 64 != 0 (src/engine.rs:419-442).
-    const bool exact = short_rows || m.N % 64 != 0;
-    const int cfg_ = gemm_w4_plan(L, m.N, m.K, exact, false, 0).cfg;
-    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, nullptr, L, m.N, m.K, exact, 1, s, cfg_, m.tiled); }});
+    if (gemv_rows(m, short_rows)) {
+        const GemvPlan gp = gemv_plan(L, m.N, m.K, m.tiled, 0, 0);
+        steps.push_back({label, [=](hipStream_t s) {
+            gemv(A, m.q, m.s, m.b, Y, 0, L, m.N, m.K, m.bits, m.group, m.asym, m.tiled, gp, s);
+        }});
+        return;
+    }
+    const int cfg_ = gemm_w4_plan(L, m.N, m.K, false, false, 0).cfg;
+    steps.push_back({label, [=](hipStream_t s) { gemm_w4(A, m.q, m.s, Y, nullptr, L, m.N, m.K, false, 1, s, cfg_, m.tiled); }});
 }
 
 YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L, bool short_rows) {
     // A projection whose output only feeds the residual add: split K until the grid covers the
     // chip, the add + RMSNorm sums the partials.
-    const bool exact = short_rows || m.N % 64 != 0;
+    if (gemv_rows(m, short_rows)) {
+        const GemvPlan gp = gemv_plan(L, m.N, m.K, m.tiled, 1, pool.ypart_elems);
+        float* part = pool.ypart;
+        steps.push_back({label, [=](hipStream_t s) {
+            gemv(A, m.q, m.s, m.b, part, 1, L, m.N, m.K, m.bits, m.group, m.asym, m.tiled, gp, s);
+        }});
+        YIn y;
+        y.yp = part;
+        y.ks = gp.ks;
+        y.slot = (size_t)L * m.N;
+        return y;
+    }
+    const bool exact = false;
     const GemmPlan gp = gemm_w4_plan(L, m.N, m.K, exact, true, pool.ypart_elems);
     const int cfg_ = gp.cfg, ks = gp.ks;
     float* part = pool.ypart;
@@ -593,12 +679,21 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
         {
             // gate_up only feeds silu * mul: from 65 rows on it runs unsplit with silu * mul in the
             // GEMM's epilogue (measured on MI355X at 120 rows: 15.7 us against 13.7 us split in two
-            // plus 4.9 us of silu_mul); otherwise silu_mul sums the split-K partials itself
-            const bool exact = sr || W.gate_up.N % 64 != 0;
+            // plus 4.9 us of silu_mul); otherwise silu_mul sums the split-K partials itself.  The
+            // GEMV rows apply silu * mul in the GEMV's epilogue when the weights are interleaved.
             const Mat m = W.gate_up;
+            const bool exact = gemv_rows(m, sr);
             const bool il = gu_il;
             const int cfu = !exact && m.K % 256 == 0 && L > 64 && L <= 1024 ? gemm_w4_plan(L, m.N, m.K, false, false, 0).cfg : -1;
-            if (il && gemm_w4_has_silu(cfu)) {
+            if (exact) {
+                const bool fused = il && m.tiled;
+                const GemvPlan gp = gemv_plan(L, m.N, m.K, m.tiled, fused ? 2 : 0, 0);
+                steps.push_back({"gate_up", [=](hipStream_t s) {
+                    gemv(P.h, m.q, m.s, m.b, fused ? (void*)P.mid : (void*)P.big, fused ? 2 : 0, L, m.N, m.K, m.bits, m.group,
+                         m.asym, m.tiled, gp, s);
+                }});
+                if (!fused) steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, nullptr, 0, L, I, il, P.mid, s); }});
+            } else if (il && gemm_w4_has_silu(cfu)) {
                 const int cg = cfu;
                 steps.push_back({"gate_up", [=](hipStream_t s) {
                     gemm_w4_silu(P.h, m.q, m.s, P.mid, L, m.N, m.K, s, cg, m.tiled);
@@ -967,6 +1062,39 @@ std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids,
     for (auto& e : kev) (void)hipEventDestroy(e);
     std::sort(by.begin(), by.end(), [](auto& a, auto& b) { return a.second > b.second; });
     return by;
+}
+
+size_t Engine::trace(const uint32_t* ids, size_t n, const Snapshot* cache, const size_t* rows, size_t n_rows,
+                     float* x_out, uint16_t* h_out, size_t cap) {
+    const size_t P = cache ? cache->len : 0;
+    if (n == 0 || P + n > SD_CONTEXT)
+        throw Error("context of " + std::to_string(P + n) + " tokens: must be 1 to " + std::to_string(SD_CONTEXT));
+    if (cache && cache->engine != this) throw Error("snapshot belongs to another engine");
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(ids[i]) + " out of range for vocab " + std::to_string(vocab));
+    for (size_t r = 0; r < n_rows; r++)
+        if (rows[r] >= n) throw Error("row " + std::to_string(rows[r]) + " out of range for " + std::to_string(n) + " tokens");
+    const int L = (int)n;
+    ensure_pool(L);
+    Plan& pl = plan(L);
+    upload(ids, n, nullptr, 0, P, cache != nullptr, 0, 0);
+    restore(cache, P);
+    const size_t d = (size_t)cfg.d;
+    size_t taps = 0;
+    for (auto& step : pl.steps) {
+        step.run(st);
+        if (std::strcmp(step.label, "norm") != 0) continue;
+        if (taps < cap) {
+            SD_HIP(hipStreamSynchronize(st));
+            for (size_t r = 0; r < n_rows; r++) {
+                SD_HIP(hipMemcpy(x_out + (taps * n_rows + r) * d, pool.x + rows[r] * d, d * 4, hipMemcpyDeviceToHost));
+                SD_HIP(hipMemcpy(h_out + (taps * n_rows + r) * d, pool.h + rows[r] * d, d * 2, hipMemcpyDeviceToHost));
+            }
+        }
+        taps++;
+    }
+    SD_HIP(hipStreamSynchronize(st));
+    return taps;
 }
 
 Snapshot::~Snapshot() {

@@ -30,8 +30,13 @@ struct Shard {
 struct Mat {
     const uint32_t* q = nullptr;
     const f16* s = nullptr;
+    const f16* b = nullptr;  // asymmetric biases [N][K/group]
     int N = 0, K = 0;
-    bool tiled = false;  // words and scales in the tiled layout (tile_w4)
+    int bits = 4, group = 32;
+    bool asym = false;
+    bool tiled = false;  // int4 g32 symmetric, words and scales in the tiled layout (tile_w4)
+    // the reference's default format: the only one its tiled matmul takes (src/engine.rs:434-442)
+    bool deflt() const { return bits == 4 && group == 32 && !asym; }
 };
 
 struct EmbedW {
@@ -187,6 +192,12 @@ struct Engine {
                    const size_t* n_opts, const double* temps, const Snapshot* cache, bool timed, double* probs,
                    double* gpu_ms);
     std::vector<std::pair<const char*, double>> profile(const uint32_t* ids, size_t n);
+    // The forward of `ids` from `cache` run step by step, copying after every residual add + RMSNorm
+    // of the layers (each layer's in_norm, then its post_norm) the residual x (f32) and the
+    // normalized h (f16 bits) of the given rows: tap i goes to x_out / h_out + i * n_rows * d.  At
+    // most `cap` taps are copied; returns the number the plan has.  A test hook for per-layer parity.
+    size_t trace(const uint32_t* ids, size_t n, const Snapshot* cache, const size_t* rows, size_t n_rows, float* x_out,
+                 uint16_t* h_out, size_t cap);
 
    private:
     void* dalloc(size_t bytes);

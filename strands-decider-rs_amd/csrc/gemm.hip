@@ -37,6 +37,7 @@
 #include <hip/hip_ext.h>
 
 #include "common.h"
+#include "device.h"
 
 namespace sd {
 namespace {
@@ -46,80 +47,6 @@ constexpr int KSTEP = 128;      // k per macro step: 4 quant blocks
 #define SD_LDA_PAD 8
 #endif
 constexpr int LDA = KSTEP + SD_LDA_PAD;  // LDS row stride in halves
-
-// The 8 nibbles of a weight word in the engine nibble order (see k_repack_w4) as 4 f16 pairs q - 8
-// (exact) for k = (0,1), (2,3), (4,5), (6,7): the nibble at bits 4p lands in the f16 mantissa as
-// 1024 + q for p = 0, 2 (and 4, 6 in the high half), as 1024 + 16 q for the others, so two masks per
-// 8-bit shift give all four pairs.
-// (a & m) | c in one v_and_or_b32 (the compiler otherwise emits separate and/or here).
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "s"(c));
-    return r;
-}
-
-
-__device__ __forceinline__ void nib_pairs(uint32_t w, f16x2& p0, f16x2& p1, f16x2& p2, f16x2& p3) {
-    const uint32_t w8 = w >> 8;
-    const f16x2 x0 = __builtin_bit_cast(f16x2, and_or(w, 0x000F000Fu, 0x64006400u));
-    const f16x2 x1 = __builtin_bit_cast(f16x2, and_or(w, 0x00F000F0u, 0x64006400u));
-    const f16x2 x2 = __builtin_bit_cast(f16x2, and_or(w8, 0x000F000Fu, 0x64006400u));
-    const f16x2 x3 = __builtin_bit_cast(f16x2, and_or(w8, 0x00F000F0u, 0x64006400u));
-    const f16x2 c1032 = {(f16)1032.0f, (f16)1032.0f}, c16 = {(f16)0.0625f, (f16)0.0625f}, c72 = {(f16)-72.0f, (f16)-72.0f};
-    p0 = x0 - c1032;
-    p1 = __builtin_elementwise_fma(x1, c16, c72);
-    p2 = x2 - c1032;
-    p3 = __builtin_elementwise_fma(x3, c16, c72);
-}
-
-// Raw buffer access (MUBUF): a 128-bit resource of base address and byte size, per-lane 32-bit
-// offsets (VGPR) plus a uniform one (SGPR); an offset at or past the size reads zeros and touches no
-// memory.  The host pass of hipcc does not see the builtins.
-#if defined(__HIP_DEVICE_COMPILE__)
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-// 16 bytes per lane straight into LDS at lds + 16 lane (lds wave-uniform).
-__device__ __forceinline__ void buf_lds16(Rsrc r, uint32_t voff, uint32_t soff, void* lds) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ u32x4 buf_b128(Rsrc r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-__device__ __forceinline__ uint32_t buf_b16(Rsrc r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
-}
-#else
-struct Rsrc {};
-__device__ inline Rsrc make_rsrc(const void*, uint32_t) { return {}; }
-__device__ inline void buf_lds16(Rsrc, uint32_t, uint32_t, void*) {}
-__device__ inline u32x4 buf_b128(Rsrc, uint32_t, uint32_t) { return u32x4{}; }
-__device__ inline uint32_t buf_b16(Rsrc, uint32_t, uint32_t) { return 0; }
-#endif
-
-// s_waitcnt with a vmcnt that counts this thread's loads in issue order: scheduling barriers on
-// both sides keep the compiler from moving loads across it, which would change what it counts.
-template <int IMM>
-__device__ __forceinline__ void wait_loads() {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(IMM);
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// Workgroup barrier without the release fence of __syncthreads, whose wait for every outstanding
-// vector-memory load would drain the loads issued for later steps.  The caller waits (vmcnt) for
-// the loads the other waves need; the "memory" clobber keeps the compiler from moving LDS
-// accesses across.
-__device__ __forceinline__ void bar_noflush() { asm volatile("s_barrier" ::: "memory"); }
-
-// Workgroup barrier after this wave's LDS accesses have completed (outstanding global stores are
-// not waited for, unlike __syncthreads).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-__device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
-    return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
 
 template <int MT, int NT, bool EXACT, bool PARTIAL>
 __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, const uint32_t* __restrict__ W,

@@ -107,17 +107,27 @@ def read_manifest(d: str) -> Manifest:
     return Manifest(cfg, shards, tensors, embed, m.get("tokenizer"))
 
 
-def embed_parts(d: str, e: Embed) -> list:
-    """The embedding table, one array per part, all rows (src/model.rs:260-283)."""
-    if e.u8 or e.wire_row_bytes is not None:
-        raise RuntimeError("packed (wire) embedding rows are a download format; convert them first")
+def embed_parts(d: str, e: Embed, decode=None) -> list:
+    """The embedding table, one array per part, all rows (src/model.rs:260-283).  Rows stored with
+    8-bit scale codes (`u8`) have their "embed.s" part decoded by `decode(src, n, g)` (the engine's
+    own, sd_decode_scale_codes, when None)."""
     data = np.fromfile(os.path.join(d, e.rows), dtype=np.uint8)
-    rb = e.row_bytes
+    rb = e.wire_row_bytes or e.row_bytes
     if data.size != e.vocab * rb:
         raise RuntimeError(f"{e.rows}: {data.size} bytes, expected {e.vocab} rows of {rb}")
     rows = data.reshape(e.vocab, rb)
     out, off = [], 0
     for name, b in e.parts:
-        out.append((name, np.ascontiguousarray(rows[:, off:off + b]).reshape(-1)))
-        off += b
+        if e.u8 and name == "embed.s":
+            if decode is None:
+                from . import decode_scale_codes as decode
+            g = b // 2
+            part = np.empty((e.vocab, g), np.uint16)
+            for r in range(e.vocab):
+                part[r] = decode(rows[r, off:off + 4 + g].tobytes(), 1, g)[0]
+            out.append((name, part.view(np.uint8).reshape(-1)))
+            off += 4 + g
+        else:
+            out.append((name, np.ascontiguousarray(rows[:, off:off + b]).reshape(-1)))
+            off += b
     return out

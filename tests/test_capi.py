@@ -78,3 +78,21 @@ def test_head_rejects_too_few_rows(sdamd, tiny_model):
         head.probs(np.zeros((1, 512), np.float32), 512, 1.0)
     with pytest.raises(sdamd.EngineError, match="do not match hidden size"):
         head.probs(np.zeros((3, 256), np.float32), 256, 1.0)
+
+
+def test_decode_scale_codes_matches_oracle(sdamd, oracle):
+    """The engine's load-time decode of 8-bit scale codes (sd_decode_scale_codes, C++, host only)
+    against the oracle's restatement of src/model.rs:217-236: bit for bit, over rows with many
+    exponents, every code and both signs."""
+    rng = np.random.default_rng(21)
+    n, g = 300, 64
+    head = np.zeros((n, 2), np.uint16)
+    head[:, 0] = rng.uniform(1e-4, 8.0, n).astype(np.float16).view(np.uint16)
+    head[:, 1] = rng.integers(0, 4096, n)
+    head[:4, 1] = [0, 1, 4096, 65535]
+    codes = rng.integers(0, 256, (n, g)).astype(np.uint8)
+    codes[0] = np.arange(g)
+    src = np.concatenate([head.view(np.uint8).reshape(-1), codes.reshape(-1)]).tobytes()
+    got = sdamd.decode_scale_codes(src, n, g)
+    want = oracle.decode_scale_codes(src, n, g)
+    assert np.array_equal(got, want)

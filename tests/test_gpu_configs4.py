@@ -1,0 +1,50 @@
+"""BASELINE configs[4] on the GPU against the oracle: the 2B hybrid encodes a long state (1536
+tokens, so the prefill takes the M > 1024 GEMM plan, a gated-delta-net scan of 24 chunks and
+attention over up to 1600 keys), then 8 questions of U[24, 64] tokens are answered from its snapshot
+as one batched forward of 8 sequences with the device head.  Each question is compared with the
+oracle's own forward of that question from its snapshot: hidden rows within 2e-2, probabilities
+within 2e-3, the same answer (tests/engine_parity.rs:58-85 at the sweep's shapes)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+HIDDEN_TOL = 2e-2
+PROB_TOL = 2e-3
+STATE_LEN, N_Q = 1536, 8
+
+
+@pytest.mark.timeout(900)
+def test_configs4_long_state_and_eight_questions(sdamd, synth, model_2b, oracle):
+    eng, head, cfg = sdamd.load_decider(model_2b)
+    try:
+        om = oracle.OracleModel(model_2b)
+        temp = float(cfg["temperature"])
+        rng = np.random.default_rng(404)
+        state = rng.integers(0, synth.VOCAB_2B, STATE_LEN).astype(np.uint32)
+        qs = [rng.integers(0, synth.VOCAB_2B, int(rng.integers(24, 65))).astype(np.uint32) for _ in range(N_Q)]
+        opts = [sorted(rng.choice(len(q) - 1, int(rng.integers(2, 6)), replace=False).tolist()) for q in qs]
+        rows = [0, 767, STATE_LEN - 1]
+
+        out = eng.forward(state, rows, keep=True)
+        print(f"configs[4]: GPU prefill of {STATE_LEN} done; oracle prefill (about a minute on the host)", flush=True)
+        want, osnap = om.forward(state, rows, keep=True)
+        err = np.abs(out.hidden - want).max()
+        print(f"configs[4] prefill of {STATE_LEN}: max |dh| {err:.3g}", flush=True)
+        assert err < HIDDEN_TOL
+
+        probs, _ = eng.ask_batch(head, qs, opts, [temp] * N_Q, cache=out.snapshot)
+        hid, _ = eng.forward_batch(qs, [list(o) + [len(q) - 1] for q, o in zip(qs, opts)], cache=out.snapshot)
+        for i, (q, o) in enumerate(zip(qs, opts)):
+            ohid, _ = om.forward(q, list(o) + [len(q) - 1], cache=osnap)
+            op = om.probs(ohid, temp)
+            herr = np.abs(hid[i] - ohid).max()
+            perr = np.abs(np.asarray(probs[i]) - op).max()
+            print(f"question {i} ({len(q)} tokens, {len(o)} options): max |dh| {herr:.3g}, max |dp| {perr:.3g}",
+                  flush=True)
+            assert herr < HIDDEN_TOL, f"question {i}: max |dh| {herr}"
+            assert perr < PROB_TOL, f"question {i}: max |dp| {perr}"
+            assert int(np.argmax(probs[i])) == int(np.argmax(op)), f"question {i}: answer differs from the oracle's"
+        out.snapshot.free()
+    finally:
+        eng.free()

@@ -157,6 +157,111 @@ def test_gemm_prepacked_weights(sdamd, synth):
         sdamd.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, exact, -1, True)
         torch.cuda.synchronize()
         np.testing.assert_array_equal(host(dY, np.float16, (M, N)), Y0)
-        assert not np.array_equal(host(dW, np.uint32, W.shape), W)  # the words were rewritten
-        if N % 32 == 0:  # tiled: the scales moved too
+        if N % 32 == 0:  # tiled: words and scales were rewritten
+            assert not np.array_equal(host(dW, np.uint32, W.shape), W)
             assert not np.array_equal(host(dS, np.float16, S.shape), S)
+        else:  # the model's layout is what the GEMV reads for this shape
+            assert np.array_equal(host(dW, np.uint32, W.shape), W)
+
+
+# ---- the f32-dequant GEMV (short inputs, non-default formats) ---------------------------------------
+
+GEMV_FORMATS = [(4, 32, False), (4, 64, True), (3, 32, False), (3, 64, True), (2, 128, False), (2, 32, True)]
+
+
+@pytest.mark.parametrize("bits,group,asym", GEMV_FORMATS)
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (8, 2048, 2048), (17, 200, 384), (20, 96, 4096), (40, 330, 640),
+                                   (130, 512, 1024), (5, 100, 160)])
+def test_gemv_formats(sdamd, oracle, bits, group, asym, M, N, K):
+    """The reference's matmul_gemv(f) for every format (src/kernels.rs:590-635) in the model's layout:
+    f32 dequant, f32 accumulation, within one f16 ulp of the oracle.  Ragged N, K not a multiple of
+    128, and M past the 32 rows of one workgroup."""
+    if K % group:
+        pytest.skip("K must be a multiple of the group")
+    rng = np.random.default_rng(bits * 1000 + group + M + N + K + asym)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    codes = rng.integers(0, 1 << bits, size=(N, K), dtype=np.uint32)
+    import cases as gcases
+    W = gcases.pack_codes(codes, bits)
+    S = rng.uniform(0.005, 0.03, size=N * K // group).astype(np.float16)
+    B = rng.uniform(-0.1, 0.1, size=N * K // group).astype(np.float16) if asym else None
+    dA, dW, dS = dev(A), dev(W), dev(S)
+    dB = dev(B) if asym else None
+    dY = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
+    sdamd.op_matmul_fmt(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dB.data_ptr() if asym else None, dY.data_ptr(),
+                        M, N, K, bits, group, asym)
+    torch.cuda.synchronize()
+    got = host(dY, np.float16, (M, N))
+    want = oracle.h2f(oracle.matmul(A.view(np.uint16), W, S.view(np.uint16), N, K, False, bits=bits, group=group,
+                                    asym=asym, Bi=None if B is None else B.view(np.uint16)))
+    err = np.abs(got.astype(np.float32) - want)
+    assert (err <= 1.01 * f16_ulp(want) + 2e-5).all(), f"max err {err.max()}"
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 20])
+@pytest.mark.parametrize("N,K", [(8256, 2048), (5120, 2048), (12288, 2048), (2048, 6144), (96, 512), (344, 256)])
+def test_gemv_short_rows(sdamd, synth, oracle, M, N, K):
+    """The engine's GEMV rows (M <= 20) on the 2B's shapes in the tiled layout, and untileable ones in
+    the model's layout: the reference GEMV's f32 dequant within one f16 ulp."""
+    rng = np.random.default_rng(M * 7 + N + K)
+    A, W, S = gemm_case(synth, rng, M, N, K)
+    Y = run_gemm(sdamd, A, W, S, M, N, K, True)
+    check_gemm(oracle, A, W, S, Y, N, K, True)
+
+
+def split_sum(part, ks, M, N):
+    """The consumer's sum of the split-K slots: slot order in f32, then one rounding to f16."""
+    p = part.reshape(ks, M, N)
+    s = p[0].copy()
+    for z in range(1, ks):
+        s += p[z]
+    return s.astype(np.float16)
+
+
+@pytest.mark.parametrize("M,N,K,exact,cfg,ks", [
+    (512, 2048, 2048, False, 24, 2),   # prefill out_proj / o_proj: (2,1) tiles with k halves, 2 splits
+    (512, 2048, 6144, False, 20, 4),   # prefill down: (4,1) tiles, 4 splits
+    (120, 2048, 6144, False, 18, 8),   # question down: (2,1) tiles, 8 splits
+    (120, 2048, 2048, False, 3, 4),    # question out_proj: 16x16 (2,1), 4 splits
+    (8, 2048, 2048, True, -1, 2),      # GEMV partials
+    (8, 2048, 6144, True, -1, 4),
+    (20, 2048, 2048, True, -1, 1),
+])
+def test_split_partials(sdamd, synth, oracle, M, N, K, exact, cfg, ks):
+    """The split-K partial slots the residual add consumes: summed in slot order and rounded to f16
+    they are within one f16 ulp of the oracle's product."""
+    rng = np.random.default_rng(M + N + K + ks)
+    A, W, S = gemm_case(synth, rng, M, N, K)
+    dA, dW, dS = dev(A), dev(W), dev(S)
+    dP = torch.empty(ks * M * N * 4, dtype=torch.uint8, device="cuda")
+    sdamd.op_matmul_split(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dP.data_ptr(), M, N, K, exact, cfg, ks)
+    torch.cuda.synchronize()
+    Y = split_sum(host(dP, np.float32, (ks * M * N,)), ks, M, N)
+    check_gemm(oracle, A, W, S, Y, N, K, exact)
+
+
+@pytest.mark.parametrize("M,exact", [(8, True), (17, True), (120, False), (512, False)])
+def test_gate_up_silu(sdamd, synth, oracle, M, exact):
+    """gate_up with silu * mul in the epilogue (the engine's fused form) against the oracle's gate_up
+    then silu_mul: the error allowed is one f16 ulp of the output plus what one f16 ulp of gate and up
+    each can move silu(g) u."""
+    N, K = 12288, 2048
+    rng = np.random.default_rng(M + exact)
+    A, W, S = gemm_case(synth, rng, M, N, K)
+    dA, dW, dS = dev(A), dev(W), dev(S)
+    dmid = torch.empty(M * N, dtype=torch.uint8, device="cuda")
+    sdamd.op_gate_up_silu(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dmid.data_ptr(), M, N, K, exact)
+    torch.cuda.synchronize()
+    got = host(dmid, np.float16, (M, N // 2)).astype(np.float32)
+    big = oracle.matmul(A.view(np.uint16), W, S.view(np.uint16), N, K, f16_deq=not exact)
+    import ctypes
+    mid = np.empty((M, N // 2), np.uint16)
+    oracle.lib().or_silu_mul(oracle.P(big), ctypes.c_int(M), ctypes.c_int(N // 2), oracle.P(mid))
+    want = oracle.h2f(mid)
+    g = oracle.h2f(big[:, :N // 2]).astype(np.float64)
+    u = oracle.h2f(big[:, N // 2:]).astype(np.float64)
+    sig = 1 / (1 + np.exp(-g))
+    dsilu = sig * (1 + g * (1 - sig))
+    tol = 1.01 * f16_ulp(want) + np.abs(dsilu * u) * f16_ulp(g) + np.abs(g * sig) * f16_ulp(u) + 1e-6
+    err = np.abs(got - want)
+    assert (err <= tol).all(), f"{(err > tol).sum()} beyond tolerance; max err {err.max()}"

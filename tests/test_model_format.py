@@ -55,12 +55,42 @@ def test_tiny_model_directory(sdamd, synth, tiny_model):
         assert o1 % 256 == 0 and o1 + b1 <= o2  # aligned, non-overlapping
 
 
-def test_wire_embedding_rows_rejected(sdamd, tiny_model):
+def test_embedding_rows_with_scale_codes(sdamd, synth, oracle, tmp_path):
+    """An int3 embedding whose rows store 8-bit scale codes (the hosted model's download format,
+    src/model.rs:260-283): the product's reader (the engine's C++ decode) and the oracle's decode
+    give the same f16 scales, and the codes do encode the writer's scales closely."""
+    d = synth.write_model(str(tmp_path / "u8"), synth.CONFIG_TINY, vocab=300, seed=4, embed_fmt=(3, 32, False),
+                          u8_embed=True)
+    m = sdamd.model.read_manifest(d)
+    assert m.embed.u8 and m.embed.wire_row_bytes == 512 * 3 // 8 + 4 + 512 // 32
+    parts = dict(sdamd.model.embed_parts(d, m.embed))
+    om = oracle.OracleModel(d)
+    assert np.array_equal(parts["embed.s"], om.embed["embed.s"])
+    assert np.array_equal(parts["embed.q"], om.embed["embed.q"])
+    assert m.tensors["embed.q"].bits == 3 and parts["embed.q"].size == 300 * 512 * 3 // 8
+
+
+def test_wire_row_size_is_checked(sdamd, tiny_model):
     m = sdamd.model.read_manifest(tiny_model)
     e = m.embed
     e.wire_row_bytes = 10
-    with pytest.raises(RuntimeError, match="wire"):
+    with pytest.raises(RuntimeError, match="expected"):
         sdamd.model.embed_parts(tiny_model, e)
+
+
+def test_other_formats_are_written(sdamd, synth, tmp_path):
+    """Adapter layers and matrices in non-default formats land in the manifest as the reference
+    describes them (src/model.rs:58-83)."""
+    cfg = dict(synth.CONFIG_TINY, layer_types=["linear_attention", "adapter", "full_attention", "adapter"])
+    d = synth.write_model(str(tmp_path / "fmt"), cfg, vocab=64, seed=5,
+                          mat_fmt={"proj": (3, 64, True), "1.proj": (2, 128, False), "down": (4, 64, False)})
+    m = sdamd.model.read_manifest(d)
+    t = m.tensors
+    assert (t["layers.1.proj.q"].bits, t["layers.1.proj.q"].group, t["layers.1.proj.q"].asym) == (2, 128, False)
+    assert (t["layers.3.proj.q"].bits, t["layers.3.proj.q"].group, t["layers.3.proj.q"].asym) == (3, 64, True)
+    assert t["layers.3.proj.b"].bytes == 512 * 512 // 64 * 2
+    assert t["layers.0.down.q"].group == 64 and t["layers.0.down.s"].bytes == 512 * 1024 // 64 * 2
+    assert t["layers.0.in_proj.q"].group == 32
 
 
 def test_manifest_missing_is_an_error(sdamd, tmp_path):

@@ -115,6 +115,84 @@ def test_matmul_matches_brute_force(oracle, name, f16_deq):
     within_ulp(oracle.h2f(Y), g[f"{name}.{'y16' if f16_deq else 'y32'}"].astype(np.float32), extra=1e-6)
 
 
+# ---- embedding and the hosted model's scale codes ---------------------------------------------
+
+EMBED_FORMATS = [(4, 32, False), (3, 32, False), (3, 64, True), (2, 128, False), (4, 64, True), (2, 32, True)]
+
+
+@pytest.mark.parametrize("bits,group,asym", EMBED_FORMATS)
+def test_embed_matches_independent_decode(oracle, bits, group, asym):
+    """or_embed (src/kernels.rs:63-89) against the float64 decode of tests/golden/make_golden.py,
+    written from the format description: (q - 2^(bits-1)) s is exact in f32, and q s + b rounds once
+    in both, so the rows agree bit for bit.  Codes, scales and biases are independent draws; the
+    ids repeat and go out of order."""
+    import make_golden
+    rng = np.random.default_rng(bits * 100 + group + asym)
+    vocab, d = 37, 256
+    codes = rng.integers(0, 1 << bits, size=(vocab, d), dtype=np.uint32)
+    Q = cases.pack_codes(codes, bits)
+    S = rng.uniform(-0.05, 0.05, size=vocab * d // group).astype(np.float16)
+    B = rng.uniform(-0.3, 0.3, size=vocab * d // group).astype(np.float16) if asym else None
+    ids = rng.integers(0, vocab, 50).astype(np.uint32)
+    ids[:3] = [vocab - 1, 0, vocab - 1]
+    x = oracle.embed(ids, Q, S.view(np.uint16), d, bits, group, asym, None if B is None else B.view(np.uint16))
+    want = make_golden.decode(codes, S, B, vocab, d, bits, group, asym)[ids].astype(np.float32)
+    assert np.array_equal(x.view(np.uint32), want.view(np.uint32))
+
+
+def test_add_bias_closed_form(oracle):
+    """or_add_bias (src/kernels.rs:138-149): one f32 add of the f16 value and the f32 bias, rounded
+    to f16 (numpy's IEEE arithmetic)."""
+    rng = np.random.default_rng(13)
+    y = (4 * rng.standard_normal((9, 48))).astype(np.float16)
+    c = rng.standard_normal(48).astype(np.float32)
+    c[:4] = [0.0, 65504.0, 1e-8, -3.0]
+    got = oracle.add_bias(y.view(np.uint16), c)
+    want = (y.astype(np.float32) + c[None, :]).astype(np.float16)
+    assert np.array_equal(got, want.view(np.uint16))
+
+
+def _scale_rows(m, j, codes):
+    head = np.zeros((len(m), 2), np.uint16)
+    head[:, 0] = np.asarray(m, np.float16).view(np.uint16)
+    head[:, 1] = j
+    return head.view(np.uint8).reshape(len(m), 4), np.asarray(codes, np.uint8)
+
+
+def test_decode_scale_codes_known_answers(oracle):
+    """src/model.rs:217-236 at the exponents whose power of two is exact: k j = 0, 4096, 8192 and
+    12288 give m, m/2, m/4, m/8; the code's top bit is the sign; j = 0 gives m for every k."""
+    m = [0.01, 3.5, 1e-3, 65504.0]
+    j = [4096, 2048, 1024, 0]
+    codes = [[0, 1, 2, 3, 128, 129], [0, 2, 4, 6, 130, 132], [0, 4, 8, 12, 128 | 8, 128 | 12],
+             [0, 17, 127, 128, 128 | 5, 255]]
+    h, c = _scale_rows(m, j, codes)
+    got = oracle.decode_scale_rows(h, c).view(np.float16).astype(np.float64)
+    m16 = np.asarray(m, np.float16).astype(np.float64)
+    want = np.array([[1, 1 / 2, 1 / 4, 1 / 8, -1, -1 / 2], [1, 1 / 2, 1 / 4, 1 / 8, -1 / 2, -1 / 4],
+                     [1, 1 / 2, 1 / 4, 1 / 8, -1 / 4, -1 / 8], [1, 1, 1, -1, -1, -1]]) * m16[:, None]
+    assert np.array_equal(got, want)
+    # the packed form (headers first, then all codes) reads the same values
+    flat = np.concatenate([h.reshape(-1), c.reshape(-1)]).tobytes()
+    assert np.array_equal(oracle.decode_scale_codes(flat, 4, 6), oracle.decode_scale_rows(h, c))
+
+
+def test_decode_scale_codes_random(oracle):
+    """Random headers and codes against exp2 in float64 (a different routine from the oracle's
+    power), within one f16 rounding of the magnitude."""
+    rng = np.random.default_rng(14)
+    n, g = 40, 64
+    m = rng.uniform(1e-3, 2.0, n)
+    j = rng.integers(0, 400, n)
+    c = rng.integers(0, 256, (n, g))
+    h, cc = _scale_rows(m, j, c)
+    got = oracle.decode_scale_rows(h, cc).view(np.float16).astype(np.float32)
+    m16 = np.asarray(m, np.float16).astype(np.float64)
+    mag = m16[:, None] * np.exp2(-(c & 127) * j[:, None] / 4096.0)
+    want = np.where(c >= 128, -mag, mag).astype(np.float32)
+    within_ulp(got, want, ulps=0.5, extra=0.0)
+
+
 # ---- row and elementwise kernels --------------------------------------------------------------
 
 def test_add_norm_closed_form(oracle):
