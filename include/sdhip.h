@@ -181,6 +181,17 @@ int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off
               int L, int H, int dk, int dv, void* state, int load_state, void* o, void* stream, char* err,
               size_t errlen);
 
+/* No counterpart in the reference: sd_op_matmul (cfg < 0, packed = 1) for callers that cannot
+ * allocate device memory, such as code under HIP graph capture or serving loops that forbid
+ * hipMalloc.  It calls no hipMalloc, hipFree or other allocating routine: the split-K partial slots
+ * go to a fixed 16 MiB device array of the library (one per GPU, held until the process ends), and a
+ * call whose shape needs more (ks * M * N f32 slots) fails with an error.  The weights must already
+ * be in what the kernels read (sd_op_repack_w4); f16 dequant (exact = 0) needs N a multiple of 32.
+ * The results are those of sd_op_matmul for the same arguments.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (other streams, other threads) race. */
+int sd_op_matmul_noalloc(const void* A, const void* Wq, const void* Sc, void* Y, int M, int N, int K, int exact,
+                         void* stream, char* err, size_t errlen);
+
 /* The reference's matmul_gemv(f) (src/kernels.rs:590-635, decode 550-576) for any of its weight
  * formats, on device buffers in the model's layout: Y[M,N] f16 = A[M,K] f16 . deq(W)^T with W
  * [N][K/32] blocks of 4*bits bytes (int2/int3/int4), scales [N][K/group] f16 and, when asym, biases

@@ -29,7 +29,7 @@ SYMBOLS = [
     "sd_ask_ids", "sd_op_matmul", "sd_op_gdn", "sd_engine_forward_batch", "sd_engine_ask_batch",
     "sd_op_repack_w4", "sd_decode_scale_codes", "sd_op_matmul_fmt", "sd_op_matmul_split", "sd_op_gate_up_silu",
     "sd_op_embed", "sd_op_add_norm", "sd_op_silu_mul", "sd_op_add_bias", "sd_op_conv", "sd_op_gnorm",
-    "sd_op_attention", "sd_engine_trace",
+    "sd_op_attention", "sd_engine_trace", "sd_op_matmul_noalloc",
 ]
 VOID_SYMBOLS = ("sd_engine_free", "sd_snapshot_free", "sd_head_free", "sd_engine_hidden_size", "sd_engine_adapter",
                 "sd_snapshot_len", "sd_decode_scale_codes")
@@ -114,6 +114,7 @@ def lib():
         L.sd_op_gnorm.argtypes = [vp, vp, i32, i32, vp, i32, i32, i32, vp, vp, err, sz]
         L.sd_op_attention.argtypes = [vp, i32, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32, vp, vp, err, sz]
         L.sd_engine_trace.argtypes = [vp, vp, sz, vp, vp, sz, vp, vp, sz, C.POINTER(sz), err, sz]
+        L.sd_op_matmul_noalloc.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, vp, err, sz]
         for name in SYMBOLS:
             if name not in VOID_SYMBOLS:
                 getattr(L, name).restype = i32
@@ -462,3 +463,9 @@ def op_gnorm(o, big, stride, z_off, w, L, H, DV, out, stream=None):
 def op_attention(big, stride, qw, kw, rope, L, P, HQ, HK, HD, RD, Q, Kc, Vt, ctx, out, stream=None):
     _call(lib().sd_op_attention, C.c_void_p(big), stride, C.c_void_p(qw), C.c_void_p(kw), C.c_void_p(rope), L, P, HQ, HK,
           HD, RD, C.c_void_p(Q), C.c_void_p(Kc), C.c_void_p(Vt), ctx, C.c_void_p(out), _sp(stream))
+
+
+def op_matmul_noalloc(A, Wq, Sc, Y, M, N, K, exact=False, stream=None):
+    """sd_op_matmul_noalloc: sd_op_matmul (engine plan, pre-packed weights) with no device allocation."""
+    _call(lib().sd_op_matmul_noalloc, C.c_void_p(A), C.c_void_p(Wq), C.c_void_p(Sc), C.c_void_p(Y), M, N, K,
+          int(exact), _sp(stream))

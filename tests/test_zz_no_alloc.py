@@ -1,0 +1,61 @@
+"""sd_op_matmul_noalloc (no counterpart in the reference; for callers that cannot allocate device
+memory) against sd_op_matmul, the entry point it mirrors, on two calls in a row (the second one
+smaller, over the same scratch array), through the C ABI.  Both use the same plan and kernels, so
+the outputs are bit-identical."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def dev(a):
+    a = np.ascontiguousarray(a)
+    return torch.from_numpy(a.view(np.uint8).reshape(-1).copy()).cuda()
+
+
+def case(synth, rng, M, N, K):
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    W = synth.pack_nibbles(rng.integers(0, 16, size=(N, K), dtype=np.uint32))
+    S = rng.uniform(0.005, 0.02, size=(N, K // 32)).astype(np.float16)
+    return dev(A), dev(W), dev(S)
+
+
+def both(sdamd, dA, dW, dS, M, N, K, exact):
+    """(sd_op_matmul, sd_op_matmul_noalloc) outputs for the same packed weights."""
+    y0 = torch.zeros(M * N * 2, dtype=torch.uint8, device="cuda")
+    y1 = torch.full((M * N * 2,), 0xAB, dtype=torch.uint8, device="cuda")
+    sdamd.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), y0.data_ptr(), M, N, K, exact, -1, True)
+    sdamd.op_matmul_noalloc(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), y1.data_ptr(), M, N, K, exact)
+    torch.cuda.synchronize()
+    return y0.cpu().numpy(), y1.cpu().numpy()
+
+
+@pytest.mark.parametrize("first,second", [
+    ((512, 2048, 6144, False), (120, 2048, 2048, False)),   # 4 split-K slots filling the array, then 4 smaller
+    ((128, 6144, 2048, False), (64, 512, 2048, False)),     # BASELINE configs[0], then a split 16x16 tile
+    ((8, 8256, 2048, True), (3, 2048, 2048, True)),        # the GEMV rows (no scratch)
+])
+def test_noalloc_matches_matmul_twice(sdamd, synth, first, second):
+    rng = np.random.default_rng(sum(first) + sum(second))
+    for (M, N, K, exact) in (first, second):
+        dA, dW, dS = case(synth, rng, M, N, K)
+        sdamd.op_repack_w4(dW.data_ptr(), dS.data_ptr(), N, K)
+        y0, y1 = both(sdamd, dA, dW, dS, M, N, K, exact)
+        assert np.array_equal(y0, y1), f"M={M} N={N} K={K}: outputs differ"
+
+
+def test_noalloc_rejects_what_does_not_fit(sdamd, synth):
+    """A prefill shape whose split-K slots exceed the 16 MiB array is refused with a clear error;
+    the entry point still works afterwards."""
+    rng = np.random.default_rng(9)
+    M, N, K = 1024, 2048, 6144  # 4 slots of 1024 x 2048 f32 = 32 MiB
+    dA, dW, dS = case(synth, rng, M, N, K)
+    sdamd.op_repack_w4(dW.data_ptr(), dS.data_ptr(), N, K)
+    y = torch.zeros(M * N * 2, dtype=torch.uint8, device="cuda")
+    with pytest.raises(sdamd.EngineError, match="scratch"):
+        sdamd.op_matmul_noalloc(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), y.data_ptr(), M, N, K, False)
+    M2 = 256
+    dA2 = dev(rng.standard_normal((M2, K)).astype(np.float16))
+    y0, y1 = both(sdamd, dA2, dW, dS, M2, N, K, False)
+    assert np.array_equal(y0, y1)
