@@ -171,24 +171,31 @@ struct GdnWs {
 };
 size_t gdn_ws_bytes(int cap, const GdnShape& s);
 void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws);
-// Every sequence's first rows read the conv history `hist`.
+// The lu block every plan reads (device, at the start of the pool): u32 [L, P, ctx, has_cache,
+// chunks, sequences, 0, 0], then at byte 32 the device address of the prefix snapshot's arena image
+// (null: the live arena's states and histories are the prefix).  A layer's state and history sit at
+// byte offsets state_off / hist_off of either arena image.
+constexpr size_t LU_PREFIX_BYTE = 32;
+// Every sequence's first rows read the conv history: the prefix's (lu) or `hist`.
 void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out,
-               const Segs& sg, hipStream_t st);
+               const Segs& sg, hipStream_t st, const uint32_t* lu = nullptr, size_t hist_off = 0);
 // hist (nullable) is updated from big afterwards (the reference's hist_update; single sequence
-// only).  nch = chunk grid size (chunks past lu[4] exit when sg.chunk is set).
+// only), its old rows from the prefix's history.  nch = chunk grid size (chunks past lu[4] exit when
+// sg.chunk is set).
 void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
-              const GdnWs& ws, f16* hist, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st);
-// lu = device [L, P, ctx, has_cache, chunks, sequences] (the state is loaded when has_cache); with
-// lu null, load_default decides.  Every sequence starts from `state`; the final state is written
-// back only for a single sequence (sg.seq null).  nseq = sequence grid size.
+              const GdnWs& ws, f16* hist, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st,
+              size_t hist_off = 0);
+// lu = device block above (the state is loaded when has_cache, from the prefix's arena image when it
+// names one); with lu null, load_default decides.  Every sequence starts from that state; the final
+// state is written to `state` only for a single sequence (sg.seq null).  nseq = sequence grid size.
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
-              const Segs& sg, int nseq, hipStream_t st);
+              const Segs& sg, int nseq, hipStream_t st, size_t state_off = 0);
 // The same recurrence token by token (the reference's own order), for short inputs: every
-// sequence starts from `state` (loaded when lu[3] / load_default); with one sequence the final
-// state is written back and hist (nullable) updated afterwards, as gdn_prep + gdn_scan do.
+// sequence starts from the prefix state as gdn_scan; with one sequence the final state is written
+// to `state` and hist (nullable) updated afterwards, as gdn_prep + gdn_scan do.
 void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
                float* state, const uint32_t* lu, int load_default, float* o, f16* hist, const Segs& sg, int nseq,
-               hipStream_t st);
+               hipStream_t st, size_t state_off = 0, size_t hist_off = 0);
 void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st);
 
 // ---- pointer head (head_gpu.hip) -------------------------------------------------------------

@@ -357,8 +357,10 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
             L.dtb = f32(p + "dt_bias", cfg.H);
             L.gnorm = f32(p + "gnorm", cfg.dv);
             L.out_proj = mat(p + "out_proj");
-            L.state = reinterpret_cast<float*>(arena + li * state_bytes);
-            L.hist = reinterpret_cast<f16*>(arena + arena_state_bytes + li * hist_bytes);
+            L.state_off = li * state_bytes;
+            L.hist_off = arena_state_bytes + li * hist_bytes;
+            L.state = reinterpret_cast<float*>(arena + L.state_off);
+            L.hist = reinterpret_cast<f16*>(arena + L.hist_off);
             li++;
         } else {
             SD_CHECK(cfg.hd == 256, "attention: only head_dim 256 is supported");
@@ -642,17 +644,24 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
             const int n = W.in_proj.N;
             const GdnShape gs{cfg.H, cfg.dk, cfg.dv, n, C + cfg.H * cfg.dv, C + cfg.H * cfg.dv + cfg.H, C, C};
             mm(steps, "in_proj", P.h, W.in_proj, P.big, L, sr);
-            steps.push_back({"conv", [=](hipStream_t s) { conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, sg, s); }});
+            // conv and the delta rule read the prefix's history and state in place (from the snapshot
+            // the lu block names, else the live arena) and write the live arena
+            steps.push_back({"conv", [=](hipStream_t s) {
+                conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, sg, s, luv, W.hist_off);
+            }});
             f16* hist_upd = nseq ? nullptr : W.hist;  // several sequences leave no history
             if (recur) {
                 steps.push_back({"gdn", [=](hipStream_t s) {
-                    gdn_recur(P.qkvc, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, hist_upd, sg, nseq, s);
+                    gdn_recur(P.qkvc, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, hist_upd, sg, nseq, s, W.state_off,
+                              W.hist_off);
                 }});
             } else {
                 steps.push_back({"gdn", [=](hipStream_t s) {
-                    gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, hist_upd, sg, nch, luv, s);
+                    gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, hist_upd, sg, nch, luv, s, W.hist_off);
                 }});
-                steps.push_back({"gdn", [=](hipStream_t s) { gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s); }});
+                steps.push_back({"gdn", [=](hipStream_t s) {
+                    gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s, W.state_off);
+                }});
             }
             steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
             y = mm_y(steps, "out_proj", P.o, W.out_proj, L, sr);
@@ -728,10 +737,13 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
 }
 
 void Engine::upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
-                    uint32_t chunks, uint32_t nseq) {
-    // lu, ids and rows (and the Segs tables a batch wrote before) in one host-to-device copy
+                    uint32_t chunks, uint32_t nseq, const Snapshot* cache) {
+    // lu, ids and rows (and the Segs tables a batch wrote before) in one host-to-device copy; the lu
+    // block names the snapshot whose states and histories the forward reads in place
     const uint32_t v[8] = {(uint32_t)n, (uint32_t)P, SD_CONTEXT, has_cache ? 1u : 0u, chunks, nseq, 0u, 0u};
     std::memcpy(up_h, v, sizeof(v));
+    const void* prefix = cache ? cache->arena : nullptr;
+    std::memcpy(up_h + LU_PREFIX_BYTE, &prefix, sizeof(prefix));
     std::memcpy(up_h + pool.off_ids, ids, n * 4);
     uint32_t* rows_h = reinterpret_cast<uint32_t*>(up_h + pool.off_rows);
     for (size_t r = 0; r < n_rows; r++) rows_h[r] = (uint32_t)rows[r];
@@ -740,13 +752,14 @@ void Engine::upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_
     up_dirty = 0;
 }
 
-// Restore (src/engine.rs:552-571): GDN state + conv history in one copy; K/V prefix rows only when
-// the live cache does not already hold this snapshot's prefix (question forwards write rows >= P
-// only, so after one restore the prefix stays valid for every later question).
+// Restore (src/engine.rs:552-571).  The GDN states and conv histories are not copied: the kernels
+// read them from the snapshot in place (upload puts its address in the lu block) and write the live
+// arena.  The K/V prefix rows are copied only when the live cache does not already hold this
+// snapshot's prefix (question forwards write rows >= P only, so after one restore the prefix stays
+// valid for every later question).
 void Engine::restore(const Snapshot* cache, size_t P) {
     if (cache) {
         std::vector<CopyDesc> cp;
-        cp.push_back(CopyDesc{static_cast<const uint8_t*>(cache->arena), arena, 1, arena_bytes, arena_bytes, arena_bytes});
         if (kv_owner != cache->id) {
             // K rows [hk][t][hd]; V transposed [hk][hd][t] (the attention kernel's layout).  The V
             // rows carry P8 keys: the live rows P..P8-1 are rewritten by the forward before any
@@ -761,7 +774,7 @@ void Engine::restore(const Snapshot* cache, size_t P) {
             }
             kv_owner = cache->id;
         }
-        copy_batch(cp.data(), cp.size(), st);
+        if (!cp.empty()) copy_batch(cp.data(), cp.size(), st);
     } else {
         fill_u32(reinterpret_cast<uint32_t*>(arena + arena_state_bytes), (arena_bytes - arena_state_bytes) / 4, 0u, st);
         kv_owner = 0;
@@ -816,7 +829,7 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
     SD_CHECK(n_rows <= SD_CONTEXT, "at most 4096 hidden rows per forward");
     ensure_pool(std::max(L, (int)n_rows));  // the row tables and outputs hold n_rows entries
     Plan& pl = plan(L);
-    upload(ids, n, rows, n_rows, P, cache != nullptr, 0, 0);
+    upload(ids, n, rows, n_rows, P, cache != nullptr, 0, 0, cache);
     restore(cache, P);
     launch_and_read(pl, n_rows, timed);
     Snapshot* snap = nullptr;
@@ -904,7 +917,7 @@ Plan& Engine::prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq
     SD_CHECK((int)nch <= pool.seg_chunk_cap, "forward_batch: chunk table overflow");
     std::memcpy(up_h + pool.off_seg_seq, seqt.data(), nseq * 4);
     up_dirty = pool.off_seg_seq + nseq * 4;  // sent with the ids by upload()
-    upload(ids, n, rows, n_rows, P, cache != nullptr, nch, (uint32_t)nseq);
+    upload(ids, n, rows, n_rows, P, cache != nullptr, nch, (uint32_t)nseq, cache);
     restore(cache, P);
     return pl;
 }
@@ -1027,7 +1040,7 @@ std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids,
     const int L = (int)n;
     ensure_pool(L);
     Plan& pl = plan(L);
-    upload(ids, n, nullptr, 0, 0, false, 0, 0);
+    upload(ids, n, nullptr, 0, 0, false, 0, 0, nullptr);
     restore(nullptr, 0);
     // A step that launched a GEMM is timed by the kernel's own start and end; any other step by
     // the events recorded between steps.
@@ -1077,7 +1090,7 @@ size_t Engine::trace(const uint32_t* ids, size_t n, const Snapshot* cache, const
     const int L = (int)n;
     ensure_pool(L);
     Plan& pl = plan(L);
-    upload(ids, n, nullptr, 0, P, cache != nullptr, 0, 0);
+    upload(ids, n, nullptr, 0, P, cache != nullptr, 0, 0, cache);
     restore(cache, P);
     const size_t d = (size_t)cfg.d;
     size_t taps = 0;

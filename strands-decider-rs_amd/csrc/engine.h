@@ -56,6 +56,7 @@ struct LayerW {
     const float *q_norm = nullptr, *k_norm = nullptr, *bias = nullptr;
     float* state = nullptr;  // [H][dk][dv] f32 (in the live arena)
     f16* hist = nullptr;     // [3][C] f16 (in the live arena)
+    size_t state_off = 0, hist_off = 0;  // their byte offsets in an arena image (live or a snapshot's)
     f16* kc = nullptr;       // [hk][CONTEXT][hd] f16
     f16* vc = nullptr;       // [hk][hd][CONTEXT] f16 (transposed for the attention kernel)
 };
@@ -211,7 +212,7 @@ struct Engine {
     // GEMV dequant (each sequence <= 20 tokens).
     Plan& plan(int L, int nseq = 0, bool short_seqs = false);
     void upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
-                uint32_t chunks, uint32_t nseq);
+                uint32_t chunks, uint32_t nseq, const Snapshot* cache);
     void restore(const Snapshot* cache, size_t P);
     void launch_and_read(Plan& pl, size_t n_rows, bool timed, bool read = true);
     // Validation, sequence tables, upload and restore of a batched forward; returns its plan.

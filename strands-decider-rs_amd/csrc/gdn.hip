@@ -73,11 +73,22 @@ __device__ __forceinline__ void get_frag(const f16* base, int KS, int rt, int s,
     lo = *reinterpret_cast<const f16x8*>(p + 64 * 8);
 }
 
+// The prefix snapshot's arena image whose GDN states and conv histories a forward continues from,
+// read from the per-forward lu block (the device address at its byte 32; null when there is no lu
+// or the prefix is the live arena's), so one captured plan serves every snapshot and the snapshot is
+// read in place instead of being copied into the live arena first.
+__device__ __forceinline__ const uint8_t* lu_prefix(const uint32_t* lu) {
+    return lu ? *reinterpret_cast<const uint8_t* const*>(lu + 8) : nullptr;
+}
+
 // qkvc[t, c] = silu(sum_j w[c][j] x[t + j - 3, c]), rows before 0 from hist (src/kernels.rs:152-170).
 // With several sequences, row t is index i of the sequence starting at row s0.
 __global__ __launch_bounds__(256) void k_conv(const f16* __restrict__ big, int stride, int L, int C,
-                                              const float* __restrict__ w, const f16* __restrict__ hist,
-                                              float* __restrict__ out, const uint32_t* __restrict__ rowt, int R) {
+                                              const float* __restrict__ w, const f16* __restrict__ hist_live,
+                                              float* __restrict__ out, const uint32_t* __restrict__ rowt, int R,
+                                              const uint32_t* __restrict__ lu, size_t hist_off) {
+    const uint8_t* pre = lu_prefix(lu);
+    const f16* __restrict__ hist = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist_live;
     // 4 consecutive channels per thread (C % 4 == 0, checked by the launcher): 8-byte row loads,
     // 16-byte weight loads and stores; R consecutive rows per workgroup, so the weights are read
     // once per R rows and the rows a window shares come from L1
@@ -120,7 +131,8 @@ constexpr size_t U_F = 64 * 128;              // U, fp32 row-major
 __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc, const f16* __restrict__ big,
                                                   GdnShape sh, const float* __restrict__ negA,
                                                   const float* __restrict__ dtb, int L, GdnWs ws, f16* hist,
-                                                  const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu) {
+                                                  const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu,
+                                                  size_t hist_off) {
     constexpr int DK = 128, DV = 128;
     constexpr int RP = DK + 8;  // f16 row pitch of row-major tiles
     constexpr int TP = CH + 8;  // f16 row pitch of transposed tiles
@@ -423,8 +435,11 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     }
     if (tid == 0) ws.gl[slot] = eG[Lc - 1];
 
-    // ---- the reference's hist_update (src/kernels.rs:173-190)
+    // ---- the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's
+    // history ++ this forward's rows) into the live history
     if (hist) {  // each workgroup of the grid takes a slice of the channels
+        const uint8_t* pre = lu_prefix(lu);
+        const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
         const int nb = gridDim.x * H, per = (C + nb - 1) / nb, b = c * H + h;
         const int lo = b * per, hi = min(C, lo + per);
         for (int ch = lo + tid; ch < hi; ch += 256) {
@@ -432,7 +447,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
 #pragma unroll
             for (int r = 0; r < 3; r++) {
                 const int src = L - 3 + r;
-                v[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : hist[(size_t)(src + 3) * C + ch];
+                v[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : old[(size_t)(src + 3) * C + ch];
             }
 #pragma unroll
             for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = v[r];
@@ -474,7 +489,8 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
                                                    const float* __restrict__ dtb, float* __restrict__ state,
                                                    const uint32_t* __restrict__ lu, int load_default,
                                                    float* __restrict__ o, const uint32_t* __restrict__ chunkt,
-                                                   const uint32_t* __restrict__ seqt, int L, f16* hist) {
+                                                   const uint32_t* __restrict__ seqt, int L, f16* hist,
+                                                   size_t state_off, size_t hist_off) {
     constexpr int DK = 128, DV = 128;
     __shared__ float4 Qs[RTB][DK / 4], Ks[RTB][DK / 4];
     __shared__ float Vs[RTB][16];
@@ -491,10 +507,12 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
         t1 = (int)(last & 0xFFFFu) + (int)(last >> 16);
     }
     const bool load = lu ? lu[3] != 0u : load_default != 0;
-    float* Sg = state + (size_t)h * DK * DV;
+    const uint8_t* pre = lu_prefix(lu);
+    float* Sg = state + (size_t)h * DK * DV;  // the live state (written back by a single sequence)
+    const float* S0 = (pre ? reinterpret_cast<const float*>(pre + state_off) : state) + (size_t)h * DK * DV;
     float S[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) S[i] = load ? Sg[(size_t)(r0 + i) * DV + col] : 0.f;
+    for (int i = 0; i < 8; i++) S[i] = load ? S0[(size_t)(r0 + i) * DV + col] : 0.f;
     const int C = sh.C;
     const float na = negA[h], db = dtb[h], qs = 1.0f / sqrtf((float)DK);
     for (int tb = t0; tb < t1; tb += RTB) {
@@ -611,8 +629,10 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     if (seqt) return;  // several sequences: their final states are not kept
 #pragma unroll
     for (int i = 0; i < 8; i++) Sg[(size_t)(r0 + i) * DV + col] = S[i];
-    // the reference's hist_update (src/kernels.rs:173-190), each workgroup on a slice of the channels
+    // the reference's hist_update (src/kernels.rs:173-190), each workgroup on a slice of the channels:
+    // the last 3 rows of (the prefix's history ++ this forward's rows) into the live history
     if (hist) {
+        const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
         const int nb = gridDim.x * gridDim.y, per = (C + nb - 1) / nb, bi = blockIdx.y * H + h;
         const int lo = bi * per, hi = min(C, lo + per);
         for (int ch = lo + tid; ch < hi; ch += 256) {
@@ -620,7 +640,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
 #pragma unroll
             for (int r = 0; r < 3; r++) {
                 const int src = L - 3 + r;
-                hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : hist[(size_t)(src + 3) * C + ch];
+                hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : old[(size_t)(src + 3) * C + ch];
             }
 #pragma unroll
             for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = hv[r];
@@ -633,7 +653,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
 __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, float* __restrict__ state,
                                                   const uint32_t* __restrict__ lu, int load_default,
                                                   float* __restrict__ o, const uint32_t* __restrict__ chunkt,
-                                                  const uint32_t* __restrict__ seqt) {
+                                                  const uint32_t* __restrict__ seqt, size_t state_off) {
     constexpr int DK = 128, DV = 128;
     constexpr int SP = DK + 4, VP = CH + 4;
     __shared__ __attribute__((aligned(16))) float St[DVS * SP];  // S^T: [column][k]
@@ -644,10 +664,12 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
     if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
     const int c0 = sl * DVS;
     const bool load = lu ? lu[3] != 0u : load_default != 0;
-    float* Sg = state + (size_t)h * DK * DV;
+    const uint8_t* pre = lu_prefix(lu);
+    float* Sg = state + (size_t)h * DK * DV;  // the live state (written back by a single sequence)
+    const float* S0 = (pre ? reinterpret_cast<const float*>(pre + state_off) : state) + (size_t)h * DK * DV;
     for (int e = tid; e < DK * DVS; e += 256) {
         const int k = e / DVS, cc = e % DVS;
-        St[cc * SP + k] = load ? Sg[k * DV + c0 + cc] : 0.f;
+        St[cc * SP + k] = load ? S0[k * DV + c0 + cc] : 0.f;
     }
     const int cfirst = seqt ? (int)(seqt[q] & 0xFFFFu) : 0;
     const int cend = seqt ? cfirst + (int)(seqt[q] >> 16) : (L + CH - 1) / CH;
@@ -794,43 +816,45 @@ void gdn_ws_carve(void* base, int cap, const GdnShape& s, GdnWs& ws) {
 }
 
 void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out, const Segs& sg,
-               hipStream_t st) {
+               hipStream_t st, const uint32_t* lu, size_t hist_off) {
     SD_CHECK(C % 4 == 0 && stride % 4 == 0, "conv: channels and row stride must be multiples of 4");
     // rows per workgroup: enough workgroups to fill the chip, at most 8 rows each
     const int cb = (C / 4 + 255) / 256;
     int R = 1;
     while (R < 8 && (size_t)cb * ((L + 2 * R - 1) / (2 * R)) >= 512) R *= 2;
-    hipLaunchKernelGGL(k_conv, dim3(cb, (L + R - 1) / R), dim3(256), 0, st, big, stride, L, C, w, hist, out, sg.row, R);
+    hipLaunchKernelGGL(k_conv, dim3(cb, (L + R - 1) / R), dim3(256), 0, st, big, stride, L, C, w, hist, out, sg.row, R, lu,
+                       hist_off);
     launched("conv");
 }
 
 void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
-              const GdnWs& ws, f16* hist, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st) {
+              const GdnWs& ws, f16* hist, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st, size_t hist_off) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     SD_CHECK(!sg.chunk || (lu && !hist), "gdn_prep: several sequences need lu and keep no conv history");
     if (!sg.chunk) nch = (L + CH - 1) / CH;
-    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H), dim3(256), 0, st, qkvc, big, s, negA, dtb, L, ws, hist, sg.chunk, lu);
+    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H), dim3(256), 0, st, qkvc, big, s, negA, dtb, L, ws, hist, sg.chunk, lu,
+                       hist_off);
     launched("gdn_prep");
 }
 
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
-              const Segs& sg, int nseq, hipStream_t st) {
+              const Segs& sg, int nseq, hipStream_t st, size_t state_off) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     SD_CHECK(!sg.seq || (lu && sg.chunk), "gdn_scan: several sequences need lu and the chunk table");
     if (!sg.seq) nseq = 1;
     hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(256), 0, st, s, L, ws, state, lu, load_default, o,
-                       sg.chunk, sg.seq);
+                       sg.chunk, sg.seq, state_off);
     launched("gdn_scan");
 }
 
 void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
                float* state, const uint32_t* lu, int load_default, float* o, f16* hist, const Segs& sg, int nseq,
-               hipStream_t st) {
+               hipStream_t st, size_t state_off, size_t hist_off) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     SD_CHECK(!sg.seq || (lu && sg.chunk && !hist), "gdn_recur: several sequences need lu and keep no history");
     if (!sg.seq) nseq = 1;
     hipLaunchKernelGGL(k_gdn_recur, dim3(s.H, s.DV / 16, nseq), dim3(256), 0, st, qkvc, big, s, negA, dtb, state, lu,
-                       load_default, o, sg.chunk, sg.seq, L, hist);
+                       load_default, o, sg.chunk, sg.seq, L, hist, state_off, hist_off);
     launched("gdn_recur");
 }
 

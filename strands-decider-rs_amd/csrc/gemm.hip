@@ -271,7 +271,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgp
     constexpr int WAIT2 = 0x0F70 | ((2 * PER_STEP) & 15) | (((2 * PER_STEP) >> 4) << 14);  // vmcnt(2 steps)
     // One array per stage, so the compiler can see that the loads into one stage never alias the
     // fragment reads of another.
-    static_assert(KH == 1 || (KH == 2 && NT2 == 1), "k halves: one column tile per wave");
+    static_assert(KH == 1 || KH == 2, "one or two k halves");
     __shared__ __attribute__((aligned(1024))) uint8_t As0[KH * STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t As1[KH * STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t As2[KH * STAGE];
@@ -435,27 +435,31 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgp
 
     if constexpr (KH == 2) {
         // The second half's accumulators go to the first half's wave of the same columns through the
-        // second half of that wave's ring array (lane-major 16-byte chunks, conflict-free).
+        // second half of that wave's ring array (lane-major 16-byte chunks, conflict-free), one column
+        // tile per pass (a pass is MT2 x 4 KiB, at most the STAGE bytes there).
         uint8_t* const xr = (wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? As2 : As3) + STAGE;
-        lds_barrier();  // every wave's loads have landed: the rings are free
-        if (kh == 1) {
 #pragma unroll
-            for (int a = 0; a < MT2; a++)
+        for (int t = 0; t < NT2; t++) {
+            lds_barrier();  // every wave's loads have landed (the rings are free), or the last pass is read
+            if (kh == 1) {
 #pragma unroll
-                for (int q = 0; q < 4; q++)
-                    *reinterpret_cast<f32x4*>(xr + ((a * 4 + q) * 64 + lane) * 16) =
-                        f32x4{acc[a][0][4 * q], acc[a][0][4 * q + 1], acc[a][0][4 * q + 2], acc[a][0][4 * q + 3]};
-        }
-        lds_barrier();
-        if (kh == 0) {
+                for (int a = 0; a < MT2; a++)
 #pragma unroll
-            for (int a = 0; a < MT2; a++)
+                    for (int q = 0; q < 4; q++)
+                        *reinterpret_cast<f32x4*>(xr + ((a * 4 + q) * 64 + lane) * 16) =
+                            f32x4{acc[a][t][4 * q], acc[a][t][4 * q + 1], acc[a][t][4 * q + 2], acc[a][t][4 * q + 3]};
+            }
+            lds_barrier();
+            if (kh == 0) {
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const f32x4 v = *reinterpret_cast<const f32x4*>(xr + ((a * 4 + q) * 64 + lane) * 16);
+                for (int a = 0; a < MT2; a++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) acc[a][0][4 * q + e] += v[e];
-                }
+                    for (int q = 0; q < 4; q++) {
+                        const f32x4 v = *reinterpret_cast<const f32x4*>(xr + ((a * 4 + q) * 64 + lane) * 16);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc[a][t][4 * q + e] += v[e];
+                    }
+            }
         }
     }
     // From here on the first half (threads 0 .. 255) stores; the second half only joins the
@@ -685,6 +689,9 @@ struct Cfg {
 #define SD_CFGMH(MT2)                                                                                            \
     Cfg{2 * MT2, 2, false, k_gemm_w4m<MT2, 1, false, false, 2>, k_gemm_w4m<MT2, 1, true, false, 2>, true,        \
         k_gemm_w4m<MT2, 1, false, true, 2>, 2}
+#define SD_CFGMH2(MT2)                                                                                           \
+    Cfg{2 * MT2, 4, false, k_gemm_w4m<MT2, 2, false, false, 2>, k_gemm_w4m<MT2, 2, true, false, 2>, true,        \
+        k_gemm_w4m<MT2, 2, false, true, 2>, 2}
 const Cfg kCfgs[] = {
     SD_CFG(1, 1, true), SD_CFG(2, 1, true),                                           // M <= 20: f32 dequant
     SD_CFG(1, 1, false), SD_CFG(2, 1, false), SD_CFG(3, 1, false), SD_CFG(4, 1, false),  // skinny
@@ -695,10 +702,13 @@ const Cfg kCfgs[] = {
     SD_CFGM(2, 1), SD_CFGM(2, 2), SD_CFGM(4, 1), SD_CFGM(3, 1), SD_CFGM(1, 1), SD_CFGM(4, 2),
     // the same with two k halves per workgroup (512 threads): (2,1), (4,1), (3,1)
     SD_CFGMH(2), SD_CFGMH(4), SD_CFGMH(3),
+    // two column tiles per wave with two k halves: (4,2), (2,2)
+    SD_CFGMH2(4), SD_CFGMH2(2),
 };
 #undef SD_CFG
 #undef SD_CFGM
 #undef SD_CFGMH
+#undef SD_CFGMH2
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 int pick_cfg(int M, bool exact) {

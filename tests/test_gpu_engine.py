@@ -219,3 +219,38 @@ def test_rotated_torso_unrotate_on_device(sdamd, synth, oracle, tmp_path_factory
             assert np.abs(g - om.probs(h, 1.0)).max() < PROB_TOL
     finally:
         eng.free()
+
+
+def test_interleaved_snapshots_read_in_place(tiny, sdamd):
+    """Question forwards read each snapshot's GDN states and conv histories in place (no restore
+    copy).  Alternating between two snapshots, batching from one, and chaining a keep-forward from a
+    snapshot must each continue their own prefix, as the oracle's copies do."""
+    eng, head, om = tiny
+    s1, s2 = ids_for(90, 70), ids_for(91, 45)
+    q1, q2, q3 = ids_for(92, 30), ids_for(93, 2), ids_for(94, 25)
+    rows1, rows2, rows3 = [0, 14, 29], [0, 1], [3, 24]
+    a = eng.forward(s1, [], keep=True).snapshot
+    b = eng.forward(s2, [], keep=True).snapshot
+    _, oa = om.forward(s1, [], keep=True)
+    _, ob = om.forward(s2, [], keep=True)
+    for snap, osnap, q, r in [(a, oa, q1, rows1), (b, ob, q2, rows2), (a, oa, q2, rows2), (b, ob, q1, rows1)]:
+        got = eng.forward(q, r, cache=snap).hidden
+        want, _ = om.forward(q, r, cache=osnap)
+        assert np.abs(got - want).max() < HIDDEN_TOL
+    got, _ = eng.forward_batch([q1, q3], [rows1, rows3], cache=b)
+    for g, q, r in zip(got, [q1, q3], [rows1, rows3]):
+        want, _ = om.forward(q, r, cache=ob)
+        assert np.abs(g - want).max() < HIDDEN_TOL
+    # a keep-forward from snapshot a, then a question from the new snapshot (a + q3)
+    c = eng.forward(q3, [], cache=a, keep=True).snapshot
+    _, oc = om.forward(q3, [], cache=oa, keep=True)
+    assert c.len == len(s1) + len(q3)
+    got = eng.forward(q1, rows1, cache=c).hidden
+    want, _ = om.forward(q1, rows1, cache=oc)
+    assert np.abs(got - want).max() < HIDDEN_TOL
+    # the snapshots are unchanged by all of it
+    again = eng.forward(q2, rows2, cache=b).hidden
+    want, _ = om.forward(q2, rows2, cache=ob)
+    assert np.abs(again - want).max() < HIDDEN_TOL
+    for s in (a, b, c):
+        s.free()

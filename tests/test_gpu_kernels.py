@@ -1,9 +1,15 @@
 """Kernel-level parity on the GPU: the int4 GEMM (BASELINE configs 0 and 1) and the gated delta
 rule (config 2), through the C ABI (sd_op_matmul / sd_op_gdn), against the C oracle."""
+import os
+import sys
+
 import numpy as np
 import pytest
 
 from conftest import f16_ulp
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import cases as gcases  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -181,7 +187,6 @@ def test_gemv_formats(sdamd, oracle, bits, group, asym, M, N, K):
     rng = np.random.default_rng(bits * 1000 + group + M + N + K + asym)
     A = rng.standard_normal((M, K)).astype(np.float16)
     codes = rng.integers(0, 1 << bits, size=(N, K), dtype=np.uint32)
-    import cases as gcases
     W = gcases.pack_codes(codes, bits)
     S = rng.uniform(0.005, 0.03, size=N * K // group).astype(np.float16)
     B = rng.uniform(-0.1, 0.1, size=N * K // group).astype(np.float16) if asym else None
