@@ -93,19 +93,267 @@ def gemm_roofline(eng, state, cfg, reps=5):
             "launches_timed": launches * reps}
 
 
-def pmc_workload(eng, state):
-    """What the rocprofv3 counter runs profile: a plain copy kernel of known size (torch.neg over
-    256 MiB of f32: 256 MiB read + 256 MiB written), then one eager 512-token forward."""
+def _marker():
+    """A one-element fill kernel of torch's: separates the segments of a profiled run."""
     import torch
+    torch.ones(1, device="cuda")
+    torch.cuda.synchronize()
+
+
+def pmc_workload(eng, head, state, questions, temp, pkg):
+    """What the rocprofv3 counter runs profile, in segments separated by marker kernels:
+    0. a plain copy kernel of known size (torch.neg over 256 MiB of f32: 256 MiB read + 256 MiB
+       written), which calibrates FETCH_SIZE and WRITE_SIZE;
+    1. one eager 512-token prefill (the launches the roofline times);
+    2. the same prefill from its captured graph, keeping the snapshot;
+    3. the batched question forward of ask_all (3 x 40 tokens from the snapshot) and the device head;
+    4. configs[1] at M = 8 (the seven GEMV-class GEMMs) and configs[2] (one gated delta net layer)."""
+    import numpy as np
+    import torch
+    import sdamd.synth as synth
     n = 64 << 20
-    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    src = torch.empty(n, dtype=torch.float32, device="cuda")  # contents do not matter to byte counts
     dst = torch.empty_like(src)
     for _ in range(3):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
+    del src, dst
+    _marker()
     eng.profile(state)
+    _marker()
+    snap = eng.forward(state, [], keep=True).snapshot
+    _marker()
+    eng.ask_batch(head, questions, OPTIONS, [temp] * len(questions), cache=snap)
+    snap.free()
+    _marker()
+    st = torch.cuda.current_stream().cuda_stream
+    rng = np.random.default_rng(0)
+    for _, N, K in CFG1_LAYER:
+        M = 8
+        dA = _dev(rng.standard_normal((M, K)).astype(np.float16))
+        dW = _dev(synth.pack_nibbles(rng.integers(0, 16, size=(N, K), dtype=np.uint32)))
+        dS = _dev(rng.uniform(0.005, 0.02, size=(N, K // 32)).astype(np.float16))
+        dY = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
+        pkg.op_repack_w4(dW.data_ptr(), dS.data_ptr(), N, K, st)
+        pkg.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, True, -1, True, st)
     torch.cuda.synchronize()
-    log(f"pmc workload done: copy kernel of {4 * n} bytes each way, one {len(state)}-token forward")
+    g = _gdn_inputs(rng)
+    pkg.op_gdn(*g["args"], st)
+    torch.cuda.synchronize()
+    log(f"pmc workload done: copy kernel of {4 * n} bytes each way, {len(state)}-token prefill (eager, graph), "
+        f"{len(questions)} batched questions, configs[1] at M = 8, configs[2]")
+
+
+# configs[1]: the GEMM set of one decoder layer (name, N, K)
+CFG1_LAYER = [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048), ("gate", 6144, 2048),
+              ("up", 6144, 2048), ("down", 2048, 6144)]
+GDN_T, GDN_H, GDN_DK, GDN_DV = 512, 16, 128, 128
+
+
+def _gdn_inputs(rng):
+    """q, k L2-normalized per head (the kernel normalizes again), v ~ N(0,1); a, b ~
+    N(0,1) with negA = -1 and dt_bias = 0 (g = -softplus(a), beta = sigmoid(b)); zero state."""
+    import numpy as np
+    import torch
+    T, H, dk, dv = GDN_T, GDN_H, GDN_DK, GDN_DV
+    C = 2 * H * dk + H * dv
+    qkv = rng.standard_normal((T, C)).astype(np.float32)
+    for j in range(2 * H):
+        blk = qkv[:, j * dk:(j + 1) * dk]
+        blk /= np.linalg.norm(blk, axis=1, keepdims=True)
+    big = np.zeros((T, 2 * H), np.float16)
+    big[:, :H] = rng.standard_normal((T, H)).astype(np.float16)
+    big[:, H:] = rng.standard_normal((T, H)).astype(np.float16)
+    keep = {"qkv": _dev(qkv), "big": _dev(big), "nA": _dev(np.full(H, -1.0, np.float32)),
+            "dtb": _dev(np.zeros(H, np.float32)),
+            "state": _dev(np.zeros(H * dk * dv, np.float32)),
+            "o": torch.empty(T * H * dv, dtype=torch.float32, device="cuda")}
+    keep["args"] = (keep["qkv"].data_ptr(), keep["big"].data_ptr(), 2 * H, 0, H, keep["nA"].data_ptr(),
+                    keep["dtb"].data_ptr(), T, H, dk, dv, keep["state"].data_ptr(), 0, keep["o"].data_ptr())
+    return keep
+
+
+def _kernel_short(name):
+    """k_gemm_w4m<2,1,false,true,1> from the (demangled or mangled) kernel name."""
+    import re
+    m = re.match(r"_ZN2sd12_GLOBAL__N_1(\d+)", name)
+    if m:  # mangled: length-prefixed name, then I<template args>E of integer/bool literals
+        n = int(m.group(1))
+        base = name[m.end():m.end() + n]
+        rest = name[m.end() + n:]
+        if rest.startswith("I"):
+            args = re.findall(r"L([ib])(\d+)E", rest[:rest.find("EE") + 2])
+            base += "<" + ",".join(v if t == "i" else ("true" if v == "1" else "false") for t, v in args) + ">"
+        return base
+    name = name.replace("void ", "").replace("sd::(anonymous namespace)::", "")
+    return name.split("(")[0]
+
+
+def _is_marker(name):
+    """torch's fill kernel (torch.ones(1) in _marker); the workloads launch no other fill."""
+    return "FillFunctor" in name
+
+
+def _segments(rows):
+    """rows: [(order, kernel name, payload)] of one profiled run of --pmc-workload, in dispatch
+    order -> the dispatches of its segments (split at the marker kernels; the copy kernel is
+    segment 0)."""
+    segs, cur = [], []
+    for r in rows:
+        if _is_marker(r[1]):
+            segs.append(cur)
+            cur = []
+        else:
+            cur.append(r)
+    segs.append(cur)
+    return segs
+
+
+def _algorithmic(cfg, seg, dispatches):
+    """Algorithmic bytes (and MFMA flops for the GEMMs) of each dispatch of a --pmc-workload
+    segment: [(bytes or None, flops or None)].  The GEMM launches follow the plan order of
+    gemm_shapes(); the per-layer kernels of the 2B have fixed shapes (L tokens after P)."""
+    d, inter = cfg["hidden_size"], cfg["intermediate_size"]
+    H, dk, dv = cfg["linear_num_key_heads"], cfg["linear_key_head_dim"], cfg["linear_value_head_dim"]
+    hq, hk, hd = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
+    C = 2 * H * dk + H * dv
+    if seg in (1, 2):
+        L, P, shapes = STATE_LEN, 0, gemm_shapes(cfg)
+    elif seg == 3:
+        L, P, shapes = N_QUESTIONS * Q_LEN, STATE_LEN, gemm_shapes(cfg)
+    else:
+        L, P, shapes = 8, 0, [(n, N, K) for n, N, K in CFG1_LAYER]
+    gi, out = 0, []
+    for name in dispatches:
+        k = _kernel_short(name)
+        b = f = None
+        if k.startswith("k_gemm_w4") or k.startswith("k_gemv"):
+            if gi < len(shapes):
+                _, N, K = shapes[gi]
+                b = N * K // 2 + N * K // 16 + 2 * L * K + 2 * L * N
+                f = 2.0 * L * N * K
+            gi += 1
+        elif seg == 4 and k.startswith("k_gdn_prep"):
+            T = GDN_T
+            b = 4 * T * GDN_H * (2 * GDN_DK + GDN_DV) + 4 * T * GDN_H
+        elif seg == 4 and k.startswith("k_gdn_scan"):
+            T = GDN_T
+            b = 4 * T * GDN_H * GDN_DV + 4 * GDN_H * GDN_DK * GDN_DV
+        elif k.startswith("k_gdn_prep"):  # q, k, v (f32), a, b (f16) in
+            b = 4 * L * C + 4 * L * H
+        elif k.startswith("k_gdn_scan"):  # o out, the state in (with a prefix) and out
+            b = 4 * L * H * dv + 4 * H * dk * dv * (2 if P else 1)
+        elif k.startswith("k_gdn_recur"):
+            b = 4 * L * C + 4 * L * H + 4 * L * H * dv + 4 * H * dk * dv * (2 if P else 1)
+        elif k.startswith("k_conv"):  # f16 channels in, f32 out, 4 taps per channel, the history
+            b = 2 * L * C + 4 * L * C + 16 * C + 2 * 3 * C
+        elif k.startswith("k_gnorm"):  # o f32 + z f16 in, f16 out
+            b = L * H * dv * (4 + 2 + 2) + 4 * dv
+        elif k.startswith("k_add_norm"):  # x f32 in and out, y f16 in, h f16 out
+            b = L * d * (4 + 4 + 2 + 2) + 4 * d
+        elif k.startswith("k_qk_prep"):  # q, gate-free k, v f16 in; Q, K, V f16 out
+            b = 2 * L * (hq * hd + 2 * hk * hd) * 2
+        elif k.startswith("k_attn<"):  # Q, gate in; K, V of P + L keys; out f16
+            b = 2 * L * hq * hd * 3 + 2 * (P + L) * hk * hd * 2
+        out.append((b, f))
+    return out
+
+
+def counter_summary(trace_dir, pmc_dirs, cfg):
+    """Per-kernel counter evidence for one --pmc-workload run: durations from a --kernel-trace run,
+    FETCH_SIZE / WRITE_SIZE scaled by the copy kernel's known bytes, and the SQ / GRBM counters
+    (MFMA busy cycles and f16 flops, LDS bank conflicts) from the other --pmc runs, per segment
+    and kernel."""
+    import csv
+    import glob
+    trace = []
+    for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                trace.append((int(r["Start_Timestamp"]), r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    trace.sort()
+    tsegs = _segments(trace)
+    counters = {}  # counter -> segments of [(order, name, value)]
+    for d in pmc_dirs:
+        per = {}
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    key = int(r.get("Dispatch_Id") or r.get("Correlation_Id"))
+                    per.setdefault(r["Counter_Name"], {}).setdefault(key, [r["Kernel_Name"], 0.0])
+                    per[r["Counter_Name"]][key][1] += float(r["Counter_Value"])
+        for cn, disp in per.items():
+            rows = [(k, v[0], v[1]) for k, v in sorted(disp.items())]
+            counters[cn] = _segments(rows)
+    copy_bytes = 4 * (64 << 20)
+    scale = {}
+    for cn in ("FETCH_SIZE", "WRITE_SIZE"):
+        if cn in counters:
+            cp = [v for _, k, v in counters[cn][0] if "neg_kernel" in k]
+            scale[cn] = copy_bytes / (statistics.median(cp) * 1024) if cp else None
+    names = ["", "eager 512-token prefill", "512-token prefill from its graph (keep)",
+             f"batched question forward ({N_QUESTIONS} x {Q_LEN} tokens after {STATE_LEN}) + device head",
+             "configs[1] at M = 8 (GEMV) and configs[2] (one gated delta net layer)"]
+    print("# per-kernel counters (rocprofv3 --pmc, one pass per counter group) and durations (--kernel-trace)")
+    print("# FETCH/WRITE scaled by the copy kernel: " +
+          ", ".join(f"{cn} x{v:.4f}" for cn, v in scale.items() if v))
+    print("# columns: dispatches, avg us (trace), algorithmic MB / dispatch, counter HBM MB / dispatch (FETCH + WRITE),")
+    print("#   algorithmic GB/s and its fraction of 8 TB/s, MFMA busy % (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024")
+    print("#   SIMDs)), f16 MFMA TFLOP/s from SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 / trace duration and its fraction of")
+    print("#   2.5 PFLOP/s, LDS bank-conflict cycles per LDS-active cycle")
+    for si in range(1, len(tsegs)):
+        tseg = tsegs[si]
+        if not tseg:
+            continue
+        alg = _algorithmic(cfg, si, [n for _, n, _ in tseg])
+        cseg = {cn: (segs[si] if si < len(segs) else []) for cn, segs in counters.items()}
+        agg = {}
+        for i, (_, name, us) in enumerate(tseg):
+            a = agg.setdefault(_kernel_short(name), {"n": 0, "us": 0.0, "alg": 0.0, "alg_n": 0, "fl": 0.0, "idx": []})
+            a["n"] += 1
+            a["us"] += us
+            a["idx"].append(i)
+            if alg[i][0] is not None:
+                a["alg"] += alg[i][0]
+                a["alg_n"] += 1
+            if alg[i][1] is not None:
+                a["fl"] += alg[i][1]
+
+        def csum(cn, idx):
+            rows = cseg.get(cn) or []
+            if len(rows) != len(tseg):
+                return None  # the counter run does not line up with the trace (missing dispatches)
+            return sum(rows[i][2] for i in idx)
+
+        print()
+        print(f"## segment {si}: {names[si] if si < len(names) else ''}: {len(tseg)} dispatches, "
+              f"{sum(u for _, _, u in tseg):.1f} us of kernels")
+        print(f"  {'kernel':36s} {'n':>4s} {'avg us':>8s} {'alg MB':>8s} {'hbm MB':>8s} {'alg GB/s':>9s} "
+              f"{'of HBM':>7s} {'mfma %':>7s} {'TFLOP/s':>8s} {'of MFMA':>8s} {'lds cf':>7s}")
+        for k, a in sorted(agg.items(), key=lambda kv: -kv[1]["us"]):
+            n, us = a["n"], a["us"]
+            algmb = a["alg"] / a["alg_n"] / 1e6 if a["alg_n"] else None
+            fe, wr = csum("FETCH_SIZE", a["idx"]), csum("WRITE_SIZE", a["idx"])
+            hbm = ((fe * scale["FETCH_SIZE"] + wr * scale["WRITE_SIZE"]) * 1024 / n / 1e6
+                   if fe is not None and wr is not None and scale.get("FETCH_SIZE") and scale.get("WRITE_SIZE") else None)
+            gbs = a["alg"] / (us * 1e-6) / 1e9 if a["alg_n"] == n else None
+            busy, gui = csum("SQ_VALU_MFMA_BUSY_CYCLES", a["idx"]), csum("GRBM_GUI_ACTIVE", a["idx"])
+            mfma = 100 * busy / (gui / 8 * 1024) if busy is not None and gui else None
+            mops = csum("SQ_INSTS_VALU_MFMA_MOPS_F16", a["idx"])
+            tf = mops * 512 / (us * 1e-6) / 1e12 if mops else None
+            bc, la = csum("SQ_LDS_BANK_CONFLICT", a["idx"]), csum("SQ_LDS_IDX_ACTIVE", a["idx"])
+            cf = bc / la if bc is not None and la else None
+
+            def fm(v, w, p):
+                return f"{v:{w}.{p}f}" if v is not None else f"{'-':>{w}s}"
+            print(f"  {k[:36]:36s} {n:4d} {us / n:8.2f} {fm(algmb, 8, 2)} {fm(hbm, 8, 2)} {fm(gbs, 9, 0)} "
+                  f"{fm(gbs / PEAK_HBM if gbs else None, 7, 3)} {fm(mfma, 7, 1)} {fm(tf, 8, 1)} "
+                  f"{fm(tf / PEAK_MFMA_F16 if tf else None, 8, 3)} {fm(cf, 7, 3)}")
+        fl = sum(a["fl"] for a in agg.values())
+        gus = sum(a["us"] for k, a in agg.items() if k.startswith("k_gemm_w4") or k.startswith("k_gemv"))
+        if fl and gus:
+            print(f"  GEMMs: {fl / 1e9:.1f} GFLOP in {gus:.1f} us = {fl / gus / 1e6:.1f} TFLOP/s "
+                  f"({fl / gus / 1e6 / PEAK_MFMA_F16:.3f} of 2.5 PFLOP/s)")
 
 
 def traffic_summary(fetch_dir, write_dir, cfg, state_len):
@@ -116,16 +364,19 @@ def traffic_summary(fetch_dir, write_dir, cfg, state_len):
     import glob
 
     def per_kernel(d, counter):
-        rows = []
+        disp = {}
         for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             with open(path) as f:
                 for r in csv.DictReader(f):
                     if r["Counter_Name"] == counter:
-                        rows.append((r["Kernel_Name"], float(r["Counter_Value"])))
-        if not rows:
+                        key = int(r.get("Dispatch_Id") or r.get("Correlation_Id"))
+                        disp.setdefault(key, [r["Kernel_Name"], 0.0])[1] += float(r["Counter_Value"])
+        if not disp:
             raise SystemExit(f"no {counter} rows under {d}")
-        copy = [v for k, v in rows if "neg_kernel" in k]
-        gemm = [v for k, v in rows if "k_gemm_w4" in k]
+        segs = _segments([(k, v[0], v[1]) for k, v in sorted(disp.items())])
+        copy = [v for _, k, v in segs[0] if "neg_kernel" in k]
+        # segment 1: the eager prefill whose GEMM launches the roofline times
+        gemm = [v for _, k, v in (segs[1] if len(segs) > 1 else []) if "k_gemm_w4" in k]
         if not copy or not gemm:
             raise SystemExit(f"{counter}: copy kernel or GEMM dispatches missing under {d}")
         return statistics.median(copy), sum(gemm) / len(gemm), len(gemm)
@@ -137,7 +388,8 @@ def traffic_summary(fetch_dir, write_dir, cfg, state_len):
     traffic = fg * 1024 * kf + wg * 1024 * kw
     shapes = gemm_shapes(cfg)
     alg = sum(N * K // 2 + N * K // 16 + 2 * state_len * K + 2 * state_len * N for _, N, K in shapes) / len(shapes)
-    print(f"# HBM traffic of k_gemm_w4 in one eager {state_len}-token prefill of the 2B (rocprofv3 --pmc)")
+    print(f"# HBM traffic of k_gemm_w4 in one eager {state_len}-token prefill of the 2B (rocprofv3 --pmc; segment 1 "
+          "of the --pmc-workload run)")
     print("# commands (R = repository root, run from /tmp):")
     print("#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d FETCH_DIR -o run -- python3 $R/bench.py --pmc-workload")
     print("#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d WRITE_DIR -o run -- python3 $R/bench.py --pmc-workload")
@@ -167,21 +419,7 @@ def trace_summary(trace_dir):
         raise SystemExit(f"no kernel_trace.csv under {trace_dir}")
     rows.sort()
 
-    import re
-
-    def short(name):
-        """k_gemm_w4<4,3,false,false> from the (demangled or mangled) kernel name."""
-        m = re.match(r"_ZN2sd12_GLOBAL__N_1(\d+)", name)
-        if m:  # mangled: length-prefixed name, then I<template args>E of integer/bool literals
-            n = int(m.group(1))
-            base = name[m.end():m.end() + n]
-            rest = name[m.end() + n:]
-            if rest.startswith("I"):
-                args = re.findall(r"L([ib])(\d+)E", rest[:rest.find("EE") + 2])
-                base += "<" + ",".join(v if t == "i" else ("true" if v == "1" else "false") for t, v in args) + ">"
-            return base
-        name = name.replace("void ", "").replace("sd::(anonymous namespace)::", "")
-        return name.split("(")[0]
+    short = _kernel_short
 
     def table(rs, title):
         agg = {}
@@ -198,9 +436,7 @@ def trace_summary(trace_dir):
 
     table(rows, "# per-kernel totals over the whole run")
 
-    def is_marker(name):
-        return "at::native" in name or name.startswith("_ZN2at6native")
-
+    is_marker = _is_marker
     mark = next((i for i, r in enumerate(rows) if is_marker(r[2])), len(rows))
     steps_rows, roof_rows = rows[:mark], [r for r in rows[mark:] if not is_marker(r[2])]
     starts = [i for i, r in enumerate(steps_rows) if "k_embed" in r[2]]
@@ -235,17 +471,29 @@ def _dev(a):
 
 
 def _timed(fn, reps):
-    """Average device ms of fn() over reps calls on torch's current stream (after one warm-up)."""
+    """Average device ms of fn(stream) over reps calls.  The calls are captured into one graph
+    (after an eager warm-up that lets the entry points size their workspaces) and the graph is
+    replayed between two events: eager launches through ctypes take several microseconds of host
+    time each, which would otherwise be what a microsecond kernel is timed at."""
     import torch
-    fn()
+    fn(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(reps):
+            fn(st)
+    g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        fn()
-    e1.record()
-    e1.synchronize()
-    return e0.elapsed_time(e1) / reps
+    best = float("inf")
+    for _ in range(3):
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) / reps)
+    return best
 
 
 def kernel_bench(pkg, reps=50):
@@ -255,7 +503,6 @@ def kernel_bench(pkg, reps=50):
     import numpy as np
     import torch
     import sdamd.synth as synth
-    stream = torch.cuda.current_stream().cuda_stream
     rng = np.random.default_rng(0)
     out = {"metric": "kernel-level configs[0..2] (int4 GEMM, layer GEMM set, gated delta net layer), 1 GPU",
            "unit": "us", "data": "synthetic (BASELINE configs distributions, seed 0)"}
@@ -266,10 +513,10 @@ def kernel_bench(pkg, reps=50):
         S = rng.uniform(0.005, 0.02, size=(N, K // 32)).astype(np.float16)
         dA, dW, dS = _dev(A), _dev(W), _dev(S)
         dY = torch.empty(M * N * 2, dtype=torch.uint8, device="cuda")
-        pkg.op_repack_w4(dW.data_ptr(), dS.data_ptr(), N, K, stream)
+        pkg.op_repack_w4(dW.data_ptr(), dS.data_ptr(), N, K, torch.cuda.current_stream().cuda_stream)
         exact = M <= 20
-        ms = _timed(lambda: pkg.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, exact,
-                                          -1, True, stream), reps)
+        ms = _timed(lambda st: pkg.op_matmul(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dY.data_ptr(), M, N, K, exact,
+                                             -1, True, st), reps)
         wbytes = N * K // 2 + N * K // 16
         io = 2 * M * K + 2 * M * N
         return {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
@@ -279,8 +526,7 @@ def kernel_bench(pkg, reps=50):
                 "hbm_frac": round((wbytes + io) / ms / 1e6 / PEAK_HBM, 4)}
 
     out["cfg0_linear"] = gemm(128, 6144, 2048)
-    layer = [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048), ("gate", 6144, 2048),
-             ("up", 6144, 2048), ("down", 2048, 6144)]
+    layer = CFG1_LAYER
     fused = [("qkv", 5120, 2048), ("in_proj", 8256, 2048), ("gate_up", 12288, 2048), ("o", 2048, 2048),
              ("down", 2048, 6144)]
     for M in (512, 8):
@@ -300,24 +546,12 @@ def kernel_bench(pkg, reps=50):
             for name, N, K in fused:
                 a16 = torch.randn(M, K, dtype=torch.float16, device="cuda")
                 b16 = torch.randn(N, K, dtype=torch.float16, device="cuda")
-                ms = _timed(lambda: torch.matmul(a16, b16.t()), reps)
+                ms = _timed(lambda st: torch.matmul(a16, b16.t()), reps)
                 out["cfg1_fused_M512"][name]["hipblaslt_f16_us"] = round(ms * 1e3, 2)
     # one gated delta net layer (prep + scan), T = 512, 16 heads, dk = dv = 128
-    T, H, dk, dv = 512, 16, 128, 128
-    C = 2 * H * dk + H * dv
-    qkv = rng.standard_normal((T, C)).astype(np.float32)
-    for j in range(2 * H):  # q and k rows L2-normalized per head (the kernel normalizes again)
-        blk = qkv[:, j * dk:(j + 1) * dk]
-        blk /= np.linalg.norm(blk, axis=1, keepdims=True)
-    big = np.zeros((T, 2 * H), np.float16)
-    big[:, :H] = rng.standard_normal((T, H)).astype(np.float16)   # a: g = -softplus(a)
-    big[:, H:] = rng.standard_normal((T, H)).astype(np.float16)   # b: beta = sigmoid(b)
-    d_qkv, d_big = _dev(qkv), _dev(big)
-    d_nA, d_dtb = _dev(np.full(H, -1.0, np.float32)), _dev(np.zeros(H, np.float32))
-    d_state = torch.zeros(H * dk * dv, dtype=torch.float32, device="cuda")
-    d_o = torch.empty(T * H * dv, dtype=torch.float32, device="cuda")
-    ms = _timed(lambda: pkg.op_gdn(d_qkv.data_ptr(), d_big.data_ptr(), 2 * H, 0, H, d_nA.data_ptr(), d_dtb.data_ptr(),
-                                   T, H, dk, dv, d_state.data_ptr(), 0, d_o.data_ptr(), stream), reps)
+    T, H, dk, dv = GDN_T, GDN_H, GDN_DK, GDN_DV
+    g = _gdn_inputs(rng)
+    ms = _timed(lambda st: pkg.op_gdn(*g["args"], st), reps)
     alg = 4 * T * H * (2 * dk + dv) + 8 * T * H + 4 * T * H * dv + 4 * H * dk * dv
     out["cfg2_gdn_layer"] = {"T": T, "H": H, "us": round(ms * 1e3, 2), "algorithmic_bytes": alg,
                              "gbps": round(alg / ms / 1e6, 1), "hbm_frac": round(alg / ms / 1e6 / PEAK_HBM, 4),
@@ -399,6 +633,8 @@ def main():
                     help="run only the workload of the rocprofv3 counter runs (copy kernel + one prefill)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print the HBM traffic summary from two rocprofv3 --pmc output folders (no GPU)")
+    ap.add_argument("--counter-summary", nargs="+", metavar="DIR",
+                    help="TRACE_DIR PMC_DIR...: per-kernel counter summary of --pmc-workload runs (no GPU)")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
                     help="print the kernel summary of a rocprofv3 --kernel-trace output folder (no GPU)")
     ap.add_argument("--kernels", action="store_true",
@@ -408,6 +644,12 @@ def main():
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary)
+        return
+    if args.counter_summary:
+        import __graft_entry__ as entry
+        entry._import_pkg()
+        import sdamd.synth as synth
+        counter_summary(args.counter_summary[0], args.counter_summary[1:], synth.CONFIG_2B)
         return
     if args.traffic_summary:
         import __graft_entry__ as entry
@@ -443,7 +685,7 @@ def main():
     questions = [rng.integers(0, synth.VOCAB_2B, Q_LEN).astype(np.uint32) for _ in range(N_QUESTIONS)]
     temp = float(dcfg["temperature"])
     if args.pmc_workload:
-        pmc_workload(eng, state)
+        pmc_workload(eng, head, state, questions, temp, pkg)
         return
     if args.sweep:
         print(json.dumps(sweep_bench(eng, head, temp)), flush=True)
