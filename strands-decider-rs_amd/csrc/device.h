@@ -92,6 +92,41 @@ __device__ __forceinline__ void bar_noflush() { asm volatile("s_barrier" ::: "me
 // not waited for, unlike __syncthreads).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// XCD-aware tile order of a (gx column blocks, gy row blocks, gz K splits) grid: the hardware gives
+// workgroup b to XCD b % 8, and each XCD has its own L2.  With a K split (gz in {2, 4, 8}) XCD x
+// takes split x % gz and a contiguous run of the column-block-major (column, row) tiles, so it reads
+// only that split's K range of the activations and of the weights.  Otherwise XCD x takes a
+// contiguous run of the tiles in column-block-major order (every row block of a column block
+// together), so a column block's weights reach one L2 only.
+__device__ __forceinline__ void xcd_tile(int b, int gx, int gy, int gz, int& bx, int& by, int& bz) {
+    const int G = gx * gy * gz, q8 = G >> 3;
+    if (gz > 1 && 8 % gz == 0 && (G & 7) == 0) {
+        const int x = b & 7, t = (x / gz) * q8 + (b >> 3);
+        bz = x % gz;
+        bx = t / gy;
+        by = t % gy;
+        return;
+    }
+    const int tile = b < 8 * q8 ? (b & 7) * q8 + (b >> 3) : b;
+    const int gyz = gy * gz;
+    bx = tile / gyz;
+    by = (tile % gyz) % gy;
+    bz = (tile % gyz) / gy;
+}
+
+// silu(g) * u = g / (1 + e^-g) * u on the hardware exp2 (v_exp_f32) and reciprocal (v_rcp_f32), each
+// within about 1 ulp in f32, where libm's expf and an IEEE divide take ~25 VALU instructions; the
+// result is rounded to f16 by the caller, as the reference stores mid (src/kernels.rs:123-135).
+// The limits hold: e^-g overflows to inf for g -> -inf and the reciprocal gives 0.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+#else
+    return g * u;
+#endif
+}
+
 __device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
     return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }

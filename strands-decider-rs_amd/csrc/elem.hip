@@ -3,6 +3,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "device.h"
 
 namespace sd {
 namespace {
@@ -189,7 +190,7 @@ __global__ void k_silu_mul(const f16* __restrict__ big, const float* __restrict_
     }
     f16x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = (f16)(gv[e] / (1.0f + expf(-gv[e])) * uv[e]);
+    for (int e = 0; e < 8; e++) o[e] = (f16)silu_mul(gv[e], uv[e]);
     *reinterpret_cast<f16x8*>(mid + i8) = o;
 }
 

@@ -63,15 +63,9 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
-    // XCD-aware tile order: workgroup b runs on XCD b % 8, so XCD x is given the contiguous run of
-    // tiles [x G/8, (x+1) G/8) in column-block-major order (every row block and K split of a column
-    // block together): a column block's weights are then fetched into one XCD's L2 only.
-    const int gy = gridDim.y, gyz = gridDim.y * gridDim.z;
-    const int G = gridDim.x * gyz;
-    const int b = blockIdx.x + gridDim.x * (blockIdx.y + gy * blockIdx.z);
-    const int q8 = G >> 3;
-    const int tile = b < 8 * q8 ? (b & 7) * q8 + (b >> 3) : b;
-    const int bx = tile / gyz, by = (tile % gyz) % gy, bz = (tile % gyz) / gy;
+    int bx, by, bz;
+    xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), gridDim.x, gridDim.y, gridDim.z, bx, by,
+             bz);
     const int m0 = by * BM, n0 = bx * BN;
     const int KB = K >> 5;
     const int steps_total = K / KSTEP;
@@ -286,13 +280,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgp
     uint8_t* const R1 = As1 + kh * STAGE;
     uint8_t* const R2 = As2 + kh * STAGE;
     uint8_t* const R3 = As3 + kh * STAGE;
-    // XCD-aware tile order, as in k_gemm_w4
-    const int gy = gridDim.y, gyz = gridDim.y * gridDim.z;
-    const int G = gridDim.x * gyz;
-    const int b = blockIdx.x + gridDim.x * (blockIdx.y + gy * blockIdx.z);
-    const int q8 = G >> 3;
-    const int tile = b < 8 * q8 ? (b & 7) * q8 + (b >> 3) : b;
-    const int bx = tile / gyz, by = (tile % gyz) % gy, bz = (tile % gyz) / gy;
+    int bx, by, bz;
+    xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), gridDim.x, gridDim.y, gridDim.z, bx, by,
+             bz);
     const int m0 = by * BM, n0 = bx * (4 * NT2 * 32);
     const int KB = K >> 5;
     const int steps = (K / KS) / ksplit / KH;  // a multiple of 4 (checked by the launcher)
@@ -508,7 +498,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgp
 #pragma unroll
                             for (int u = 0; u < 2; u++) {
                                 const float gv = (float)(f16)acc[a][t][k + u], uv = (float)(f16)acc[a][t][8 + k + u];
-                                o[u] = (f16)(gv / (1.0f + expf(-gv)) * uv);
+                                o[u] = (f16)silu_mul(gv, uv);
                             }
                             P[k / 2] = __builtin_bit_cast(uint32_t, f16x2{o[0], o[1]});
                         }
@@ -540,7 +530,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgp
                         if (i >= 8) continue;  // N % 32 == 0: the tile is whole
                         const float gv = (float)(f16)acc[a][t][i], uv = (float)(f16)acc[a][t][8 + i];
                         const int j = (cb >> 1) + 8 * (i >> 2) + 4 * g + (i & 3);
-                        Y[(size_t)m * ow + j] = (f16)(gv / (1.0f + expf(-gv)) * uv);
+                        Y[(size_t)m * ow + j] = (f16)silu_mul(gv, uv);
                     } else {
                         const int n = cb + 8 * (i >> 2) + 4 * g + (i & 3);
                         if (n < N) Y[(size_t)m * N + n] = (f16)acc[a][t][i];
@@ -566,7 +556,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgp
 #pragma unroll
                 for (int k = 0; k < 8; k++) {
                     const float gv = (float)(f16)acc[a][t][k], uv = (float)(f16)acc[a][t][8 + k];
-                    o[k] = (f16)(gv / (1.0f + expf(-gv)) * uv);
+                    o[k] = (f16)silu_mul(gv, uv);
                 }
                 *reinterpret_cast<f16x4*>(wst + rho * 32 + 8 * g) = f16x4{o[0], o[1], o[2], o[3]};
                 *reinterpret_cast<f16x4*>(wst + rho * 32 + 16 + 8 * g) = f16x4{o[4], o[5], o[6], o[7]};

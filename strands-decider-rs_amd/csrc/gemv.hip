@@ -241,7 +241,7 @@ __global__ __launch_bounds__(256) void k_gemv(const f16* __restrict__ A, const u
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float gg = (float)(f16)gv[r], uu = (float)(f16)uv[r];
-                o[r] = (f16)(gg / (1.0f + expf(-gg)) * uu);
+                o[r] = (f16)silu_mul(gg, uu);
             }
             *reinterpret_cast<f16x4*>(mid + (size_t)m * half + j) = o;
         }
