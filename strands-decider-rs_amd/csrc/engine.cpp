@@ -364,6 +364,9 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
             li++;
         } else {
             SD_CHECK(cfg.hd == 256, "attention: only head_dim 256 is supported");
+            // qk_prep pairs rotate-half partners with a lane shuffle over 8-element groups
+            SD_CHECK(cfg.rd >= 8 && cfg.rd % 8 == 0 && cfg.rd <= cfg.hd,
+                     "attention: rotary_dim must be a multiple of 8 from 8 to head_dim");
             SD_CHECK(cfg.hk > 0 && cfg.hq % cfg.hk == 0, "attention: q heads must be a multiple of kv heads");
             L.qkv = mat(p + "qkv");
             SD_CHECK(L.qkv.N >= 2 * cfg.hq * cfg.hd + 2 * cfg.hk * cfg.hd, p + "qkv: too few rows");
@@ -609,7 +612,17 @@ YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, cons
 Plan& Engine::plan(int L, int nseq, bool short_seqs) {
     const int key = (L << 8) | (nseq << 1) | (short_seqs ? 1 : 0);
     auto it = plans.find(key);
-    if (it != plans.end()) return it->second;
+    if (it != plans.end()) {
+        it->second.used = ++plan_clock;
+        return it->second;
+    }
+    // Every forward ends with the device idle, so no evicted graph is still running.
+    if (plans.size() >= kMaxPlans) {
+        auto lru = std::min_element(plans.begin(), plans.end(),
+                                    [](const auto& a, const auto& b) { return a.second.used < b.second.used; });
+        lru->second.destroy();
+        plans.erase(lru);
+    }
     Plan pl;
     pl.L = L;
     const bool sr = nseq ? short_seqs : L <= 20;  // the reference's GEMV rows
@@ -733,6 +746,7 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
         SD_HIP(hipStreamEndCapture(st, &pl.graph));
         SD_HIP(hipGraphInstantiate(&pl.exec, pl.graph, nullptr, nullptr, 0));
     }
+    pl.used = ++plan_clock;
     return plans.emplace(key, std::move(pl)).first->second;
 }
 

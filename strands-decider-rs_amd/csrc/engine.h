@@ -97,6 +97,7 @@ struct Plan {
     int L = 0;
     std::vector<Step> steps;
     YIn last_y;  // where the last sublayer output lives (read by the final norm)
+    uint64_t used = 0;  // Engine::plan_clock at the last use (least recently used plans are evicted)
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     void destroy();
@@ -153,6 +154,10 @@ struct Engine {
     bool gu_il = false;  // gate_up weights interleaved in groups of 16 rows (interleave_gate_up)
     Pool pool;
     std::map<int, Plan> plans;
+    uint64_t plan_clock = 0;
+    // Captured plans kept at most (each holds an instantiated graph of ~230 kernel nodes): traffic
+    // with many distinct lengths evicts the least recently used one.
+    static constexpr size_t kMaxPlans = 64;
     float* out_h = nullptr;
     int out_h_cap = 0;
     std::vector<void*> device_allocs, host_allocs;

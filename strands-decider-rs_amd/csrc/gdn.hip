@@ -51,11 +51,27 @@ __device__ __forceinline__ void split8(const float* v, f16x8& hi, f16x8& lo) {
 // loads in flight (__syncthreads waits for those too, which undoes a prefetch).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// e^x on the hardware exp2 (v_exp_f32, about 1 ulp in f32); x <= 0 here, so the result is in (0, 1].
+__device__ __forceinline__ float fexp(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+#else
+    return expf(x);
+#endif
+}
+
 __device__ __forceinline__ f32x4 mma3(const f16x8& ah, const f16x8& al, const f16x8& bh, const f16x8& bl, f32x4 acc) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
     return acc;
+}
+
+// The same three products into three separate accumulators acc[0..2] (independent MFMA chains).
+__device__ __forceinline__ void mma3s(const f16x8& ah, const f16x8& al, const f16x8& bh, const f16x8& bl, f32x4* acc) {
+    acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc[2], 0, 0, 0);
 }
 
 // A-operand fragment store: matrix with KS k-steps of 32, layout [row tile][k step][hi|lo][lane][8].
@@ -234,7 +250,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
     // qn e^G as A fragments: (row tile ri/16, k step rp, lanes (ri%16) + 16g)
     {
         const float e = eG[ri];
@@ -278,7 +294,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
                 aqk[t] = mma3(qah, qal, kbh, kbl, aqk[t]);
             }
         }
-        __syncthreads();  // Q rows are consumed: R2 becomes the Qk staging area
+        lds_barrier();  // Q rows are consumed: R2 becomes the Qk staging area
         float* Qs = reinterpret_cast<float*>(R2);
         constexpr float UNS = 1.0f / (QK_SCALE * QK_SCALE);
 #pragma unroll
@@ -286,11 +302,11 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int i = wv * 16 + fg * 4 + r, j = t * 16 + fr;
-                const float dec = i >= j ? expf(G[i] - G[j]) : 0.f;
+                const float dec = i >= j ? fexp(G[i] - G[j]) : 0.f;
                 Ts[i * FP + j] = i > j ? -beta[i] * (akk[t][r] * UNS) * dec : (i == j ? 1.f : 0.f);
                 Qs[i * FP + j] = i >= j ? aqk[t][r] * UNS * dec : 0.f;
             }
-        __syncthreads();
+        lds_barrier();
         // Qk as A fragments: 4 row tiles x 2 k steps x 64 lanes, 2 per thread
 #pragma unroll
         for (int q = 0; q < 2; q++) {
@@ -302,7 +318,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
             for (int u = 0; u < 8; u++) v8[u] = src[u];
             put_frag(Qkf, 2, rt, st, ln, v8);
         }
-        __syncthreads();  // R2 becomes V^T (hi, lo)
+        lds_barrier();  // R2 becomes V^T (hi, lo)
         f16* VTh = reinterpret_cast<f16*>(R2);
         f16* VTl = VTh + DK * TP;
         const float* row = qkvc + (size_t)(t0 + ri) * C + 2 * sh.H * DK + h * DV + rp * 32;
@@ -348,7 +364,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
 #pragma unroll
             for (int i = 0; i < 16; i++) Ts[(base + i) * FP + base + lane] = x[i];
         }
-        __syncthreads();
+        lds_barrier();
     }
     // Off-diagonal blocks: column block q by wave q, block rows p = q+1..3 in order (no workgroup
     // barrier: a wave reads only the final diagonal blocks, the copied A blocks and its own column):
@@ -378,7 +394,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
             for (int rr = 0; rr < 4; rr++) Ts[(16 * p + 4 * lg + rr) * FP + 16 * q + lr] = y[rr];
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // X is read before the next p writes it
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // ---- phase 3: W = T diag(beta e^G) Kn and U = T diag(beta) V; wave w: row tile w x 8 column tiles
@@ -421,7 +437,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
                 Uo[i * DV + d] = au[t][r];
                 Ws[i * WP + d] = aw[t][r] * (1.0f / QK_SCALE);
             }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int slotf = tid + 256 * q;  // 4 row tiles x 4 k steps x 64 lanes
@@ -708,7 +724,10 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
         const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - c * CH);
         lds_barrier();  // St holds this chunk's starting state; Vt is free
-        f32x4 av = {0.f, 0.f, 0.f, 0.f}, ao = av;
+        // the three terms of each split product accumulate separately (six independent MFMA
+        // chains of 4 instead of two of 12) and are added at the end
+        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+        f32x4 av[3] = {z4, z4, z4}, ao[3] = {z4, z4, z4};
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             float s8[8];
@@ -717,11 +736,11 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
             for (int u = 0; u < 8; u++) s8[u] = sp[u];
             f16x8 sh8, sl8;
             split8(s8, sh8, sl8);
-            av = mma3(cur.wh[s], cur.wl[s], sh8, sl8, av);
-            ao = mma3(cur.qh[s], cur.ql[s], sh8, sl8, ao);
+            mma3s(cur.wh[s], cur.wl[s], sh8, sl8, av);
+            mma3s(cur.qh[s], cur.ql[s], sh8, sl8, ao);
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) Vt[fr * VP + wv * 16 + fg * 4 + r] = cur.ur[r] - av[r];
+        for (int r = 0; r < 4; r++) Vt[fr * VP + wv * 16 + fg * 4 + r] = cur.ur[r] - (av[0][r] + av[1][r] + av[2][r]);
         lds_barrier();
         // V'^T fragments (B operand), used by Qk V' and by the state update
         f16x8 vh[2], vl[2];
@@ -734,19 +753,19 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
             split8(v8, vh[s], vl[s]);
         }
 #pragma unroll
-        for (int s = 0; s < 2; s++) ao = mma3(qkh[s], qkl[s], vh[s], vl[s], ao);
+        for (int s = 0; s < 2; s++) mma3s(qkh[s], qkl[s], vh[s], vl[s], ao);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int i = wv * 16 + fg * 4 + r;
-            if (i < Lc) o[(size_t)(t0 + i) * sh.H * DV + h * DV + c0 + fr] = ao[r];
+            if (i < Lc) o[(size_t)(t0 + i) * sh.H * DV + h * DV + c0 + fr] = ao[0][r] + ao[1][r] + ao[2][r];
         }
         // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
-        f32x4 as[2];
+        f32x4 as[2][3];
 #pragma unroll
         for (int q2 = 0; q2 < 2; q2++) {
-            as[q2] = f32x4{0.f, 0.f, 0.f, 0.f};
+            as[q2][0] = as[q2][1] = as[q2][2] = z4;
 #pragma unroll
-            for (int s = 0; s < 2; s++) as[q2] = mma3(kh[q2][s], kl[q2][s], vh[s], vl[s], as[q2]);
+            for (int s = 0; s < 2; s++) mma3s(kh[q2][s], kl[q2][s], vh[s], vl[s], as[q2]);
         }
         const float g_c = gl;
         if (c + 1 < cend) load_qk(c + 1);  // Qk, Kg, gl are consumed
@@ -755,7 +774,7 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int k = (wv * 2 + q2) * 16 + fg * 4 + r;
-                St[fr * SP + k] = g_c * St[fr * SP + k] + as[q2][r];
+                St[fr * SP + k] = g_c * St[fr * SP + k] + (as[q2][0][r] + as[q2][1][r] + as[q2][2][r]);
             }
     };
     if (cfirst < cend) {

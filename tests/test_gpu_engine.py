@@ -254,3 +254,23 @@ def test_interleaved_snapshots_read_in_place(tiny, sdamd):
     assert np.abs(again - want).max() < HIDDEN_TOL
     for s in (a, b, c):
         s.free()
+
+
+def test_rotary_dim_checked_at_load(sdamd, synth, tmp_path):
+    """qk_prep pairs rotate-half partners with a lane shuffle over groups of 8: a rotary_dim it
+    cannot rotate fails at load instead of giving wrong Q/K."""
+    cfg = dict(synth.CONFIG_TINY, rotary_dim=12)
+    d = synth.write_model(str(tmp_path / "rd12"), cfg, vocab=512, seed=5)
+    with pytest.raises(sdamd.EngineError, match="rotary_dim must be a multiple of 8"):
+        sdamd.Engine.load(d)
+
+
+def test_plan_cache_evicts_and_recaptures(tiny):
+    """More distinct lengths than the plan cache holds: the least recently used plans are evicted,
+    and a length whose plan was evicted is captured again with the same result, bit for bit."""
+    eng, head, om = tiny
+    first = eng.forward(ids_for(11, 23), [0, 22]).hidden
+    for L in range(30, 30 + 70):
+        eng.forward(ids_for(L, L), [L - 1])
+    again = eng.forward(ids_for(11, 23), [0, 22]).hidden
+    assert np.array_equal(first, again)
