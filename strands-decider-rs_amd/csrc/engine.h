@@ -155,9 +155,11 @@ struct Engine {
     Pool pool;
     std::map<int, Plan> plans;
     uint64_t plan_clock = 0;
-    // Captured plans kept at most (each holds an instantiated graph of ~230 kernel nodes): traffic
-    // with many distinct lengths evicts the least recently used one.
-    static constexpr size_t kMaxPlans = 64;
+    // Captured plans kept at most: each holds an instantiated graph of ~230 kernel nodes (the pool's
+    // buffers are shared, so a plan costs no activation memory of its own).  Traffic with more
+    // distinct (length, sequences) keys evicts the least recently used one; the configs[4] sweep
+    // (64 state lengths and 64 question batches) stays cached.
+    static constexpr size_t kMaxPlans = 512;
     float* out_h = nullptr;
     int out_h_cap = 0;
     std::vector<void*> device_allocs, host_allocs;

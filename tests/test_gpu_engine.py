@@ -270,7 +270,11 @@ def test_plan_cache_evicts_and_recaptures(tiny):
     and a length whose plan was evicted is captured again with the same result, bit for bit."""
     eng, head, om = tiny
     first = eng.forward(ids_for(11, 23), [0, 22]).hidden
-    for L in range(30, 30 + 70):
+    # longest first, so the pool grows once (which drops every plan) and then only evictions follow
+    for L in range(640, 640 - 530, -1):
         eng.forward(ids_for(L, L), [L - 1])
     again = eng.forward(ids_for(11, 23), [0, 22]).hidden
     assert np.array_equal(first, again)
+    # the cache holds at most 512 plans: the lengths used first were evicted and are captured again
+    h = eng.forward(ids_for(640, 640), [639]).hidden
+    assert np.isfinite(h).all()
