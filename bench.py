@@ -604,20 +604,30 @@ def sweep_bench(eng, head, temp, n_states=64, n_q=8, seed=4):
                     "2-5 options each"}
 
 
-def cpu_baseline(model_dir, vocab, n_tokens=STATE_LEN):
-    """The C oracle (a CPU port of the reference kernels) on the host cores: one prefill of
-    n_tokens random ids (the 512-token state of the workload; about 15-20 s on 16 cores)."""
+def cpu_baseline(model_dir, vocab, temp, n_tokens=STATE_LEN):
+    """The C oracle (a CPU port of the reference kernels) on the host cores, one step of the same
+    workload: the prefill of n_tokens random ids with a snapshot (`value` is its tokens/s, the bench
+    line's metric), then the 3 x 40-token questions, each from the snapshot, and the f64 pointer head
+    (about 12 s on 16 cores)."""
     import numpy as np
     from oracle import torso
     om = torso.OracleModel(model_dir)
-    ids = np.random.default_rng(7).integers(0, vocab, n_tokens)
+    rng = np.random.default_rng(7)
+    ids = rng.integers(0, vocab, n_tokens)
+    questions = [rng.integers(0, vocab, Q_LEN) for _ in range(N_QUESTIONS)]
     t = time.perf_counter()
-    om.forward(ids, [n_tokens - 1])
+    _, snap = om.forward(ids, [n_tokens - 1], keep=True)
     dt = time.perf_counter() - t
+    for q, o in zip(questions, OPTIONS):
+        hid, _ = om.forward(q, list(o) + [len(q) - 1], cache=snap)
+        om.probs(hid, temp)
+    dq = time.perf_counter() - t - dt
     return {"value": round(n_tokens / dt, 3), "unit": "tokens/s", "cores": torso.lib().or_num_threads(),
-            "kind": "port",
-            "sample": f"prefill of {n_tokens} random tokens on the same 2B model ({dt:.1f} s of CPU time; "
-                      f"the reference's wgpu/lavapipe path cannot be built here: no cargo, no Vulkan ICD)"}
+            "kind": "port", "ask_all_ms": round(1e3 * (dt + dq), 1), "questions_ms": round(1e3 * dq, 1),
+            "sample": f"one ask_all step on the same 2B model: the prefill of {n_tokens} random tokens "
+                      f"({dt:.1f} s) and {N_QUESTIONS} x {Q_LEN}-token questions from its snapshot with the head "
+                      f"({dq:.1f} s); the reference's wgpu/lavapipe path cannot be built here: no cargo, no "
+                      f"Vulkan ICD"}
 
 
 def main():
@@ -757,7 +767,7 @@ def main():
         res["roofline"] = gemm_roofline(eng, state, synth.CONFIG_2B)
     if not args.no_cpu_baseline:
         eng.free()
-        res["cpu_baseline"] = cpu_baseline(model_dir, synth.VOCAB_2B)
+        res["cpu_baseline"] = cpu_baseline(model_dir, synth.VOCAB_2B, temp)
     print(json.dumps(res), flush=True)
 
 

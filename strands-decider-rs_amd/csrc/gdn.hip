@@ -514,7 +514,11 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int h = blockIdx.x, H = gridDim.x, q = blockIdx.z;
     if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
-    const int cb = blockIdx.y * 16, cl = wv * 4 + (lane >> 4), col = cb + cl, r0 = 8 * (lane & 15);
+    // lane l of a 16-lane row owns state rows 4l .. 4l + 3 and 64 + 4l .. 64 + 4l + 3: its q and k
+    // values are then float4 l and 16 + l of a token's row, so the 16 lanes of each read cover 256
+    // contiguous bytes (every LDS bank once)
+    const int cb = blockIdx.y * 16, cl = wv * 4 + (lane >> 4), col = cb + cl, l4 = lane & 15;
+    auto srow = [&](int i) { return (i < 4 ? 0 : 60) + 4 * l4 + i; };
     int t0 = 0, t1 = L;
     if (seqt) {
         const int f = (int)(seqt[q] & 0xFFFFu), n = (int)(seqt[q] >> 16);
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     const float* S0 = (pre ? reinterpret_cast<const float*>(pre + state_off) : state) + (size_t)h * DK * DV;
     float S[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) S[i] = load ? S0[(size_t)(r0 + i) * DV + col] : 0.f;
+    for (int i = 0; i < 8; i++) S[i] = load ? S0[(size_t)srow(i) * DV + col] : 0.f;
     const int C = sh.C;
     const float na = negA[h], db = dtb[h], qs = 1.0f / sqrtf((float)DK);
     for (int tb = t0; tb < t1; tb += RTB) {
@@ -610,7 +614,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
             float dc, bt, v, kq;
         };
         auto tok = [&](int tt) {
-            return Tok{Qs[tt][r0 / 4], Qs[tt][r0 / 4 + 1], Ks[tt][r0 / 4], Ks[tt][r0 / 4 + 1],
+            return Tok{Qs[tt][l4], Qs[tt][16 + l4], Ks[tt][l4], Ks[tt][16 + l4],
                        Dc[tt],         Bt[tt],             Vs[tt][cl],     KQ[tt]};
         };
         auto run = [&](const Tok& x, int tt) {
@@ -644,7 +648,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     }
     if (seqt) return;  // several sequences: their final states are not kept
 #pragma unroll
-    for (int i = 0; i < 8; i++) Sg[(size_t)(r0 + i) * DV + col] = S[i];
+    for (int i = 0; i < 8; i++) Sg[(size_t)srow(i) * DV + col] = S[i];
     // the reference's hist_update (src/kernels.rs:173-190), each workgroup on a slice of the channels:
     // the last 3 rows of (the prefix's history ++ this forward's rows) into the live history
     if (hist) {
@@ -739,8 +743,10 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
             mma3s(cur.wh[s], cur.wl[s], sh8, sl8, av);
             mma3s(cur.qh[s], cur.ql[s], sh8, sl8, ao);
         }
-#pragma unroll
-        for (int r = 0; r < 4; r++) Vt[fr * VP + wv * 16 + fg * 4 + r] = cur.ur[r] - (av[0][r] + av[1][r] + av[2][r]);
+        // rows wv * 16 + fg * 4 .. + 3 of column fr: one 16-byte store (conflict-free at this pitch)
+        *reinterpret_cast<float4*>(&Vt[fr * VP + wv * 16 + fg * 4]) =
+            float4{cur.ur[0] - (av[0][0] + av[1][0] + av[2][0]), cur.ur[1] - (av[0][1] + av[1][1] + av[2][1]),
+                   cur.ur[2] - (av[0][2] + av[1][2] + av[2][2]), cur.ur[3] - (av[0][3] + av[1][3] + av[2][3])};
         lds_barrier();
         // V'^T fragments (B operand), used by Qk V' and by the state update
         f16x8 vh[2], vl[2];
@@ -770,12 +776,15 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         const float g_c = gl;
         if (c + 1 < cend) load_qk(c + 1);  // Qk, Kg, gl are consumed
 #pragma unroll
-        for (int q2 = 0; q2 < 2; q2++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int k = (wv * 2 + q2) * 16 + fg * 4 + r;
-                St[fr * SP + k] = g_c * St[fr * SP + k] + (as[q2][0][r] + as[q2][1][r] + as[q2][2][r]);
-            }
+        for (int q2 = 0; q2 < 2; q2++) {
+            // state rows k0 .. k0 + 3 of column fr: one 16-byte read-modify-write
+            float4* sp4 = reinterpret_cast<float4*>(&St[fr * SP + (wv * 2 + q2) * 16 + fg * 4]);
+            const float4 s4 = *sp4;
+            *sp4 = float4{g_c * s4.x + (as[q2][0][0] + as[q2][1][0] + as[q2][2][0]),
+                          g_c * s4.y + (as[q2][0][1] + as[q2][1][1] + as[q2][2][1]),
+                          g_c * s4.z + (as[q2][0][2] + as[q2][1][2] + as[q2][2][2]),
+                          g_c * s4.w + (as[q2][0][3] + as[q2][1][3] + as[q2][2][3])};
+        }
     };
     if (cfirst < cend) {
         load_wq(set0, cfirst);
