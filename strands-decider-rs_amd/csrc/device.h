@@ -56,6 +56,13 @@ __device__ __forceinline__ u32x3 buf_b96(Rsrc r, uint32_t voff, uint32_t soff) {
 __device__ __forceinline__ u32x2 buf_b64(Rsrc r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
 }
+__device__ __forceinline__ uint32_t buf_b32(Rsrc r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+// A 32-bit store; an offset at or past the resource's size writes nothing.
+__device__ __forceinline__ void buf_st32(Rsrc r, uint32_t voff, uint32_t soff, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, soff, 0);
+}
 #else
 struct Rsrc {};
 __device__ inline Rsrc make_rsrc(const void*, uint32_t) { return {}; }
@@ -64,6 +71,8 @@ __device__ inline u32x4 buf_b128(Rsrc, uint32_t, uint32_t) { return u32x4{}; }
 __device__ inline uint32_t buf_b16(Rsrc, uint32_t, uint32_t) { return 0; }
 __device__ inline u32x3 buf_b96(Rsrc, uint32_t, uint32_t) { return u32x3{}; }
 __device__ inline u32x2 buf_b64(Rsrc, uint32_t, uint32_t) { return u32x2{}; }
+__device__ inline uint32_t buf_b32(Rsrc, uint32_t, uint32_t) { return 0; }
+__device__ inline void buf_st32(Rsrc, uint32_t, uint32_t, uint32_t) {}
 #endif
 
 // A per-lane buffer offset that is out of range for every buffer here: the load returns zeros and

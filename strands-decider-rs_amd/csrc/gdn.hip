@@ -24,6 +24,7 @@
 //  * gdn_scan: one workgroup per (head, 16 value columns), sequential over chunks; the state slice
 //    lives in LDS (transposed, the B operand of every product).
 #include "common.h"
+#include "device.h"
 
 namespace sd {
 namespace {
@@ -61,9 +62,6 @@ __device__ __forceinline__ void split8(const float* v, f16x8& hi, f16x8& lo) {
     }
 }
 
-// Workgroup barrier for LDS data only: waits for this wave's LDS operations but not for its global
-// loads in flight (__syncthreads waits for those too, which undoes a prefetch).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // e^x on the hardware exp2 (v_exp_f32, about 1 ulp in f32); x <= 0 here, so the result is in (0, 1].
 __device__ __forceinline__ float fexp(float x) {
@@ -97,11 +95,6 @@ __device__ __forceinline__ void put_frag(f16* base, int KS, int rt, int s, int l
     *reinterpret_cast<f16x8*>(p + 64 * 8) = lo;
 }
 
-__device__ __forceinline__ void get_frag(const f16* base, int KS, int rt, int s, int lane, f16x8& hi, f16x8& lo) {
-    const f16* p = base + ((size_t)((rt * KS + s) * 2) * 64 + lane) * 8;
-    hi = *reinterpret_cast<const f16x8*>(p);
-    lo = *reinterpret_cast<const f16x8*>(p + 64 * 8);
-}
 
 // The prefix snapshot's arena image whose GDN states and conv histories a forward continues from,
 // read from the per-forward lu block (the device address at its byte 32; null when there is no lu
@@ -692,7 +685,7 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
     constexpr int SP = DK + 4, VP = CH + 4;
     __shared__ __attribute__((aligned(16))) float St[DVS * SP];  // S^T: [column][k]
     __shared__ __attribute__((aligned(16))) float Vt[DVS * VP];  // V'^T: [column][token]
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fr = lane & 15, fg = lane >> 4;
     const int h = blockIdx.x, sl = blockIdx.y, H = gridDim.x, q = blockIdx.z;
     if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
@@ -717,26 +710,48 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
     WQ set0, set1;
     f16x8 kh[2][2], kl[2][2], qkh[2], qkl[2];
     float gl = 0.f;
+    // The workspace is one allocation (W | Qg | Qk | Kg | U | e^G_last regions): every operand load
+    // is a buffer load of it with this lane's fixed offset in a VGPR and the region, slot and
+    // fragment offsets in SGPRs, so no per-load address arithmetic runs on the VALU.
+    const uint8_t* wsb = reinterpret_cast<const uint8_t*>(ws.wf);
+    const Rsrc rws = make_rsrc(wsb, 0x7FFFFFF0u);  // every offset below lies inside the workspace
+    const uint32_t o_qg = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.qgf) - wsb),
+                   o_qk = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.qkf) - wsb),
+                   o_kg = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.kgf) - wsb),
+                   o_u = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.u) - wsb);
+    const uint32_t vfrag = (uint32_t)lane * 16u;                              // fragment layout
+    const uint32_t vu = (uint32_t)((fg * 4 * DV + fr) * 4);                   // U rows fg*4 + r, column fr
+    auto frag = [&](uint32_t region, int KS, int rt, int s, f16x8& hi, f16x8& lo) {
+        const uint32_t so = region + (uint32_t)((rt * KS + s) * 2) * 1024u;
+        hi = __builtin_bit_cast(f16x8, buf_b128(rws, vfrag, so));
+        lo = __builtin_bit_cast(f16x8, buf_b128(rws, vfrag, so + 1024u));
+    };
     auto load_wq = [&](WQ& d, int c) {
-        const size_t slot = (size_t)c * H + h;
+        const uint32_t slot = (uint32_t)(c * H + h);
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            get_frag(ws.wf + slot * WF_H, 4, wv, s, lane, d.wh[s], d.wl[s]);
-            get_frag(ws.qgf + slot * QGF_H, 4, wv, s, lane, d.qh[s], d.ql[s]);
+            frag(slot * (uint32_t)(WF_H * 2), 4, wv, s, d.wh[s], d.wl[s]);
+            frag(o_qg + slot * (uint32_t)(QGF_H * 2), 4, wv, s, d.qh[s], d.ql[s]);
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) d.ur[r] = ws.u[slot * U_F + (wv * 16 + fg * 4 + r) * DV + c0 + fr];
+        for (int r = 0; r < 4; r++)
+            d.ur[r] = __builtin_bit_cast(
+                float, buf_b32(rws, vu, o_u + slot * (uint32_t)(U_F * 4) + (uint32_t)(((wv * 16 + r) * DV + c0) * 4)));
     };
     auto load_qk = [&](int c) {
-        const size_t slot = (size_t)c * H + h;
+        const uint32_t slot = (uint32_t)(c * H + h);
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            get_frag(ws.qkf + slot * QKF_H, 2, wv, s, lane, qkh[s], qkl[s]);
+            frag(o_qk + slot * (uint32_t)(QKF_H * 2), 2, wv, s, qkh[s], qkl[s]);
 #pragma unroll
-            for (int q2 = 0; q2 < 2; q2++) get_frag(ws.kgf + slot * KGF_H, 2, wv * 2 + q2, s, lane, kh[q2][s], kl[q2][s]);
+            for (int q2 = 0; q2 < 2; q2++) frag(o_kg + slot * (uint32_t)(KGF_H * 2), 2, wv * 2 + q2, s, kh[q2][s], kl[q2][s]);
         }
         gl = ws.gl[slot];
     };
+    // o rows t0 + wv*16 + fg*4 + r (r < 4), column h*DV + c0 + fr; rows past the chunk get an
+    // out-of-range offset and are not written
+    const Rsrc ro = make_rsrc(o, (uint32_t)L * sh.H * DV * 4);
+    const uint32_t vo = (uint32_t)((fg * 4 * sh.H * DV + fr) * 4);
     auto chunk = [&](int c, const WQ& cur, WQ& nxt) {
         if (c + 1 < cend) load_wq(nxt, c + 1);
         const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
@@ -774,10 +789,14 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         }
 #pragma unroll
         for (int s = 0; s < 2; s++) mma3s(qkh[s], qkl[s], vh[s], vl[s], ao);
+        {
+            const uint32_t so = (uint32_t)(((t0 + wv * 16) * sh.H * DV + h * DV + c0) * 4);
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int i = wv * 16 + fg * 4 + r;
-            if (i < Lc) o[(size_t)(t0 + i) * sh.H * DV + h * DV + c0 + fr] = ao[0][r] + ao[1][r] + ao[2][r];
+            for (int r = 0; r < 4; r++) {
+                const bool in = wv * 16 + fg * 4 + r < Lc;
+                buf_st32(ro, in ? vo + (uint32_t)(r * sh.H * DV * 4) : OOB, so,
+                         __builtin_bit_cast(uint32_t, ao[0][r] + ao[1][r] + ao[2][r]));
+            }
         }
         // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
         f32x4 as[2][3];
