@@ -33,9 +33,10 @@ constexpr int CH = 64;   // chunk length
 constexpr int DVS = 16;  // value columns per scan workgroup (one MFMA column tile)
 constexpr float QK_SCALE = 256.0f;
 
-__device__ __forceinline__ float warp_sum4(float v) {  // sum over aligned groups of 4 lanes
+__device__ __forceinline__ float warp_sum8(float v) {  // sum over aligned groups of 8 lanes
     v += __shfl_xor(v, 1);
     v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
     return v;
 }
 
@@ -151,31 +152,40 @@ constexpr size_t QKF_H = 4 * 2 * 2 * 64 * 8;  // Qk: 4 row tiles x 2 k steps
 constexpr size_t KGF_H = 8 * 2 * 2 * 64 * 8;  // KgT: 8 row tiles x 2 k steps
 constexpr size_t U_F = 64 * 128;              // U, fp32 row-major
 
-__global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc, const f16* __restrict__ big,
+constexpr int PREP_T = 512;  // k_gdn_prep threads: 8 waves
+
+// One workgroup per (chunk, head).  Two thread views of the chunk's rows:
+//  - row view, thread (i, p) = (tid / 8, tid % 8): columns 16p..16p+15 of q and k in row i, for the
+//    norms, the Q/K rows in LDS (the K Kn^T and Qn Kn^T operands) and the qn e^G fragments;
+//  - column view, wave w, lane (n, g) = (lane % 16, lane / 16): column 16w + n of k and v at tokens
+//    32s + 8g + u (s < 2, u < 8), loaded straight from global memory in that order, which is both an
+//    MFMA B fragment over tokens (W = T diag(beta e^G) Kn and U = T diag(beta) V, column tile w) and
+//    the scan's (Kn e^(G_last - G))^T A fragment (row tile w): no transpose passes through LDS.
+__global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ qkvc, const f16* __restrict__ big,
                                                   GdnShape sh, const float* __restrict__ negA,
                                                   const float* __restrict__ dtb, int L, GdnWs ws, f16* hist,
                                                   const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu,
                                                   size_t hist_off) {
     constexpr int DK = 128, DV = 128;
-    constexpr int RP = DK + 8;  // f16 row pitch of row-major tiles
-    constexpr int TP = CH + 8;  // f16 row pitch of transposed tiles
-    constexpr int FP = CH + 4;  // fp32 pitch of T
+    constexpr int RP = DK + 8;  // f16 row pitch of the Q/K row tiles
+    constexpr int FP = CH + 4;  // fp32 pitch of T and of the Qk staging
+    constexpr int WP = DK + 4;  // fp32 pitch of the W staging
     // LDS regions: R1 = K rows (hi, lo), later W staging (fp32); R2 = Q rows (hi, lo), later Qk
-    // staging (fp32), then V^T (hi, lo); R3 = K^T (hi, lo); T; scratch.
-    __shared__ __attribute__((aligned(16))) uint8_t R1[2 * CH * RP * 2 > CH * (DK + 4) * 4 ? 2 * CH * RP * 2 : CH * (DK + 4) * 4];
-    __shared__ __attribute__((aligned(16))) uint8_t R2[2 * DK * TP * 2];
-    __shared__ __attribute__((aligned(16))) f16 KT[2][DK * TP];
+    // staging (fp32); T; the blocks of the inversion; per-token vectors.
+    constexpr size_t R1B = 2 * CH * RP * 2 > CH * WP * 4 ? 2 * CH * RP * 2 : CH * WP * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t R1[R1B];
+    __shared__ __attribute__((aligned(16))) uint8_t R2[2 * CH * RP * 2];
     __shared__ __attribute__((aligned(16))) float Ts[CH * FP];
     __shared__ float Xs[4][16][17];
     __shared__ float Nb[6][16][17];  // the off-diagonal 16 x 16 blocks of A, (p, r) at p (p - 1) / 2 + r
-    __shared__ float beta[CH], G[CH], eG[CH], eL[CH];
+    __shared__ __attribute__((aligned(16))) float beta[CH], G[CH], eG[CH], eL[CH], rkv[CH];
     f16* Kh = reinterpret_cast<f16*>(R1);
     f16* Kl = Kh + CH * RP;
     f16* Qh = reinterpret_cast<f16*>(R2);
     f16* Ql = Qh + CH * RP;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int fr = lane & 15, fg = lane >> 4;  // fragment row / k group of this lane
+    const int fr = lane & 15, fg = lane >> 4;  // fragment row (column) / k group of this lane
     const int c = blockIdx.x, h = blockIdx.y, H = gridDim.y;
     if (chunkt && c >= (int)lu[4]) return;  // the grid is sized for the most chunks L can split into
     const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
@@ -188,13 +198,67 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     f16* Kgf = ws.kgf + slot * KGF_H;
     float* Uo = ws.u + slot * U_F;
 
-    // ---- phase 0: gates (wave 0), normalised q/k rows: thread (i, p) owns columns 32p..32p+31
+    // Every global load of the kernel is issued here, before its first store: vector memory
+    // operations retire in issue order, so a load issued after a store would wait for its ack.  The
+    // loads are unconditional (rows past the chunk read its last row; their scales and v are zeroed),
+    // so no branch makes the wave wait for one load before it issues the next.
+    const int ri = tid >> 3, rp = tid & 7;
+    f16 ga16, gb16;  // the gate inputs of row tid % 64 (used by wave 0)
+    {
+        const size_t gr = (size_t)(t0 + min(tid & (CH - 1), Lc - 1)) * sh.stride + h;
+        ga16 = big[gr + sh.a_off];
+        gb16 = big[gr + sh.b_off];
+    }
+    float qv[16], kv[16];
+    {
+        const float* row = qkvc + (size_t)(t0 + min(ri, Lc - 1)) * C;
+        float4 q4[4], k4[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            q4[e] = *reinterpret_cast<const float4*>(row + h * DK + rp * 16 + 4 * e);
+            k4[e] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + rp * 16 + 4 * e);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            qv[4 * e] = q4[e].x, qv[4 * e + 1] = q4[e].y, qv[4 * e + 2] = q4[e].z, qv[4 * e + 3] = q4[e].w;
+            kv[4 * e] = k4[e].x, kv[4 * e + 1] = k4[e].y, kv[4 * e + 2] = k4[e].z, kv[4 * e + 3] = k4[e].w;
+        }
+    }
+    float kT[2][8], vT[2][8];  // column view
+    {
+        const float* ck = qkvc + sh.H * DK + h * DK + wv * 16 + fr;
+        const float* cv = qkvc + 2 * sh.H * DK + h * DV + wv * 16 + fr;
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const size_t jr = (size_t)(t0 + min(s * 32 + fg * 8 + u, Lc - 1)) * C;
+                kT[s][u] = ck[jr];
+                vT[s][u] = cv[jr];
+            }
+    }
+    // the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's history
+    // ++ this forward's rows) become the live history; each workgroup of the grid takes a slice of
+    // the channels, this thread channel lo + tid (stored at the end, a longer slice in a loop there)
+    const int hnb = gridDim.x * H, hper = (C + hnb - 1) / hnb;
+    const int hlo = (c * H + h) * hper, hhi = min(C, hlo + hper);
+    const f16* hold = hist ? (lu_prefix(lu) ? reinterpret_cast<const f16*>(lu_prefix(lu) + hist_off) : hist) : nullptr;
+    f16 hv[3] = {};
+    if (hist) {  // channel hlo + tid clamped into the slice (stored only when inside it)
+        const int ch = min(hlo + tid, hhi - 1);
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            const int src = L - 3 + r;
+            hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : hold[(size_t)(src + 3) * C + ch];
+        }
+    }
+
+    // ---- phase 0: gates (wave 0), normalised q/k rows
     if (tid < CH) {
         const int i = tid;
         float b = 0.f, gl = 0.f;
         if (i < Lc) {
-            const float a = (float)big[(size_t)(t0 + i) * sh.stride + sh.a_off + h];
-            const float bb = (float)big[(size_t)(t0 + i) * sh.stride + sh.b_off + h];
+            const float a = (float)ga16, bb = (float)gb16;
             b = 1.0f / (1.0f + expf(-bb));
             const float x = a + dtb[h];
             const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
@@ -212,154 +276,133 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
         eG[i] = expf(sc);
         eL[i] = expf(glast - sc);
     }
-    const int ri = tid >> 2, rp = tid & 3;
-    float qv[32], kv[32];
+    float rq;  // row view: 1 / |q_i| / sqrt(dk) (0 past the chunk)
     {
         float sq = 0.f, sk = 0.f;
-        const float* row = qkvc + (size_t)(t0 + ri) * C;
 #pragma unroll
-        for (int e = 0; e < 32; e += 4) {
-            float4 q4 = {0.f, 0.f, 0.f, 0.f}, k4 = q4;
-            if (ri < Lc) {
-                q4 = *reinterpret_cast<const float4*>(row + h * DK + rp * 32 + e);
-                k4 = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + rp * 32 + e);
-            }
-            qv[e] = q4.x, qv[e + 1] = q4.y, qv[e + 2] = q4.z, qv[e + 3] = q4.w;
-            kv[e] = k4.x, kv[e + 1] = k4.y, kv[e + 2] = k4.z, kv[e + 3] = k4.w;
-            sq += q4.x * q4.x + q4.y * q4.y + q4.z * q4.z + q4.w * q4.w;
-            sk += k4.x * k4.x + k4.y * k4.y + k4.z * k4.z + k4.w * k4.w;
+        for (int e = 0; e < 16; e++) {
+            sq += qv[e] * qv[e];
+            sk += kv[e] * kv[e];
         }
-        sq = warp_sum4(sq);
-        sk = warp_sum4(sk);
-        const float rq = ri < Lc ? (1.0f / sqrtf(sq + 1e-6f)) * (1.0f / sqrtf((float)DK)) : 0.f;
-        const float rk = ri < Lc ? 1.0f / sqrtf(sk + 1e-6f) : 0.f;
+        sq = warp_sum8(sq);
+        sk = warp_sum8(sk);
+        const bool rin = ri < Lc;
+        rq = rin ? (1.0f / sqrtf(sq + 1e-6f)) * (1.0f / sqrtf((float)DK)) : 0.f;
+        const float rk = rin ? 1.0f / sqrtf(sk + 1e-6f) : 0.f;
+        if (rp == 0) rkv[ri] = rk;
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            qv[e] *= rq;
-            kv[e] *= rk;
-        }
-#pragma unroll
-        for (int e = 0; e < 32; e += 8) {
+        for (int e = 0; e < 16; e += 8) {
             float q8[8], k8[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) q8[u] = qv[e + u] * QK_SCALE, k8[u] = kv[e + u] * QK_SCALE;
+            for (int u = 0; u < 8; u++) q8[u] = qv[e + u] * rq * QK_SCALE, k8[u] = kv[e + u] * rk * QK_SCALE;
             f16x8 hi, lo;
             split8(q8, hi, lo);
-            *reinterpret_cast<f16x8*>(&Qh[ri * RP + rp * 32 + e]) = hi;
-            *reinterpret_cast<f16x8*>(&Ql[ri * RP + rp * 32 + e]) = lo;
+            *reinterpret_cast<f16x8*>(&Qh[ri * RP + rp * 16 + e]) = hi;
+            *reinterpret_cast<f16x8*>(&Ql[ri * RP + rp * 16 + e]) = lo;
             split8(k8, hi, lo);
-            *reinterpret_cast<f16x8*>(&Kh[ri * RP + rp * 32 + e]) = hi;
-            *reinterpret_cast<f16x8*>(&Kl[ri * RP + rp * 32 + e]) = lo;
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                KT[0][(rp * 32 + e + u) * TP + ri] = hi[u];
-                KT[1][(rp * 32 + e + u) * TP + ri] = lo[u];
-            }
+            *reinterpret_cast<f16x8*>(&Kh[ri * RP + rp * 16 + e]) = hi;
+            *reinterpret_cast<f16x8*>(&Kl[ri * RP + rp * 16 + e]) = lo;
         }
     }
     lds_barrier();
-    // qn e^G as A fragments: (row tile ri/16, k step rp, lanes (ri%16) + 16g)
+    // qn e^G as A fragments: (row tile ri/16, k step rp/2, lanes (ri%16) + 16g, g = 2 (rp%2) + gg)
     {
-        const float e = eG[ri];
+        const float e = eG[ri] * rq;
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
+        for (int gg = 0; gg < 2; gg++) {
             float v8[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) v8[u] = qv[g * 8 + u] * e;
-            put_frag(Qgf, 4, ri >> 4, rp, (ri & 15) + 16 * g, v8);
+            for (int u = 0; u < 8; u++) v8[u] = qv[gg * 8 + u] * e;
+            put_frag(Qgf, 4, ri >> 4, rp >> 1, (ri & 15) + 16 * (2 * (rp & 1) + gg), v8);
         }
     }
-    // (Kn e^(G_last - G))^T as A fragments: rows d (8 tiles), k = token (2 steps); 4 per thread
+    // column view: (Kn e^(G_last - G))^T fragments (row tile w), and the B fragments of phase 3
+    f16x8 kbh[2], kbl[2], vbh[2], vbl[2];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int slotf = tid + 256 * q;  // (tile, step, lane)
-        const int ln = slotf & 63, st = (slotf >> 6) & 1, kt = slotf >> 7;
-        const int d = kt * 16 + (ln & 15), i0 = st * 32 + (ln >> 4) * 8;
-        const f16x8 hi = *reinterpret_cast<const f16x8*>(&KT[0][d * TP + i0]);
-        const f16x8 lo = *reinterpret_cast<const f16x8*>(&KT[1][d * TP + i0]);
-        float v8[8];
+    for (int s = 0; s < 2; s++) {
+        const int j0 = s * 32 + fg * 8;
+        const float4 r0 = *reinterpret_cast<const float4*>(&rkv[j0]), r1 = *reinterpret_cast<const float4*>(&rkv[j0 + 4]);
+        const float4 l0 = *reinterpret_cast<const float4*>(&eL[j0]), l1 = *reinterpret_cast<const float4*>(&eL[j0 + 4]);
+        const float rk8[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+        const float el8[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+        float g8[8], k8[8], v8[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v8[u] = ((float)hi[u] + (float)lo[u]) * (1.0f / QK_SCALE) * eL[i0 + u];
-        put_frag(Kgf, 2, kt, st, ln, v8);
+        for (int u = 0; u < 8; u++) {
+            const float kn = kT[s][u] * rk8[u];
+            g8[u] = kn * el8[u];
+            k8[u] = kn * QK_SCALE;
+            v8[u] = j0 + u < Lc ? vT[s][u] : 0.f;
+        }
+        put_frag(Kgf, 2, wv, s, lane, g8);
+        split8(k8, kbh[s], kbl[s]);
+        split8(v8, vbh[s], vbl[s]);
     }
 
-    // ---- phase 1: Kn Kn^T and Qn Kn^T; wave w computes row tile w x 4 column tiles
+    // ---- phase 1: Kn Kn^T (waves 0-3) and Qn Kn^T (waves 4-7); wave w computes row tile w % 4 x 4
+    // column tiles of its product
     {
-        f32x4 akk[4], aqk[4];
+        const int wr = wv & 3;
+        const bool second = wv >= 4;
+        f32x4 acc[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) akk[t] = aqk[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 4; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const f16* Ah = second ? Qh : Kh;
+        const f16* Al = second ? Ql : Kl;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            const int ar = (wv * 16 + fr) * RP + s * 32 + fg * 8;
-            const f16x8 kah = *reinterpret_cast<const f16x8*>(&Kh[ar]), kal = *reinterpret_cast<const f16x8*>(&Kl[ar]);
-            const f16x8 qah = *reinterpret_cast<const f16x8*>(&Qh[ar]), qal = *reinterpret_cast<const f16x8*>(&Ql[ar]);
+            const int ar = (wr * 16 + fr) * RP + s * 32 + fg * 8;
+            const f16x8 ah = *reinterpret_cast<const f16x8*>(&Ah[ar]), al = *reinterpret_cast<const f16x8*>(&Al[ar]);
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const int br = (t * 16 + fr) * RP + s * 32 + fg * 8;
-                const f16x8 kbh = *reinterpret_cast<const f16x8*>(&Kh[br]), kbl = *reinterpret_cast<const f16x8*>(&Kl[br]);
-                akk[t] = mma3(kah, kal, kbh, kbl, akk[t]);
-                aqk[t] = mma3(qah, qal, kbh, kbl, aqk[t]);
+                const f16x8 kbh2 = *reinterpret_cast<const f16x8*>(&Kh[br]), kbl2 = *reinterpret_cast<const f16x8*>(&Kl[br]);
+                acc[t] = mma3(ah, al, kbh2, kbl2, acc[t]);
             }
         }
+        // the decays and beta this lane needs, read once: rows wr*16 + fg*4 + r, columns t*16 + fr
+        float Gi[4], Bi[4], Gj[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) Gi[r] = G[wr * 16 + fg * 4 + r], Bi[r] = beta[wr * 16 + fg * 4 + r];
+#pragma unroll
+        for (int t = 0; t < 4; t++) Gj[t] = G[t * 16 + fr];
         lds_barrier();  // Q rows are consumed: R2 becomes the Qk staging area
         float* Qs = reinterpret_cast<float*>(R2);
+        float* dst = second ? Qs : Ts;
         constexpr float UNS = 1.0f / (QK_SCALE * QK_SCALE);
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int i = wv * 16 + fg * 4 + r, j = t * 16 + fr;
-                const float dec = i >= j ? fexp(G[i] - G[j]) : 0.f;
-                Ts[i * FP + j] = i > j ? -beta[i] * (akk[t][r] * UNS) * dec : (i == j ? 1.f : 0.f);
-                Qs[i * FP + j] = i >= j ? aqk[t][r] * UNS * dec : 0.f;
+                const int i = wr * 16 + fg * 4 + r, j = t * 16 + fr;
+                const float a = acc[t][r] * UNS * fexp(Gi[r] - Gj[t]);  // masked below where i < j
+                const float vq = i >= j ? a : 0.f;
+                const float vt = i > j ? -Bi[r] * a : (i == j ? 1.f : 0.f);
+                dst[i * FP + j] = second ? vq : vt;
             }
         lds_barrier();
-        // Qk as A fragments: 4 row tiles x 2 k steps x 64 lanes, 2 per thread
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int slotf = tid + 256 * q;
-            const int ln = slotf & 63, st = (slotf >> 6) & 1, rt = slotf >> 7;
+        // Qk as A fragments: 4 row tiles x 2 k steps x 64 lanes, one per thread
+        {
+            const int ln = tid & 63, st = (tid >> 6) & 1, rt = tid >> 7;
             const float* src = &Qs[(rt * 16 + (ln & 15)) * FP + st * 32 + (ln >> 4) * 8];
             float v8[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) v8[u] = src[u];
             put_frag(Qkf, 2, rt, st, ln, v8);
         }
-        lds_barrier();  // R2 becomes V^T (hi, lo)
-        f16* VTh = reinterpret_cast<f16*>(R2);
-        f16* VTl = VTh + DK * TP;
-        const float* row = qkvc + (size_t)(t0 + ri) * C + 2 * sh.H * DK + h * DV + rp * 32;
-#pragma unroll
-        for (int e = 0; e < 32; e += 8) {
-            float v8[8];
-#pragma unroll
-            for (int u = 0; u < 8; u += 4) {
-                float4 v4 = {0.f, 0.f, 0.f, 0.f};
-                if (ri < Lc) v4 = *reinterpret_cast<const float4*>(row + e + u);
-                v8[u] = v4.x, v8[u + 1] = v4.y, v8[u + 2] = v4.z, v8[u + 3] = v4.w;
-            }
-            f16x8 hi, lo;
-            split8(v8, hi, lo);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                VTh[(rp * 32 + e + u) * TP + ri] = hi[u];
-                VTl[(rp * 32 + e + u) * TP + ri] = lo[u];
-            }
-        }
     }
 
     // ---- phase 2: T = (I - A)^-1 in place (Ts holds I + A, A strictly lower), in 16 x 16 blocks.
-    // Diagonal block b (wave b): forward substitution, lane j < 16 holding column j of
+    // Diagonal block b (wave b < 4): forward substitution, lane j < 16 holding column j of
     // T_bb = (I - A_bb)^-1 in registers: T[i][j] = delta_ij + sum_{k<i} A[i][k] T[k][j].
     // The off-diagonal blocks of A are copied aside first, since T_pq overwrites A_pq.
     {
         const int base = wv * 16;
-        for (int e = tid; e < 6 * 256; e += 256) {
+        for (int e = tid; e < 6 * 256; e += PREP_T) {
             const int blk = e >> 8, a = (e >> 4) & 15, b = e & 15;
             const int p = blk == 0 ? 1 : (blk < 3 ? 2 : 3), r = blk - p * (p - 1) / 2;
             Nb[blk][a][b] = Ts[(16 * p + a) * FP + 16 * r + b];
         }
-        if (lane < 16) {
+        if (wv < 4 && lane < 16) {
             float x[16];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
@@ -373,15 +416,15 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
         }
         lds_barrier();
     }
-    // Off-diagonal blocks: column block q by wave q, block rows p = q+1..3 in order (no workgroup
+    // Off-diagonal blocks: column block q by wave q < 4, block rows p = q+1..3 in order (no workgroup
     // barrier: a wave reads only the final diagonal blocks, the copied A blocks and its own column):
     // T_pq = T_pp X, X = sum_{r=q}^{p-1} A_pr T_rq, each 16 x 16 x 16 product as 4 f32 MFMAs
     // (v_mfma_f32_16x16x4_f32: lane l holds A[l % 16][k0 + l / 16], B[k0 + l / 16][l % 16] and
     // D[4 (l / 16) + r][l % 16]).  X passes through the wave's own LDS block to become an operand.
     {
         const int q = wv, lr = lane & 15, lg = lane >> 4;
-        float(&Xw)[16][17] = Xs[wv];
-        for (int p = q + 1; p < 4; p++) {
+        float(&Xw)[16][17] = Xs[wv & 3];
+        for (int p = q + 1; p < 4; p++) {  // waves 4-7: no block rows
             f32x4 x = {0.f, 0.f, 0.f, 0.f};
             for (int r = q; r < p; r++) {
                 const int blk = p * (p - 1) / 2 + r;
@@ -404,50 +447,49 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
         lds_barrier();
     }
 
-    // ---- phase 3: W = T diag(beta e^G) Kn and U = T diag(beta) V; wave w: row tile w x 8 column tiles
+    // ---- phase 3: W = T diag(beta e^G) Kn and U = T diag(beta) V, column tile w of each (wave w),
+    // all 4 row tiles; the B fragments are this lane's column view
     {
-        const f16* VTh = reinterpret_cast<const f16*>(R2);
-        const f16* VTl = VTh + DK * TP;
-        f32x4 aw[8], au[8];
-#pragma unroll
-        for (int t = 0; t < 8; t++) aw[t] = au[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float bw[2][8], bu[2][8];  // beta e^G and beta at tokens 32s + 8g + u
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const int i = wv * 16 + fr, j0 = s * 32 + fg * 8;
-            float xw[8], xu[8];
+            const int j0 = s * 32 + fg * 8;
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const float tv = Ts[i * FP + j0 + u] * beta[j0 + u];
-                xu[u] = tv;
-                xw[u] = tv * eG[j0 + u];
-            }
-            f16x8 wh, wl, uh, ul;
-            split8(xw, wh, wl);
-            split8(xu, uh, ul);
+            for (int u = 0; u < 8; u++) bu[s][u] = beta[j0 + u], bw[s][u] = beta[j0 + u] * eG[j0 + u];
+        }
+        f32x4 aw[4], au[4];
 #pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const int br = (t * 16 + fr) * TP + s * 32 + fg * 8;
-                const f16x8 kh = *reinterpret_cast<const f16x8*>(&KT[0][br]), kl = *reinterpret_cast<const f16x8*>(&KT[1][br]);
-                const f16x8 vh = *reinterpret_cast<const f16x8*>(&VTh[br]), vl = *reinterpret_cast<const f16x8*>(&VTl[br]);
-                aw[t] = mma3(wh, wl, kh, kl, aw[t]);
-                au[t] = mma3(uh, ul, vh, vl, au[t]);
+        for (int rt = 0; rt < 4; rt++) {
+            aw[rt] = au[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const float* tp = &Ts[(rt * 16 + fr) * FP + s * 32 + fg * 8];
+                const float4 t0v = *reinterpret_cast<const float4*>(tp), t1v = *reinterpret_cast<const float4*>(tp + 4);
+                const float t8[8] = {t0v.x, t0v.y, t0v.z, t0v.w, t1v.x, t1v.y, t1v.z, t1v.w};
+                float xw[8], xu[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) xw[u] = t8[u] * bw[s][u], xu[u] = t8[u] * bu[s][u];
+                f16x8 ah, al;
+                split8(xw, ah, al);
+                aw[rt] = mma3(ah, al, kbh[s], kbl[s], aw[rt]);
+                split8(xu, ah, al);
+                au[rt] = mma3(ah, al, vbh[s], vbl[s], au[rt]);
             }
         }
-        // U straight to global (fp32 row-major); W through LDS (R1: K rows are no longer needed)
+        // U straight to global (fp32 row-major); W through LDS (R1: the K rows are consumed)
         float* Ws = reinterpret_cast<float*>(R1);
-        constexpr int WP = DK + 4;
 #pragma unroll
-        for (int t = 0; t < 8; t++)
+        for (int rt = 0; rt < 4; rt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int i = wv * 16 + fg * 4 + r, d = t * 16 + fr;
-                Uo[i * DV + d] = au[t][r];
-                Ws[i * WP + d] = aw[t][r] * (1.0f / QK_SCALE);
+                const int i = rt * 16 + fg * 4 + r, d = wv * 16 + fr;
+                Uo[i * DV + d] = au[rt][r];
+                Ws[i * WP + d] = aw[rt][r] * (1.0f / QK_SCALE);
             }
         lds_barrier();
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int slotf = tid + 256 * q;  // 4 row tiles x 4 k steps x 64 lanes
+        for (int q = 0; q < 1024 / PREP_T; q++) {
+            const int slotf = tid + PREP_T * q;  // 4 row tiles x 4 k steps x 64 lanes
             const int ln = slotf & 63, st = (slotf >> 6) & 3, rt = slotf >> 8;
             const float* src = &Ws[(rt * 16 + (ln & 15)) * WP + st * 32 + (ln >> 4) * 8];
             float v8[8];
@@ -458,19 +500,18 @@ __global__ __launch_bounds__(256) void k_gdn_prep(const float* __restrict__ qkvc
     }
     if (tid == 0) ws.gl[slot] = eG[Lc - 1];
 
-    // ---- the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's
-    // history ++ this forward's rows) into the live history
-    if (hist) {  // each workgroup of the grid takes a slice of the channels
-        const uint8_t* pre = lu_prefix(lu);
-        const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
-        const int nb = gridDim.x * H, per = (C + nb - 1) / nb, b = c * H + h;
-        const int lo = b * per, hi = min(C, lo + per);
-        for (int ch = lo + tid; ch < hi; ch += 256) {
+    // ---- the history rows loaded at the start (and the rest of a longer slice)
+    if (hist) {
+        if (hlo + tid < hhi) {
+#pragma unroll
+            for (int r = 0; r < 3; r++) hist[(size_t)r * C + hlo + tid] = hv[r];
+        }
+        for (int ch = hlo + tid + PREP_T; ch < hhi; ch += PREP_T) {
             f16 v[3];
 #pragma unroll
             for (int r = 0; r < 3; r++) {
                 const int src = L - 3 + r;
-                v[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : old[(size_t)(src + 3) * C + ch];
+                v[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : hold[(size_t)(src + 3) * C + ch];
             }
 #pragma unroll
             for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = v[r];
@@ -701,8 +742,11 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
     const int cfirst = seqt ? (int)(seqt[q] & 0xFFFFu) : 0;
     const int cend = seqt ? cfirst + (int)(seqt[q] >> 16) : (L + CH - 1) / CH;
     // A chunk's operands (prep's output, not written here) are loaded ahead of their use: W, Qg and
-    // U of chunk c + 1 into a second register set when chunk c starts, its Qk and Kg once chunk c
-    // has used its own, so the load latency overlaps a chunk's MFMA work instead of following it.
+    // U of chunk c + 1 into a second register set when chunk c starts, its Qk, Kg and e^(G_last)
+    // once chunk c has used its own, so the load latency overlaps a chunk's MFMA work instead of
+    // following it.  Vector memory operations retire in issue order (vmcnt), so chunk c's o stores
+    // are issued after those loads: a wait for the loads never waits for the stores to be acked.
+    // e^(G_last) is a vector load too, so no scalar load is outstanding at an LDS barrier.
     struct WQ {
         f16x8 wh[4], wl[4], qh[4], ql[4];
         float ur[4];
@@ -718,7 +762,8 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
     const uint32_t o_qg = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.qgf) - wsb),
                    o_qk = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.qkf) - wsb),
                    o_kg = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.kgf) - wsb),
-                   o_u = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.u) - wsb);
+                   o_u = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.u) - wsb),
+                   o_gl = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.gl) - wsb);
     const uint32_t vfrag = (uint32_t)lane * 16u;                              // fragment layout
     const uint32_t vu = (uint32_t)((fg * 4 * DV + fr) * 4);                   // U rows fg*4 + r, column fr
     auto frag = [&](uint32_t region, int KS, int rt, int s, f16x8& hi, f16x8& lo) {
@@ -746,7 +791,7 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
 #pragma unroll
             for (int q2 = 0; q2 < 2; q2++) frag(o_kg + slot * (uint32_t)(KGF_H * 2), 2, wv * 2 + q2, s, kh[q2][s], kl[q2][s]);
         }
-        gl = ws.gl[slot];
+        gl = __builtin_bit_cast(float, buf_b32(rws, 0u, o_gl + slot * 4u));
     };
     // o rows t0 + wv*16 + fg*4 + r (r < 4), column h*DV + c0 + fr; rows past the chunk get an
     // out-of-range offset and are not written
@@ -789,15 +834,6 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         }
 #pragma unroll
         for (int s = 0; s < 2; s++) mma3s(qkh[s], qkl[s], vh[s], vl[s], ao);
-        {
-            const uint32_t so = (uint32_t)(((t0 + wv * 16) * sh.H * DV + h * DV + c0) * 4);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const bool in = wv * 16 + fg * 4 + r < Lc;
-                buf_st32(ro, in ? vo + (uint32_t)(r * sh.H * DV * 4) : OOB, so,
-                         __builtin_bit_cast(uint32_t, ao[0][r] + ao[1][r] + ao[2][r]));
-            }
-        }
         // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
         f32x4 as[2][3];
 #pragma unroll
@@ -808,6 +844,15 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         }
         const float g_c = gl;
         if (c + 1 < cend) load_qk(c + 1);  // Qk, Kg, gl are consumed
+        {
+            const uint32_t so = (uint32_t)(((t0 + wv * 16) * sh.H * DV + h * DV + c0) * 4);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const bool in = wv * 16 + fg * 4 + r < Lc;
+                buf_st32(ro, in ? vo + (uint32_t)(r * sh.H * DV * 4) : OOB, so,
+                         __builtin_bit_cast(uint32_t, ao[0][r] + ao[1][r] + ao[2][r]));
+            }
+        }
 #pragma unroll
         for (int q2 = 0; q2 < 2; q2++) {
             // state rows k0 .. k0 + 3 of column fr: one 16-byte read-modify-write
@@ -893,7 +938,7 @@ void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float*
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     SD_CHECK(!sg.chunk || (lu && !hist), "gdn_prep: several sequences need lu and keep no conv history");
     if (!sg.chunk) nch = (L + CH - 1) / CH;
-    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H), dim3(256), 0, st, qkvc, big, s, negA, dtb, L, ws, hist, sg.chunk, lu,
+    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H), dim3(PREP_T), 0, st, qkvc, big, s, negA, dtb, L, ws, hist, sg.chunk, lu,
                        hist_off);
     launched("gdn_prep");
 }
