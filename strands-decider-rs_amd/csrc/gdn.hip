@@ -150,11 +150,14 @@ constexpr size_t WF_H = 4 * 4 * 2 * 64 * 8;   // W: 4 row tiles x 4 k steps
 constexpr size_t QGF_H = WF_H;                // qn e^G
 constexpr size_t QKF_H = 4 * 2 * 2 * 64 * 8;  // Qk: 4 row tiles x 2 k steps
 constexpr size_t KGF_H = 8 * 2 * 2 * 64 * 8;  // KgT: 8 row tiles x 2 k steps
-constexpr size_t U_F = 64 * 128;              // U, fp32 row-major
+constexpr size_t U_F = 64 * 128;              // U^T, fp32 [value column][token]
 
 constexpr int PREP_T = 512;  // k_gdn_prep threads: 8 waves
 
-// One workgroup per (chunk, head).  Two thread views of the chunk's rows:
+// Two workgroups per (chunk, head), by role (blockIdx.z): role 0 builds T = (I - A)^-1 and from it
+// W and U; role 1 the fragments that need no T (Qk, qn e^G, (Kn e^(G_last - G))^T) and the history
+// update, so the grid fills twice the CUs and the critical path is role 0 alone.  Two thread views
+// of the chunk's rows:
 //  - row view, thread (i, p) = (tid / 8, tid % 8): columns 16p..16p+15 of q and k in row i, for the
 //    norms, the Q/K rows in LDS (the K Kn^T and Qn Kn^T operands) and the qn e^G fragments;
 //  - column view, wave w, lane (n, g) = (lane % 16, lane / 16): column 16w + n of k and v at tokens
@@ -187,6 +190,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int fr = lane & 15, fg = lane >> 4;  // fragment row (column) / k group of this lane
     const int c = blockIdx.x, h = blockIdx.y, H = gridDim.y;
+    const bool qside = blockIdx.z != 0;  // role 1
     if (chunkt && c >= (int)lu[4]) return;  // the grid is sized for the most chunks L can split into
     const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
     const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - t0);
@@ -196,7 +200,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
     f16* Qgf = ws.qgf + slot * QGF_H;
     f16* Qkf = ws.qkf + slot * QKF_H;
     f16* Kgf = ws.kgf + slot * KGF_H;
-    float* Uo = ws.u + slot * U_F;
+    float* Uo = ws.u + slot * U_F;  // U^T: [value column][token]
 
     // Every global load of the kernel is issued here, before its first store: vector memory
     // operations retire in issue order, so a load issued after a store would wait for its ack.  The
@@ -212,10 +216,12 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
     float qv[16], kv[16];
     {
         const float* row = qkvc + (size_t)(t0 + min(ri, Lc - 1)) * C;
+        // the T side has no use for q: its "q" rows re-read k (same lines, no extra traffic)
+        const float* rq4 = row + (qside ? h * DK : sh.H * DK + h * DK) + rp * 16;
         float4 q4[4], k4[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            q4[e] = *reinterpret_cast<const float4*>(row + h * DK + rp * 16 + 4 * e);
+            q4[e] = *reinterpret_cast<const float4*>(rq4 + 4 * e);
             k4[e] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + rp * 16 + 4 * e);
         }
 #pragma unroll
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
             kv[4 * e] = k4[e].x, kv[4 * e + 1] = k4[e].y, kv[4 * e + 2] = k4[e].z, kv[4 * e + 3] = k4[e].w;
         }
     }
-    float kT[2][8], vT[2][8];  // column view
+    float kT[2][8], vT[2][8];  // column view (v on the T side only)
     {
         const float* ck = qkvc + sh.H * DK + h * DK + wv * 16 + fr;
         const float* cv = qkvc + 2 * sh.H * DK + h * DV + wv * 16 + fr;
@@ -234,7 +240,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
             for (int u = 0; u < 8; u++) {
                 const size_t jr = (size_t)(t0 + min(s * 32 + fg * 8 + u, Lc - 1)) * C;
                 kT[s][u] = ck[jr];
-                vT[s][u] = cv[jr];
+                vT[s][u] = qside ? 0.f : cv[jr];
             }
     }
     // the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's history
@@ -244,7 +250,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
     const int hlo = (c * H + h) * hper, hhi = min(C, hlo + hper);
     const f16* hold = hist ? (lu_prefix(lu) ? reinterpret_cast<const f16*>(lu_prefix(lu) + hist_off) : hist) : nullptr;
     f16 hv[3] = {};
-    if (hist) {  // channel hlo + tid clamped into the slice (stored only when inside it)
+    if (hist && qside) {  // channel hlo + tid clamped into the slice (stored only when inside it)
         const int ch = min(hlo + tid, hhi - 1);
 #pragma unroll
         for (int r = 0; r < 3; r++) {
@@ -296,9 +302,11 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
 #pragma unroll
             for (int u = 0; u < 8; u++) q8[u] = qv[e + u] * rq * QK_SCALE, k8[u] = kv[e + u] * rk * QK_SCALE;
             f16x8 hi, lo;
-            split8(q8, hi, lo);
-            *reinterpret_cast<f16x8*>(&Qh[ri * RP + rp * 16 + e]) = hi;
-            *reinterpret_cast<f16x8*>(&Ql[ri * RP + rp * 16 + e]) = lo;
+            if (qside) {
+                split8(q8, hi, lo);
+                *reinterpret_cast<f16x8*>(&Qh[ri * RP + rp * 16 + e]) = hi;
+                *reinterpret_cast<f16x8*>(&Ql[ri * RP + rp * 16 + e]) = lo;
+            }
             split8(k8, hi, lo);
             *reinterpret_cast<f16x8*>(&Kh[ri * RP + rp * 16 + e]) = hi;
             *reinterpret_cast<f16x8*>(&Kl[ri * RP + rp * 16 + e]) = lo;
@@ -306,7 +314,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
     }
     lds_barrier();
     // qn e^G as A fragments: (row tile ri/16, k step rp/2, lanes (ri%16) + 16g, g = 2 (rp%2) + gg)
-    {
+    if (qside) {
         const float e = eG[ri] * rq;
 #pragma unroll
         for (int gg = 0; gg < 2; gg++) {
@@ -333,61 +341,81 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
             k8[u] = kn * QK_SCALE;
             v8[u] = j0 + u < Lc ? vT[s][u] : 0.f;
         }
-        put_frag(Kgf, 2, wv, s, lane, g8);
-        split8(k8, kbh[s], kbl[s]);
-        split8(v8, vbh[s], vbl[s]);
+        if (qside) {
+            put_frag(Kgf, 2, wv, s, lane, g8);
+        } else {
+            split8(k8, kbh[s], kbl[s]);
+            split8(v8, vbh[s], vbl[s]);
+        }
     }
 
-    // ---- phase 1: Kn Kn^T (waves 0-3) and Qn Kn^T (waves 4-7); wave w computes row tile w % 4 x 4
-    // column tiles of its product
+    // ---- phase 1: Kn Kn^T (T side) or Qn Kn^T (q side); wave w computes row tile w % 4 x column
+    // tiles 2 (w / 4), 2 (w / 4) + 1
     {
-        const int wr = wv & 3;
-        const bool second = wv >= 4;
-        f32x4 acc[4];
+        const int wr = wv & 3, tc = 2 * (wv >> 2);
+        f32x4 acc[2];
 #pragma unroll
-        for (int t = 0; t < 4; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const f16* Ah = second ? Qh : Kh;
-        const f16* Al = second ? Ql : Kl;
+        for (int t = 0; t < 2; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const f16* Ah = qside ? Qh : Kh;
+        const f16* Al = qside ? Ql : Kl;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const int ar = (wr * 16 + fr) * RP + s * 32 + fg * 8;
             const f16x8 ah = *reinterpret_cast<const f16x8*>(&Ah[ar]), al = *reinterpret_cast<const f16x8*>(&Al[ar]);
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int br = (t * 16 + fr) * RP + s * 32 + fg * 8;
+            for (int t = 0; t < 2; t++) {
+                const int br = ((tc + t) * 16 + fr) * RP + s * 32 + fg * 8;
                 const f16x8 kbh2 = *reinterpret_cast<const f16x8*>(&Kh[br]), kbl2 = *reinterpret_cast<const f16x8*>(&Kl[br]);
                 acc[t] = mma3(ah, al, kbh2, kbl2, acc[t]);
             }
         }
-        // the decays and beta this lane needs, read once: rows wr*16 + fg*4 + r, columns t*16 + fr
-        float Gi[4], Bi[4], Gj[4];
+        // the decays and beta this lane needs, read once: rows wr*16 + fg*4 + r, columns (tc+t)*16 + fr
+        float Gi[4], Bi[4], Gj[2];
 #pragma unroll
         for (int r = 0; r < 4; r++) Gi[r] = G[wr * 16 + fg * 4 + r], Bi[r] = beta[wr * 16 + fg * 4 + r];
 #pragma unroll
-        for (int t = 0; t < 4; t++) Gj[t] = G[t * 16 + fr];
+        for (int t = 0; t < 2; t++) Gj[t] = G[(tc + t) * 16 + fr];
         lds_barrier();  // Q rows are consumed: R2 becomes the Qk staging area
         float* Qs = reinterpret_cast<float*>(R2);
-        float* dst = second ? Qs : Ts;
+        float* dst = qside ? Qs : Ts;
         constexpr float UNS = 1.0f / (QK_SCALE * QK_SCALE);
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int i = wr * 16 + fg * 4 + r, j = t * 16 + fr;
+                const int i = wr * 16 + fg * 4 + r, j = (tc + t) * 16 + fr;
                 const float a = acc[t][r] * UNS * fexp(Gi[r] - Gj[t]);  // masked below where i < j
                 const float vq = i >= j ? a : 0.f;
                 const float vt = i > j ? -Bi[r] * a : (i == j ? 1.f : 0.f);
-                dst[i * FP + j] = second ? vq : vt;
+                dst[i * FP + j] = qside ? vq : vt;
             }
         lds_barrier();
-        // Qk as A fragments: 4 row tiles x 2 k steps x 64 lanes, one per thread
-        {
+        if (qside) {
+            // Qk as A fragments: 4 row tiles x 2 k steps x 64 lanes, one per thread
             const int ln = tid & 63, st = (tid >> 6) & 1, rt = tid >> 7;
             const float* src = &Qs[(rt * 16 + (ln & 15)) * FP + st * 32 + (ln >> 4) * 8];
             float v8[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) v8[u] = src[u];
             put_frag(Qkf, 2, rt, st, ln, v8);
+            // the history rows loaded at the start (and the rest of a longer slice)
+            if (hist) {
+                if (hlo + tid < hhi) {
+#pragma unroll
+                    for (int r = 0; r < 3; r++) hist[(size_t)r * C + hlo + tid] = hv[r];
+                }
+                for (int ch = hlo + tid + PREP_T; ch < hhi; ch += PREP_T) {
+                    f16 v[3];
+#pragma unroll
+                    for (int r = 0; r < 3; r++) {
+                        const int src2 = L - 3 + r;
+                        v[r] = src2 >= 0 ? big[(size_t)src2 * sh.stride + ch] : hold[(size_t)(src2 + 3) * C + ch];
+                    }
+#pragma unroll
+                    for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = v[r];
+                }
+            }
+            return;
         }
     }
 
@@ -403,14 +431,15 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
             Nb[blk][a][b] = Ts[(16 * p + a) * FP + 16 * r + b];
         }
         if (wv < 4 && lane < 16) {
+            // right-looking: once x[k] is final it is added into every later row's sum, so the 16
+            // rows' sums run side by side (the terms of each still add in k order)
             float x[16];
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float acc = i == lane ? 1.f : 0.f;
+            for (int i = 0; i < 16; i++) x[i] = i == lane ? 1.f : 0.f;
 #pragma unroll
-                for (int k = 0; k < i; k++) acc += Ts[(base + i) * FP + base + k] * x[k];
-                x[i] = acc;
-            }
+            for (int k = 0; k < 15; k++)
+#pragma unroll
+                for (int i = k + 1; i < 16; i++) x[i] += Ts[(base + i) * FP + base + k] * x[k];
 #pragma unroll
             for (int i = 0; i < 16; i++) Ts[(base + i) * FP + base + lane] = x[i];
         }
@@ -476,16 +505,17 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
                 au[rt] = mma3(ah, al, vbh[s], vbl[s], au[rt]);
             }
         }
-        // U straight to global (fp32 row-major); W through LDS (R1: the K rows are consumed)
+        // U^T straight to global (a lane's 4 tokens of one column: one 16-byte store per row tile); W
+        // through LDS (R1: the K rows are consumed)
         float* Ws = reinterpret_cast<float*>(R1);
 #pragma unroll
-        for (int rt = 0; rt < 4; rt++)
+        for (int rt = 0; rt < 4; rt++) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int i = rt * 16 + fg * 4 + r, d = wv * 16 + fr;
-                Uo[i * DV + d] = au[rt][r];
-                Ws[i * WP + d] = aw[rt][r] * (1.0f / QK_SCALE);
+                Uo[(rt * 16 + fg * 4 + r) * DV + wv * 16 + fr] = au[rt][r];
+                Ws[(rt * 16 + fg * 4 + r) * WP + wv * 16 + fr] = aw[rt][r] * (1.0f / QK_SCALE);
             }
+        }
         lds_barrier();
 #pragma unroll
         for (int q = 0; q < 1024 / PREP_T; q++) {
@@ -499,24 +529,6 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
         }
     }
     if (tid == 0) ws.gl[slot] = eG[Lc - 1];
-
-    // ---- the history rows loaded at the start (and the rest of a longer slice)
-    if (hist) {
-        if (hlo + tid < hhi) {
-#pragma unroll
-            for (int r = 0; r < 3; r++) hist[(size_t)r * C + hlo + tid] = hv[r];
-        }
-        for (int ch = hlo + tid + PREP_T; ch < hhi; ch += PREP_T) {
-            f16 v[3];
-#pragma unroll
-            for (int r = 0; r < 3; r++) {
-                const int src = L - 3 + r;
-                v[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : hold[(size_t)(src + 3) * C + ch];
-            }
-#pragma unroll
-            for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = v[r];
-        }
-    }
 }
 
 // Sum over the 16 lanes of this lane's DPP row, the same bits in every lane: partners by mirror,
@@ -765,7 +777,7 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
                    o_u = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.u) - wsb),
                    o_gl = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.gl) - wsb);
     const uint32_t vfrag = (uint32_t)lane * 16u;                              // fragment layout
-    const uint32_t vu = (uint32_t)((fg * 4 * DV + fr) * 4);                   // U rows fg*4 + r, column fr
+    const uint32_t vu = (uint32_t)((fg * 4 * DV + fr) * 4);  // U rows fg*4 + r, column fr
     auto frag = [&](uint32_t region, int KS, int rt, int s, f16x8& hi, f16x8& lo) {
         const uint32_t so = region + (uint32_t)((rt * KS + s) * 2) * 1024u;
         hi = __builtin_bit_cast(f16x8, buf_b128(rws, vfrag, so));
@@ -938,7 +950,7 @@ void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float*
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     SD_CHECK(!sg.chunk || (lu && !hist), "gdn_prep: several sequences need lu and keep no conv history");
     if (!sg.chunk) nch = (L + CH - 1) / CH;
-    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H), dim3(PREP_T), 0, st, qkvc, big, s, negA, dtb, L, ws, hist, sg.chunk, lu,
+    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H, 2), dim3(PREP_T), 0, st, qkvc, big, s, negA, dtb, L, ws, hist, sg.chunk, lu,
                        hist_off);
     launched("gdn_prep");
 }
