@@ -377,7 +377,7 @@ int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off
         sd::gdn_ws_carve(w.gdn, L, s, ws);
         const hipStream_t st = static_cast<hipStream_t>(stream);
         sd::gdn_prep(static_cast<const float*>(qkv), static_cast<const sd::f16*>(big), s, static_cast<const float*>(negA),
-                     static_cast<const float*>(dtb), L, ws, nullptr, sd::Segs{}, 0, nullptr, st);
+                     static_cast<const float*>(dtb), L, ws, sd::ConvIn{}, sd::Segs{}, 0, nullptr, st);
         sd::gdn_scan(s, L, ws, static_cast<float*>(state), nullptr, load_state, static_cast<float*>(o), sd::Segs{}, 1, st);
     });
 }

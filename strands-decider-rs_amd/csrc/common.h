@@ -159,6 +159,15 @@ struct Segs {
 struct GdnShape {
     int H, DK, DV, stride, a_off, b_off, z_off, C;
 };
+
+// What a GDN prep needs to compute the causal conv + SiLU of the in_proj rows itself (w null: the
+// caller passes the conv output instead).
+struct ConvIn {
+    const float* w = nullptr;        // [C][4] taps
+    const f16* hist = nullptr;       // the live history [3][C]; a prefix snapshot's (named by lu) wins
+    const uint32_t* rowt = nullptr;  // per row: index in its sequence | start row << 16 (null: one sequence)
+    size_t hist_off = 0;             // the layer's history in a snapshot arena image
+};
 // Workspace of the chunked recurrence, sized for `cap` tokens: per (chunk, head) the scan's A
 // operands split into f16 hi/lo in MFMA fragment order, U (fp32) and e^(G_last).
 struct GdnWs {
@@ -179,17 +188,18 @@ constexpr size_t LU_PREFIX_BYTE = 32;
 // Every sequence's first rows read the conv history: the prefix's (lu) or `hist`.
 void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f16* hist, float* out,
                const Segs& sg, hipStream_t st, const uint32_t* lu = nullptr, size_t hist_off = 0);
-// hist (nullable) is updated from big afterwards (the reference's hist_update; single sequence
-// only), its old rows from the prefix's history.  nch = chunk grid size (chunks past lu[4] exit when
-// sg.chunk is set).
+// With cv.w set, q, k and v are the conv + SiLU of big's rows (qkvc unused), else read from qkvc.
+// nch = chunk grid size (chunks past lu[4] exit when sg.chunk is set).
 void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
-              const GdnWs& ws, f16* hist, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st,
-              size_t hist_off = 0);
+              const GdnWs& ws, const ConvIn& cv, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st);
 // lu = device block above (the state is loaded when has_cache, from the prefix's arena image when it
 // names one); with lu null, load_default decides.  Every sequence starts from that state; the final
 // state is written to `state` only for a single sequence (sg.seq null).  nseq = sequence grid size.
+// hist (nullable) is updated from big at the end (the reference's hist_update; single sequence
+// only), its old rows from the prefix's history.
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
-              const Segs& sg, int nseq, hipStream_t st, size_t state_off = 0);
+              const Segs& sg, int nseq, hipStream_t st, size_t state_off = 0, f16* hist = nullptr,
+              const f16* big = nullptr, size_t hist_off = 0);
 // The same recurrence token by token (the reference's own order), for short inputs: every
 // sequence starts from the prefix state as gdn_scan; with one sequence the final state is written
 // to `state` and hist (nullable) updated afterwards, as gdn_prep + gdn_scan do.

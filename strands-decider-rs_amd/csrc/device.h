@@ -136,6 +136,16 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 #endif
 }
 
+// silu(x) = x / (1 + e^-x) the same way, kept in f32 (the conv output of the chunked delta rule;
+// the reference's WGSL exp is no more exact than v_exp_f32).
+__device__ __forceinline__ float silu(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+#else
+    return x;
+#endif
+}
+
 __device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
     return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }

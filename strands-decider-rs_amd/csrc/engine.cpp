@@ -659,21 +659,24 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
             mm(steps, "in_proj", P.h, W.in_proj, P.big, L, sr);
             // conv and the delta rule read the prefix's history and state in place (from the snapshot
             // the lu block names, else the live arena) and write the live arena
-            steps.push_back({"conv", [=](hipStream_t s) {
-                conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, sg, s, luv, W.hist_off);
-            }});
             f16* hist_upd = nseq ? nullptr : W.hist;  // several sequences leave no history
             if (recur) {
+                steps.push_back({"conv", [=](hipStream_t s) {
+                    conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, sg, s, luv, W.hist_off);
+                }});
                 steps.push_back({"gdn", [=](hipStream_t s) {
                     gdn_recur(P.qkvc, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, hist_upd, sg, nseq, s, W.state_off,
                               W.hist_off);
                 }});
             } else {
+                // the chunked path computes the conv inside prep (no conv output in HBM); the history
+                // is updated by the scan, after every prep workgroup has read the old one
+                const ConvIn cin{W.conv, W.hist, sg.row, W.hist_off};
                 steps.push_back({"gdn", [=](hipStream_t s) {
-                    gdn_prep(P.qkvc, P.big, gs, W.negA, W.dtb, L, P.gdn, hist_upd, sg, nch, luv, s, W.hist_off);
+                    gdn_prep(nullptr, P.big, gs, W.negA, W.dtb, L, P.gdn, cin, sg, nch, luv, s);
                 }});
                 steps.push_back({"gdn", [=](hipStream_t s) {
-                    gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s, W.state_off);
+                    gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s, W.state_off, hist_upd, P.big, W.hist_off);
                 }});
             }
             steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});

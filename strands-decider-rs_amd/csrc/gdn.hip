@@ -155,8 +155,8 @@ constexpr size_t U_F = 64 * 128;              // U^T, fp32 [value column][token]
 constexpr int PREP_T = 512;  // k_gdn_prep threads: 8 waves
 
 // Two workgroups per (chunk, head), by role (blockIdx.z): role 0 builds T = (I - A)^-1 and from it
-// W and U; role 1 the fragments that need no T (Qk, qn e^G, (Kn e^(G_last - G))^T) and the history
-// update, so the grid fills twice the CUs and the critical path is role 0 alone.  Two thread views
+// W and U; role 1 the fragments that need no T (Qk, qn e^G, (Kn e^(G_last - G))^T), so the grid
+// fills twice the CUs and the critical path is role 0 alone.  Two thread views
 // of the chunk's rows:
 //  - row view, thread (i, p) = (tid / 8, tid % 8): columns 16p..16p+15 of q and k in row i, for the
 //    norms, the Q/K rows in LDS (the K Kn^T and Qn Kn^T operands) and the qn e^G fragments;
@@ -164,20 +164,27 @@ constexpr int PREP_T = 512;  // k_gdn_prep threads: 8 waves
 //    32s + 8g + u (s < 2, u < 8), loaded straight from global memory in that order, which is both an
 //    MFMA B fragment over tokens (W = T diag(beta e^G) Kn and U = T diag(beta) V, column tile w) and
 //    the scan's (Kn e^(G_last - G))^T A fragment (row tile w): no transpose passes through LDS.
+// CONV: q, k and v are the causal conv + SiLU of big's rows, computed here (the reference's conv,
+// src/kernels.rs:152-170: rows before a sequence's start from the history, the prefix snapshot's when
+// lu names one); otherwise they are read from qkvc.
+template <bool CONV>
 __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ qkvc, const f16* __restrict__ big,
                                                   GdnShape sh, const float* __restrict__ negA,
-                                                  const float* __restrict__ dtb, int L, GdnWs ws, f16* hist,
-                                                  const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu,
-                                                  size_t hist_off) {
+                                                  const float* __restrict__ dtb, int L, GdnWs ws, ConvIn cv,
+                                                  const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu) {
     constexpr int DK = 128, DV = 128;
     constexpr int RP = DK + 8;  // f16 row pitch of the Q/K row tiles
     constexpr int FP = CH + 4;  // fp32 pitch of T and of the Qk staging
     constexpr int WP = DK + 4;  // fp32 pitch of the W staging
     // LDS regions: R1 = K rows (hi, lo), later W staging (fp32); R2 = Q rows (hi, lo), later Qk
-    // staging (fp32); T; the blocks of the inversion; per-token vectors.
+    // staging (fp32); before both, the conv output (fp32 [token][XP], over R1 and R2); T; the blocks
+    // of the inversion; per-token vectors.
     constexpr size_t R1B = 2 * CH * RP * 2 > CH * WP * 4 ? 2 * CH * RP * 2 : CH * WP * 4;
-    __shared__ __attribute__((aligned(16))) uint8_t R1[R1B];
-    __shared__ __attribute__((aligned(16))) uint8_t R2[2 * CH * RP * 2];
+    constexpr int XP = 2 * 128 + 4;  // fp32 pitch of the conv output: two 128-channel matrices
+    static_assert((size_t)CH * XP * 4 <= R1B + 2 * CH * RP * 2, "the conv output fits R1 and R2");
+    __shared__ __attribute__((aligned(16))) uint8_t RR[R1B + 2 * CH * RP * 2];
+    uint8_t* const R1 = RR;
+    uint8_t* const R2 = RR + R1B;
     __shared__ __attribute__((aligned(16))) float Ts[CH * FP];
     __shared__ float Xs[4][16][17];
     __shared__ float Nb[6][16][17];  // the off-diagonal 16 x 16 blocks of A, (p, r) at p (p - 1) / 2 + r
@@ -214,49 +221,92 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
         gb16 = big[gr + sh.b_off];
     }
     float qv[16], kv[16];
-    {
-        const float* row = qkvc + (size_t)(t0 + min(ri, Lc - 1)) * C;
-        // the T side has no use for q: its "q" rows re-read k (same lines, no extra traffic)
-        const float* rq4 = row + (qside ? h * DK : sh.H * DK + h * DK) + rp * 16;
-        float4 q4[4], k4[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            q4[e] = *reinterpret_cast<const float4*>(rq4 + 4 * e);
-            k4[e] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + rp * 16 + 4 * e);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            qv[4 * e] = q4[e].x, qv[4 * e + 1] = q4[e].y, qv[4 * e + 2] = q4[e].z, qv[4 * e + 3] = q4[e].w;
-            kv[4 * e] = k4[e].x, kv[4 * e + 1] = k4[e].y, kv[4 * e + 2] = k4[e].z, kv[4 * e + 3] = k4[e].w;
-        }
-    }
     float kT[2][8], vT[2][8];  // column view (v on the T side only)
-    {
+    if constexpr (!CONV) {
+        {
+            const float* row = qkvc + (size_t)(t0 + min(ri, Lc - 1)) * C;
+            // the T side has no use for q: its "q" rows re-read k (same lines, no extra traffic)
+            const float* rq4 = row + (qside ? h * DK : sh.H * DK + h * DK) + rp * 16;
+            float4 q4[4], k4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                q4[e] = *reinterpret_cast<const float4*>(rq4 + 4 * e);
+                k4[e] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + rp * 16 + 4 * e);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                qv[4 * e] = q4[e].x, qv[4 * e + 1] = q4[e].y, qv[4 * e + 2] = q4[e].z, qv[4 * e + 3] = q4[e].w;
+                kv[4 * e] = k4[e].x, kv[4 * e + 1] = k4[e].y, kv[4 * e + 2] = k4[e].z, kv[4 * e + 3] = k4[e].w;
+            }
+        }
         const float* ck = qkvc + sh.H * DK + h * DK + wv * 16 + fr;
-        const float* cv = qkvc + 2 * sh.H * DK + h * DV + wv * 16 + fr;
+        const float* cvp = qkvc + 2 * sh.H * DK + h * DV + wv * 16 + fr;
 #pragma unroll
         for (int s = 0; s < 2; s++)
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const size_t jr = (size_t)(t0 + min(s * 32 + fg * 8 + u, Lc - 1)) * C;
                 kT[s][u] = ck[jr];
-                vT[s][u] = qside ? 0.f : cv[jr];
+                vT[s][u] = qside ? 0.f : cvp[jr];
             }
-    }
-    // the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's history
-    // ++ this forward's rows) become the live history; each workgroup of the grid takes a slice of
-    // the channels, this thread channel lo + tid (stored at the end, a longer slice in a loop there)
-    const int hnb = gridDim.x * H, hper = (C + hnb - 1) / hnb;
-    const int hlo = (c * H + h) * hper, hhi = min(C, hlo + hper);
-    const f16* hold = hist ? (lu_prefix(lu) ? reinterpret_cast<const f16*>(lu_prefix(lu) + hist_off) : hist) : nullptr;
-    f16 hv[3] = {};
-    if (hist && qside) {  // channel hlo + tid clamped into the slice (stored only when inside it)
-        const int ch = min(hlo + tid, hhi - 1);
+    } else {
+        // conv view: wave w takes tokens 8w..8w+7, lane l 4 channels of matrix l / 32 (q side: q, k;
+        // T side: k, v); the 11 rows a wave's tokens read are the same for all its lanes, so whether
+        // a row comes from big or from the history is wave-uniform.
+        const int wvu = __builtin_amdgcn_readfirstlane(wv);
+        const int mat = lane >> 5, c4 = (lane & 31) * 4;
+        const int m0 = qside ? (mat == 0 ? h * DK : sh.H * DK + h * DK) : (mat == 0 ? sh.H * DK + h * DK : 2 * sh.H * DK + h * DV);
+        const int cg = m0 + c4;
+        float4 wk[4];  // taps of the 4 channels
 #pragma unroll
-        for (int r = 0; r < 3; r++) {
-            const int src = L - 3 + r;
-            hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : hold[(size_t)(src + 3) * C + ch];
+        for (int u = 0; u < 4; u++) wk[u] = *reinterpret_cast<const float4*>(cv.w + 4 * (cg + u));
+        const uint32_t rt0 = cv.rowt ? cv.rowt[t0] : (uint32_t)t0;  // index in the sequence | start row << 16
+        const int i0 = (int)(rt0 & 0xFFFFu), s0 = (int)(rt0 >> 16);
+        const uint8_t* pre = lu_prefix(lu);
+        const f16* hsrc = pre ? reinterpret_cast<const f16*>(pre + cv.hist_off) : cv.hist;
+        const Rsrc rb = make_rsrc(big, (uint32_t)(s0 + i0 + Lc) * (uint32_t)sh.stride * 2u);
+        const Rsrc rh = make_rsrc(hsrc, 3u * (uint32_t)C * 2u);
+        f16x4 xr[11];
+#pragma unroll
+        for (int m = 0; m < 11; m++) {
+            const int ii = min(i0 + 8 * wvu - 3 + m, i0 + Lc - 1);  // sequence index of the row (uniform)
+            const bool fromh = ii < 0;
+            const Rsrc r = fromh ? rh : rb;
+            const uint32_t so = fromh ? (uint32_t)((ii + 3) * C) * 2u : (uint32_t)(s0 + ii) * (uint32_t)sh.stride * 2u;
+            xr[m] = __builtin_bit_cast(f16x4, buf_b64(r, (uint32_t)cg * 2u, so));
         }
+        float* X = reinterpret_cast<float*>(RR);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            float o4[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float kj[4] = {wk[u].x, wk[u].y, wk[u].z, wk[u].w};
+                float a = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; j++) a += kj[j] * (float)xr[t + j][u];
+                o4[u] = silu(a);
+            }
+            *reinterpret_cast<float4*>(&X[(8 * wvu + t) * XP + mat * 128 + c4]) = float4{o4[0], o4[1], o4[2], o4[3]};
+        }
+        lds_barrier();
+        const int mq = 0, mk = qside ? 128 : 0, mv = 128;
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(&X[ri * XP + mq + rp * 16 + e]);
+            const float4 k4 = *reinterpret_cast<const float4*>(&X[ri * XP + mk + rp * 16 + e]);
+            qv[e] = q4.x, qv[e + 1] = q4.y, qv[e + 2] = q4.z, qv[e + 3] = q4.w;
+            kv[e] = k4.x, kv[e + 1] = k4.y, kv[e + 2] = k4.z, kv[e + 3] = k4.w;
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = s * 32 + fg * 8 + u;
+                kT[s][u] = X[j * XP + mk + wv * 16 + fr];
+                vT[s][u] = qside ? 0.f : X[j * XP + mv + wv * 16 + fr];
+            }
+        lds_barrier();  // the conv output is consumed: R1 and R2 take the K and Q rows
     }
 
     // ---- phase 0: gates (wave 0), normalised q/k rows
@@ -398,23 +448,6 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
 #pragma unroll
             for (int u = 0; u < 8; u++) v8[u] = src[u];
             put_frag(Qkf, 2, rt, st, ln, v8);
-            // the history rows loaded at the start (and the rest of a longer slice)
-            if (hist) {
-                if (hlo + tid < hhi) {
-#pragma unroll
-                    for (int r = 0; r < 3; r++) hist[(size_t)r * C + hlo + tid] = hv[r];
-                }
-                for (int ch = hlo + tid + PREP_T; ch < hhi; ch += PREP_T) {
-                    f16 v[3];
-#pragma unroll
-                    for (int r = 0; r < 3; r++) {
-                        const int src2 = L - 3 + r;
-                        v[r] = src2 >= 0 ? big[(size_t)src2 * sh.stride + ch] : hold[(size_t)(src2 + 3) * C + ch];
-                    }
-#pragma unroll
-                    for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = v[r];
-                }
-            }
             return;
         }
     }
@@ -733,7 +766,8 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
 __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, float* __restrict__ state,
                                                   const uint32_t* __restrict__ lu, int load_default,
                                                   float* __restrict__ o, const uint32_t* __restrict__ chunkt,
-                                                  const uint32_t* __restrict__ seqt, size_t state_off) {
+                                                  const uint32_t* __restrict__ seqt, size_t state_off,
+                                                  const f16* __restrict__ big, f16* hist, size_t hist_off) {
     constexpr int DK = 128, DV = 128;
     constexpr int SP = DK + 4, VP = CH + 4;
     __shared__ __attribute__((aligned(16))) float St[DVS * SP];  // S^T: [column][k]
@@ -890,6 +924,24 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         const int k = e / DVS, cc = e % DVS;
         Sg[k * DV + c0 + cc] = St[cc * SP + k];
     }
+    // the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's history
+    // ++ this forward's rows) into the live history, each workgroup on a slice of the channels; here,
+    // after the prep that read the old history for its conv
+    if (hist) {
+        const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
+        const int C = sh.C, nb = gridDim.x * gridDim.y, per = (C + nb - 1) / nb, bi = blockIdx.y * H + h;
+        const int lo = bi * per, hi = min(C, lo + per);
+        for (int ch = lo + tid; ch < hi; ch += 256) {
+            f16 hv[3];
+#pragma unroll
+            for (int r = 0; r < 3; r++) {
+                const int src = L - 3 + r;
+                hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : old[(size_t)(src + 3) * C + ch];
+            }
+#pragma unroll
+            for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = hv[r];
+        }
+    }
 }
 
 // out[t, h*DV + c] = f16(w[c] o rsqrt(mean(o^2) + 1e-6) silu(z)); one wave per (t, h), DV = 128.
@@ -946,22 +998,28 @@ void conv_silu(const f16* big, int stride, int L, int C, const float* w, const f
 }
 
 void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
-              const GdnWs& ws, f16* hist, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st, size_t hist_off) {
+              const GdnWs& ws, const ConvIn& cv, const Segs& sg, int nch, const uint32_t* lu, hipStream_t st) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
-    SD_CHECK(!sg.chunk || (lu && !hist), "gdn_prep: several sequences need lu and keep no conv history");
+    SD_CHECK(!sg.chunk || lu, "gdn_prep: several sequences need lu");
+    SD_CHECK(!cv.w || cv.hist, "gdn_prep: the conv needs the history");
+    SD_CHECK(!cv.w || (s.C % 4 == 0 && s.stride % 4 == 0), "gdn_prep: channels and row stride must be multiples of 4");
     if (!sg.chunk) nch = (L + CH - 1) / CH;
-    hipLaunchKernelGGL(k_gdn_prep, dim3(nch, s.H, 2), dim3(PREP_T), 0, st, qkvc, big, s, negA, dtb, L, ws, hist, sg.chunk, lu,
-                       hist_off);
+    const dim3 grid(nch, s.H, 2);
+    if (cv.w)
+        hipLaunchKernelGGL(k_gdn_prep<true>, grid, dim3(PREP_T), 0, st, qkvc, big, s, negA, dtb, L, ws, cv, sg.chunk, lu);
+    else
+        hipLaunchKernelGGL(k_gdn_prep<false>, grid, dim3(PREP_T), 0, st, qkvc, big, s, negA, dtb, L, ws, cv, sg.chunk, lu);
     launched("gdn_prep");
 }
 
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
-              const Segs& sg, int nseq, hipStream_t st, size_t state_off) {
+              const Segs& sg, int nseq, hipStream_t st, size_t state_off, f16* hist, const f16* big, size_t hist_off) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     SD_CHECK(!sg.seq || (lu && sg.chunk), "gdn_scan: several sequences need lu and the chunk table");
+    SD_CHECK(!hist || (!sg.seq && big), "gdn_scan: the history update needs one sequence and big");
     if (!sg.seq) nseq = 1;
     hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(256), 0, st, s, L, ws, state, lu, load_default, o,
-                       sg.chunk, sg.seq, state_off);
+                       sg.chunk, sg.seq, state_off, big, hist, hist_off);
     launched("gdn_scan");
 }
 
