@@ -785,6 +785,21 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         const int k = e / DVS, cc = e % DVS;
         St[cc * SP + k] = load ? S0[k * DV + c0 + cc] : 0.f;
     }
+    // the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's history
+    // ++ this forward's rows) become the live history, each workgroup on a slice of the channels;
+    // here, after the prep that read the old history for its conv.  This thread's channel lo + tid
+    // is loaded now, before any store, and stored at the end (a longer slice loops there).
+    const int hC = sh.C, hnb = gridDim.x * gridDim.y, hper = (hC + hnb - 1) / hnb;
+    const int hlo = (blockIdx.y * H + h) * hper, hhi = min(hC, hlo + hper);
+    const f16* hold = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
+    f16 hv[3] = {};
+    if (hist && hlo + tid < hhi) {
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            const int src = L - 3 + r;
+            hv[r] = src >= 0 ? big[(size_t)src * sh.stride + hlo + tid] : hold[(size_t)(src + 3) * hC + hlo + tid];
+        }
+    }
     const int cfirst = seqt ? (int)(seqt[q] & 0xFFFFu) : 0;
     const int cend = seqt ? cfirst + (int)(seqt[q] >> 16) : (L + CH - 1) / CH;
     // A chunk's operands (prep's output, not written here) are loaded ahead of their use: W, Qg and
@@ -924,22 +939,20 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
         const int k = e / DVS, cc = e % DVS;
         Sg[k * DV + c0 + cc] = St[cc * SP + k];
     }
-    // the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's history
-    // ++ this forward's rows) into the live history, each workgroup on a slice of the channels; here,
-    // after the prep that read the old history for its conv
     if (hist) {
-        const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
-        const int C = sh.C, nb = gridDim.x * gridDim.y, per = (C + nb - 1) / nb, bi = blockIdx.y * H + h;
-        const int lo = bi * per, hi = min(C, lo + per);
-        for (int ch = lo + tid; ch < hi; ch += 256) {
-            f16 hv[3];
+        if (hlo + tid < hhi) {
+#pragma unroll
+            for (int r = 0; r < 3; r++) hist[(size_t)r * hC + hlo + tid] = hv[r];
+        }
+        for (int ch = hlo + tid + 256; ch < hhi; ch += 256) {
+            f16 v3[3];
 #pragma unroll
             for (int r = 0; r < 3; r++) {
                 const int src = L - 3 + r;
-                hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : old[(size_t)(src + 3) * C + ch];
+                v3[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : hold[(size_t)(src + 3) * hC + ch];
             }
 #pragma unroll
-            for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = hv[r];
+            for (int r = 0; r < 3; r++) hist[(size_t)r * hC + ch] = v3[r];
         }
     }
 }
