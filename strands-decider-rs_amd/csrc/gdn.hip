@@ -827,39 +827,45 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
                    o_gl = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.gl) - wsb);
     const uint32_t vfrag = (uint32_t)lane * 16u;                              // fragment layout
     const uint32_t vu = (uint32_t)((fg * 4 * DV + fr) * 4);  // U rows fg*4 + r, column fr
-    auto frag = [&](uint32_t region, int KS, int rt, int s, f16x8& hi, f16x8& lo) {
+    // Every chunk issues the same loads with no branch around any of them: a chunk past the last
+    // one gets out-of-range offsets (zeros, no memory access).  The compiler then counts exactly
+    // which loads a wait must cover; a load under a branch leaves it unsure and it waits for more.
+    auto frag = [&](uint32_t region, int KS, int rt, int s, f16x8& hi, f16x8& lo, uint32_t vf) {
         const uint32_t so = region + (uint32_t)((rt * KS + s) * 2) * 1024u;
-        hi = __builtin_bit_cast(f16x8, buf_b128(rws, vfrag, so));
-        lo = __builtin_bit_cast(f16x8, buf_b128(rws, vfrag, so + 1024u));
+        hi = __builtin_bit_cast(f16x8, buf_b128(rws, vf, so));
+        lo = __builtin_bit_cast(f16x8, buf_b128(rws, vf, so + 1024u));
     };
     auto load_wq = [&](WQ& d, int c) {
-        const uint32_t slot = (uint32_t)(c * H + h);
+        const bool in = c < cend;
+        const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vf = in ? vfrag : OOB, vuu = in ? vu : OOB;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            frag(slot * (uint32_t)(WF_H * 2), 4, wv, s, d.wh[s], d.wl[s]);
-            frag(o_qg + slot * (uint32_t)(QGF_H * 2), 4, wv, s, d.qh[s], d.ql[s]);
+            frag(slot * (uint32_t)(WF_H * 2), 4, wv, s, d.wh[s], d.wl[s], vf);
+            frag(o_qg + slot * (uint32_t)(QGF_H * 2), 4, wv, s, d.qh[s], d.ql[s], vf);
         }
 #pragma unroll
         for (int r = 0; r < 4; r++)
             d.ur[r] = __builtin_bit_cast(
-                float, buf_b32(rws, vu, o_u + slot * (uint32_t)(U_F * 4) + (uint32_t)(((wv * 16 + r) * DV + c0) * 4)));
+                float, buf_b32(rws, vuu, o_u + slot * (uint32_t)(U_F * 4) + (uint32_t)(((wv * 16 + r) * DV + c0) * 4)));
     };
     auto load_qk = [&](int c) {
-        const uint32_t slot = (uint32_t)(c * H + h);
+        const bool in = c < cend;
+        const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vf = in ? vfrag : OOB;
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            frag(o_qk + slot * (uint32_t)(QKF_H * 2), 2, wv, s, qkh[s], qkl[s]);
+            frag(o_qk + slot * (uint32_t)(QKF_H * 2), 2, wv, s, qkh[s], qkl[s], vf);
 #pragma unroll
-            for (int q2 = 0; q2 < 2; q2++) frag(o_kg + slot * (uint32_t)(KGF_H * 2), 2, wv * 2 + q2, s, kh[q2][s], kl[q2][s]);
+            for (int q2 = 0; q2 < 2; q2++)
+                frag(o_kg + slot * (uint32_t)(KGF_H * 2), 2, wv * 2 + q2, s, kh[q2][s], kl[q2][s], vf);
         }
-        gl = __builtin_bit_cast(float, buf_b32(rws, 0u, o_gl + slot * 4u));
+        gl = __builtin_bit_cast(float, buf_b32(rws, in ? 0u : OOB, o_gl + slot * 4u));
     };
     // o rows t0 + wv*16 + fg*4 + r (r < 4), column h*DV + c0 + fr; rows past the chunk get an
     // out-of-range offset and are not written
     const Rsrc ro = make_rsrc(o, (uint32_t)L * sh.H * DV * 4);
     const uint32_t vo = (uint32_t)((fg * 4 * sh.H * DV + fr) * 4);
     auto chunk = [&](int c, const WQ& cur, WQ& nxt) {
-        if (c + 1 < cend) load_wq(nxt, c + 1);
+        load_wq(nxt, c + 1);
         const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
         const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - c * CH);
         lds_barrier();  // St holds this chunk's starting state; Vt is free
@@ -904,7 +910,7 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
             for (int s = 0; s < 2; s++) mma3s(kh[q2][s], kl[q2][s], vh[s], vl[s], as[q2]);
         }
         const float g_c = gl;
-        if (c + 1 < cend) load_qk(c + 1);  // Qk, Kg, gl are consumed
+        load_qk(c + 1);  // Qk, Kg, gl are consumed
         {
             const uint32_t so = (uint32_t)(((t0 + wv * 16) * sh.H * DV + h * DV + c0) * 4);
 #pragma unroll
@@ -925,14 +931,14 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
                           g_c * s4.w + (as[q2][0][3] + as[q2][1][3] + as[q2][2][3])};
         }
     };
-    if (cfirst < cend) {
-        load_wq(set0, cfirst);
-        load_qk(cfirst);
-    }
-    for (int c = cfirst; c < cend; c += 2) {
+    load_wq(set0, cfirst);
+    load_qk(cfirst);
+    int c = cfirst;
+    for (; c + 1 < cend; c += 2) {  // no branch inside the loop body
         chunk(c, set0, set1);
-        if (c + 1 < cend) chunk(c + 1, set1, set0);
+        chunk(c + 1, set1, set0);
     }
+    if (c < cend) chunk(c, set0, set1);
     if (seqt) return;  // several sequences: their final states are not kept
     __syncthreads();
     for (int e = tid; e < DK * DVS; e += 256) {
