@@ -24,8 +24,9 @@ __device__ double block_sum_f64(double v, double* red) {
 }
 
 // Row r: LayerNorm in f64 into LDS, then 16 outputs [16 y, 16 y + 16) of the q (answer row) or k
-// projection.  Wave w takes columns [w d/4, (w + 1) d/4) of all 16 outputs (its 16-byte weight
-// loads all issued before the f64 FMAs), and the 4 partial dot products meet in LDS.
+// projection.  Wave w takes columns [w d/4, (w + 1) d/4) of all 16 outputs, and the 4 partial dot
+// products meet in LDS.  Every global load is unconditional (indices clamped, values masked after
+// they arrive): a load under a branch would make the wave wait for it before issuing the next.
 __global__ __launch_bounds__(256) void k_head_rows(const float* __restrict__ hid, int d, HeadW w,
                                                    const uint8_t* __restrict__ is_answer, double* __restrict__ proj) {
     extern __shared__ double xn[];  // d values
@@ -33,16 +34,22 @@ __global__ __launch_bounds__(256) void k_head_rows(const float* __restrict__ hid
     __shared__ double part[4][16];
     const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* x = hid + (size_t)r * d;
+#pragma unroll 4
+    for (int j = 4 * tid; j < d; j += 1024) {
+        const float4 v = *reinterpret_cast<const float4*>(x + j);
+        xn[j] = (double)v.x, xn[j + 1] = (double)v.y, xn[j + 2] = (double)v.z, xn[j + 3] = (double)v.w;
+    }
+    __syncthreads();
     double s = 0.0;
-    for (int j = tid; j < d; j += 256) s += (double)x[j];
+    for (int j = tid; j < d; j += 256) s += xn[j];
     const double mean = block_sum_f64(s, red) / (double)d;
     double v = 0.0;
     for (int j = tid; j < d; j += 256) {
-        const double t = (double)x[j] - mean;
+        const double t = xn[j] - mean;
         v += t * t;
     }
     const double rs = 1.0 / sqrt(block_sum_f64(v, red) / (double)d + 1e-5);
-    for (int j = tid; j < d; j += 256) xn[j] = ((double)x[j] - mean) * rs * (double)w.nw[j] + (double)w.nb[j];
+    for (int j = tid; j < d; j += 256) xn[j] = (xn[j] - mean) * rs * (double)w.nw[j] + (double)w.nb[j];
     __syncthreads();
     const bool ans = is_answer[r] != 0;
     const float* W = ans ? w.qw : w.kw;
@@ -56,8 +63,7 @@ __global__ __launch_bounds__(256) void k_head_rows(const float* __restrict__ hid
     for (int j0 = wave * span + 4 * lane; j0 < (wave + 1) * span; j0 += 256) {
         float4 wv[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++)
-            wv[u] = u < no ? *reinterpret_cast<const float4*>(W + (size_t)(ob + u) * d + j0) : float4{0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < 16; u++) wv[u] = *reinterpret_cast<const float4*>(W + (size_t)min(ob + u, w.dim - 1) * d + j0);
         const double x0 = xn[j0], x1 = xn[j0 + 1], x2 = xn[j0 + 2], x3 = xn[j0 + 3];
 #pragma unroll
         for (int u = 0; u < 16; u++)
@@ -72,7 +78,8 @@ __global__ __launch_bounds__(256) void k_head_rows(const float* __restrict__ hid
     if (tid < no) proj[(size_t)r * w.dim + ob + tid] = (double)B[ob + tid] + ((part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]));
 }
 
-// Question q (one wave): rows [first, first + n) are its options, row first + n its answer.
+// Question q (one wave): rows [first, first + n) are its options, row first + n its answer.  The
+// loads are unconditional (option rows past n read row first + n - 1, their sums unused).
 __global__ __launch_bounds__(64) void k_head_probs(const double* __restrict__ proj, int dim,
                                                     const uint32_t* __restrict__ qtab, const double* __restrict__ scale,
                                                     const uint32_t* __restrict__ ooff, double* __restrict__ probs) {
@@ -85,12 +92,12 @@ __global__ __launch_bounds__(64) void k_head_probs(const double* __restrict__ pr
     for (int i0 = 0; i0 < n; i0 += 8) {
         double sv[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            sv[u] = 0.0;
-            if (i0 + u < n) {
-                const double* k = proj + (size_t)(first + i0 + u) * dim;
-                for (int o = lane; o < dim; o += 64) sv[u] += k[o] * qa[o];
-            }
+        for (int u = 0; u < 8; u++) sv[u] = 0.0;
+#pragma unroll 4
+        for (int o = lane; o < dim; o += 64) {
+            const double a = qa[o];
+#pragma unroll
+            for (int u = 0; u < 8; u++) sv[u] += proj[(size_t)(first + min(i0 + u, n - 1)) * dim + o] * a;
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
