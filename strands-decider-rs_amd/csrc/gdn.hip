@@ -623,43 +623,44 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     const uint8_t* pre = lu_prefix(lu);
     float* Sg = state + (size_t)h * DK * DV;  // the live state (written back by a single sequence)
     const float* S0 = (pre ? reinterpret_cast<const float*>(pre + state_off) : state) + (size_t)h * DK * DV;
+    // Every global load below is unconditional (indices clamped, values zeroed after they arrive): a
+    // load under a branch makes the wave wait for it before it issues the next.
+    // The state is read through a buffer resource: a flat load (the prefix or live pointer is not
+    // known to be global) would also count as an LDS operation and hold up the first LDS barrier.
     float S[8];
+    {
+        const Rsrc rs = make_rsrc(S0, (uint32_t)(DK * DV * 4));
 #pragma unroll
-    for (int i = 0; i < 8; i++) S[i] = load ? S0[(size_t)srow(i) * DV + col] : 0.f;
+        for (int i = 0; i < 8; i++) S[i] = __builtin_bit_cast(float, buf_b32(rs, (uint32_t)((srow(i) * DV + col) * 4), 0u));
+    }
+    bool fresh = !load;  // the state starts at zero: applied at the first token, after the block's loads
     const int C = sh.C;
     const float na = negA[h], db = dtb[h], qs = 1.0f / sqrtf((float)DK);
     for (int tb = t0; tb < t1; tb += RTB) {
         const int nt = min(RTB, t1 - tb);
-        __syncthreads();  // the previous block is consumed
+        lds_barrier();  // the previous block's LDS is consumed
         // q and k of a token: one DPP row of 16 lanes x 8 values, normalised on the way into LDS
         // (the sums over the row are one row_allsum16).  Every load of the block is issued before
         // the first is used.
         constexpr int NIT = RTB * 16 / 256;  // tokens per wave-pass: 16 per workgroup
         float4 qr[NIT][2], kr[NIT][2];
+        float vr[RTB * 16 / 256];
 #pragma unroll
         for (int it = 0; it < NIT; it++) {
             const int e = it * 256 + tid, tt = e >> 4, j = e & 15;
+            const float* row = qkvc + (size_t)(tb + min(tt, nt - 1)) * C;  // tokens past the block: unused
 #pragma unroll
-            for (int u = 0; u < 2; u++) qr[it][u] = kr[it][u] = float4{0.f, 0.f, 0.f, 0.f};
-            if (tt < nt) {
-                const float* row = qkvc + (size_t)(tb + tt) * C;
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    qr[it][u] = *reinterpret_cast<const float4*>(row + h * DK + 8 * j + 4 * u);
-                    kr[it][u] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + 8 * j + 4 * u);
-                }
+            for (int u = 0; u < 2; u++) {
+                qr[it][u] = *reinterpret_cast<const float4*>(row + h * DK + 8 * j + 4 * u);
+                kr[it][u] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + 8 * j + 4 * u);
             }
+            vr[it] = row[2 * sh.H * DK + h * DV + cb + j];
         }
-        float vr[RTB * 16 / 256];
-#pragma unroll
-        for (int it = 0; it < RTB * 16 / 256; it++) {
-            const int e = it * 256 + tid, tt = e >> 4, j = e & 15;
-            vr[it] = tt < nt ? qkvc[(size_t)(tb + tt) * C + 2 * sh.H * DK + h * DV + cb + j] : 0.f;
-        }
-        float ga = 0.f, gb = 0.f;
-        if (tid < nt) {
-            ga = (float)big[(size_t)(tb + tid) * sh.stride + sh.a_off + h];
-            gb = (float)big[(size_t)(tb + tid) * sh.stride + sh.b_off + h];
+        float ga, gb;  // the gate inputs of token tid (used for tid < nt)
+        {
+            const size_t gr = (size_t)(tb + min(tid, nt - 1)) * sh.stride + h;
+            ga = (float)big[gr + sh.a_off];
+            gb = (float)big[gr + sh.b_off];
         }
 #pragma unroll
         for (int it = 0; it < NIT; it++) {
@@ -698,6 +699,11 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
             Dc[tid] = expf(na * sp);
         }
         __syncthreads();
+        if (fresh) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) S[i] = 0.f;
+            fresh = false;
+        }
         // Both column sums come from the previous state, so they are independent:
         //   S_t = dc S + kn delta^T, delta = beta (v - dc S^T kn), o = S_t^T qn = dc S^T qn + (kn . qn) delta
         // A token's operands do not depend on the state: those of token tt + 1 are read from LDS
