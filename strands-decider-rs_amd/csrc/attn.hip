@@ -149,11 +149,12 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
             for (int e = 0; e < 8; e++) qf[st][e] = (f16)((float)v[e] * scale);
         }
     }
-    // the output gates of this block's queries (dimension tid), loaded while the keys are processed
+    // the output gates of this block's queries (dimension tid), loaded while the keys are processed;
+    // unconditionally (queries past nq read the last one's), as a load under a branch would be
+    // waited for before the next is issued
     float gq[16];
 #pragma unroll
-    for (int q = 0; q < 16; q++)
-        gq[q] = ks == 1 && q < nq ? (float)big[(size_t)(t0 + q) * s.stride + h * 2 * HD + HD + tid] : 0.f;
+    for (int q = 0; q < 16; q++) gq[q] = (float)big[(size_t)(t0 + min(q, nq - 1)) * s.stride + h * 2 * HD + HD + tid];
     f32x4 acc[ND];
 #pragma unroll
     for (int dt = 0; dt < ND; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
