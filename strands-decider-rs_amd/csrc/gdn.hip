@@ -150,7 +150,7 @@ constexpr size_t WF_H = 4 * 4 * 2 * 64 * 8;   // W: 4 row tiles x 4 k steps
 constexpr size_t QGF_H = WF_H;                // qn e^G
 constexpr size_t QKF_H = 4 * 2 * 2 * 64 * 8;  // Qk: 4 row tiles x 2 k steps
 constexpr size_t KGF_H = 8 * 2 * 2 * 64 * 8;  // KgT: 8 row tiles x 2 k steps
-constexpr size_t U_F = 64 * 128;              // U^T, fp32 [value column][token]
+constexpr size_t U_F = 64 * 128;              // U, fp32 [token][value column]
 
 constexpr int PREP_T = 512;  // k_gdn_prep threads: 8 waves
 
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
     f16* Qgf = ws.qgf + slot * QGF_H;
     f16* Qkf = ws.qkf + slot * QKF_H;
     f16* Kgf = ws.kgf + slot * KGF_H;
-    float* Uo = ws.u + slot * U_F;  // U^T: [value column][token]
+    float* Uo = ws.u + slot * U_F;  // U: [token][value column]
 
     // Every global load of the kernel is issued here, before its first store: vector memory
     // operations retire in issue order, so a load issued after a store would wait for its ack.  The
@@ -538,8 +538,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ q
                 au[rt] = mma3(ah, al, vbh[s], vbl[s], au[rt]);
             }
         }
-        // U^T straight to global (a lane's 4 tokens of one column: one 16-byte store per row tile); W
-        // through LDS (R1: the K rows are consumed)
+        // U straight to global (row-major); W through LDS (R1: the K rows are consumed)
         float* Ws = reinterpret_cast<float*>(R1);
 #pragma unroll
         for (int rt = 0; rt < 4; rt++) {
