@@ -539,6 +539,14 @@ def kernel_bench(pkg, reps=50):
                                    "mfma_frac": round(flops / tot_us / 1e6 / PEAK_MFMA_F16, 4),
                                    "weight_gbps": round(wbytes / tot_us / 1e3, 1),
                                    "hbm_frac": round(wbytes / tot_us / 1e3 / PEAK_HBM, 4)}
+        if M == 8:
+            # the same layer as the engine launches it at M <= 20 (the f32-dequant GEMV): q/k/v (or
+            # the GDN layer's in_proj) and gate/up as one fused matrix each; gate_up timed with f16
+            # output (the engine applies SiLU * mul in the same kernel's epilogue)
+            fz = {name: gemm(M, N, K) for name, N, K in fused}
+            att = fz["qkv"]["us"] + fz["o"]["us"] + fz["gate_up"]["us"] + fz["down"]["us"]
+            gdn = fz["in_proj"]["us"] + fz["o"]["us"] + fz["gate_up"]["us"] + fz["down"]["us"]
+            out["cfg1_fused_M8"] = {"shapes": fz, "attention_layer_us": round(att, 2), "gdn_layer_us": round(gdn, 2)}
         if M == 512:
             out["cfg1_fused_M512"] = {name: gemm(M, N, K) for name, N, K in fused}
             # the vendor library's f16 GEMM (torch.matmul -> hipBLASLt) on the same shapes, with f16
