@@ -5,8 +5,9 @@
 // Attention runs on MFMA (k_attn below).  When the query blocks alone cannot fill the GPU (the
 // short question suffix over a long cached prefix), the key range is also split over workgroups
 // and a combine kernel merges the partial (max, sum, acc).  As in the reference, q is pre-scaled
-// by 1/sqrt(hd) and rounded to f16 before the dot products.  The V cache is kept transposed,
-// [hk][hd][ctx].
+// by 1/sqrt(hd) and rounded to f16 before the dot products.  The V cache is kept transposed in
+// blocks of 32 keys, [hk][ctx / 32][hd][32]: a block's V^T is 16 KB of consecutive bytes, so the
+// fragment loads of a key block touch whole cache lines.
 #include <cmath>
 
 #include "common.h"
@@ -31,16 +32,16 @@ __global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, At
     const bool isq = slot < s.HQ;
     const int k_off = 2 * s.HQ * HD, v_off = k_off + s.HK * HD;
     const int nt = min(4, L - t0);
-    if (!isq) {  // V cache is stored transposed, [hk][hd][ctx]: thread d writes rows t0 .. t0+3
+    if (!isq) {  // V^T in 32-key blocks, [hk][ctx / 32][hd][32]: thread d writes rows t0 .. t0+3
         const int kh = slot - s.HQ, d = tid;
         f16 v[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) v[i] = i < nt ? big[(size_t)(t0 + i) * s.stride + v_off + kh * HD + d] : (f16)0.f;
-        f16* dst = Vc + ((size_t)kh * HD + d) * s.ctx + P + t0;
-        if (nt == 4 && ((P + t0) & 3) == 0) {
-            *reinterpret_cast<f16x4*>(dst) = f16x4{v[0], v[1], v[2], v[3]};
+        auto at = [&](int pos) { return Vc + (((size_t)kh * (s.ctx / 32) + pos / 32) * HD + d) * 32 + pos % 32; };
+        if (nt == 4 && ((P + t0) & 3) == 0) {  // the 4 rows lie in one block
+            *reinterpret_cast<f16x4*>(at(P + t0)) = f16x4{v[0], v[1], v[2], v[3]};
         } else {
-            for (int i = 0; i < nt; i++) dst[i] = v[i];
+            for (int i = 0; i < nt; i++) *at(P + t0 + i) = v[i];
         }
     }
     const float* nw = isq ? qw : kw;
@@ -107,8 +108,9 @@ __device__ __forceinline__ float wave_sum16(float v) {
 // v_mfma_f32_16x16x32_f16 over the 256 dims), the online softmax per query (column), then
 // O^T += V^T P^T (256 dims x 16 queries); with S^T in the MFMA output layout, P^T is already in
 // the B-operand layout (lane = query, 8 keys), and the V cache is stored transposed so V^T
-// fragments are contiguous (the keys of a block are permuted so that they are 8 consecutive).  P is split into f16 hi + lo (two MFMAs) so that the product keeps the
-// reference's f32 P.V to about 22 bits.  With ks > 1 the workgroups along z also split the keys
+// fragments are contiguous (the keys of a block are permuted so that they are 8 consecutive).  P is
+// split into f16 hi + lo (two MFMAs) so that the product keeps the reference's f32 P.V to about 22
+// bits.  With ks > 1 the workgroups along z also split the keys
 // and write unnormalised (acc, max, sum) for k_attn_combine.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f16* __restrict__ Kc,
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         }
 #pragma unroll
         for (int dt = 0; dt < ND; dt++)
-            vf[dt] = *reinterpret_cast<const f16x8*>(Vb + (size_t)(dt * 16 + fq) * s.ctx + j0 + fg * 8);
+            vf[dt] = *reinterpret_cast<const f16x8*>(Vb + (size_t)(j0 >> 5) * (HD * 32) + (dt * 16 + fq) * 32 + fg * 8);
         f32x4 st2[2];
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
@@ -316,6 +318,7 @@ void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* k
     SD_CHECK(s.HD == 256, "attention: only head_dim 256 is supported");
     SD_CHECK(s.RD % 2 == 0 && s.RD <= s.HD, "attention: bad rotary_dim");
     SD_CHECK(s.RD % 8 == 0 && s.stride % 4 == 0, "attention: rotary_dim must be a multiple of 8, the row stride of 4");
+    SD_CHECK(s.ctx % 32 == 0, "attention: the cache length must be a multiple of 32");
     hipLaunchKernelGGL(k_qk_prep<256>, dim3((L + 3) / 4, s.HQ + s.HK), dim3(256), 0, st, big, s, qw, kw, rope, L, lu,
                        sg.row, Q, Kc, Vc);
     launched("qk_prep");

@@ -514,6 +514,7 @@ int sd_op_attention(const void* big, int stride, const void* qw, const void* kw,
     return guarded(err, errlen, [&] {
         if (!big || !qw || !kw || !rope || !Q || !Kc || !Vt || !out) throw sd::Error("sd_op_attention: null argument");
         if (L < 1 || P < 0 || P + L > ctx) throw sd::Error("sd_op_attention: need 1 <= L and P + L <= ctx");
+        if (ctx % 32) throw sd::Error("sd_op_attention: ctx must be a multiple of 32");
         if (HK < 1 || HQ % HK) throw sd::Error("sd_op_attention: q heads must be a multiple of kv heads");
         const sd::AttnShape as{HQ, HK, HD, RD, stride, ctx};
         // the engine's key split: query blocks of 16 that cannot fill the chip split the keys too

@@ -778,16 +778,16 @@ void Engine::restore(const Snapshot* cache, size_t P) {
     if (cache) {
         std::vector<CopyDesc> cp;
         if (kv_owner != cache->id) {
-            // K rows [hk][t][hd]; V transposed [hk][hd][t] (the attention kernel's layout).  The V
-            // rows carry P8 keys: the live rows P..P8-1 are rewritten by the forward before any
-            // read (a forward writes rows >= P of its own ids first)
-            const size_t row = (size_t)cfg.hd * 2, P8 = (P + 7) & ~size_t(7);
+            // K rows [hk][t][hd]; V^T in 32-key blocks [hk][t / 32][hd][32] (the attention kernel's
+            // layout), whole blocks: the live rows P..P32-1 are rewritten by the forward before any
+            // read (a forward writes rows >= P of its own ids first) or lie past every key it reads
+            const size_t row = (size_t)cfg.hd * 2, P32 = (P + 31) & ~size_t(31);
             for (size_t a = 0; a < attn_layers.size(); a++) {
                 const LayerW& W = layers[attn_layers[a]];
                 cp.push_back(CopyDesc{cache->kv(a, 0), reinterpret_cast<uint8_t*>(W.kc), (uint64_t)cfg.hk, P * row, P * row,
                                       SD_CONTEXT * row});
-                cp.push_back(CopyDesc{cache->kv(a, 1), reinterpret_cast<uint8_t*>(W.vc), (uint64_t)cfg.hk * cfg.hd, P8 * 2,
-                                      P8 * 2, SD_CONTEXT * 2});
+                cp.push_back(CopyDesc{cache->kv(a, 1), reinterpret_cast<uint8_t*>(W.vc), (uint64_t)cfg.hk, P32 * row,
+                                      P32 * row, SD_CONTEXT * row});
             }
             kv_owner = cache->id;
         }
@@ -856,8 +856,8 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
         snap->engine = this;
         snap->len = T;
         snap->id = ++snapshot_ids;
-        const size_t T8 = (T + 7) & ~size_t(7);
-        snap->kv_stride = (size_t)cfg.hk * T8 * cfg.hd * 2;
+        const size_t T32 = (T + 31) & ~size_t(31);
+        snap->kv_stride = (size_t)cfg.hk * T32 * cfg.hd * 2;
         snap->arena_bytes = arena_bytes;
         snap->alloc_bytes = arena_bytes + attn_layers.size() * 2 * snap->kv_stride;
         try {
@@ -866,8 +866,8 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
             delete snap;
             throw;
         }
-        // the arena image, then K rows [hk][T][hd] and V [hk][hd][T8] (V rows rounded up to 8 keys so
-        // that every copy moves whole 16-byte chunks; the keys past T are not read back)
+        // the arena image, then K rows [hk][T][hd] and V^T blocks [hk][T32 / 32][hd][32] (whole 32-key
+        // blocks; the keys past T are not read back)
         std::vector<CopyDesc> cp;
         cp.push_back(CopyDesc{arena, static_cast<uint8_t*>(snap->arena), 1, arena_bytes, arena_bytes, arena_bytes});
         const size_t row = (size_t)cfg.hd * 2;
@@ -875,8 +875,8 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
             const LayerW& W = layers[attn_layers[a]];
             cp.push_back(CopyDesc{reinterpret_cast<const uint8_t*>(W.kc), snap->kv(a, 0), (uint64_t)cfg.hk, T * row,
                                   SD_CONTEXT * row, T * row});
-            cp.push_back(CopyDesc{reinterpret_cast<const uint8_t*>(W.vc), snap->kv(a, 1), (uint64_t)cfg.hk * cfg.hd, T8 * 2,
-                                  SD_CONTEXT * 2, T8 * 2});
+            cp.push_back(CopyDesc{reinterpret_cast<const uint8_t*>(W.vc), snap->kv(a, 1), (uint64_t)cfg.hk, T32 * row,
+                                  SD_CONTEXT * row, T32 * row});
         }
         copy_batch(cp.data(), cp.size(), st);
         kv_owner = snap->id;

@@ -111,9 +111,9 @@ struct Snapshot {
     const Engine* engine = nullptr;
     size_t len = 0;
     uint64_t id = 0;
-    void* arena = nullptr;  // [arena image | per attention layer: K [hk][len][hd], V [hk][hd][len8]]
+    void* arena = nullptr;  // [arena image | per attention layer: K [hk][len][hd], V^T [hk][len32 / 32][hd][32]]
     size_t alloc_bytes = 0;
-    size_t arena_bytes = 0, kv_stride = 0;  // kv_stride: hk * len8 * hd * 2, len8 = len rounded up to 8
+    size_t arena_bytes = 0, kv_stride = 0;  // kv_stride: hk * len32 * hd * 2, len32 = len rounded up to 32
     uint8_t* kv(size_t attn_index, int which) const {
         return static_cast<uint8_t*>(arena) + arena_bytes + (attn_index * 2 + which) * kv_stride;
     }

@@ -189,7 +189,8 @@ class AttnCase:
                         I(CTX), I(HQ), I(HK), I(HD), o.P(out))
         gotQ = host(dQ, np.float16, (HQ, L, HD))
         gotK = host(self.dK, np.float16, (HK, CTX, HD))[:, P:P + L]
-        gotVt = host(self.dV, np.float16, (HK, HD, CTX))[:, :, P:P + L]
+        # V^T in blocks of 32 rows: [HK][CTX/32][HD][32] -> [HK][HD][CTX]
+        gotVt = host(self.dV, np.float16, (HK, CTX // 32, HD, 32)).transpose(0, 2, 1, 3).reshape(HK, HD, CTX)[:, :, P:P + L]
         # q/k norm + RoPE: f32 math rounded to f16, within one f16 ulp; rotate-half can cancel terms
         # of size ~1 down to ~1e-4, where f32 rounding of the terms (a few 1e-7 either side) is
         # several f16 ulps of the result, hence the absolute allowance
