@@ -241,9 +241,9 @@ int sd_op_gnorm(const void* o, const void* big, int stride, int z_off, const voi
                 void* stream, char* err, size_t errlen);
 
 /* qk_prep then attn (src/kernels.rs:400-541) for one sequence at cache rows P .. P+L-1: Q [HQ][L][HD]
- * f16 receives the normed, rotated queries; K cache Kc [HK][ctx][HD] and the V cache Vt, transposed
- * in blocks of 32 rows, [HK][ctx/32][HD][32] (f16, the engine's layouts), receive rows P .. P+L-1,
- * rows below P are the prefix; out [L][HQ*HD] f16 the gated attention output.  big [L][stride]
+ * f16 receives the normed, rotated queries; the K cache Kc, in blocks of 32 rows [HK][ctx/32][HD/32]
+ * [32 rows][32 dims], and the V cache Vt, transposed in blocks of 32 rows [HK][ctx/32][HD][32] (f16,
+ * the engine's layouts), receive rows P .. P+L-1, rows below P are the prefix; out [L][HQ*HD] f16 the gated attention output.  big [L][stride]
  * holds [q | gate] per q head, then K, V heads; rope [ctx][RD/2][2] f32 (cos, sin).  head_dim 256
  * only, ctx a multiple of 32. */
 int sd_op_attention(const void* big, int stride, const void* qw, const void* kw, const void* rope, int L, int P, int HQ,

@@ -5,9 +5,10 @@
 // Attention runs on MFMA (k_attn below).  When the query blocks alone cannot fill the GPU (the
 // short question suffix over a long cached prefix), the key range is also split over workgroups
 // and a combine kernel merges the partial (max, sum, acc).  As in the reference, q is pre-scaled
-// by 1/sqrt(hd) and rounded to f16 before the dot products.  The V cache is kept transposed in
-// blocks of 32 keys, [hk][ctx / 32][hd][32]: a block's V^T is 16 KB of consecutive bytes, so the
-// fragment loads of a key block touch whole cache lines.
+// by 1/sqrt(hd) and rounded to f16 before the dot products.  The cache is kept in blocks of 32
+// keys, so that the fragment loads of a key block touch whole cache lines: K as [hk][ctx / 32]
+// [hd / 32][32 keys][32 dims] (a load of 16 keys x 8 dims reads pairs of consecutive keys' 64 bytes),
+// V transposed as [hk][ctx / 32][hd][32 keys] (a block's V^T is 16 KB of consecutive bytes).
 #include <cmath>
 
 #include "common.h"
@@ -83,7 +84,9 @@ __global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, At
             r4[u] = (f16)r;
         }
         if (isq) *reinterpret_cast<f16x4*>(Q + ((size_t)slot * L + t) * HD + 4 * lane) = r4;
-        else *reinterpret_cast<f16x4*>(Kc + ((size_t)(slot - s.HQ) * s.ctx + pos) * HD + 4 * lane) = r4;
+        else
+            *reinterpret_cast<f16x4*>(Kc + (((size_t)(slot - s.HQ) * (s.ctx / 32) + pos / 32) * (HD / 32) + lane / 8) * 1024 +
+                                      (pos % 32) * 32 + 4 * (lane % 8)) = r4;
     }
 }
 
@@ -173,9 +176,9 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
             const int key = min(j0 + 8 * (fq >> 2) + 4 * tt + (fq & 3), kend - 1);
-            const f16* krow = Kb + (size_t)key * HD + fg * 8;
+            const f16* krow = Kb + (size_t)(key >> 5) * (HD * 32) + (key & 31) * 32 + fg * 8;
 #pragma unroll
-            for (int st = 0; st < NS; st++) kf[tt][st] = *reinterpret_cast<const f16x8*>(krow + st * 32);
+            for (int st = 0; st < NS; st++) kf[tt][st] = *reinterpret_cast<const f16x8*>(krow + st * 1024);
         }
 #pragma unroll
         for (int dt = 0; dt < ND; dt++)

@@ -778,14 +778,14 @@ void Engine::restore(const Snapshot* cache, size_t P) {
     if (cache) {
         std::vector<CopyDesc> cp;
         if (kv_owner != cache->id) {
-            // K rows [hk][t][hd]; V^T in 32-key blocks [hk][t / 32][hd][32] (the attention kernel's
-            // layout), whole blocks: the live rows P..P32-1 are rewritten by the forward before any
-            // read (a forward writes rows >= P of its own ids first) or lie past every key it reads
+            // K and V^T in 32-key blocks (the attention kernel's layouts, one kv head's first P32 keys
+            // contiguous), whole blocks: the live rows P..P32-1 are rewritten by the forward before
+            // any read (a forward writes rows >= P of its own ids first) or lie past every key it reads
             const size_t row = (size_t)cfg.hd * 2, P32 = (P + 31) & ~size_t(31);
             for (size_t a = 0; a < attn_layers.size(); a++) {
                 const LayerW& W = layers[attn_layers[a]];
-                cp.push_back(CopyDesc{cache->kv(a, 0), reinterpret_cast<uint8_t*>(W.kc), (uint64_t)cfg.hk, P * row, P * row,
-                                      SD_CONTEXT * row});
+                cp.push_back(CopyDesc{cache->kv(a, 0), reinterpret_cast<uint8_t*>(W.kc), (uint64_t)cfg.hk, P32 * row,
+                                      P32 * row, SD_CONTEXT * row});
                 cp.push_back(CopyDesc{cache->kv(a, 1), reinterpret_cast<uint8_t*>(W.vc), (uint64_t)cfg.hk, P32 * row,
                                       P32 * row, SD_CONTEXT * row});
             }
@@ -866,15 +866,15 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
             delete snap;
             throw;
         }
-        // the arena image, then K rows [hk][T][hd] and V^T blocks [hk][T32 / 32][hd][32] (whole 32-key
+        // the arena image, then the K and V^T blocks of the first T32 keys of each kv head (whole 32-key
         // blocks; the keys past T are not read back)
         std::vector<CopyDesc> cp;
         cp.push_back(CopyDesc{arena, static_cast<uint8_t*>(snap->arena), 1, arena_bytes, arena_bytes, arena_bytes});
         const size_t row = (size_t)cfg.hd * 2;
         for (size_t a = 0; a < attn_layers.size(); a++) {
             const LayerW& W = layers[attn_layers[a]];
-            cp.push_back(CopyDesc{reinterpret_cast<const uint8_t*>(W.kc), snap->kv(a, 0), (uint64_t)cfg.hk, T * row,
-                                  SD_CONTEXT * row, T * row});
+            cp.push_back(CopyDesc{reinterpret_cast<const uint8_t*>(W.kc), snap->kv(a, 0), (uint64_t)cfg.hk, T32 * row,
+                                  SD_CONTEXT * row, T32 * row});
             cp.push_back(CopyDesc{reinterpret_cast<const uint8_t*>(W.vc), snap->kv(a, 1), (uint64_t)cfg.hk, T32 * row,
                                   SD_CONTEXT * row, T32 * row});
         }

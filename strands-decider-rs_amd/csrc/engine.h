@@ -111,7 +111,7 @@ struct Snapshot {
     const Engine* engine = nullptr;
     size_t len = 0;
     uint64_t id = 0;
-    void* arena = nullptr;  // [arena image | per attention layer: K [hk][len][hd], V^T [hk][len32 / 32][hd][32]]
+    void* arena = nullptr;  // [arena image | per attention layer: K, V^T blocks of the first len32 keys per kv head]
     size_t alloc_bytes = 0;
     size_t arena_bytes = 0, kv_stride = 0;  // kv_stride: hk * len32 * hd * 2, len32 = len rounded up to 32
     uint8_t* kv(size_t attn_index, int which) const {

@@ -188,7 +188,8 @@ class AttnCase:
         o.lib().or_attn(o.P(Q), o.P(self.oK), o.P(self.oV), o.P(big.view(np.uint16)), I(self.stride), I(L), I(P),
                         I(CTX), I(HQ), I(HK), I(HD), o.P(out))
         gotQ = host(dQ, np.float16, (HQ, L, HD))
-        gotK = host(self.dK, np.float16, (HK, CTX, HD))[:, P:P + L]
+        # K in blocks of 32 rows: [HK][CTX/32][HD/32][32 rows][32 dims] -> [HK][CTX][HD]
+        gotK = host(self.dK, np.float16, (HK, CTX // 32, HD // 32, 32, 32)).transpose(0, 1, 3, 2, 4).reshape(HK, CTX, HD)[:, P:P + L]
         # V^T in blocks of 32 rows: [HK][CTX/32][HD][32] -> [HK][HD][CTX]
         gotVt = host(self.dV, np.float16, (HK, CTX // 32, HD, 32)).transpose(0, 2, 1, 3).reshape(HK, HD, CTX)[:, :, P:P + L]
         # q/k norm + RoPE: f32 math rounded to f16, within one f16 ulp; rotate-half can cancel terms
