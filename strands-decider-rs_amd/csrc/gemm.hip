@@ -219,6 +219,216 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
             }
 }
 
+// The 16x16 product with the loads issued three k steps ahead (batched questions and other short M,
+// where a workgroup's k chain is short and every step would otherwise wait for its weights):
+//  * a workgroup is 4 waves side by side along N (NT 16-column tiles each) over MT 16-row tiles,
+//    k in steps of 128 through a ring of 4 LDS stages, one barrier per step;
+//  * the A tile of a step (BM rows x 256 B) goes straight from HBM to LDS (buffer_load_dwordx4 lds):
+//    16-byte chunk q of the stage (q = (i * 4 + wave) * 64 + lane for the thread's i-th load) holds
+//    row q / 16, k-chunk (q % 16) ^ (row % 16), so a wave instruction fills 4 whole rows and the
+//    fragment reads (16 rows at one k-chunk) fall in 16 different 16-byte bank groups;
+//  * lane (j = l % 16, g = l / 16) holds column j of its tiles and loads quant block g of the step
+//    and its scale into a ring of 4 register stages; MFMA k-slice s takes word s of that block, so
+//    the A fragment of lane (j, g) in slice s is row j at k-chunk 4g + s;
+//  * loads of a step past the workgroup's range carry out-of-range buffer offsets (no memory
+//    access), so every step issues the same loads and the explicit vector-memory waits are exact;
+//  * SILU (gate_up with rows interleaved in groups of 16, see k_gemm_w4m): mid = f16(silu(g) u), g
+//    and u rounded to f16 first.  With NT even a wave's tiles 2u and 2u + 1 hold gate and up of the
+//    same 16 outputs; with NT = 1 the pairs are in neighbouring waves and meet in LDS.
+template <int MT, int NT, bool PARTIAL, bool SILU = false>
+__global__ __launch_bounds__(256) void k_gemm_w4p(const f16* __restrict__ A, const uint32_t* __restrict__ W,
+                                                  const f16* __restrict__ S, f16* __restrict__ Y,
+                                                  float* __restrict__ part, int M, int N, int K, int ksplit,
+                                                  int tiled) {
+    constexpr int BM = MT * 16;
+    constexpr int STAGE = BM * 256;           // bytes of one A stage (128 k of BM rows)
+    constexpr int NLD = MT;                   // direct-to-LDS loads per thread per step
+    constexpr int PER_STEP = NLD + 2 * NT;    // vector-memory loads a thread issues per step
+    constexpr int WAIT2 = vmcnt_imm(2 * PER_STEP);
+    __shared__ __attribute__((aligned(1024))) uint8_t As0[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As1[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As2[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t As3[STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, g = lane >> 4;
+    int bx, by, bz;
+    xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), gridDim.x, gridDim.y, gridDim.z, bx, by,
+             bz);
+    const int m0 = by * BM, n0 = bx * (4 * NT * 16);
+    const int KB = K >> 5;
+    const int steps = K / KSTEP / ksplit;  // a multiple of 4 (checked by the launcher)
+    const int step0 = bz * steps;
+
+    const Rsrc ra = make_rsrc(A, (uint32_t)M * K * 2), rw = make_rsrc(W, (uint32_t)N * K / 2),
+               rs = make_rsrc(S, (uint32_t)N * KB * 2);
+    uint32_t aoff[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; i++) {
+        const int q = (i * 4 + wave) * 64 + lane;
+        const int row = q >> 4, c = (q & 15) ^ (row & 15);
+        aoff[i] = (uint32_t)(min(m0 + row, M - 1) * K + c * 8) * 2u;
+    }
+    // fragment read of tile a, slice s: row 16a + j, k-chunk 4g + s
+    uint32_t foff[MT][4];
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int s = 0; s < 4; s++) foff[a][s] = (a * 16 + j) * 256 + (((4 * g + s) ^ j) << 4);
+
+    int ncol[NT];
+    uint32_t woff[NT], soff[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        ncol[t] = n0 + (wave * NT + t) * 16 + j;
+        const uint32_t n = (uint32_t)min(ncol[t], N - 1);
+        const uint32_t i0 = tiled ? ((n >> 5) * (uint32_t)(KB >> 1) + (g >> 1)) * 64 + (n & 31) * 2 + (g & 1) : n * KB + g;
+        woff[t] = i0 * 16u;
+        soff[t] = i0 * 2u;
+    }
+    const uint32_t wstep = tiled ? 2048u : 64u, sstep = tiled ? 256u : 8u;
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[a][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 bw[4][NT];
+    uint32_t bs[4][NT];
+    auto issue = [&](int it, uint8_t* dst, u32x4* bwd, uint32_t* bsd) {
+        const bool in = it < steps;
+        const uint32_t ka = in ? (uint32_t)(step0 + it) * KSTEP * 2 : OOB;
+        const uint32_t kw = in ? (uint32_t)(step0 + it) * wstep : OOB;
+        const uint32_t ks_ = in ? (uint32_t)(step0 + it) * sstep : OOB;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) buf_lds16(ra, aoff[i], ka, dst + (i * 4 + wave) * 1024);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            bwd[t] = buf_b128(rw, woff[t], kw);
+            bsd[t] = buf_b16(rs, soff[t], ks_);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto frag = [&](const uint8_t* cur, int s, f16x8* af) {
+#pragma unroll
+        for (int a = 0; a < MT; a++) af[a] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(cur + foff[a][s]));
+    };
+    auto deq = [&](const u32x4* bwc, const uint32_t* bsc, int s, f16x8* bf) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const f16 scv = __builtin_bit_cast(f16, (uint16_t)bsc[t]);
+            const f16x2 sc2 = f16x2{scv, scv};
+            f16x2 p0, p1, p2, p3;
+            nib_pairs(bwc[t][s], p0, p1, p2, p3);
+            bf[t] = cat4(p0 * sc2, p1 * sc2, p2 * sc2, p3 * sc2);
+        }
+    };
+    // Step it reads stage `cur` and refills stage `fill` (read at it - 1) for step it + 3; slice
+    // s + 1's fragments and weights are produced while slice s's MFMAs run.
+    auto step = [&](const uint8_t* cur, uint8_t* fill, const u32x4* bwc, const uint32_t* bsc, u32x4* bwf,
+                    uint32_t* bsf, int it) {
+        issue(it + 3, fill, bwf, bsf);
+        f16x8 af[2][MT], bf[2][NT];
+        frag(cur, 0, af[0]);
+        deq(bwc, bsc, 0, bf[0]);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int cu = s & 1, nx = cu ^ 1;
+            if (s < 3) {
+                frag(cur, s + 1, af[nx]);
+                deq(bwc, bsc, s + 1, bf[nx]);
+            }
+#pragma unroll
+            for (int a = 0; a < MT; a++)
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                    acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[cu][a], bf[cu][t], acc[a][t], 0, 0, 0);
+        }
+        wait_loads<WAIT2>();  // the loads of steps it + 2, it + 3 may still be in flight
+        bar_noflush();
+    };
+
+    issue(0, As0, bw[0], bs[0]);
+    issue(1, As1, bw[1], bs[1]);
+    issue(2, As2, bw[2], bs[2]);
+    wait_loads<WAIT2>();
+    bar_noflush();
+    int it = 0;
+    do {
+        step(As0, As3, bw[0], bs[0], bw[3], bs[3], it);
+        step(As1, As0, bw[1], bs[1], bw[0], bs[0], it + 1);
+        step(As2, As1, bw[2], bs[2], bw[1], bs[1], it + 2);
+        step(As3, As2, bw[3], bs[3], bw[2], bs[2], it + 3);
+        it += 4;
+    } while (it < steps);
+    wait_loads<vmcnt_imm(0)>();  // the trailing out-of-range loads, before the workgroup ends
+
+    // Output: acc[a][t][r] is row m0 + 16a + 4g + r, column ncol[t].
+    if constexpr (SILU) {
+        const int ow = N >> 1;
+        if constexpr (NT % 2 == 0) {
+#pragma unroll
+            for (int u = 0; u < NT / 2; u++) {
+                const int cb = n0 + (wave * NT + 2 * u) * 16;
+                if (cb >= N) continue;
+#pragma unroll
+                for (int a = 0; a < MT; a++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int m = m0 + a * 16 + g * 4 + r;
+                        const float gv = (float)(f16)acc[a][2 * u][r], uv = (float)(f16)acc[a][2 * u + 1][r];
+                        if (m < M) Y[(size_t)m * ow + (cb >> 1) + j] = (f16)silu_mul(gv, uv);
+                    }
+            }
+        } else {
+            static_assert(NT == 1, "odd tile counts: one tile per wave");
+            // staged as f16 rows of 64 gate/up columns (+ 8 halves of padding); wave w's tile is
+            // columns 16w .. 16w + 15, so waves 2v and 2v + 1 hold gate and up of mid columns 16v ..
+            constexpr int LDW = 72;
+            static_assert(BM * LDW * 2 <= STAGE, "the staged tile fits one ring stage");
+            f16* st = reinterpret_cast<f16*>(As0);
+            lds_barrier();  // every wave's ring reads and loads are done
+#pragma unroll
+            for (int a = 0; a < MT; a++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) st[(a * 16 + g * 4 + r) * LDW + wave * 16 + j] = (f16)acc[a][0][r];
+            lds_barrier();
+#pragma unroll
+            for (int e = 0; e < BM / 8; e++) {
+                const int idx = e * 256 + tid, row = idx >> 5, mc = idx & 31, v = mc >> 4, jj = mc & 15;
+                const int m = m0 + row;
+                const float gv = (float)st[row * LDW + 32 * v + jj], uv = (float)st[row * LDW + 32 * v + 16 + jj];
+                if (m < M && n0 + 32 * v < N) Y[(size_t)m * ow + (n0 >> 1) + mc] = (f16)silu_mul(gv, uv);
+            }
+        }
+        return;
+    }
+    if constexpr (!PARTIAL) {
+#pragma unroll
+        for (int a = 0; a < MT; a++)
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + a * 16 + g * 4 + r;
+                    if (m < M && ncol[t] < N) Y[(size_t)m * N + ncol[t]] = (f16)acc[a][t][r];
+                }
+        return;
+    }
+    float* mine = part + (size_t)bz * M * N;
+#pragma unroll
+    for (int a = 0; a < MT; a++)
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + a * 16 + g * 4 + r;
+                if (m < M && ncol[t] < N) __builtin_nontemporal_store(acc[a][t][r], mine + (size_t)m * N + ncol[t]);
+            }
+}
+
 // The same product on v_mfma_f32_32x32x16_f16 (measured on MI355X: 2.2 PFLOP/s with 4 independent
 // accumulators per wave; the 16x16x32 form needs 16 to get close).  Prefill and batched questions
 // (f16 dequant).
@@ -668,8 +878,9 @@ struct Cfg {
     bool exact;
     GemmFn f16_out, part_out;
     bool wide;  // k_gemm_w4m (k steps of 64 in a ring of 4)
-    GemmFn silu_out;  // k_gemm_w4m with the SiLU * mul epilogue (wide configurations only)
+    GemmFn silu_out;  // the SiLU * mul epilogue (k_gemm_w4m and k_gemm_w4p configurations)
     int kh;           // k halves per workgroup (256 threads each)
+    bool pipe = false;  // k_gemm_w4p (loads three 128-k steps ahead; k steps per split a multiple of 4)
 };
 
 #define SD_CFG(MT, NT, EX) Cfg{MT, NT, EX, k_gemm_w4<MT, NT, EX, false>, k_gemm_w4<MT, NT, EX, true>, false, nullptr, 1}
@@ -679,6 +890,9 @@ struct Cfg {
 #define SD_CFGMH(MT2)                                                                                            \
     Cfg{2 * MT2, 2, false, k_gemm_w4m<MT2, 1, false, false, 2>, k_gemm_w4m<MT2, 1, true, false, 2>, true,        \
         k_gemm_w4m<MT2, 1, false, true, 2>, 2}
+#define SD_CFGP(MT, NT)                                                                                    \
+    Cfg{MT, NT, false, k_gemm_w4p<MT, NT, false>, k_gemm_w4p<MT, NT, true>, false,                          \
+        k_gemm_w4p<MT, NT, false, true>, 1, true}
 #define SD_CFGMH2(MT2)                                                                                           \
     Cfg{2 * MT2, 4, false, k_gemm_w4m<MT2, 2, false, false, 2>, k_gemm_w4m<MT2, 2, true, false, 2>, true,        \
         k_gemm_w4m<MT2, 2, false, true, 2>, 2}
@@ -694,11 +908,15 @@ const Cfg kCfgs[] = {
     SD_CFGMH(2), SD_CFGMH(4), SD_CFGMH(3),
     // two column tiles per wave with two k halves: (4,2), (2,2)
     SD_CFGMH2(4), SD_CFGMH2(2),
+    // 16x16 tiles with loads three steps ahead: (1,1), (2,1), (3,1), (4,1), (2,2), (3,2), (4,2), (1,2)
+    SD_CFGP(1, 1), SD_CFGP(2, 1), SD_CFGP(3, 1), SD_CFGP(4, 1), SD_CFGP(2, 2), SD_CFGP(3, 2), SD_CFGP(4, 2),
+    SD_CFGP(1, 2),
 };
 #undef SD_CFG
 #undef SD_CFGM
 #undef SD_CFGMH
 #undef SD_CFGMH2
+#undef SD_CFGP
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 int pick_cfg(int M, bool exact) {
@@ -722,11 +940,13 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
     // 256), the same with two k halves per workgroup (K a multiple of 512), and 16x16 tiles.
     constexpr int W21 = 18, W41 = 20, W31 = 21, W21h = 24, W31h = 26;
     constexpr int T21 = 3, T31 = 4, T41 = 5;  // 16x16 (2,1), (3,1), (4,1)
+    constexpr int P21 = 30, P31 = 31, P41 = 32;  // 16x16 (2,1), (3,1), (4,1), loads three steps ahead
     const bool wide_ok = K % 256 == 0, halves_ok = K % 512 == 0;
     auto fit = [&](GemmPlan q) {  // largest usable split <= q.ks
         const int steps = K / KSTEP;
         while (q.ks > 1 && (steps % q.ks || (size_t)q.ks * M * N > max_part_elems ||
-                            (kCfgs[q.cfg].wide && (K / 64 / q.ks) % (4 * kCfgs[q.cfg].kh))))
+                            (kCfgs[q.cfg].wide && (K / 64 / q.ks) % (4 * kCfgs[q.cfg].kh)) ||
+                            (kCfgs[q.cfg].pipe && (steps / q.ks) % 4)))
             q.ks /= 2;
         return q;
     };
@@ -760,13 +980,19 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
         return p;
     }
     if (!exact && wide_ok && M > 64 && M < 256) {
-        // Batched questions (M = 120): in_proj (N = 8256, f16 out) (2,1) with k halves 13.0 us;
-        // gate_up (N = 12288) the same 13.9 us; qkv (N = 5120, f16 out) 16x16 (3,1) 10.7 us; down
-        // (K = 6144) (2,1) with 8 splits 8.3 us; out_proj / o_proj 16x16 (2,1) with 4 splits 5.2 us.
-        if (!partial_ok) p.cfg = N >= 7000 ? (halves_ok ? W21h : W21) : T31;
+        // Batched questions (M = 120), chosen inside the 2B's question forward (whole-forward A/B on
+        // one box, one plan changed at a time; weights are cold there, unlike in a loop over one
+        // GEMM): the 16x16 tiles with loads three steps ahead for in_proj (N = 8256) and qkv
+        // (N = 5120), (3,1) (0.4 and 2 us per layer better than the 32x32 (2,1) with k halves and the
+        // 16x16 (3,1)); out_proj / o_proj (2,1) with 2 splits (0.8 us per layer better than 16x16
+        // (2,1) with 4); down (K = 6144) (4,1) with 4 splits (0.6 us better than 32x32 (2,1) with 8).
+        // gate_up (N = 12288, SiLU) stays on 32x32 (2,1) with k halves: every 16x16 plan was 1-2 us
+        // per layer slower there, though 5 us faster in a loop over the one GEMM.
+        const bool pipe_ok = K % 512 == 0;
+        if (!partial_ok) p.cfg = N >= 10000 || (N >= 7000 && !pipe_ok) ? (halves_ok ? W21h : W21) : pipe_ok ? P31 : T31;
         else if (N >= 10000) p = GemmPlan{W41, 2};
-        else if (K > 3000) p = GemmPlan{W21, 8};
-        else p = GemmPlan{T21, 4};
+        else if (K > 3000) p = pipe_ok && (K / KSTEP) % 16 == 0 ? GemmPlan{P41, 4} : GemmPlan{W21, 8};
+        else p = pipe_ok ? GemmPlan{P21, 2} : GemmPlan{T21, 4};
         return fit(p);
     }
     if (!exact && M > 64 && M < 256) p.cfg = partial_ok ? T41 : 4;
@@ -781,7 +1007,8 @@ int gemm_w4_split(int M, int N, int K, int cfg, int target_groups, size_t max_pa
     const int steps = K / KSTEP;
     int ks = 1;
     while (groups * ks < target_groups && ks < 8 && steps % (ks * 2) == 0 && steps / (ks * 2) >= 2 &&
-           (!c.wide || (steps / (ks * 2)) % (2 * c.kh) == 0) && (size_t)(ks * 2) * M * N <= max_part_elems)
+           (!c.wide || (steps / (ks * 2)) % (2 * c.kh) == 0) && (!c.pipe || (steps / (ks * 2)) % 4 == 0) &&
+           (size_t)(ks * 2) * M * N <= max_part_elems)
         ks *= 2;
     return ks;
 }
@@ -815,6 +1042,7 @@ void gemm_w4(const f16* A, const uint32_t* W, const f16* S, f16* Y, float* part,
     SD_CHECK(c.exact == exact, "gemm_w4: configuration does not match the dequant mode");
     SD_CHECK(ks >= 1 && (K / KSTEP) % ks == 0, "gemm_w4: split count must divide the k steps");
     SD_CHECK(part || (Y && ks == 1), "gemm_w4: split-K writes partials and needs a partial buffer");
+    SD_CHECK(!c.pipe || (K / KSTEP / ks) % 4 == 0, "gemm_w4: this configuration needs K / ks a multiple of 512");
     SD_CHECK(!c.wide || (K / 64 / ks) % (4 * c.kh) == 0,
              c.kh == 1 ? "gemm_w4: this configuration needs K / ks a multiple of 256"
                        : "gemm_w4: this configuration needs K / ks a multiple of 256 per k half");
@@ -828,10 +1056,11 @@ bool gemm_w4_has_silu(int cfg) { return cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg]
 
 void gemm_w4_silu(const f16* A, const uint32_t* W, const f16* S, f16* mid, int M, int N, int K, hipStream_t st,
                   int cfg, bool tiled) {
-    SD_CHECK(cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg].silu_out, "gemm_w4_silu: not a 32x32-tile configuration");
+    SD_CHECK(cfg >= 0 && cfg < kNumCfgs && kCfgs[cfg].silu_out, "gemm_w4_silu: no SiLU epilogue in this configuration");
     const Cfg& c = kCfgs[cfg];
-    SD_CHECK(M >= 1 && N >= 32 && N % 32 == 0 && K % (256 * c.kh) == 0,
-             "gemm_w4_silu: need N a multiple of 32 and K of 256 per k half");
+    SD_CHECK(M >= 1 && N >= 32 && N % 32 == 0 && K % ((c.pipe ? 512 : 256) * c.kh) == 0,
+             c.pipe ? "gemm_w4_silu: need N a multiple of 32 and K of 512"
+                    : "gemm_w4_silu: need N a multiple of 32 and K of 256 per k half");
     const int bm = c.mt * 16, bn = 4 * c.nt * 16;
     dim3 grid((N + bn - 1) / bn, (M + bm - 1) / bm, 1);
     launch_gemm(c.silu_out, grid, 256 * c.kh, st, A, W, S, mid, (float*)nullptr, M, N, K, 1, tiled);

@@ -80,9 +80,10 @@ def test_gemm_every_config(sdamd, synth, oracle):
                     if "no configuration" in str(e):
                         assert cfg >= 2 and ran > 0
                         return
-                    # f16-dequant configuration asked for f32 dequant (or the reverse), or a
-                    # 64-wide-step configuration given K / ks not a multiple of 256
-                    assert "does not match" in str(e) or "multiple of 256" in str(e)
+                    # f16-dequant configuration asked for f32 dequant (or the reverse), a
+                    # 64-wide-step configuration given K / ks not a multiple of 256, or a
+                    # three-steps-ahead one given K / ks not a multiple of 512
+                    assert "does not match" in str(e) or "multiple of 256" in str(e) or "multiple of 512" in str(e)
                     continue
                 check_gemm(oracle, A, W, S, Y, N, K, exact)
                 ran += 1
@@ -229,6 +230,8 @@ def split_sum(part, ks, M, N):
     (512, 2048, 6144, False, 20, 4),   # prefill down: (4,1) tiles, 4 splits
     (120, 2048, 6144, False, 18, 8),   # question down: (2,1) tiles, 8 splits
     (120, 2048, 2048, False, 3, 4),    # question out_proj: 16x16 (2,1), 4 splits
+    (120, 2048, 2048, False, 30, 4),   # the same, loads three steps ahead
+    (120, 2048, 6144, False, 32, 4),   # 16x16 (4,1) three steps ahead, 4 splits
     (8, 2048, 2048, True, -1, 2),      # GEMV partials
     (8, 2048, 6144, True, -1, 4),
     (20, 2048, 2048, True, -1, 1),
@@ -246,8 +249,9 @@ def test_split_partials(sdamd, synth, oracle, M, N, K, exact, cfg, ks):
     check_gemm(oracle, A, W, S, Y, N, K, exact)
 
 
-@pytest.mark.parametrize("M,exact", [(8, True), (17, True), (120, False), (512, False)])
-def test_gate_up_silu(sdamd, synth, oracle, M, exact):
+@pytest.mark.parametrize("M,exact,cfg", [(8, True, -1), (17, True, -1), (120, False, 24), (120, False, 30),
+                                         (120, False, 33), (200, False, 30), (512, False, 18)])
+def test_gate_up_silu(sdamd, synth, oracle, M, exact, cfg):
     """gate_up with silu * mul in the epilogue (the engine's fused form).  (1) Against silu_mul of the
     same kernel family's unfused gate_up output: within one f16 ulp (the epilogue itself).  (2)
     Against the oracle's gate_up then silu_mul: one f16 ulp of gate or up (the product's own
@@ -259,7 +263,7 @@ def test_gate_up_silu(sdamd, synth, oracle, M, exact):
     A, W, S = gemm_case(synth, rng, M, N, K)
     dA, dW, dS = dev(A), dev(W), dev(S)
     dmid = torch.empty(M * N, dtype=torch.uint8, device="cuda")
-    sdamd.op_gate_up_silu(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dmid.data_ptr(), M, N, K, exact)
+    sdamd.op_gate_up_silu(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dmid.data_ptr(), M, N, K, exact, cfg)
     torch.cuda.synchronize()
     got = host(dmid, np.float16, (M, N // 2)).astype(np.float32)
 
@@ -270,9 +274,9 @@ def test_gate_up_silu(sdamd, synth, oracle, M, exact):
         return oracle.h2f(mid)
 
     # the same kernel configuration without the epilogue: one f32 partial slot (ks = 1) rounded to
-    # f16 holds exactly the gate and up values the fused epilogue sees (GEMV rows, or the engine's
-    # (2,1) tiles with k halves at question sizes and without at prefill sizes)
-    cfg = -1 if exact else (24 if M < 256 else 18)
+    # f16 holds exactly the gate and up values the fused epilogue sees (GEMV rows, the 32x32 tiles
+    # (24: (2,1) with k halves, 18: (2,1)), the 16x16 three-steps-ahead tiles (30: (2,1), pairs
+    # meeting in LDS; 33: (2,2), pairs in one wave))
     dP = torch.empty(M * N * 4, dtype=torch.uint8, device="cuda")
     sdamd.op_matmul_split(dA.data_ptr(), dW.data_ptr(), dS.data_ptr(), dP.data_ptr(), M, N, K, exact, cfg, 1)
     torch.cuda.synchronize()
