@@ -148,6 +148,7 @@ void copy_batch(const CopyDesc* d, size_t n, hipStream_t st);
 //   row[r]   = local index i | first row of r's sequence << 16
 //   chunk[c] = first row | length << 16 of chunk c (chunks of <= 64 rows never cross sequences)
 //   seq[q]   = first chunk | chunk count << 16 of sequence q
+//   seq[SD_MAX_SEQS + q] = first row | row count << 16 of sequence q
 // The chunk and sequence counts are lu[4] and lu[5].
 constexpr int SD_MAX_SEQS = 32;  // sequences per forward
 struct Segs {

@@ -493,7 +493,7 @@ void Engine::ensure_pool(int l) {
     up.off_seg_row = up.off_rows + align256((size_t)cap * 4);
     up.off_seg_chunk = up.off_seg_row + align256((size_t)cap * 4);
     up.off_seg_seq = up.off_seg_chunk + align256((size_t)(cap / 64 + SD_MAX_SEQS) * 4);
-    up.up_bytes = up.off_seg_seq + align256((size_t)SD_MAX_SEQS * 4);
+    up.up_bytes = up.off_seg_seq + align256((size_t)SD_MAX_SEQS * 8);
     const size_t sizes[] = {
         up.up_bytes,                                   // upload block
         (size_t)cap * cfg.d * 4,                       // x
@@ -922,8 +922,9 @@ Plan& Engine::prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq
     uint32_t* chunkt = reinterpret_cast<uint32_t*>(up_h + pool.off_seg_chunk);
     uint32_t nch = 0;
     size_t s0 = 0;
-    std::vector<uint32_t> seqt(nseq);
+    std::vector<uint32_t> seqt(SD_MAX_SEQS + nseq);
     for (size_t q = 0; q < nseq; q++) {
+        seqt[SD_MAX_SEQS + q] = (uint32_t)s0 | (uint32_t)(lens[q] << 16);
         for (size_t i = 0; i < lens[q]; i++) rowt[s0 + i] = (uint32_t)i | (uint32_t)(s0 << 16);
         const uint32_t first = nch;
         for (size_t k = 0; k < lens[q]; k += 64)
@@ -932,8 +933,8 @@ Plan& Engine::prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq
         s0 += lens[q];
     }
     SD_CHECK((int)nch <= pool.seg_chunk_cap, "forward_batch: chunk table overflow");
-    std::memcpy(up_h + pool.off_seg_seq, seqt.data(), nseq * 4);
-    up_dirty = pool.off_seg_seq + nseq * 4;  // sent with the ids by upload()
+    std::memcpy(up_h + pool.off_seg_seq, seqt.data(), seqt.size() * 4);
+    up_dirty = pool.off_seg_seq + seqt.size() * 4;  // sent with the ids by upload()
     upload(ids, n, rows, n_rows, P, cache != nullptr, nch, (uint32_t)nseq, cache);
     restore(cache, P);
     return pl;

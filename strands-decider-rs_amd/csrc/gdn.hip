@@ -601,8 +601,8 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
                                                    size_t state_off, size_t hist_off) {
     constexpr int DK = 128, DV = 128;
     __shared__ float4 Qs[RTB][DK / 4], Ks[RTB][DK / 4];
-    __shared__ float Vs[RTB][16];
-    __shared__ float Bt[RTB], Dc[RTB], KQ[RTB];  // beta, decay and kn . qn per token
+    __shared__ float Vs[RTB][16], Os[RTB][16];
+    __shared__ float4 Tg[RTB];  // decay, beta and kn . qn of a token (one 16-byte read)
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int h = blockIdx.x, H = gridDim.x, q = blockIdx.z;
     if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
@@ -612,11 +612,10 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     const int cb = blockIdx.y * 16, cl = wv * 4 + (lane >> 4), col = cb + cl, l4 = lane & 15;
     auto srow = [&](int i) { return (i < 4 ? 0 : 60) + 4 * l4 + i; };
     int t0 = 0, t1 = L;
-    if (seqt) {
-        const int f = (int)(seqt[q] & 0xFFFFu), n = (int)(seqt[q] >> 16);
-        const uint32_t last = chunkt[f + n - 1];
-        t0 = (int)(chunkt[f] & 0xFFFFu);
-        t1 = (int)(last & 0xFFFFu) + (int)(last >> 16);
+    if (seqt) {  // the sequence's rows (one load; the chunk table would be a second, dependent one)
+        const uint32_t rr = seqt[SD_MAX_SEQS + q];
+        t0 = (int)(rr & 0xFFFFu);
+        t1 = t0 + (int)(rr >> 16);
     }
     const bool load = lu ? lu[3] != 0u : load_default != 0;
     const uint8_t* pre = lu_prefix(lu);
@@ -683,7 +682,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
                     Qs[tt][2 * j + u] = float4{q4.x * rq * qs, q4.y * rq * qs, q4.z * rq * qs, q4.w * rq * qs};
                     Ks[tt][2 * j + u] = float4{k4.x * rk, k4.y * rk, k4.z * rk, k4.w * rk};
                 }
-                if (j == 0) KQ[tt] = kq * rq * qs * rk;
+                if (j == 0) Tg[tt].z = kq * rq * qs * rk;
             }
         }
 #pragma unroll
@@ -692,10 +691,10 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
             if ((e >> 4) < nt) Vs[e >> 4][e & 15] = vr[it];
         }
         if (tid < nt) {
-            Bt[tid] = 1.0f / (1.0f + expf(-gb));
             const float x = ga + db;
             const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
-            Dc[tid] = expf(na * sp);
+            Tg[tid].x = expf(na * sp);
+            Tg[tid].y = 1.0f / (1.0f + expf(-gb));
         }
         __syncthreads();
         if (fresh) {
@@ -708,17 +707,14 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
         // A token's operands do not depend on the state: those of token tt + 1 are read from LDS
         // while token tt runs (the chain per token is then FMAs and DPP sums only).
         struct Tok {
-            float4 qa, qb, ka, kb;
-            float dc, bt, v, kq;
+            float4 qa, qb, ka, kb, gt;
+            float v;
         };
-        auto tok = [&](int tt) {
-            return Tok{Qs[tt][l4], Qs[tt][16 + l4], Ks[tt][l4], Ks[tt][16 + l4],
-                       Dc[tt],         Bt[tt],             Vs[tt][cl],     KQ[tt]};
-        };
+        auto tok = [&](int tt) { return Tok{Qs[tt][l4], Qs[tt][16 + l4], Ks[tt][l4], Ks[tt][16 + l4], Tg[tt], Vs[tt][cl]}; };
         auto run = [&](const Tok& x, int tt) {
             const float qn[8] = {x.qa.x, x.qa.y, x.qa.z, x.qa.w, x.qb.x, x.qb.y, x.qb.z, x.qb.w};
             const float kn[8] = {x.ka.x, x.ka.y, x.ka.z, x.ka.w, x.kb.x, x.kb.y, x.kb.z, x.kb.w};
-            const float dc = x.dc;
+            const float dc = x.gt.x;
             float sk = 0.f, sq = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -727,11 +723,11 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
             }
             sk = row_allsum16(sk);
             sq = row_allsum16(sq);
-            const float delta = (x.v - dc * sk) * x.bt;
-            const float oc = dc * sq + x.kq * delta;
+            const float delta = (x.v - dc * sk) * x.gt.y;
+            const float oc = dc * sq + x.gt.z * delta;
 #pragma unroll
             for (int i = 0; i < 8; i++) S[i] = dc * S[i] + kn[i] * delta;
-            if ((lane & 15) == 0) o[(size_t)(tb + tt) * sh.H * DV + h * DV + col] = oc;
+            if ((lane & 15) == 0) Os[tt][cl] = oc;
         };
         // two tokens per iteration, their operand sets alternating (no register copies)
         Tok ta = tok(0);
@@ -743,6 +739,13 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
             run(tb2, tt + 1);
         }
         if (tt < nt) run(ta, tt);
+        // the block's outputs leave as whole 64-byte rows (16 columns of a token)
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < RTB * 16 / 256; it++) {
+            const int e = it * 256 + tid, r = e >> 4;
+            if (r < nt) o[(size_t)(tb + r) * sh.H * DV + h * DV + cb + (e & 15)] = Os[r][e & 15];
+        }
     }
     if (seqt) return;  // several sequences: their final states are not kept
 #pragma unroll
