@@ -204,9 +204,11 @@ void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uin
 // The same recurrence token by token (the reference's own order), for short inputs: every
 // sequence starts from the prefix state as gdn_scan; with one sequence the final state is written
 // to `state` and hist (nullable) updated afterwards, as gdn_prep + gdn_scan do.
+// With cv.w set, q, k and v are the conv + SiLU of big's rows (qkvc unused; the history is read, so
+// hist must be null).
 void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
                float* state, const uint32_t* lu, int load_default, float* o, f16* hist, const Segs& sg, int nseq,
-               hipStream_t st, size_t state_off = 0, size_t hist_off = 0);
+               hipStream_t st, size_t state_off = 0, size_t hist_off = 0, const ConvIn& cv = ConvIn{});
 void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st);
 
 // ---- pointer head (head_gpu.hip) -------------------------------------------------------------

@@ -660,7 +660,15 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
             // conv and the delta rule read the prefix's history and state in place (from the snapshot
             // the lu block names, else the live arena) and write the live arena
             f16* hist_upd = nseq ? nullptr : W.hist;  // several sequences leave no history
-            if (recur) {
+            if (recur && nseq) {
+                // several sequences update no history: the recurrence computes the conv itself
+                const ConvIn cin{W.conv, W.hist, sg.row, W.hist_off};
+                steps.push_back({"gdn", [=](hipStream_t s) {
+                    gdn_recur(nullptr, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, nullptr, sg, nseq, s,
+                              W.state_off, W.hist_off, cin);
+                }});
+            } else if (recur) {
+                // one sequence: the conv reads the old history before the recurrence updates it
                 steps.push_back({"conv", [=](hipStream_t s) {
                     conv_silu(P.big, n, L, C, W.conv, W.hist, P.qkvc, sg, s, luv, W.hist_off);
                 }});

@@ -587,21 +587,36 @@ __device__ __forceinline__ float row_allsum16(float x) {
 // + 1e-6), beta = sigmoid(b), decay = exp(negA softplus(a + dt_bias)); per value column:
 // S *= decay; delta = (v - S^T kn) beta; S += kn delta; o = S^T qn (evaluated as below, with both
 // column sums taken from the previous state).
-// Workgroup (head, 16 value columns, sequence): wave w owns columns 16 y + 4 w + l / 16 and lane l
-// state rows 8 (l % 16) .. + 7, so every reduction over a column's 128 rows is one DPP row.  The
+// Workgroup (head, 32 value columns, sequence), 8 waves: wave w owns columns 32 y + 4 w + l / 16 and
+// lane l state rows 8 (l % 16) .. + 7, so every reduction over a column's 128 rows is one DPP row.  The
 // state stays in registers.  The inputs of up to 64 tokens are staged in LDS by the whole
 // workgroup with wide loads (their latency is paid once per block, not per token).
-constexpr int RTB = 64;  // tokens per LDS block
-__global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkvc, const f16* __restrict__ big,
+// CONV: q, k and v are the causal conv + SiLU of big's rows, computed here per block (the
+// reference's conv, src/kernels.rs:152-170; a sequence's first rows read the prefix's history): q
+// and k in a conv view (wave w takes the block's tokens 8w .. 8w + 7, lane l 4 channels of q or k,
+// so whether a row comes from big or from the history is wave-uniform) into LDS, over the Q/K
+// tiles; the 32 v columns one (token, 4 channels) per thread.  Otherwise they are read from qkvc.
+// Every workgroup of a head computes the head's q/k conv: 8 waves halve each one's share of it
+// (and of the norms), and a head takes 4 workgroups instead of 8.
+// With CONV the history is only read: the caller updates no history in the same launch.
+constexpr int RTB = 64;           // tokens per LDS block
+constexpr int RT = 512, RC = 32;  // threads and value columns per workgroup
+template <bool CONV>
+__global__ __launch_bounds__(RT) void k_gdn_recur(const float* __restrict__ qkvc, const f16* __restrict__ big,
                                                    GdnShape sh, const float* __restrict__ negA,
                                                    const float* __restrict__ dtb, float* __restrict__ state,
                                                    const uint32_t* __restrict__ lu, int load_default,
                                                    float* __restrict__ o, const uint32_t* __restrict__ chunkt,
                                                    const uint32_t* __restrict__ seqt, int L, f16* hist,
-                                                   size_t state_off, size_t hist_off) {
+                                                   size_t state_off, size_t hist_off, ConvIn cv) {
     constexpr int DK = 128, DV = 128;
-    __shared__ float4 Qs[RTB][DK / 4], Ks[RTB][DK / 4];
-    __shared__ float Vs[RTB][16], Os[RTB][16];
+    // Q and K tiles of a block; with CONV first the conv output of q and k, f32 [token][256]
+    __shared__ __attribute__((aligned(16))) float4 QKs[2 * RTB * DK / 4];
+    float4 (*const Qs)[DK / 4] = reinterpret_cast<float4 (*)[DK / 4]>(QKs);
+    float4 (*const Ks)[DK / 4] = reinterpret_cast<float4 (*)[DK / 4]>(QKs + RTB * DK / 4);
+    float* const X = reinterpret_cast<float*>(QKs);
+    __shared__ __attribute__((aligned(16))) float Vs[RTB][RC];
+    __shared__ float Os[RTB][RC];
     __shared__ float4 Tg[RTB];  // decay, beta and kn . qn of a token (one 16-byte read)
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int h = blockIdx.x, H = gridDim.x, q = blockIdx.z;
@@ -609,7 +624,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     // lane l of a 16-lane row owns state rows 4l .. 4l + 3 and 64 + 4l .. 64 + 4l + 3: its q and k
     // values are then float4 l and 16 + l of a token's row, so the 16 lanes of each read cover 256
     // contiguous bytes (every LDS bank once)
-    const int cb = blockIdx.y * 16, cl = wv * 4 + (lane >> 4), col = cb + cl, l4 = lane & 15;
+    const int cb = blockIdx.y * RC, cl = wv * 4 + (lane >> 4), col = cb + cl, l4 = lane & 15;
     auto srow = [&](int i) { return (i < 4 ? 0 : 60) + 4 * l4 + i; };
     int t0 = 0, t1 = L;
     if (seqt) {  // the sequence's rows (one load; the chunk table would be a second, dependent one)
@@ -634,35 +649,120 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
     bool fresh = !load;  // the state starts at zero: applied at the first token, after the block's loads
     const int C = sh.C;
     const float na = negA[h], db = dtb[h], qs = 1.0f / sqrtf((float)DK);
+    // conv views: lane l of the q/k view takes channels cg .. cg + 3 (matrix l / 32); thread (tv, vq)
+    // of the v view takes token tv of the block and channels vg .. vg + 3
+    const int cmat = lane >> 5, c4 = (lane & 31) * 4;
+    const int cg = (cmat == 0 ? h * DK : sh.H * DK + h * DK) + c4;
+    const int vq = tid & 7, tv = tid >> 3;
+    const int vg = 2 * sh.H * DK + h * DV + cb + 4 * vq;
+    float4 wk[4], wvt[4];
+    const f16* hsrc = nullptr;
+    if constexpr (CONV) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            wk[u] = *reinterpret_cast<const float4*>(cv.w + 4 * (cg + u));
+            wvt[u] = *reinterpret_cast<const float4*>(cv.w + 4 * (vg + u));
+        }
+        hsrc = pre ? reinterpret_cast<const f16*>(pre + cv.hist_off) : cv.hist;
+    }
     for (int tb = t0; tb < t1; tb += RTB) {
         const int nt = min(RTB, t1 - tb);
         lds_barrier();  // the previous block's LDS is consumed
         // q and k of a token: one DPP row of 16 lanes x 8 values, normalised on the way into LDS
         // (the sums over the row are one row_allsum16).  Every load of the block is issued before
         // the first is used.
-        constexpr int NIT = RTB * 16 / 256;  // tokens per wave-pass: 16 per workgroup
+        constexpr int NIT = RTB * 16 / RT;  // token passes: 32 tokens per pass of the workgroup
+        constexpr int NV = RTB * RC / RT;   // v values per thread
         float4 qr[NIT][2], kr[NIT][2];
-        float vr[RTB * 16 / 256];
-#pragma unroll
-        for (int it = 0; it < NIT; it++) {
-            const int e = it * 256 + tid, tt = e >> 4, j = e & 15;
-            const float* row = qkvc + (size_t)(tb + min(tt, nt - 1)) * C;  // tokens past the block: unused
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                qr[it][u] = *reinterpret_cast<const float4*>(row + h * DK + 8 * j + 4 * u);
-                kr[it][u] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + 8 * j + 4 * u);
-            }
-            vr[it] = row[2 * sh.H * DK + h * DV + cb + j];
-        }
+        float vr[NV];
         float ga, gb;  // the gate inputs of token tid (used for tid < nt)
-        {
+        if constexpr (CONV) {
+            // rows of the block by sequence index (rows past the sequence read its last row; the
+            // outputs they feed are never used); index < 0: the history
+            const int wvu = __builtin_amdgcn_readfirstlane(wv);
+            const int ib = tb - t0, ilast = t1 - t0 - 1;
+            const Rsrc rb = make_rsrc(big, (uint32_t)t1 * (uint32_t)sh.stride * 2u);
+            const Rsrc rh = make_rsrc(hsrc, 3u * (uint32_t)C * 2u);
+            f16x4 xr[11];
+#pragma unroll
+            for (int m = 0; m < 11; m++) {
+                const int ii = min(ib + 8 * wvu - 3 + m, ilast);
+                const bool fromh = ii < 0;
+                const uint32_t so = fromh ? (uint32_t)((ii + 3) * C) * 2u : (uint32_t)(t0 + ii) * (uint32_t)sh.stride * 2u;
+                xr[m] = __builtin_bit_cast(f16x4, buf_b64(fromh ? rh : rb, (uint32_t)cg * 2u, so));
+            }
+            f16x4 vx[4];
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int ii = min(ib + tv - 3 + m, ilast);
+                typedef __attribute__((address_space(1))) const f16x4 gf16x4;
+                const f16* src = ii < 0 ? hsrc + (size_t)(ii + 3) * C + vg : big + (size_t)(t0 + ii) * sh.stride + vg;
+                vx[m] = *(gf16x4*)src;  // a global load (a flat one would also count as an LDS operation)
+            }
+            {
+                const size_t gr = (size_t)(tb + min(tid, nt - 1)) * sh.stride + h;
+                ga = (float)big[gr + sh.a_off];
+                gb = (float)big[gr + sh.b_off];
+            }
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                float o4[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float kj[4] = {wk[u].x, wk[u].y, wk[u].z, wk[u].w};
+                    float a = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) a += kj[j] * (float)xr[t + j][u];
+                    o4[u] = silu(a);
+                }
+                *reinterpret_cast<float4*>(&X[(8 * wvu + t) * 256 + cmat * 128 + c4]) = float4{o4[0], o4[1], o4[2], o4[3]};
+            }
+            {
+                float o4[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float kj[4] = {wvt[u].x, wvt[u].y, wvt[u].z, wvt[u].w};
+                    float a = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) a += kj[j] * (float)vx[j][u];
+                    o4[u] = silu(a);
+                }
+                *reinterpret_cast<float4*>(&Vs[tv][4 * vq]) = float4{o4[0], o4[1], o4[2], o4[3]};
+            }
+            lds_barrier();
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                const int e = it * RT + tid, tt = e >> 4, j = e & 15;
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    qr[it][u] = *reinterpret_cast<const float4*>(&X[tt * 256 + 8 * j + 4 * u]);
+                    kr[it][u] = *reinterpret_cast<const float4*>(&X[tt * 256 + 128 + 8 * j + 4 * u]);
+                }
+            }
+            lds_barrier();  // X is read: the Q/K tiles overwrite it
+        } else {
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                const int e = it * RT + tid, tt = e >> 4, j = e & 15;
+                const float* row = qkvc + (size_t)(tb + min(tt, nt - 1)) * C;  // tokens past the block: unused
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    qr[it][u] = *reinterpret_cast<const float4*>(row + h * DK + 8 * j + 4 * u);
+                    kr[it][u] = *reinterpret_cast<const float4*>(row + sh.H * DK + h * DK + 8 * j + 4 * u);
+                }
+            }
+#pragma unroll
+            for (int it = 0; it < NV; it++) {
+                const int e = it * RT + tid;
+                vr[it] = qkvc[(size_t)(tb + min(e / RC, nt - 1)) * C + 2 * sh.H * DK + h * DV + cb + e % RC];
+            }
             const size_t gr = (size_t)(tb + min(tid, nt - 1)) * sh.stride + h;
             ga = (float)big[gr + sh.a_off];
             gb = (float)big[gr + sh.b_off];
         }
 #pragma unroll
         for (int it = 0; it < NIT; it++) {
-            const int e = it * 256 + tid, tt = e >> 4, j = e & 15;
+            const int e = it * RT + tid, tt = e >> 4, j = e & 15;
             float sq = 0.f, sk = 0.f, kq = 0.f;
 #pragma unroll
             for (int u = 0; u < 2; u++) {
@@ -685,10 +785,12 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
                 if (j == 0) Tg[tt].z = kq * rq * qs * rk;
             }
         }
+        if constexpr (!CONV) {
 #pragma unroll
-        for (int it = 0; it < RTB * 16 / 256; it++) {
-            const int e = it * 256 + tid;
-            if ((e >> 4) < nt) Vs[e >> 4][e & 15] = vr[it];
+            for (int it = 0; it < NV; it++) {
+                const int e = it * RT + tid;
+                if (e / RC < nt) Vs[e / RC][e % RC] = vr[it];
+            }
         }
         if (tid < nt) {
             const float x = ga + db;
@@ -739,12 +841,12 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
             run(tb2, tt + 1);
         }
         if (tt < nt) run(ta, tt);
-        // the block's outputs leave as whole 64-byte rows (16 columns of a token)
+        // the block's outputs leave as whole 128-byte rows (32 columns of a token)
         __syncthreads();
 #pragma unroll
-        for (int it = 0; it < RTB * 16 / 256; it++) {
-            const int e = it * 256 + tid, r = e >> 4;
-            if (r < nt) o[(size_t)(tb + r) * sh.H * DV + h * DV + cb + (e & 15)] = Os[r][e & 15];
+        for (int it = 0; it < RTB * RC / RT; it++) {
+            const int e = it * RT + tid, r = e / RC;
+            if (r < nt) o[(size_t)(tb + r) * sh.H * DV + h * DV + cb + e % RC] = Os[r][e % RC];
         }
     }
     if (seqt) return;  // several sequences: their final states are not kept
@@ -756,7 +858,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float* __restrict__ qkv
         const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
         const int nb = gridDim.x * gridDim.y, per = (C + nb - 1) / nb, bi = blockIdx.y * H + h;
         const int lo = bi * per, hi = min(C, lo + per);
-        for (int ch = lo + tid; ch < hi; ch += 256) {
+        for (int ch = lo + tid; ch < hi; ch += RT) {
             f16 hv[3];
 #pragma unroll
             for (int r = 0; r < 3; r++) {
@@ -1052,12 +1154,18 @@ void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uin
 
 void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
                float* state, const uint32_t* lu, int load_default, float* o, f16* hist, const Segs& sg, int nseq,
-               hipStream_t st, size_t state_off, size_t hist_off) {
+               hipStream_t st, size_t state_off, size_t hist_off, const ConvIn& cv) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     SD_CHECK(!sg.seq || (lu && sg.chunk && !hist), "gdn_recur: several sequences need lu and keep no history");
+    SD_CHECK(!cv.w || (cv.hist && !hist), "gdn_recur: the conv needs the history, and updates none");
+    SD_CHECK(!cv.w || (s.C % 4 == 0 && s.stride % 4 == 0), "gdn_recur: channels and row stride must be multiples of 4");
     if (!sg.seq) nseq = 1;
-    hipLaunchKernelGGL(k_gdn_recur, dim3(s.H, s.DV / 16, nseq), dim3(256), 0, st, qkvc, big, s, negA, dtb, state, lu,
-                       load_default, o, sg.chunk, sg.seq, L, hist, state_off, hist_off);
+    if (cv.w)
+        hipLaunchKernelGGL(k_gdn_recur<true>, dim3(s.H, s.DV / RC, nseq), dim3(RT), 0, st, qkvc, big, s, negA, dtb, state,
+                           lu, load_default, o, sg.chunk, sg.seq, L, hist, state_off, hist_off, cv);
+    else
+        hipLaunchKernelGGL(k_gdn_recur<false>, dim3(s.H, s.DV / RC, nseq), dim3(RT), 0, st, qkvc, big, s, negA, dtb,
+                           state, lu, load_default, o, sg.chunk, sg.seq, L, hist, state_off, hist_off, cv);
     launched("gdn_recur");
 }
 
