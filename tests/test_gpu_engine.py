@@ -100,10 +100,13 @@ def test_profile_labels(tiny):
     assert all(ms >= 0 for _, ms in prof)
 
 
-@pytest.mark.parametrize("lens", [(40, 25, 70, 64, 129), (5, 12, 20), (33,)])
+@pytest.mark.parametrize("lens", [(40, 25, 70, 64, 129), (5, 12, 20), (33,), (100, 24, 30)])
 def test_forward_batch_matches_separate_forwards(tiny, lens):
     """Independent sequences in one forward == each sequence's own forward from the snapshot
-    (conv history, GDN state, RoPE positions and attention masks per sequence)."""
+    (conv history, GDN state, RoPE positions and attention masks per sequence).  Batches of at most
+    64 tokens per sequence on average take the token-by-token delta rule with the conv inside it;
+    (100, 24, 30) gives it a sequence of two 64-token blocks, whose second block's conv reads the
+    first block's rows."""
     eng, head, om = tiny
     state = ids_for(20, 150)
     seqs = [ids_for(30 + i, n) for i, n in enumerate(lens)]
