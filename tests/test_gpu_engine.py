@@ -128,6 +128,28 @@ def test_forward_batch_matches_separate_forwards(tiny, lens):
     prefix.free()
 
 
+def test_forward_batch_random_mixes(tiny):
+    """Seeded random batches (1 to 6 sequences of 21 to 90 tokens, or of 1 to 20) from one snapshot
+    against each sequence's own forward.  The batch and its parts run different plans: the chunked or
+    the token-by-token delta rule (with the conv inside it) by average length, the question-size or
+    prefill GEMM tiles by total rows, the short-row GEMV below 21 rows."""
+    eng, head, om = tiny
+    rng = np.random.default_rng(77)
+    prefix = eng.forward(ids_for(60, 90), [], keep=True).snapshot
+    for case in range(8):
+        nseq = int(rng.integers(1, 7))
+        lo, hi = (1, 21) if case == 7 else (21, 91)
+        lens = [int(rng.integers(lo, hi)) for _ in range(nseq)]
+        seqs = [ids_for(1000 + 10 * case + i, n) for i, n in enumerate(lens)]
+        rows = [sorted({0, n // 2, n - 1}) for n in lens]
+        got, _ = eng.forward_batch(seqs, rows, cache=prefix)
+        for q, r, g in zip(seqs, rows, got):
+            want = eng.forward(q, r, cache=prefix).hidden
+            err = np.abs(g - want).max()
+            assert err < HIDDEN_TOL, f"case {case}, lens {lens}: max |dh| {err} vs the separate forward"
+    prefix.free()
+
+
 def test_forward_batch_without_prefix(tiny):
     eng, head, om = tiny
     seqs = [ids_for(40, 50), ids_for(41, 90)]
