@@ -59,15 +59,17 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
     const size_t row = rows ? rows[r] : (size_t)r;
     float* xr = x + row * d;
     auto col = [&](int i) { return VEC ? (int)threadIdx.x * D + i : (int)threadIdx.x + 256 * i; };
-    float v[D];
+    float v[D], wv[D];
     float part[D][KS > 0 ? KS : 1];
-    // issue every load of the row before using any
+    // issue every load of the row (and the norm weights) before using any
     if constexpr (VEC) {
 #pragma unroll
         for (int i = 0; i < D; i += 4) {
             const int c = col(i);
             const float4 x4 = *reinterpret_cast<const float4*>(xr + c);
+            const float4 w4 = *reinterpret_cast<const float4*>(w + c);
             v[i] = x4.x, v[i + 1] = x4.y, v[i + 2] = x4.z, v[i + 3] = x4.w;
+            wv[i] = w4.x, wv[i + 1] = w4.y, wv[i + 2] = w4.z, wv[i + 3] = w4.w;
             if constexpr (KS > 0) {
 #pragma unroll
                 for (int z = 0; z < KS; z++) {
@@ -84,6 +86,7 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
         for (int i = 0; i < D; i++) {
             const int c = col(i);
             v[i] = xr[c];
+            wv[i] = w[c];
             if constexpr (KS > 0) {
 #pragma unroll
                 for (int z = 0; z < KS; z++) part[i][z] = yp[z * slot + row * d + c];
@@ -120,16 +123,15 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
+    lds_barrier();  // not __syncthreads, which would also wait for the x stores above
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / sqrtf(tot / (float)d + 1e-6f);
     if constexpr (VEC) {
 #pragma unroll
         for (int i = 0; i < D; i += 4) {
             const int c = col(i);
-            const float4 w4 = *reinterpret_cast<const float4*>(w + c);
-            const float o0 = v[i] * inv * w4.x, o1 = v[i + 1] * inv * w4.y, o2 = v[i + 2] * inv * w4.z,
-                        o3 = v[i + 3] * inv * w4.w;
+            const float o0 = v[i] * inv * wv[i], o1 = v[i + 1] * inv * wv[i + 1], o2 = v[i + 2] * inv * wv[i + 2],
+                        o3 = v[i + 3] * inv * wv[i + 3];
             if (h16) {
                 const f16x4 o4 = {(f16)o0, (f16)o1, (f16)o2, (f16)o3};
                 *reinterpret_cast<f16x4*>(h16 + (size_t)r * d + c) = o4;
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(256) void k_add_norm(float* __restrict__ x, const f
 #pragma unroll
         for (int i = 0; i < D; i++) {
             const int c = col(i);
-            const float o = v[i] * inv * w[c];
+            const float o = v[i] * inv * wv[i];
             if (h16) h16[(size_t)r * d + c] = (f16)o;
             else h32[(size_t)r * d + c] = o;
         }

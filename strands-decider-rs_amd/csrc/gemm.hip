@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
             bcur[t] = bnext[t];
             scur[t] = snext[t];
         }
-        __syncthreads();  // Anext is complete and Acur is no longer read
+        lds_barrier();  // Anext is complete and Acur is no longer read (the loads ahead stay in flight)
     };
 
     load_a(step0);
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
     }
     store_a(As0);
     if (steps > 1) load_a(step0 + 1);
-    __syncthreads();
+    lds_barrier();
     for (int it = 0; it < steps; it += 2) {
         step(As0, As1, it);
         if (it + 1 < steps) step(As1, As0, it + 1);
