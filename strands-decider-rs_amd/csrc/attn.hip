@@ -18,11 +18,15 @@ namespace {
 
 constexpr int BQ = 16;  // queries per workgroup
 
+// Kernel arguments: what the prologue needs first, and the head shape as ints, lead (the first 16
+// dwords are preloaded into SGPRs, up to the first struct argument).
 template <int HD>
-__global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, AttnShape s, const float* __restrict__ qw,
-                                                 const float* __restrict__ kw, const float* __restrict__ rope, int L,
-                                                 const uint32_t* __restrict__ lu, const uint32_t* __restrict__ rowt,
+__global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, const uint32_t* __restrict__ lu, int L,
+                                                 int HQ, int HK, int RD, int stride, int ctx,
+                                                 const uint32_t* __restrict__ rowt, const float* __restrict__ qw,
+                                                 const float* __restrict__ kw, const float* __restrict__ rope,
                                                  f16* __restrict__ Q, f16* __restrict__ Kc, f16* __restrict__ Vc) {
+    const AttnShape s{HQ, HK, HD, RD, stride, ctx};
     // Workgroup (4 rows, one q or kv head): wave w takes row w, lane l the 4 dimensions 4l..4l+3
     // (8-byte loads and stores, the norm a wave reduction).  A kv head also writes the 4 rows of
     // V^T, dimension by dimension: 8 contiguous bytes per dimension.
@@ -117,10 +121,11 @@ __device__ __forceinline__ float wave_sum16(float v) {
 // and write unnormalised (acc, max, sum) for k_attn_combine.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f16* __restrict__ Kc,
-                                              const f16* __restrict__ Vt, const f16* __restrict__ big, AttnShape s,
-                                              int L, const uint32_t* __restrict__ lu,
-                                              const uint32_t* __restrict__ rowt, f16* __restrict__ out,
-                                              float* __restrict__ pacc, float* __restrict__ pml, int ks) {
+                                              const f16* __restrict__ Vt, const uint32_t* __restrict__ lu, int L,
+                                              int HQ, int HK, int stride, int ctx, int ks,
+                                              const uint32_t* __restrict__ rowt, const f16* __restrict__ big,
+                                              f16* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml) {
+    const AttnShape s{HQ, HK, HD, 0, stride, ctx};
     static_assert(HD == 256, "attention is written for 256-wide heads");
     constexpr int ND = HD / 16;   // 16 output dimension tiles
     constexpr int NS = HD / 32;   // 8 k steps over the head dimension
@@ -292,8 +297,9 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
 
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ pacc, const float* __restrict__ pml,
-                                                     const f16* __restrict__ big, AttnShape s, int L, int ks,
-                                                     f16* __restrict__ out) {
+                                                     const f16* __restrict__ big, f16* __restrict__ out, int L, int ks,
+                                                     int HQ, int stride) {
+    const AttnShape s{HQ, 0, HD, 0, stride, 0};
     const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
     float m = -INFINITY;
     for (int z = 0; z < ks; z++) {
@@ -322,8 +328,8 @@ void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* k
     SD_CHECK(s.RD % 2 == 0 && s.RD <= s.HD, "attention: bad rotary_dim");
     SD_CHECK(s.RD % 8 == 0 && s.stride % 4 == 0, "attention: rotary_dim must be a multiple of 8, the row stride of 4");
     SD_CHECK(s.ctx % 32 == 0, "attention: the cache length must be a multiple of 32");
-    hipLaunchKernelGGL(k_qk_prep<256>, dim3((L + 3) / 4, s.HQ + s.HK), dim3(256), 0, st, big, s, qw, kw, rope, L, lu,
-                       sg.row, Q, Kc, Vc);
+    hipLaunchKernelGGL(k_qk_prep<256>, dim3((L + 3) / 4, s.HQ + s.HK), dim3(256), 0, st, big, lu, L, s.HQ, s.HK, s.RD,
+                       s.stride, s.ctx, sg.row, qw, kw, rope, Q, Kc, Vc);
     launched("qk_prep");
 }
 
@@ -336,11 +342,12 @@ void attention_split(const f16* Q, const f16* Kc, const f16* Vc, const f16* big,
     const int nb = (L + BQ - 1) / BQ;
     float* pacc = ws;
     float* pml = ws + (size_t)ks * L * s.HQ * s.HD;
-    hipLaunchKernelGGL(k_attn<256>, dim3(nb, s.HQ, ks), dim3(256), 0, st, Q, Kc, Vc, big, s, L, lu, sg.row, out, pacc,
-                       pml, ks);
+    hipLaunchKernelGGL(k_attn<256>, dim3(nb, s.HQ, ks), dim3(256), 0, st, Q, Kc, Vc, lu, L, s.HQ, s.HK, s.stride, s.ctx,
+                       ks, sg.row, big, out, pacc, pml);
     launched("attn");
     if (ks > 1) {
-        hipLaunchKernelGGL(k_attn_combine<256>, dim3(L, s.HQ), dim3(256), 0, st, pacc, pml, big, s, L, ks, out);
+        hipLaunchKernelGGL(k_attn_combine<256>, dim3(L, s.HQ), dim3(256), 0, st, pacc, pml, big, out, L, ks, s.HQ,
+                           s.stride);
         launched("attn_combine");
     }
 }

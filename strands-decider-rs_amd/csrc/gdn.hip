@@ -168,10 +168,12 @@ constexpr int PREP_T = 512;  // k_gdn_prep threads: 8 waves
 // src/kernels.rs:152-170: rows before a sequence's start from the history, the prefix snapshot's when
 // lu names one); otherwise they are read from qkvc.
 template <bool CONV>
-__global__ __launch_bounds__(PREP_T) void k_gdn_prep(const float* __restrict__ qkvc, const f16* __restrict__ big,
-                                                  GdnShape sh, const float* __restrict__ negA,
-                                                  const float* __restrict__ dtb, int L, GdnWs ws, ConvIn cv,
-                                                  const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu) {
+// Kernel arguments: the pointers and ints first, the structs last (the first 16 dwords are preloaded
+// into SGPRs, up to the first struct; the prologue needs the tables and big before anything else).
+__global__ __launch_bounds__(PREP_T) void k_gdn_prep(const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu,
+                                                  const f16* __restrict__ big, const float* __restrict__ qkvc,
+                                                  const float* __restrict__ negA, const float* __restrict__ dtb, int L,
+                                                  GdnShape sh, GdnWs ws, ConvIn cv) {
     constexpr int DK = 128, DV = 128;
     constexpr int RP = DK + 8;  // f16 row pitch of the Q/K row tiles
     constexpr int FP = CH + 4;  // fp32 pitch of T and of the Qk staging
@@ -602,13 +604,13 @@ __device__ __forceinline__ float row_allsum16(float x) {
 constexpr int RTB = 64;           // tokens per LDS block
 constexpr int RT = 512, RC = 32;  // threads and value columns per workgroup
 template <bool CONV>
-__global__ __launch_bounds__(RT) void k_gdn_recur(const float* __restrict__ qkvc, const f16* __restrict__ big,
-                                                   GdnShape sh, const float* __restrict__ negA,
-                                                   const float* __restrict__ dtb, float* __restrict__ state,
-                                                   const uint32_t* __restrict__ lu, int load_default,
-                                                   float* __restrict__ o, const uint32_t* __restrict__ chunkt,
-                                                   const uint32_t* __restrict__ seqt, int L, f16* hist,
-                                                   size_t state_off, size_t hist_off, ConvIn cv) {
+__global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ lu, const uint32_t* __restrict__ seqt,
+                                                   float* __restrict__ state, const f16* __restrict__ big,
+                                                   const float* __restrict__ qkvc, int L, int load_default,
+                                                   size_t state_off, const float* __restrict__ negA,
+                                                   const float* __restrict__ dtb, float* __restrict__ o,
+                                                   const uint32_t* __restrict__ chunkt, f16* hist, size_t hist_off,
+                                                   GdnShape sh, ConvIn cv) {
     constexpr int DK = 128, DV = 128;
     // Q and K tiles of a block; with CONV first the conv output of q and k, f32 [token][256]
     __shared__ __attribute__((aligned(16))) float4 QKs[2 * RTB * DK / 4];
@@ -873,11 +875,11 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const float* __restrict__ qkvc
 
 // Sequential over chunks for one head and 16 value columns; wave w owns rows 16w..16w+15 of the
 // chunk (and state rows 32w..32w+31 for the update).
-__global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, float* __restrict__ state,
-                                                  const uint32_t* __restrict__ lu, int load_default,
-                                                  float* __restrict__ o, const uint32_t* __restrict__ chunkt,
-                                                  const uint32_t* __restrict__ seqt, size_t state_off,
-                                                  const f16* __restrict__ big, f16* hist, size_t hist_off) {
+__global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ lu, const uint32_t* __restrict__ seqt,
+                                                  const uint32_t* __restrict__ chunkt, float* __restrict__ state,
+                                                  int L, int load_default, size_t state_off, float* __restrict__ o,
+                                                  const f16* __restrict__ big, f16* hist, size_t hist_off, GdnShape sh,
+                                                  GdnWs ws) {
     constexpr int DK = 128, DV = 128;
     constexpr int SP = DK + 4, VP = CH + 4;
     __shared__ __attribute__((aligned(16))) float St[DVS * SP];  // S^T: [column][k]
@@ -1075,8 +1077,9 @@ __global__ __launch_bounds__(256) void k_gdn_scan(GdnShape sh, int L, GdnWs ws, 
 
 // out[t, h*DV + c] = f16(w[c] o rsqrt(mean(o^2) + 1e-6) silu(z)); one wave per (t, h), DV = 128.
 __global__ __launch_bounds__(256) void k_gnorm(const float* __restrict__ o, const f16* __restrict__ big,
-                                               GdnShape sh, const float* __restrict__ w, int L,
-                                               f16* __restrict__ out) {
+                                               const float* __restrict__ w, f16* __restrict__ out, int L, int H,
+                                               int DV, int stride, int z_off) {
+    const struct { int H, DV, stride, z_off; } sh{H, DV, stride, z_off};
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= L * sh.H) return;
@@ -1135,9 +1138,9 @@ void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float*
     if (!sg.chunk) nch = (L + CH - 1) / CH;
     const dim3 grid(nch, s.H, 2);
     if (cv.w)
-        hipLaunchKernelGGL(k_gdn_prep<true>, grid, dim3(PREP_T), 0, st, qkvc, big, s, negA, dtb, L, ws, cv, sg.chunk, lu);
+        hipLaunchKernelGGL(k_gdn_prep<true>, grid, dim3(PREP_T), 0, st, sg.chunk, lu, big, qkvc, negA, dtb, L, s, ws, cv);
     else
-        hipLaunchKernelGGL(k_gdn_prep<false>, grid, dim3(PREP_T), 0, st, qkvc, big, s, negA, dtb, L, ws, cv, sg.chunk, lu);
+        hipLaunchKernelGGL(k_gdn_prep<false>, grid, dim3(PREP_T), 0, st, sg.chunk, lu, big, qkvc, negA, dtb, L, s, ws, cv);
     launched("gdn_prep");
 }
 
@@ -1147,8 +1150,8 @@ void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uin
     SD_CHECK(!sg.seq || (lu && sg.chunk), "gdn_scan: several sequences need lu and the chunk table");
     SD_CHECK(!hist || (!sg.seq && big), "gdn_scan: the history update needs one sequence and big");
     if (!sg.seq) nseq = 1;
-    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(256), 0, st, s, L, ws, state, lu, load_default, o,
-                       sg.chunk, sg.seq, state_off, big, hist, hist_off);
+    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(256), 0, st, lu, sg.seq, sg.chunk, state, L,
+                       load_default, state_off, o, big, hist, hist_off, s, ws);
     launched("gdn_scan");
 }
 
@@ -1161,11 +1164,11 @@ void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float
     SD_CHECK(!cv.w || (s.C % 4 == 0 && s.stride % 4 == 0), "gdn_recur: channels and row stride must be multiples of 4");
     if (!sg.seq) nseq = 1;
     if (cv.w)
-        hipLaunchKernelGGL(k_gdn_recur<true>, dim3(s.H, s.DV / RC, nseq), dim3(RT), 0, st, qkvc, big, s, negA, dtb, state,
-                           lu, load_default, o, sg.chunk, sg.seq, L, hist, state_off, hist_off, cv);
+        hipLaunchKernelGGL(k_gdn_recur<true>, dim3(s.H, s.DV / RC, nseq), dim3(RT), 0, st, lu, sg.seq, state, big, qkvc,
+                           L, load_default, state_off, negA, dtb, o, sg.chunk, hist, hist_off, s, cv);
     else
-        hipLaunchKernelGGL(k_gdn_recur<false>, dim3(s.H, s.DV / RC, nseq), dim3(RT), 0, st, qkvc, big, s, negA, dtb,
-                           state, lu, load_default, o, sg.chunk, sg.seq, L, hist, state_off, hist_off, cv);
+        hipLaunchKernelGGL(k_gdn_recur<false>, dim3(s.H, s.DV / RC, nseq), dim3(RT), 0, st, lu, sg.seq, state, big, qkvc,
+                           L, load_default, state_off, negA, dtb, o, sg.chunk, hist, hist_off, s, cv);
     launched("gdn_recur");
 }
 
@@ -1173,7 +1176,7 @@ void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, in
     SD_CHECK(s.DV == 128, "gnorm: only 128-wide value heads are supported");
     SD_CHECK(s.stride % 2 == 0 && s.z_off % 2 == 0, "gnorm: gate row stride and offset must be even");
     const int rows = L * s.H;
-    hipLaunchKernelGGL(k_gnorm, dim3((rows + 3) / 4), dim3(256), 0, st, o, big, s, w, L, out);
+    hipLaunchKernelGGL(k_gnorm, dim3((rows + 3) / 4), dim3(256), 0, st, o, big, w, out, L, s.H, s.DV, s.stride, s.z_off);
     launched("gnorm");
 }
 
