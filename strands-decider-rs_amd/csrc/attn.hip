@@ -12,11 +12,13 @@
 #include <cmath>
 
 #include "common.h"
+#include "device.h"
 
 namespace sd {
 namespace {
 
 constexpr int BQ = 16;  // queries per workgroup
+constexpr int ATTN_KS_MAX = 8;  // key splits the workspace and k_attn_combine provide for
 
 // Kernel arguments: what the prologue needs first, and the head shape as ints, lead (the first 16
 // dwords are preloaded into SGPRs, up to the first struct argument).
@@ -135,6 +137,7 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int fq = lane & 15, fg = lane >> 4;
     const int P = (int)lu[1];
+    SGPR_BATCH("s"(P), "s"(rowt), "s"(big), "s"(out), "s"(pacc), "s"(pml));
     const int t0 = blockIdx.x * 16, h = blockIdx.y, z = blockIdx.z;
     const int kh = h / (s.HQ / s.HK);
     const int nq = min(16, L - t0);
@@ -301,22 +304,29 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ p
                                                      int HQ, int stride) {
     const AttnShape s{HQ, 0, HD, 0, stride, 0};
     const int t = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-    float m = -INFINITY;
-    for (int z = 0; z < ks; z++) {
-        const size_t r = ((size_t)z * L + t) * s.HQ + h;
-        if (pml[r * 2 + 1] > 0.f) m = fmaxf(m, pml[r * 2]);
-    }
-    float l = 0.f, a = 0.f;
-    for (int z = 0; z < ks; z++) {
-        const size_t r = ((size_t)z * L + t) * s.HQ + h;
-        const float lz = pml[r * 2 + 1];
-        if (lz > 0.f) {
-            const float f = exp2_fast(pml[r * 2] - m);
-            l += lz * f;
-            a += pacc[r * HD + d] * f;
-        }
+    // Every load is issued up front and unconditionally (splits past ks re-read the last one and are
+    // then skipped), so none waits behind a branch or another load; the sums run in split order.
+    float mz[ATTN_KS_MAX], lz[ATTN_KS_MAX], az[ATTN_KS_MAX];
+#pragma unroll
+    for (int z = 0; z < ATTN_KS_MAX; z++) {
+        const size_t r = ((size_t)min(z, ks - 1) * L + t) * s.HQ + h;
+        mz[z] = pml[r * 2];
+        lz[z] = pml[r * 2 + 1];
+        az[z] = pacc[r * HD + d];
     }
     const float g = (float)big[(size_t)t * s.stride + h * 2 * HD + HD + d];
+    float m = -INFINITY;
+#pragma unroll
+    for (int z = 0; z < ATTN_KS_MAX; z++)
+        if (z < ks && lz[z] > 0.f) m = fmaxf(m, mz[z]);
+    float l = 0.f, a = 0.f;
+#pragma unroll
+    for (int z = 0; z < ATTN_KS_MAX; z++)
+        if (z < ks && lz[z] > 0.f) {
+            const float f = exp2_fast(mz[z] - m);
+            l += lz[z] * f;
+            a += az[z] * f;
+        }
     out[(size_t)t * s.HQ * HD + h * HD + d] = (f16)(a / l / (1.0f + expf(-g)));
 }
 
@@ -334,11 +344,12 @@ void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* k
 }
 
 // Workspace (floats) the key-split path needs for up to `rows` query rows.
-size_t attn_ws_floats(int rows, const AttnShape& s) { return (size_t)8 * rows * s.HQ * (s.HD + 2); }
+size_t attn_ws_floats(int rows, const AttnShape& s) { return (size_t)ATTN_KS_MAX * rows * s.HQ * (s.HD + 2); }
 
 void attention_split(const f16* Q, const f16* Kc, const f16* Vc, const f16* big, const AttnShape& s, int L,
                      const uint32_t* lu, const Segs& sg, int ks, float* ws, f16* out, hipStream_t st) {
     SD_CHECK(s.HD == 256 && s.HQ % s.HK == 0, "attention: unsupported head shape");
+    SD_CHECK(ks >= 1 && ks <= ATTN_KS_MAX, "attention: 1 to 8 key splits");
     const int nb = (L + BQ - 1) / BQ;
     float* pacc = ws;
     float* pml = ws + (size_t)ks * L * s.HQ * s.HD;

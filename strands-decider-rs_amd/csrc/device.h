@@ -101,6 +101,13 @@ __device__ __forceinline__ void bar_noflush() { asm volatile("s_barrier" ::: "me
 // not waited for, unlike __syncthreads).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// SGPR_BATCH("s"(x), "s"(y), ...): x, y, ... are in SGPRs at this point.  The scalar loads that
+// produce them (kernel arguments past the preloaded ones, lu fields, table entries) are then issued
+// as one batch and waited for together, one memory round trip, where the compiler would sink each
+// load to its first use, behind branches, and wait for each in turn (scalar loads return out of
+// order, so every wait is for all of them).
+#define SGPR_BATCH(...) asm volatile("" ::__VA_ARGS__)
+
 // XCD-aware tile order of a (gx column blocks, gy row blocks, gz K splits) grid: the hardware gives
 // workgroup b to XCD b % 8, and each XCD has its own L2.  With a K split (gz in {2, 4, 8}) XCD x
 // takes split x % gz and a contiguous run of the column-block-major (column, row) tiles, so it reads

@@ -198,11 +198,23 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const uint32_t* __restrict_
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int fr = lane & 15, fg = lane >> 4;  // fragment row (column) / k group of this lane
-    const int c = blockIdx.x, h = blockIdx.y, H = gridDim.y;
+    const int c = blockIdx.x, h = blockIdx.y, H = sh.H;
     const bool qside = blockIdx.z != 0;  // role 1
-    if (chunkt && c >= (int)lu[4]) return;  // the grid is sized for the most chunks L can split into
-    const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
-    const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - t0);
+    // The lu fields and the chunk's entry in one batch of scalar loads, issued before any branch:
+    // the pointers are selected first, with `big` standing in for a null table (values then unused).
+    const uint32_t* lp = lu ? lu : reinterpret_cast<const uint32_t*>(big);
+    const uint32_t* cp = chunkt ? chunkt + c : lp;
+    const uint32_t lu_chunks = lp[4], ce = *cp;
+    const uint8_t* const lu_pre = *reinterpret_cast<const uint8_t* const*>(lp + 8);
+    SGPR_BATCH("s"(lu_chunks), "s"(ce), "s"(lu_pre), "s"(H), "s"(sh.C), "s"(sh.stride), "s"(sh.a_off), "s"(sh.b_off),
+               "s"(sh.z_off), "s"(ws.wf), "s"(ws.qgf), "s"(ws.qkf), "s"(ws.kgf), "s"(ws.u), "s"(ws.gl), "s"(cv.w),
+               "s"(cv.hist), "s"(cv.rowt), "s"(cv.hist_off), "s"(negA), "s"(dtb));
+    if (chunkt && c >= (int)lu_chunks) return;  // the grid is sized for the most chunks L can split into
+    const int t0 = chunkt ? (int)(ce & 0xFFFFu) : c * CH;
+    const int Lc = chunkt ? (int)(ce >> 16) : min(CH, L - t0);
+    // negA[h] and dtb[h] as vector loads (a scalar load would be waited for at the first LDS barrier)
+    const float na = __builtin_bit_cast(float, buf_b32(make_rsrc(negA, (uint32_t)H * 4u), (uint32_t)h * 4u, 0u));
+    const float db = __builtin_bit_cast(float, buf_b32(make_rsrc(dtb, (uint32_t)H * 4u), (uint32_t)h * 4u, 0u));
     const int C = sh.C;
     const size_t slot = (size_t)c * H + h;
     f16* Wf = ws.wf + slot * WF_H;
@@ -264,7 +276,7 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const uint32_t* __restrict_
         for (int u = 0; u < 4; u++) wk[u] = *reinterpret_cast<const float4*>(cv.w + 4 * (cg + u));
         const uint32_t rt0 = cv.rowt ? cv.rowt[t0] : (uint32_t)t0;  // index in the sequence | start row << 16
         const int i0 = (int)(rt0 & 0xFFFFu), s0 = (int)(rt0 >> 16);
-        const uint8_t* pre = lu_prefix(lu);
+        const uint8_t* pre = lu ? lu_pre : nullptr;
         const f16* hsrc = pre ? reinterpret_cast<const f16*>(pre + cv.hist_off) : cv.hist;
         const Rsrc rb = make_rsrc(big, (uint32_t)(s0 + i0 + Lc) * (uint32_t)sh.stride * 2u);
         const Rsrc rh = make_rsrc(hsrc, 3u * (uint32_t)C * 2u);
@@ -318,9 +330,9 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const uint32_t* __restrict_
         if (i < Lc) {
             const float a = (float)ga16, bb = (float)gb16;
             b = 1.0f / (1.0f + expf(-bb));
-            const float x = a + dtb[h];
+            const float x = a + db;
             const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
-            gl = negA[h] * sp;
+            gl = na * sp;
         }
         float sc = gl;  // inclusive prefix sum over the 64 lanes of wave 0
 #pragma unroll
@@ -621,21 +633,29 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     __shared__ float Os[RTB][RC];
     __shared__ float4 Tg[RTB];  // decay, beta and kn . qn of a token (one 16-byte read)
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int h = blockIdx.x, H = gridDim.x, q = blockIdx.z;
-    if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
+    const int h = blockIdx.x, H = sh.H, q = blockIdx.z;
+    // The lu fields and the sequence's row range in one batch of scalar loads, issued before any
+    // branch (a load behind one waits for the loads the branch needs): the pointers are selected
+    // first, with `state` standing in for a null table (values then unused).
+    const uint32_t* lp = lu ? lu : reinterpret_cast<const uint32_t*>(state);
+    const uint32_t* sp = seqt ? seqt + SD_MAX_SEQS + q : lp;
+    const uint32_t lu_nseq = lp[5], lu_load = lp[3], rr = *sp;
+    const uint8_t* const lu_pre = *reinterpret_cast<const uint8_t* const*>(lp + 8);
+    SGPR_BATCH("s"(lu_nseq), "s"(lu_load), "s"(rr), "s"(lu_pre), "s"(sh.H), "s"(sh.C), "s"(sh.stride), "s"(sh.a_off),
+               "s"(sh.b_off), "s"(negA), "s"(dtb), "s"(o), "s"(cv.w), "s"(cv.hist), "s"(cv.hist_off));
+    if (seqt && q >= (int)lu_nseq) return;  // the grid is sized for the most sequences
     // lane l of a 16-lane row owns state rows 4l .. 4l + 3 and 64 + 4l .. 64 + 4l + 3: its q and k
     // values are then float4 l and 16 + l of a token's row, so the 16 lanes of each read cover 256
     // contiguous bytes (every LDS bank once)
     const int cb = blockIdx.y * RC, cl = wv * 4 + (lane >> 4), col = cb + cl, l4 = lane & 15;
     auto srow = [&](int i) { return (i < 4 ? 0 : 60) + 4 * l4 + i; };
     int t0 = 0, t1 = L;
-    if (seqt) {  // the sequence's rows (one load; the chunk table would be a second, dependent one)
-        const uint32_t rr = seqt[SD_MAX_SEQS + q];
+    if (seqt) {  // the sequence's rows (the chunk table would be a second, dependent load)
         t0 = (int)(rr & 0xFFFFu);
         t1 = t0 + (int)(rr >> 16);
     }
-    const bool load = lu ? lu[3] != 0u : load_default != 0;
-    const uint8_t* pre = lu_prefix(lu);
+    const bool load = lu ? lu_load != 0u : load_default != 0;
+    const uint8_t* pre = lu ? lu_pre : nullptr;
     float* Sg = state + (size_t)h * DK * DV;  // the live state (written back by a single sequence)
     const float* S0 = (pre ? reinterpret_cast<const float*>(pre + state_off) : state) + (size_t)h * DK * DV;
     // Every global load below is unconditional (indices clamped, values zeroed after they arrive): a
@@ -650,7 +670,11 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     }
     bool fresh = !load;  // the state starts at zero: applied at the first token, after the block's loads
     const int C = sh.C;
-    const float na = negA[h], db = dtb[h], qs = 1.0f / sqrtf((float)DK);
+    // negA[h] and dtb[h] as vector loads: a scalar load would be waited for at the block's first LDS
+    // barrier (s_waitcnt lgkmcnt(0)), and they are needed only after the block's inputs arrive
+    const float na = __builtin_bit_cast(float, buf_b32(make_rsrc(negA, (uint32_t)H * 4u), (uint32_t)h * 4u, 0u));
+    const float db = __builtin_bit_cast(float, buf_b32(make_rsrc(dtb, (uint32_t)H * 4u), (uint32_t)h * 4u, 0u));
+    const float qs = 1.0f / sqrtf((float)DK);
     // conv views: lane l of the q/k view takes channels cg .. cg + 3 (matrix l / 32); thread (tv, vq)
     // of the v view takes token tv of the block and channels vg .. vg + 3
     const int cmat = lane >> 5, c4 = (lane & 31) * 4;
@@ -858,7 +882,7 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     // the last 3 rows of (the prefix's history ++ this forward's rows) into the live history
     if (hist) {
         const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
-        const int nb = gridDim.x * gridDim.y, per = (C + nb - 1) / nb, bi = blockIdx.y * H + h;
+        const int nb = H * (DV / RC), per = (C + nb - 1) / nb, bi = blockIdx.y * H + h;
         const int lo = bi * per, hi = min(C, lo + per);
         for (int ch = lo + tid; ch < hi; ch += RT) {
             f16 hv[3];
@@ -886,22 +910,44 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
     __shared__ __attribute__((aligned(16))) float Vt[DVS * VP];  // V'^T: [column][token]
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fr = lane & 15, fg = lane >> 4;
-    const int h = blockIdx.x, sl = blockIdx.y, H = gridDim.x, q = blockIdx.z;
-    if (seqt && q >= (int)lu[5]) return;  // the grid is sized for the most sequences
+    const int h = blockIdx.x, sl = blockIdx.y, H = sh.H, q = blockIdx.z;
+    // The lu fields and the sequence's chunk range in one batch of scalar loads, issued before any
+    // branch: the pointers are selected first, with `state` standing in for a null table (values
+    // then unused).
+    const uint32_t* lp = lu ? lu : reinterpret_cast<const uint32_t*>(state);
+    const uint32_t* sp = seqt ? seqt + q : lp;
+    const uint32_t lu_nseq = lp[5], lu_load = lp[3], se = *sp;
+    const uint8_t* const lu_pre = *reinterpret_cast<const uint8_t* const*>(lp + 8);
+    SGPR_BATCH("s"(lu_nseq), "s"(lu_load), "s"(se), "s"(lu_pre), "s"(hist), "s"(hist_off));
+    if (seqt && q >= (int)lu_nseq) return;  // the grid is sized for the most sequences
     const int c0 = sl * DVS;
-    const bool load = lu ? lu[3] != 0u : load_default != 0;
-    const uint8_t* pre = lu_prefix(lu);
+    const bool load = lu ? lu_load != 0u : load_default != 0;
+    const uint8_t* pre = lu ? lu_pre : nullptr;
     float* Sg = state + (size_t)h * DK * DV;  // the live state (written back by a single sequence)
     const float* S0 = (pre ? reinterpret_cast<const float*>(pre + state_off) : state) + (size_t)h * DK * DV;
-    for (int e = tid; e < DK * DVS; e += 256) {
-        const int k = e / DVS, cc = e % DVS;
-        St[cc * SP + k] = load ? S0[k * DV + c0 + cc] : 0.f;
+    {
+        // The slice through a buffer resource, every load issued before the first LDS store (a load
+        // under a branch, or a flat one, would be waited for before the next is issued); a fresh
+        // state gets an empty resource, whose loads return 0 without touching memory.
+        static_assert(DK * DVS % 256 == 0, "whole passes of the workgroup");
+        const Rsrc rs = make_rsrc(S0, load ? (uint32_t)(DK * DV * 4) : 0u);
+        float sv[DK * DVS / 256];
+#pragma unroll
+        for (int i = 0; i < DK * DVS / 256; i++) {
+            const int e = tid + 256 * i, k = e / DVS, cc = e % DVS;
+            sv[i] = __builtin_bit_cast(float, buf_b32(rs, (uint32_t)((k * DV + c0 + cc) * 4), 0u));
+        }
+#pragma unroll
+        for (int i = 0; i < DK * DVS / 256; i++) {
+            const int e = tid + 256 * i, k = e / DVS, cc = e % DVS;
+            St[cc * SP + k] = sv[i];
+        }
     }
     // the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's history
     // ++ this forward's rows) become the live history, each workgroup on a slice of the channels;
     // here, after the prep that read the old history for its conv.  This thread's channel lo + tid
     // is loaded now, before any store, and stored at the end (a longer slice loops there).
-    const int hC = sh.C, hnb = gridDim.x * gridDim.y, hper = (hC + hnb - 1) / hnb;
+    const int hC = sh.C, hnb = H * (DV / DVS), hper = (hC + hnb - 1) / hnb;
     const int hlo = (blockIdx.y * H + h) * hper, hhi = min(hC, hlo + hper);
     const f16* hold = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
     f16 hv[3] = {};
@@ -912,8 +958,8 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
             hv[r] = src >= 0 ? big[(size_t)src * sh.stride + hlo + tid] : hold[(size_t)(src + 3) * hC + hlo + tid];
         }
     }
-    const int cfirst = seqt ? (int)(seqt[q] & 0xFFFFu) : 0;
-    const int cend = seqt ? cfirst + (int)(seqt[q] >> 16) : (L + CH - 1) / CH;
+    const int cfirst = seqt ? (int)(se & 0xFFFFu) : 0;
+    const int cend = seqt ? cfirst + (int)(se >> 16) : (L + CH - 1) / CH;
     // A chunk's operands (prep's output, not written here) are loaded ahead of their use: W, Qg and
     // U of chunk c + 1 into a second register set when chunk c starts, its Qk, Kg and e^(G_last)
     // once chunk c has used its own, so the load latency overlaps a chunk's MFMA work instead of

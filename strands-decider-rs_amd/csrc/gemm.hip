@@ -51,10 +51,10 @@ constexpr int LDA = KSTEP + SD_LDA_PAD;  // LDS row stride in halves
 template <int MT, int NT, bool EXACT, bool PARTIAL>
 __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, const uint32_t* __restrict__ W,
                                                  const f16* __restrict__ S, f16* __restrict__ Y,
-                                                 float* __restrict__ part, int M, int N, int K, int ksplit,
-                                                 int tiled) {
+                                                 float* __restrict__ part, int M, int N, int K, int ks_tiled) {
     constexpr int BM = MT * 16;
     constexpr int BN = 4 * NT * 16;
+    const int ksplit = ks_tiled >> 1, tiled = ks_tiled & 1;
     constexpr int ACH = BM * 16 / 256;  // 16-byte A chunks per thread per macro step (== MT)
     // Double-buffered A tile: two separate arrays so that the compiler can see that the stores of
     // the next tile never alias the fragment reads of the current one.
@@ -64,8 +64,10 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
     int bx, by, bz;
-    xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), gridDim.x, gridDim.y, gridDim.z, bx, by,
-             bz);
+    // the launch grid (ceil(N / BN), ceil(M / BM), ksplit) from the arguments, not from the dispatch
+    // packet's grid size (one more scalar load before the first weight load could be issued)
+    xcd_tile(blockIdx.x + (N + BN - 1) / BN * (blockIdx.y + (M + BM - 1) / BM * blockIdx.z), (N + BN - 1) / BN,
+             (M + BM - 1) / BM, ksplit, bx, by, bz);
     const int m0 = by * BM, n0 = bx * BN;
     const int KB = K >> 5;
     const int steps_total = K / KSTEP;
@@ -238,9 +240,10 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const f16* __restrict__ A, cons
 template <int MT, int NT, bool PARTIAL, bool SILU = false>
 __global__ __launch_bounds__(256) void k_gemm_w4p(const f16* __restrict__ A, const uint32_t* __restrict__ W,
                                                   const f16* __restrict__ S, f16* __restrict__ Y,
-                                                  float* __restrict__ part, int M, int N, int K, int ksplit,
-                                                  int tiled) {
+                                                  float* __restrict__ part, int M, int N, int K, int ks_tiled) {
     constexpr int BM = MT * 16;
+    constexpr int BN = 4 * NT * 16;
+    const int ksplit = ks_tiled >> 1, tiled = ks_tiled & 1;
     constexpr int STAGE = BM * 256;           // bytes of one A stage (128 k of BM rows)
     constexpr int NLD = MT;                   // direct-to-LDS loads per thread per step
     constexpr int PER_STEP = NLD + 2 * NT;    // vector-memory loads a thread issues per step
@@ -254,9 +257,11 @@ __global__ __launch_bounds__(256) void k_gemm_w4p(const f16* __restrict__ A, con
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
     int bx, by, bz;
-    xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), gridDim.x, gridDim.y, gridDim.z, bx, by,
-             bz);
-    const int m0 = by * BM, n0 = bx * (4 * NT * 16);
+    // the launch grid (ceil(N / BN), ceil(M / BM), ksplit) from the arguments, not from the dispatch
+    // packet's grid size (one more scalar load before the first weight load could be issued)
+    xcd_tile(blockIdx.x + (N + BN - 1) / BN * (blockIdx.y + (M + BM - 1) / BM * blockIdx.z), (N + BN - 1) / BN,
+             (M + BM - 1) / BM, ksplit, bx, by, bz);
+    const int m0 = by * BM, n0 = bx * BN;
     const int KB = K >> 5;
     const int steps = K / KSTEP / ksplit;  // a multiple of 4 (checked by the launcher)
     const int step0 = bz * steps;
@@ -466,9 +471,11 @@ __global__ __launch_bounds__(256) void k_gemm_w4p(const f16* __restrict__ A, con
 template <int MT2, int NT2, bool PARTIAL, bool SILU = false, int KH = 1>
 __global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgpu_waves_per_eu(2))) void k_gemm_w4m(
     const f16* __restrict__ A, const uint32_t* __restrict__ W, const f16* __restrict__ S, f16* __restrict__ Y,
-    float* __restrict__ part, int M, int N, int K, int ksplit, int tiled) {
+    float* __restrict__ part, int M, int N, int K, int ks_tiled) {
     constexpr int KS = 64;                   // k per step
     constexpr int BM = MT2 * 32;
+    constexpr int BN = 4 * NT2 * 32;
+    const int ksplit = ks_tiled >> 1, tiled = ks_tiled & 1;
     constexpr int STAGE = BM * KS * 2;       // bytes of one A stage
     constexpr int NLD = BM / 32;             // direct-to-LDS loads per thread per step
     constexpr int PER_STEP = NLD + 2 * NT2;  // vector-memory loads a thread issues per step
@@ -491,9 +498,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256 * KH, 256 * KH), amdgp
     uint8_t* const R2 = As2 + kh * STAGE;
     uint8_t* const R3 = As3 + kh * STAGE;
     int bx, by, bz;
-    xcd_tile(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), gridDim.x, gridDim.y, gridDim.z, bx, by,
-             bz);
-    const int m0 = by * BM, n0 = bx * (4 * NT2 * 32);
+    // the launch grid (ceil(N / BN), ceil(M / BM), ksplit) from the arguments, not from the dispatch
+    // packet's grid size (one more scalar load before the first weight load could be issued)
+    xcd_tile(blockIdx.x + (N + BN - 1) / BN * (blockIdx.y + (M + BM - 1) / BM * blockIdx.z), (N + BN - 1) / BN,
+             (M + BM - 1) / BM, ksplit, bx, by, bz);
+    const int m0 = by * BM, n0 = bx * BN;
     const int KB = K >> 5;
     const int steps = (K / KS) / ksplit / KH;  // a multiple of 4 (checked by the launcher)
     const int step0 = (bz * KH + kh) * steps;
@@ -872,7 +881,9 @@ __global__ void k_reduce_partials(const float* __restrict__ part, int ks, size_t
     }
 }
 
-typedef void (*GemmFn)(const f16*, const uint32_t*, const f16*, f16*, float*, int, int, int, int, int);
+// Kernel arguments: A, W, S, Y, part, M, N, K, split count << 1 | tiled layout (14 dwords, all of
+// them preloaded into SGPRs before the waves start).
+typedef void (*GemmFn)(const f16*, const uint32_t*, const f16*, f16*, float*, int, int, int, int);
 struct Cfg {
     int mt, nt;
     bool exact;
@@ -1018,14 +1029,13 @@ namespace {
 // and end (see KernelEvents).
 void launch_gemm(GemmFn kern, dim3 grid, int threads, hipStream_t st, const f16* A, const uint32_t* W, const f16* S,
                  f16* Y, float* part, int M, int N, int K, int ks, bool tiled) {
-    const int tl = tiled ? 1 : 0;
+    const int kt = ks << 1 | (tiled ? 1 : 0);
     KernelEvents* ke = kernel_events();
     if (ke && ke->launches == 0) {
-        hipExtLaunchKernelGGL(kern, grid, dim3(threads), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, ks,
-                              tl);
+        hipExtLaunchKernelGGL(kern, grid, dim3(threads), 0, st, ke->start, ke->stop, 0u, A, W, S, Y, part, M, N, K, kt);
         ke->launches++;
     } else {
-        hipLaunchKernelGGL(kern, grid, dim3(threads), 0, st, A, W, S, Y, part, M, N, K, ks, tl);
+        hipLaunchKernelGGL(kern, grid, dim3(threads), 0, st, A, W, S, Y, part, M, N, K, kt);
     }
 }
 }  // namespace
