@@ -632,6 +632,8 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     __shared__ __attribute__((aligned(16))) float Vs[RTB][RC];
     __shared__ float Os[RTB][RC];
     __shared__ float4 Tg[RTB];  // decay, beta and kn . qn of a token (one 16-byte read)
+    __shared__ float4 Wt[64 + RC / 4][4];  // CONV: the taps of the q/k view's 64 lane groups, then the v view's 8
+    __shared__ float Ss[DK][RC + 1];      // the state slice on its way into the token loop's registers
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int h = blockIdx.x, H = sh.H, q = blockIdx.z;
     // The lu fields and the sequence's row range in one batch of scalar loads, issued before any
@@ -660,14 +662,23 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     const float* S0 = (pre ? reinterpret_cast<const float*>(pre + state_off) : state) + (size_t)h * DK * DV;
     // Every global load below is unconditional (indices clamped, values zeroed after they arrive): a
     // load under a branch makes the wave wait for it before it issues the next.
-    // The state is read through a buffer resource: a flat load (the prefix or live pointer is not
-    // known to be global) would also count as an LDS operation and hold up the first LDS barrier.
-    float S[8];
+    // The state slice (128 rows x 32 columns) in 16-byte loads, two per thread, through a buffer
+    // resource (a flat load, the prefix or live pointer not being known to be global, would also
+    // count as an LDS operation and hold up the first LDS barrier); it reaches the token loop's
+    // register layout through LDS with the first block's inputs.  One 4-byte load per register
+    // would be 4x the vector-memory instructions, which the workgroup's prologue is bound by.
+    // (The 16 bytes are reinterpreted as a whole: a bit_cast of one element of the loaded vector
+    // compiles to a 4-byte load of element 0 with this compiler.)
+    float4 sl[2];
     {
         const Rsrc rs = make_rsrc(S0, (uint32_t)(DK * DV * 4));
 #pragma unroll
-        for (int i = 0; i < 8; i++) S[i] = __builtin_bit_cast(float, buf_b32(rs, (uint32_t)((srow(i) * DV + col) * 4), 0u));
+        for (int j = 0; j < 2; j++) {
+            const int e = tid + RT * j;
+            sl[j] = __builtin_bit_cast(float4, buf_b128(rs, (uint32_t)(((e >> 3) * DV + cb + 4 * (e & 7)) * 4), 0u));
+        }
     }
+    float S[8];
     bool fresh = !load;  // the state starts at zero: applied at the first token, after the block's loads
     const int C = sh.C;
     // negA[h] and dtb[h] as vector loads: a scalar load would be waited for at the block's first LDS
@@ -681,19 +692,21 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     const int cg = (cmat == 0 ? h * DK : sh.H * DK + h * DK) + c4;
     const int vq = tid & 7, tv = tid >> 3;
     const int vg = 2 * sh.H * DK + h * DV + cb + 4 * vq;
-    float4 wk[4], wvt[4];
+    // CONV: the taps the views use (72 groups of 4 channels x 4 taps, 4.5 KB) are loaded once per
+    // workgroup, one float4 per thread (threads past 287 re-read the last), and shared through LDS;
+    // every lane loading its own 8 float4 was 64 KB of vector-memory traffic per workgroup
+    float4 wk[4], wvt[4], tap = {};
     const f16* hsrc = nullptr;
     if constexpr (CONV) {
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            wk[u] = *reinterpret_cast<const float4*>(cv.w + 4 * (cg + u));
-            wvt[u] = *reinterpret_cast<const float4*>(cv.w + 4 * (vg + u));
-        }
+        const int g = min(tid >> 2, 64 + RC / 4 - 1), p = tid & 3;
+        const int ch = g < 64 ? ((g >> 5) == 0 ? h * DK : sh.H * DK + h * DK) + (g & 31) * 4 + p
+                              : 2 * sh.H * DK + h * DV + cb + 4 * (g - 64) + p;
+        tap = *reinterpret_cast<const float4*>(cv.w + 4 * ch);
         hsrc = pre ? reinterpret_cast<const f16*>(pre + cv.hist_off) : cv.hist;
     }
     for (int tb = t0; tb < t1; tb += RTB) {
         const int nt = min(RTB, t1 - tb);
-        lds_barrier();  // the previous block's LDS is consumed
+        if (tb != t0) lds_barrier();  // the previous block's LDS is consumed
         // q and k of a token: one DPP row of 16 lanes x 8 values, normalised on the way into LDS
         // (the sums over the row are one row_allsum16).  Every load of the block is issued before
         // the first is used.
@@ -729,6 +742,15 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
                 const size_t gr = (size_t)(tb + min(tid, nt - 1)) * sh.stride + h;
                 ga = (float)big[gr + sh.a_off];
                 gb = (float)big[gr + sh.b_off];
+            }
+            if (tb == t0) {  // the taps into LDS, then into the registers of both views
+                if (tid < (64 + RC / 4) * 4) Wt[tid >> 2][tid & 3] = tap;
+                lds_barrier();
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    wk[u] = Wt[lane][u];  // the q/k view's group of lane l is l
+                    wvt[u] = Wt[64 + vq][u];
+                }
             }
 #pragma unroll
             for (int t = 0; t < 8; t++) {
@@ -824,7 +846,19 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
             Tg[tid].x = expf(na * sp);
             Tg[tid].y = 1.0f / (1.0f + expf(-gb));
         }
+        if (tb == t0) {  // the state slice: Ss[row][c] = S0[row][cb + c]
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int e = tid + RT * j, r = e >> 3, c = 4 * (e & 7);
+#pragma unroll
+                for (int k = 0; k < 4; k++) Ss[r][c + k] = k == 0 ? sl[j].x : k == 1 ? sl[j].y : k == 2 ? sl[j].z : sl[j].w;
+            }
+        }
         __syncthreads();
+        if (tb == t0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) S[i] = Ss[srow(i)][cl];
+        }
         if (fresh) {
 #pragma unroll
             for (int i = 0; i < 8; i++) S[i] = 0.f;
