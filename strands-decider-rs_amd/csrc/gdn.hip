@@ -683,8 +683,12 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     const int C = sh.C;
     // negA[h] and dtb[h] as vector loads: a scalar load would be waited for at the block's first LDS
     // barrier (s_waitcnt lgkmcnt(0)), and they are needed only after the block's inputs arrive
-    const float na = __builtin_bit_cast(float, buf_b32(make_rsrc(negA, (uint32_t)H * 4u), (uint32_t)h * 4u, 0u));
-    const float db = __builtin_bit_cast(float, buf_b32(make_rsrc(dtb, (uint32_t)H * 4u), (uint32_t)h * 4u, 0u));
+    // (wave 0 only: the gates are computed for tokens tid < 64)
+    float na = 0.f, db = 0.f;
+    if (__builtin_amdgcn_readfirstlane(wv) == 0) {
+        na = __builtin_bit_cast(float, buf_b32(make_rsrc(negA, (uint32_t)H * 4u), (uint32_t)h * 4u, 0u));
+        db = __builtin_bit_cast(float, buf_b32(make_rsrc(dtb, (uint32_t)H * 4u), (uint32_t)h * 4u, 0u));
+    }
     const float qs = 1.0f / sqrtf((float)DK);
     // conv views: lane l of the q/k view takes channels cg .. cg + 3 (matrix l / 32); thread (tv, vq)
     // of the v view takes token tv of the block and channels vg .. vg + 3
@@ -714,7 +718,8 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
         constexpr int NV = RTB * RC / RT;   // v values per thread
         float4 qr[NIT][2], kr[NIT][2];
         float vr[NV];
-        float ga, gb;  // the gate inputs of token tid (used for tid < nt)
+        f16 ga = 0, gb = 0;  // the gate inputs of token tid (used for tid < nt; converted there, so that
+                             // no wait for the loads follows them)
         if constexpr (CONV) {
             // rows of the block by sequence index (rows past the sequence read its last row; the
             // outputs they feed are never used); index < 0: the history
@@ -730,18 +735,24 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
                 const uint32_t so = fromh ? (uint32_t)((ii + 3) * C) * 2u : (uint32_t)(t0 + ii) * (uint32_t)sh.stride * 2u;
                 xr[m] = __builtin_bit_cast(f16x4, buf_b64(fromh ? rh : rb, (uint32_t)cg * 2u, so));
             }
-            f16x4 vx[4];
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const int ii = min(ib + tv - 3 + m, ilast);
-                typedef __attribute__((address_space(1))) const f16x4 gf16x4;
+            // the v view: each thread loads its own token's row, the threads of the block's first 3
+            // tokens also the row 3 before (the history at a sequence start); the conv reads its 4 rows
+            // from LDS (Vr, over Os, which only the token loop writes) after the barrier.  Global loads
+            // (a flat one would also count as an LDS operation).
+            typedef __attribute__((address_space(1))) const f16x4 gf16x4;
+            f16x4 (*const Vr)[RC / 4] = reinterpret_cast<f16x4 (*)[RC / 4]>(&Os[0][0]);
+            const f16x4 vown = *(gf16x4*)(big + (size_t)(t0 + min(ib + tv, ilast)) * sh.stride + vg);
+            f16x4 vprev = {};
+            if (tv < 3) {
+                const int ii = min(ib + tv - 3, ilast);
                 const f16* src = ii < 0 ? hsrc + (size_t)(ii + 3) * C + vg : big + (size_t)(t0 + ii) * sh.stride + vg;
-                vx[m] = *(gf16x4*)src;  // a global load (a flat one would also count as an LDS operation)
+                vprev = *(gf16x4*)src;
             }
-            {
+            {  // the gate inputs of token tid (used for tid < nt <= 64; under a branch, the wave would
+               // wait for them there)
                 const size_t gr = (size_t)(tb + min(tid, nt - 1)) * sh.stride + h;
-                ga = (float)big[gr + sh.a_off];
-                gb = (float)big[gr + sh.b_off];
+                ga = big[gr + sh.a_off];
+                gb = big[gr + sh.b_off];
             }
             if (tb == t0) {  // the taps into LDS, then into the registers of both views
                 if (tid < (64 + RC / 4) * 4) Wt[tid >> 2][tid & 3] = tap;
@@ -765,7 +776,13 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
                 }
                 *reinterpret_cast<float4*>(&X[(8 * wvu + t) * 256 + cmat * 128 + c4]) = float4{o4[0], o4[1], o4[2], o4[3]};
             }
+            Vr[tv + 3][vq] = vown;  // Vr row i: token i - 3 of the block
+            if (tv < 3) Vr[tv][vq] = vprev;
+            lds_barrier();
             {
+                f16x4 vx[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) vx[j] = Vr[tv + j][vq];
                 float o4[4];
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
@@ -777,7 +794,6 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
                 }
                 *reinterpret_cast<float4*>(&Vs[tv][4 * vq]) = float4{o4[0], o4[1], o4[2], o4[3]};
             }
-            lds_barrier();
 #pragma unroll
             for (int it = 0; it < NIT; it++) {
                 const int e = it * RT + tid, tt = e >> 4, j = e & 15;
@@ -805,8 +821,8 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
                 vr[it] = qkvc[(size_t)(tb + min(e / RC, nt - 1)) * C + 2 * sh.H * DK + h * DV + cb + e % RC];
             }
             const size_t gr = (size_t)(tb + min(tid, nt - 1)) * sh.stride + h;
-            ga = (float)big[gr + sh.a_off];
-            gb = (float)big[gr + sh.b_off];
+            ga = big[gr + sh.a_off];
+            gb = big[gr + sh.b_off];
         }
 #pragma unroll
         for (int it = 0; it < NIT; it++) {
@@ -841,10 +857,10 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
             }
         }
         if (tid < nt) {
-            const float x = ga + db;
+            const float x = (float)ga + db;
             const float sp = x > 20.0f ? x : logf(1.0f + expf(x));
             Tg[tid].x = expf(na * sp);
-            Tg[tid].y = 1.0f / (1.0f + expf(-gb));
+            Tg[tid].y = 1.0f / (1.0f + expf(-(float)gb));
         }
         if (tb == t0) {  // the state slice: Ss[row][c] = S0[row][cb + c]
 #pragma unroll
