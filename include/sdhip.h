@@ -3,9 +3,9 @@
  *
  * This is the drop-in boundary for the reference crate's engine (mircodz/strands-decider-rs,
  * src/engine.rs).  Each entry point below replaces one item of the reference's `Engine` API; the
- * reference item is cited next to it.  A Rust `engine.rs` shim binds these 1:1 (see
- * INTEGRATION.md); the crate's `Decider::new/load/ask/ask_all` (src/lib.rs:113-145) then run
- * unchanged on top.
+ * reference item is cited next to it.  A Rust `engine.rs` shim binds these 1:1 (extern "C"
+ * declarations of the functions below and a safe wrapper per reference item); the crate's
+ * `Decider::new/load/ask/ask_all` (src/lib.rs:113-145) then run unchanged on top.
  *
  * Conventions (as in the reference):
  *  - Functions returning int return 0 on success and nonzero on failure, writing a
