@@ -86,6 +86,10 @@ def gemm_roofline(eng, state, cfg, reps=5):
     achieved = flops / avg_s / 1e12
     return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_MFMA_F16, 4), "traffic": read_traffic(),
+            # rocprofv3 counters cannot be read from inside this run: traffic is the committed
+            # two-pass FETCH_SIZE / WRITE_SIZE measurement of the same prefill GEMMs
+            "traffic_source": "profiles/gemm_w4_prefill_512_traffic.txt (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE "
+                              "of bench.py --pmc-workload segment 1, copy-kernel scaled); not measured in this run",
             "kernel": "k_gemm_w4 (int4 g32 fused-dequant MFMA GEMM, prefill M=512, the 2B's 96 GEMMs)",
             "avg_launch_us": round(avg_s * 1e6, 2), "flops_per_launch": flops,
             "algorithmic_bytes_per_launch": sum(N * K // 2 + N * K // 16 + 2 * M * K + 2 * M * N

@@ -79,8 +79,10 @@ int sd_engine_load(const sd_config* cfg, const sd_tensor* tensors, size_t n_tens
 /* `decode_scales` (src/model.rs:217-236), the load-time decode of 8-bit scale codes: n rows of g
  * codes at src (first a 4-byte header per row: m as f16 bits and j as u16, little-endian; then the
  * n*g codes, sign << 7 | k) into n*g f16 scales (bits) at dst: |scale| = f16(f32(m 2^(-k j / 4096))).
- * Host only; no device is used. */
-void sd_decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst);
+ * src holds src_bytes bytes (at least n * (4 + g)), dst dst_count scales (at least n * g); the power
+ * table lives for this call only.  Host only; no device is used. */
+int sd_decode_scale_codes(const uint8_t* src, size_t src_bytes, size_t n, size_t g, uint16_t* dst, size_t dst_count,
+                          char* err, size_t errlen);
 
 /* Drop of `Engine`. */
 void sd_engine_free(sd_engine* e);
@@ -184,11 +186,15 @@ int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off
 /* No counterpart in the reference: sd_op_matmul (cfg < 0, packed = 1) for callers that cannot
  * allocate device memory, such as code under HIP graph capture or serving loops that forbid
  * hipMalloc.  It calls no hipMalloc, hipFree or other allocating routine: the split-K partial slots
- * go to a fixed 16 MiB device array of the library (one per GPU, held until the process ends), and a
- * call whose shape needs more (ks * M * N f32 slots) fails with an error.  The weights must already
- * be in what the kernels read (sd_op_repack_w4); f16 dequant (exact = 0) needs N a multiple of 32.
- * The results are those of sd_op_matmul for the same arguments.  Every call on one GPU shares that
- * array: calls that overlap on one GPU (other streams, other threads) race. */
+ * go to a fixed 16 MiB device array of the library (one per GPU, held until the process ends).  The
+ * weights must already be in what the kernels read (sd_op_repack_w4); f16 dequant (exact = 0) needs
+ * N a multiple of 32.  The results are those of sd_op_matmul for the same arguments, except where
+ * sd_op_matmul's split-K slots (ks * M * N f32) exceed the array (prefill shapes from about 520 rows
+ * at K = 6144): those run with the largest split that fits, down to none, and their slot sums can
+ * differ from sd_op_matmul's by one f16 rounding.  The array's device address is looked up on the
+ * first call on a device: before capturing calls into a graph, make one call outside the capture.
+ * Every call on one GPU shares that array: calls that overlap on one GPU (other streams, other
+ * threads) race. */
 int sd_op_matmul_noalloc(const void* A, const void* Wq, const void* Sc, void* Y, int M, int N, int K, int exact,
                          void* stream, char* err, size_t errlen);
 

@@ -32,7 +32,7 @@ SYMBOLS = [
     "sd_op_attention", "sd_engine_trace", "sd_op_matmul_noalloc",
 ]
 VOID_SYMBOLS = ("sd_engine_free", "sd_snapshot_free", "sd_head_free", "sd_engine_hidden_size", "sd_engine_adapter",
-                "sd_snapshot_len", "sd_decode_scale_codes")
+                "sd_snapshot_len")
 
 
 class EngineError(RuntimeError):
@@ -101,8 +101,7 @@ def lib():
         L.sd_op_matmul.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, err, sz]
         L.sd_op_repack_w4.argtypes = [vp, vp, i32, i32, vp, err, sz]
         L.sd_op_gdn.argtypes = [vp, vp, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, err, sz]
-        L.sd_decode_scale_codes.argtypes = [vp, sz, sz, vp]
-        L.sd_decode_scale_codes.restype = None
+        L.sd_decode_scale_codes.argtypes = [vp, sz, sz, sz, vp, sz, err, sz]
         L.sd_op_matmul_fmt.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, err, sz]
         L.sd_op_matmul_split.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, err, sz]
         L.sd_op_gate_up_silu.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, err, sz]
@@ -408,7 +407,7 @@ def decode_scale_codes(src: bytes, n: int, g: int) -> np.ndarray:
     """sd_decode_scale_codes (src/model.rs:217-236): n rows of g 8-bit scale codes -> f16 bits [n, g]."""
     buf = np.frombuffer(bytes(src), np.uint8).copy()
     out = np.empty((n, g), np.uint16)
-    lib().sd_decode_scale_codes(_ptr(buf), n, g, _ptr(out))
+    _call(lib().sd_decode_scale_codes, _ptr(buf), buf.size, n, g, _ptr(out), out.size)
     return out
 
 

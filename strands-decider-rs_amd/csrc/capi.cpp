@@ -382,8 +382,18 @@ int sd_op_gdn(const void* qkv, const void* big, int stride, int a_off, int b_off
     });
 }
 
-void sd_decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst) {
-    if (src && dst) sd::decode_scale_codes(src, n, g, dst);
+int sd_decode_scale_codes(const uint8_t* src, size_t src_bytes, size_t n, size_t g, uint16_t* dst, size_t dst_count,
+                          char* err, size_t errlen) {
+    return guarded(err, errlen, [&] {
+        if (!src || !dst) throw sd::Error("sd_decode_scale_codes: null argument");
+        if (g == 0 || n > SIZE_MAX / (4 + g)) throw sd::Error("sd_decode_scale_codes: bad row shape");
+        if (src_bytes < n * (4 + g))
+            throw sd::Error("sd_decode_scale_codes: " + std::to_string(n) + " rows of " + std::to_string(g) +
+                            " codes need " + std::to_string(n * (4 + g)) + " source bytes, got " + std::to_string(src_bytes));
+        if (dst_count < n * g) throw sd::Error("sd_decode_scale_codes: the destination holds fewer than n * g scales");
+        std::vector<double> pw;  // for this call only
+        sd::decode_scale_codes(src, n, g, dst, pw);
+    });
 }
 
 int sd_op_matmul_fmt(const void* A, const void* Wq, const void* Sc, const void* Bi, void* Y, int M, int N, int K,

@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace sd {
 
@@ -52,7 +53,7 @@ struct KernelEvents {
 KernelEvents*& kernel_events();
 
 // 8-bit scale codes -> f16 bits (src/model.rs:217-236); host only (engine.cpp).
-void decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst);
+void decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst, std::vector<double>& pw);
 
 // ---- quantized matmul (gemm.hip) -----------------------------------------------------------
 // Y[M,N] f16 = A[M,K] f16 . deq(W[N,K])^T with W int4 group-32 symmetric in the reference's

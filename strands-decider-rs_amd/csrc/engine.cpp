@@ -43,10 +43,9 @@ void fwht(float* x, size_t n) {
 
 }  // namespace
 
-void decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst) {
-    // 2^(-i / 4096) for every exponent the rows use, in f64, kept across calls and grown on demand
-    // (the loader decodes one row at a time)
-    thread_local std::vector<double> pw;
+void decode_scale_codes(const uint8_t* src, size_t n, size_t g, uint16_t* dst, std::vector<double>& pw) {
+    // pw: 2^(-i / 4096) in f64 for every exponent the rows use, grown on demand; the caller keeps it
+    // for one load (the loader decodes one row at a time) and then drops it
     size_t jmax = 0;
     for (size_t r = 0; r < n; r++) jmax = std::max<size_t>(jmax, (size_t)src[4 * r + 2] | ((size_t)src[4 * r + 3] << 8));
     if (pw.size() < 127 * jmax + 1) {
@@ -179,8 +178,13 @@ Mat Engine::mat(const std::string& name) const {
 }
 
 // The reference's GEMV (f32 dequant) serves M <= 20 rows, non-default formats and N % 64 != 0
-// (src/engine.rs:419-442).
-static bool gemv_rows(const Mat& m, bool short_rows) { return short_rows || !m.deflt() || m.N % 64 != 0; }
+// (src/engine.rs:419-442).  Every other matrix is in the engine layout (the load rewrites each
+// default-format matrix of such a shape); the f16-dequant kernels read nothing else.
+static bool gemv_rows(const Mat& m, bool short_rows) {
+    const bool gemv = short_rows || !m.deflt() || m.N % 64 != 0;
+    SD_CHECK(gemv || m.tiled, "a default-format matrix was not rewritten into the engine layout");
+    return gemv;
+}
 
 const float* Engine::f32(const std::string& name, size_t count) const {
     const TensorRef& t = tensor(name);
@@ -285,6 +289,7 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         for (size_t p = 0; p < em->n_parts; p++) parts[p].resize(em->vocab * em->part_bytes[p]);
         const size_t rows_per = std::max<size_t>(1, chunk / rb);
         std::vector<uint8_t> buf(rows_per * rb);
+        std::vector<double> pw;  // the scale-code power table, for this load only
         for (uint64_t r0 = 0; r0 < em->vocab; r0 += rows_per) {
             const size_t nr = (size_t)std::min<uint64_t>(rows_per, em->vocab - r0);
             if (std::fread(buf.data(), rb, nr, f) != nr) {
@@ -298,7 +303,7 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
                     const uint8_t* src = buf.data() + r * rb + off;
                     if (coded[p]) {
                         const size_t g = em->part_bytes[p] / 2;
-                        decode_scale_codes(src, 1, g, reinterpret_cast<uint16_t*>(dst));
+                        decode_scale_codes(src, 1, g, reinterpret_cast<uint16_t*>(dst), pw);
                         off += 4 + g;
                     } else {
                         std::memcpy(dst, src, em->part_bytes[p]);
@@ -393,16 +398,20 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         for (LayerW& L : layers)
             for (Mat* m : {&L.in_proj, &L.out_proj, &L.qkv, &L.o_proj, &L.gate_up, &L.down, &L.proj})
                 if (m->q) all.push_back(m);
+        // Matrices that share memory must agree in shape and format: the rewrite into the engine
+        // layout below is done once per memory, and a GEMM reading the rewritten words as another
+        // shape would read the model's bit order as the engine's.
+        for (const Mat* a : all)
+            for (const Mat* b : all)
+                if (a->q == b->q && (a->N != b->N || a->K != b->K || a->bits != b->bits || a->group != b->group ||
+                                     a->asym != b->asym))
+                    throw Error("two matrices share memory with different shapes or formats (" + std::to_string(a->N) +
+                                " x " + std::to_string(a->K) + " and " + std::to_string(b->N) + " x " +
+                                std::to_string(b->K) + ")");
         // Only int4 g32 symmetric matrices of a tileable shape are rewritten (the kernels with f16
         // dequant read nothing else); every other matrix keeps the reference's layout and bit order,
-        // which the GEMV reads.  A matrix sharing memory with another of a different format or
-        // shape is left as it is.
-        auto rewritable = [&](const Mat* m) {
-            if (!m->deflt() || !w4_tileable(m->N, m->K)) return false;
-            for (const Mat* o : all)
-                if (o->q == m->q && (o->N != m->N || o->K != m->K || !o->deflt())) return false;
-            return true;
-        };
+        // which the GEMV reads.
+        auto rewritable = [&](const Mat* m) { return m->deflt() && w4_tileable(m->N, m->K); };
         std::vector<const uint32_t*> done;
         size_t tmp_bytes = 0;
         for (const Mat* m : all) {

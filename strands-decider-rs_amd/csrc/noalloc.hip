@@ -15,7 +15,8 @@ constexpr size_t SCRATCH_FLOATS = size_t(4) << 20;
 static __device__ __align__(256) float scratch[SCRATCH_FLOATS];
 
 // The device address of `scratch` on each device, looked up once per device with that device
-// current.
+// current, on the first call that needs it (so a caller about to capture a graph makes one call
+// first: the lookup is then not part of the capture).
 std::mutex scratch_mu;
 float* scratch_dev[64] = {};
 
@@ -60,17 +61,15 @@ extern "C" int sd_op_matmul_noalloc(const void* A, const void* Wq, const void* S
             if (!tiled)
                 throw sd::Error("sd_op_matmul_noalloc: the f16-dequant kernels need N a multiple of 32 here "
                                 "(other shapes are rewritten into a workspace: use sd_op_matmul)");
-            // the plan sd_op_matmul takes for this shape (the same kernels, splits and results)
-            const sd::GemmPlan p = sd::gemm_w4_plan(M, N, K, false, true, size_t(64) << 20);
+            // the plan sd_op_matmul takes for this shape (the same kernels, splits and results); when
+            // its split-K slots do not fit the array, the same kernel with the largest split that
+            // fits (down to none), whose slots add in another order
+            sd::GemmPlan p = sd::gemm_w4_plan(M, N, K, false, true, size_t(64) << 20);
+            if ((size_t)p.ks * M * N > SCRATCH_FLOATS) p = sd::gemm_w4_plan(M, N, K, false, true, SCRATCH_FLOATS);
             if (p.ks == 1) {
                 sd::gemm_w4(a, wq, sc, static_cast<sd::f16*>(Y), nullptr, M, N, K, false, 1, st, p.cfg, true);
             } else {
-                const size_t need = (size_t)p.ks * M * N;
-                if (need > SCRATCH_FLOATS)
-                    throw sd::Error("sd_op_matmul_noalloc: " + std::to_string(p.ks) + " split-K slots of " +
-                                    std::to_string(M) + " x " + std::to_string(N) + " need " +
-                                    std::to_string(need * 4) + " bytes of scratch, more than its " +
-                                    std::to_string(SCRATCH_FLOATS * 4) + "; use sd_op_matmul");
+                SD_CHECK((size_t)p.ks * M * N <= SCRATCH_FLOATS, "sd_op_matmul_noalloc: the split does not fit the scratch array");
                 float* part = scratch_ptr();
                 sd::gemm_w4(a, wq, sc, nullptr, part, M, N, K, false, p.ks, st, p.cfg, true);
                 sd::reduce_partials(part, p.ks, (size_t)M * N, static_cast<sd::f16*>(Y), st);

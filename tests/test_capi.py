@@ -96,3 +96,19 @@ def test_decode_scale_codes_matches_oracle(sdamd, oracle):
     got = sdamd.decode_scale_codes(src, n, g)
     want = oracle.decode_scale_codes(src, n, g)
     assert np.array_equal(got, want)
+
+
+def test_decode_scale_codes_checks_lengths(sdamd):
+    """sd_decode_scale_codes refuses buffers shorter than n rows of g codes need (and decodes again
+    afterwards): a short source would otherwise be read past its end."""
+    import ctypes as C
+    n, g = 2, 8
+    src = np.zeros(n * (4 + g), np.uint8)
+    out = np.zeros(n * g, np.uint16)
+    L = sdamd.lib()
+    ptr = lambda a: a.ctypes.data_as(C.c_void_p)
+    with pytest.raises(sdamd.EngineError, match="source bytes"):
+        sdamd._call(L.sd_decode_scale_codes, ptr(src), src.size - 1, n, g, ptr(out), out.size)
+    with pytest.raises(sdamd.EngineError, match="destination"):
+        sdamd._call(L.sd_decode_scale_codes, ptr(src), src.size, n, g, ptr(out), out.size - 1)
+    assert sdamd.decode_scale_codes(src.tobytes(), n, g).shape == (n, g)

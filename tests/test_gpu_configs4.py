@@ -1,7 +1,8 @@
-"""BASELINE configs[4] on the GPU against the oracle: the 2B hybrid encodes a long state (1536
-tokens, so the prefill takes the M > 1024 GEMM plan, a gated-delta-net scan of 24 chunks and
-attention over up to 1600 keys), then 8 questions of U[24, 64] tokens are answered from its snapshot
-as one batched forward of 8 sequences with the device head.  Each question is compared with the
+"""BASELINE configs[4] on the GPU against the oracle, at the top of its range: the 2B hybrid encodes a
+2048-token state (the longest configs[4] draws: the M > 1024 GEMM plan, a gated-delta-net scan of 32
+chunks, attention over up to 2048 keys), then 8 questions of 64 tokens (the longest it draws) are
+answered from its snapshot as one batched forward of 8 sequences (512 rows, each question attending
+over 2048 + 64 keys) with the device head.  Each question is compared with the
 oracle's own forward of that question from its snapshot: hidden rows within 2e-2, probabilities
 within 2e-3, the same answer (tests/engine_parity.rs:58-85 at the sweep's shapes)."""
 import numpy as np
@@ -11,7 +12,7 @@ pytestmark = pytest.mark.gpu
 
 HIDDEN_TOL = 2e-2
 PROB_TOL = 2e-3
-STATE_LEN, N_Q = 1536, 8
+STATE_LEN, N_Q, Q_LEN = 2048, 8, 64
 
 
 @pytest.mark.timeout(900)
@@ -22,12 +23,12 @@ def test_configs4_long_state_and_eight_questions(sdamd, synth, model_2b, oracle)
         temp = float(cfg["temperature"])
         rng = np.random.default_rng(404)
         state = rng.integers(0, synth.VOCAB_2B, STATE_LEN).astype(np.uint32)
-        qs = [rng.integers(0, synth.VOCAB_2B, int(rng.integers(24, 65))).astype(np.uint32) for _ in range(N_Q)]
+        qs = [rng.integers(0, synth.VOCAB_2B, Q_LEN).astype(np.uint32) for _ in range(N_Q)]
         opts = [sorted(rng.choice(len(q) - 1, int(rng.integers(2, 6)), replace=False).tolist()) for q in qs]
-        rows = [0, 767, STATE_LEN - 1]
+        rows = [0, STATE_LEN // 2 - 1, STATE_LEN - 1]
 
         out = eng.forward(state, rows, keep=True)
-        print(f"configs[4]: GPU prefill of {STATE_LEN} done; oracle prefill (about a minute on the host)", flush=True)
+        print(f"configs[4]: GPU prefill of {STATE_LEN} done; oracle prefill (one to two minutes on the host)", flush=True)
         want, osnap = om.forward(state, rows, keep=True)
         err = np.abs(out.hidden - want).max()
         print(f"configs[4] prefill of {STATE_LEN}: max |dh| {err:.3g}", flush=True)

@@ -68,7 +68,8 @@ def test_ask_ids_matches_oracle(tiny, sdamd):
         h, _ = om.forward(q, rows, cache=snap)
         want = om.probs(h, t)
         assert np.abs(g - want).max() < PROB_TOL
-        assert int(np.argmax(g)) == int(np.argmax(want)) or np.sort(want)[-1] - np.sort(want)[-2] < PROB_TOL
+        # the answer must match exactly (these seeds' top-two margins are 0.076 to 0.87, far above PROB_TOL)
+        assert int(np.argmax(g)) == int(np.argmax(want))
     # one question: a single forward of state ++ question
     one = sdamd.ask_ids(eng, head, state, qs[:1], options[:1], temps[:1])[0]
     assert np.abs(one - got[0]).max() < PROB_TOL
@@ -303,3 +304,39 @@ def test_plan_cache_evicts_and_recaptures(tiny):
     # the cache holds at most 512 plans: the lengths used first were evicted and are captured again
     h = eng.forward(ids_for(640, 640), [639]).hidden
     assert np.isfinite(h).all()
+
+
+def test_load_rejects_matrices_sharing_memory_with_other_shapes(sdamd, tiny_model, tmp_path):
+    """Two manifest matrices at the same offset with different shapes are refused at load: the
+    rewrite into the engine layout happens once per memory, so a GEMM would otherwise read one of
+    them in the wrong bit order.  Same-shaped aliases still load."""
+    import json
+    import os
+    import shutil
+    d = tmp_path / "alias"
+    shutil.copytree(tiny_model, d)
+    with open(d / "manifest.json") as f:
+        man = json.load(f)
+    t = man["tensors"]
+    a, b = "layers.0.in_proj", "layers.0.gate_up"
+    assert (t[a + ".q"]["N"], t[a + ".q"]["K"]) != (t[b + ".q"]["N"], t[b + ".q"]["K"])
+    bad = json.loads(json.dumps(man))
+    for part in (".q", ".s"):  # point in_proj at gate_up's larger words and scales
+        bad["tensors"][a + part]["offset"] = t[b + part]["offset"]
+    with open(d / "manifest.json", "w") as f:
+        json.dump(bad, f)
+    with pytest.raises(sdamd.EngineError, match="share memory with different shapes"):
+        sdamd.Engine.load(str(d))
+    # an alias of the same shape and format loads, and the shared matrix is rewritten once
+    same = json.loads(json.dumps(man))
+    for part in (".q", ".s"):
+        same["tensors"]["layers.4.gate_up" + part]["offset"] = t[b + part]["offset"]
+    assert (t["layers.4.gate_up.q"]["N"], t["layers.4.gate_up.q"]["K"]) == (t[b + ".q"]["N"], t[b + ".q"]["K"])
+    with open(d / "manifest.json", "w") as f:
+        json.dump(same, f)
+    eng = sdamd.Engine.load(str(d))
+    try:
+        h = eng.forward(ids_for(11, 30), [29]).hidden
+        assert np.isfinite(h).all()
+    finally:
+        eng.free()
