@@ -468,3 +468,40 @@ def op_matmul_noalloc(A, Wq, Sc, Y, M, N, K, exact=False, stream=None):
     """sd_op_matmul_noalloc: sd_op_matmul (engine plan, pre-packed weights) with no device allocation."""
     _call(lib().sd_op_matmul_noalloc, C.c_void_p(A), C.c_void_p(Wq), C.c_void_p(Sc), C.c_void_p(Y), M, N, K,
           int(exact), _sp(stream))
+
+
+# ---- achievable-peak microbenchmarks (libsdpeak.so, include/sdpeak.h; used by bench.py) ----------
+
+PEAK_LIB_PATH = os.path.join(HERE, "libsdpeak.so")
+PEAK_SYMBOLS = ["sd_peak_mfma", "sd_peak_hbm"]
+_peak = None
+
+
+def peak_lib():
+    """The loaded libsdpeak.so; raises if it is not built."""
+    global _peak
+    if _peak is None:
+        if not os.path.exists(PEAK_LIB_PATH):
+            raise EngineError(f"{PEAK_LIB_PATH} is missing: build it with `make -C strands-decider-rs_amd`")
+        L = C.CDLL(PEAK_LIB_PATH)
+        vp, sz, i32, err = C.c_void_p, C.c_size_t, C.c_int, C.c_char_p
+        L.sd_peak_mfma.argtypes = [i32, i32, i32, i32, vp, vp, err, sz]
+        L.sd_peak_hbm.argtypes = [i32, sz, i32, vp, vp, err, sz]
+        for name in PEAK_SYMBOLS:
+            getattr(L, name).restype = i32
+        _peak = L
+    return _peak
+
+
+def peak_mfma(variant: int, wg_per_cu: int, iters: int, launches: int, stream=None) -> dict:
+    """sd_peak_mfma: 0 MFMA alone, 1 the (2,1) GEMM loop mix, 2 the (4,1) mix (include/sdpeak.h)."""
+    out = np.zeros(4, np.float64)
+    _call(peak_lib().sd_peak_mfma, variant, wg_per_cu, iters, launches, _sp(stream), _ptr(out))
+    return {"ms": float(out[0]), "tflops": float(out[1]), "clock_ghz": float(out[2]), "cus": int(out[3])}
+
+
+def peak_hbm(variant: int, nbytes: int, launches: int, stream=None) -> dict:
+    """sd_peak_hbm: 0 streaming read, 1 copy (read + write counted) over nbytes."""
+    out = np.zeros(4, np.float64)
+    _call(peak_lib().sd_peak_hbm, variant, nbytes, launches, _sp(stream), _ptr(out))
+    return {"ms": float(out[0]), "gbps": float(out[1]), "clock_ghz": float(out[2]), "cus": int(out[3])}

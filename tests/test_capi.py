@@ -112,3 +112,14 @@ def test_decode_scale_codes_checks_lengths(sdamd):
     with pytest.raises(sdamd.EngineError, match="destination"):
         sdamd._call(L.sd_decode_scale_codes, ptr(src), src.size, n, g, ptr(out), out.size - 1)
     assert sdamd.decode_scale_codes(src.tobytes(), n, g).shape == (n, g)
+
+
+def test_peak_library_exports_every_declared_symbol(sdamd):
+    """libsdpeak.so (the achievable-peak microbenchmarks bench.py reports beside the published
+    peaks) loads without a GPU and exports every entry point include/sdpeak.h declares."""
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "sdpeak.h").read_text(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(sd_[a-z_0-9]+)\s*\(", text)))
+    assert names == sorted(sdamd.PEAK_SYMBOLS)
+    lib = ctypes.CDLL(sdamd.PEAK_LIB_PATH)
+    assert all(hasattr(lib, n) for n in names)
+    sdamd.peak_lib()
