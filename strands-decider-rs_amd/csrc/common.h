@@ -170,19 +170,6 @@ struct ConvIn {
     const uint32_t* rowt = nullptr;  // per row: index in its sequence | start row << 16 (null: one sequence)
     size_t hist_off = 0;             // the layer's history in a snapshot arena image
 };
-// The gated RMSNorm (src/kernels.rs:377-396) fused into the delta rule's own kernel: the last of a
-// head's column workgroups to finish normalizes the head's rows (group_last, device.h).  out null:
-// not fused (k_gnorm runs after the kernel).
-constexpr int GN_PS = 8;  // partial sums per (row, head): one per column workgroup, at most 8
-struct GnormOut {
-    f16* out = nullptr;          // [L][H * DV] f16, what k_gnorm would write
-    const float* w = nullptr;    // [DV] the layer's gnorm weights
-    float* ps = nullptr;         // [L][H][GN_PS] sums of o^2 over each column workgroup's columns
-    uint32_t* ctr = nullptr;     // one counter per (sequence, head), 0 between launches
-    uint32_t* xs = nullptr;      // [sequence][head][GN_PS] the XCD of each member
-    uint32_t* status = nullptr;  // pinned host word: set to 1 when a placement check fails
-};
-
 // Workspace of the chunked recurrence, sized for `cap` tokens: per (chunk, head) the scan's A
 // operands split into f16 hi/lo in MFMA fragment order, U (fp32) and e^(G_last).
 struct GdnWs {
@@ -222,8 +209,7 @@ void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uin
 // hist must be null).
 void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
                float* state, const uint32_t* lu, int load_default, float* o, f16* hist, const Segs& sg, int nseq,
-               hipStream_t st, size_t state_off = 0, size_t hist_off = 0, const ConvIn& cv = ConvIn{},
-               const GnormOut& gn = GnormOut{});
+               hipStream_t st, size_t state_off = 0, size_t hist_off = 0, const ConvIn& cv = ConvIn{});
 void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, int L, f16* out, hipStream_t st);
 
 // ---- pointer head (head_gpu.hip) -------------------------------------------------------------

@@ -157,52 +157,5 @@ __device__ __forceinline__ f16x8 cat4(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
     return f16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
-#if defined(__HIP_DEVICE_COMPILE__)
-// The XCD (accelerator complex die) this wave runs on.
-__device__ __forceinline__ uint32_t xcc_id() {
-    uint32_t v;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-    return v & 0xFu;
-}
-// 16 bytes that bypass this CU's L1 (sc0): read from the XCD's L2.
-__device__ __forceinline__ u32x4 buf_b128_l2(Rsrc r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 1));
-}
-
-// Hand-off to the last workgroup of a group.  The members of a group sit on one XCD by their grid
-// positions (the hardware gives workgroup b of a launch to XCD b % 8), so they share that XCD's L2.
-// Every member stores its part of the shared data, then calls this with all its threads: each
-// thread waits until its stores are acknowledged (the L1 is write-through, so they are in the L2),
-// and the member counts itself in with an atomic on the group's counter (executed in the L2).  The
-// member that counts in last resets the counter to 0 (for the next launch) and returns true; it may
-// then read the other members' data with loads that bypass its L1 (buf_b128_l2).  No workgroup
-// waits for another.  Each member records its XCD in xs[member]; the last one compares them with
-// its own and, if one differs (the placement this relies on did not hold, so what it reads could be
-// stale), stores 1 to *status (pinned host memory, checked by the host after the forward).
-__device__ __forceinline__ bool group_last(uint32_t* ctr, uint32_t* xs, int n, int member, uint32_t* status) {
-    __shared__ uint32_t arrived;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        xs[member] = xcc_id();
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        arrived = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (arrived != (uint32_t)(n - 1)) return false;
-    // the reset is an atomic too, so that every access to the counter is made in the L2, as the adds are
-    if (threadIdx.x == 0) (void)__hip_atomic_exchange(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((int)threadIdx.x < n) {
-        const uint32_t x = __hip_atomic_load(xs + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (x != xcc_id()) *status = 1u;
-    }
-    return true;
-}
-#else
-__device__ inline uint32_t xcc_id() { return 0; }
-__device__ inline u32x4 buf_b128_l2(Rsrc, uint32_t, uint32_t) { return u32x4{}; }
-__device__ inline bool group_last(uint32_t*, uint32_t*, int, int, uint32_t*) { return false; }
-#endif
-
 }  // namespace
 }  // namespace sd

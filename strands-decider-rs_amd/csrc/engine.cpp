@@ -238,8 +238,6 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
     SD_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
     SD_HIP(hipEventCreate(&ev0));
     SD_HIP(hipEventCreate(&ev1));
-    placement_h = static_cast<uint32_t*>(halloc(sizeof(uint32_t)));
-    *placement_h = 0;
 
     // Shards: one device buffer each, streamed from the file through a pinned staging buffer.
     const size_t chunk = size_t(64) << 20;
@@ -521,8 +519,6 @@ void Engine::ensure_pool(int l) {
         attn_ws_floats(std::min(cap, 256), as) * 4,    // attention key-split workspace
         ypart * 4,                                     // split-K partials of y
         gpart * 4,                                     // split-K partials of gate_up
-        (size_t)cap * cfg.H * GN_PS * 4,               // partial sums of the fused gated norm
-        (size_t)SD_MAX_SEQS * cfg.H * (1 + GN_PS) * 4,  // its hand-off counters and XCD slots
     };
     size_t total = 0;
     for (size_t s : sizes) total += align256(s);
@@ -567,10 +563,6 @@ void Engine::ensure_pool(int l) {
     pool.ypart_elems = ypart;
     pool.gpart = (float*)ptrs[14];
     pool.gpart_elems = gpart;
-    pool.gps = (float*)ptrs[15];
-    pool.gn_ctr = (uint32_t*)ptrs[16];
-    pool.gn_xs = pool.gn_ctr + SD_MAX_SEQS * cfg.H;
-    SD_HIP(hipMemset(pool.gn_ctr, 0, (size_t)SD_MAX_SEQS * cfg.H * (1 + GN_PS) * 4));  // counters start at 0
     SD_HIP(hipMemset(pool.x, 0, (size_t)cap * cfg.d * 4));
     SD_HIP(hipMemset(upb, 0, up.up_bytes));
     if (up_h_bytes < up.up_bytes) {
@@ -677,16 +669,12 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
             // conv and the delta rule read the prefix's history and state in place (from the snapshot
             // the lu block names, else the live arena) and write the live arena
             f16* hist_upd = nseq ? nullptr : W.hist;  // several sequences leave no history
-            // the token-by-token recurrence finishes with the gated norm itself: the last of a head's
-            // column workgroups normalizes the head's rows (no gnorm launch)
-            const bool fuse_gn = recur;
-            const GnormOut gno = fuse_gn ? GnormOut{P.o, W.gnorm, P.gps, P.gn_ctr, P.gn_xs, placement_h} : GnormOut{};
             if (recur && nseq) {
                 // several sequences update no history: the recurrence computes the conv itself
                 const ConvIn cin{W.conv, W.hist, sg.row, W.hist_off};
                 steps.push_back({"gdn", [=](hipStream_t s) {
                     gdn_recur(nullptr, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, nullptr, sg, nseq, s,
-                              W.state_off, W.hist_off, cin, gno);
+                              W.state_off, W.hist_off, cin);
                 }});
             } else if (recur) {
                 // one sequence: the conv reads the old history before the recurrence updates it
@@ -695,7 +683,7 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
                 }});
                 steps.push_back({"gdn", [=](hipStream_t s) {
                     gdn_recur(P.qkvc, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, hist_upd, sg, nseq, s, W.state_off,
-                              W.hist_off, ConvIn{}, gno);
+                              W.hist_off);
                 }});
             } else {
                 // the chunked path computes the conv inside prep (no conv output in HBM); the history
@@ -708,7 +696,7 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
                     gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s, W.state_off, hist_upd, P.big, W.hist_off);
                 }});
             }
-            if (!fuse_gn) steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
+            steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
             y = mm_y(steps, "out_proj", P.o, W.out_proj, L, sr);
         } else {
             const AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, W.qkv.N, SD_CONTEXT};
@@ -840,15 +828,7 @@ void Engine::launch_and_read(Plan& pl, size_t n_rows, bool timed, bool read) {
     if (n_rows) SD_HIP(hipMemcpyAsync(out_h, pool.out, n_rows * cfg.d * 4, hipMemcpyDeviceToHost, st));
 }
 
-void Engine::check_placement() {
-    if (!*placement_h) return;
-    *placement_h = 0;
-    throw Error("a fused kernel's workgroups did not run on the XCDs their grid positions assume "
-                "(the hardware gives workgroup b to XCD b % 8): this forward's results are invalid");
-}
-
 void Engine::finish(size_t n_rows, float* hidden, bool timed, double* gpu_ms) {
-    check_placement();
     if (n_rows) {
         std::memcpy(hidden, out_h, n_rows * cfg.d * 4);
         // A rotated torso: the head's basis is unrotate * FWHT(row) (src/engine.rs:652-660).
@@ -1117,7 +1097,6 @@ std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids,
         SD_HIP(hipEventRecord(evs[i + 1], st));
     }
     SD_HIP(hipStreamSynchronize(st));
-    check_placement();
     std::vector<std::pair<const char*, double>> by;
     for (size_t i = 0; i < ns; i++) {
         float ms = 0.f;
@@ -1163,7 +1142,6 @@ size_t Engine::trace(const uint32_t* ids, size_t n, const Snapshot* cache, const
         taps++;
     }
     SD_HIP(hipStreamSynchronize(st));
-    check_placement();
     return taps;
 }
 

@@ -85,10 +85,6 @@ struct Pool {
     size_t gpart_elems = 0;
     uint32_t *seg_row = nullptr, *seg_chunk = nullptr, *seg_seq = nullptr;  // Segs tables
     int seg_chunk_cap = 0;
-    // hand-off buffers of the kernels that finish a group's work in its last workgroup (group_last):
-    // partial sums of the fused gated norm, and counters (0 between launches) with XCD slots
-    float* gps = nullptr;  // [cap][H][GN_PS]
-    uint32_t *gn_ctr = nullptr, *gn_xs = nullptr;  // [SD_MAX_SEQS][H], [SD_MAX_SEQS][H][GN_PS]
 };
 
 struct Step {
@@ -166,10 +162,6 @@ struct Engine {
     static constexpr size_t kMaxPlans = 512;
     float* out_h = nullptr;
     int out_h_cap = 0;
-    // Pinned host word the fused kernels set to 1 when their workgroups did not run on the XCDs their
-    // grid positions assume (group_last); checked after every forward (check_placement).
-    uint32_t* placement_h = nullptr;
-    void check_placement();
     std::vector<void*> device_allocs, host_allocs;
     // Device copy of the last head used by ask_batch, and the head's per-call buffers.
     HeadW headw;

@@ -622,9 +622,8 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
                                                    size_t state_off, const float* __restrict__ negA,
                                                    const float* __restrict__ dtb, float* __restrict__ o,
                                                    const uint32_t* __restrict__ chunkt, f16* hist, size_t hist_off,
-                                                   GdnShape sh, ConvIn cv, GnormOut gn) {
+                                                   GdnShape sh, ConvIn cv) {
     constexpr int DK = 128, DV = 128;
-    constexpr int NCG = DV / RC;  // column workgroups per head
     // Q and K tiles of a block; with CONV first the conv output of q and k, f32 [token][256]
     __shared__ __attribute__((aligned(16))) float4 QKs[2 * RTB * DK / 4];
     float4 (*const Qs)[DK / 4] = reinterpret_cast<float4 (*)[DK / 4]>(QKs);
@@ -636,13 +635,7 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     __shared__ float4 Wt[64 + RC / 4][4];  // CONV: the taps of the q/k view's 64 lane groups, then the v view's 8
     __shared__ float Ss[DK][RC + 1];      // the state slice on its way into the token loop's registers
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    // 1-D grid: group G = (sequence q, head h) = q H + h has its NCG column workgroups cy at linear
-    // positions G % 8 + 8 (NCG (G / 8) + cy), all on XCD G % 8 (the hardware gives workgroup b to XCD
-    // b % 8), which the fused gated norm's hand-off needs (group_last); positions past the last
-    // group exit at once
-    const int H = sh.H;
-    const int cy = (blockIdx.x >> 3) % NCG, G = (blockIdx.x & 7) + 8 * ((blockIdx.x >> 3) / NCG);
-    const int h = G % H, q = G / H;
+    const int h = blockIdx.x, H = sh.H, q = blockIdx.z;
     // The lu fields and the sequence's row range in one batch of scalar loads, issued before any
     // branch (a load behind one waits for the loads the branch needs): the pointers are selected
     // first, with `state` standing in for a null table (values then unused).
@@ -652,11 +645,11 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     const uint8_t* const lu_pre = *reinterpret_cast<const uint8_t* const*>(lp + 8);
     SGPR_BATCH("s"(lu_nseq), "s"(lu_load), "s"(rr), "s"(lu_pre), "s"(sh.H), "s"(sh.C), "s"(sh.stride), "s"(sh.a_off),
                "s"(sh.b_off), "s"(negA), "s"(dtb), "s"(o), "s"(cv.w), "s"(cv.hist), "s"(cv.hist_off));
-    if (seqt ? q >= (int)lu_nseq : q > 0) return;  // the grid is sized for the most sequences
+    if (seqt && q >= (int)lu_nseq) return;  // the grid is sized for the most sequences
     // lane l of a 16-lane row owns state rows 4l .. 4l + 3 and 64 + 4l .. 64 + 4l + 3: its q and k
     // values are then float4 l and 16 + l of a token's row, so the 16 lanes of each read cover 256
     // contiguous bytes (every LDS bank once)
-    const int cb = cy * RC, cl = wv * 4 + (lane >> 4), col = cb + cl, l4 = lane & 15;
+    const int cb = blockIdx.y * RC, cl = wv * 4 + (lane >> 4), col = cb + cl, l4 = lane & 15;
     auto srow = [&](int i) { return (i < 4 ? 0 : 60) + 4 * l4 + i; };
     int t0 = 0, t1 = L;
     if (seqt) {  // the sequence's rows (the chunk table would be a second, dependent load)
@@ -924,64 +917,32 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
             run(tb2, tt + 1);
         }
         if (tt < nt) run(ta, tt);
-        // the block's outputs leave as whole 128-byte rows (32 columns of a token); with the gated
-        // norm fused, the sum of a token's 32 squares (the 32 lanes of a half wave) goes with them
+        // the block's outputs leave as whole 128-byte rows (32 columns of a token)
         __syncthreads();
 #pragma unroll
         for (int it = 0; it < RTB * RC / RT; it++) {
             const int e = it * RT + tid, r = e / RC;
-            const float v = Os[r][e % RC];
-            if (r < nt) o[(size_t)(tb + r) * sh.H * DV + h * DV + cb + e % RC] = v;
-            if (gn.out) {
-                float s2 = v * v;
-#pragma unroll
-                for (int m = 16; m > 0; m >>= 1) s2 += __shfl_xor(s2, m);
-                if (e % RC == 0 && r < nt) gn.ps[((size_t)(tb + r) * H + h) * GN_PS + cy] = s2;
-            }
+            if (r < nt) o[(size_t)(tb + r) * sh.H * DV + h * DV + cb + e % RC] = Os[r][e % RC];
         }
     }
-    if (!seqt) {  // one sequence: its final state is kept (several sequences keep none)
+    if (seqt) return;  // several sequences: their final states are not kept
 #pragma unroll
-        for (int i = 0; i < 8; i++) Sg[(size_t)srow(i) * DV + col] = S[i];
-        // the reference's hist_update (src/kernels.rs:173-190), each workgroup on a slice of the
-        // channels: the last 3 rows of (the prefix's history ++ this forward's rows) into the live history
-        if (hist) {
-            const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
-            const int nb = H * (DV / RC), per = (C + nb - 1) / nb, bi = cy * H + h;
-            const int lo = bi * per, hi = min(C, lo + per);
-            for (int ch = lo + tid; ch < hi; ch += RT) {
-                f16 hv[3];
+    for (int i = 0; i < 8; i++) Sg[(size_t)srow(i) * DV + col] = S[i];
+    // the reference's hist_update (src/kernels.rs:173-190), each workgroup on a slice of the channels:
+    // the last 3 rows of (the prefix's history ++ this forward's rows) into the live history
+    if (hist) {
+        const f16* old = pre ? reinterpret_cast<const f16*>(pre + hist_off) : hist;
+        const int nb = H * (DV / RC), per = (C + nb - 1) / nb, bi = blockIdx.y * H + h;
+        const int lo = bi * per, hi = min(C, lo + per);
+        for (int ch = lo + tid; ch < hi; ch += RT) {
+            f16 hv[3];
 #pragma unroll
-                for (int r = 0; r < 3; r++) {
-                    const int src = L - 3 + r;
-                    hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : old[(size_t)(src + 3) * C + ch];
-                }
-#pragma unroll
-                for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = hv[r];
+            for (int r = 0; r < 3; r++) {
+                const int src = L - 3 + r;
+                hv[r] = src >= 0 ? big[(size_t)src * sh.stride + ch] : old[(size_t)(src + 3) * C + ch];
             }
-        }
-    }
-    // The gated RMSNorm of this sequence's rows of head h (src/kernels.rs:377-396), by the last of the
-    // group's NCG column workgroups to finish (all on one XCD, see the grid above).
-    if (gn.out && group_last(gn.ctr + G, gn.xs + G * GN_PS, NCG, cy, gn.status)) {
-        const Rsrc ro = make_rsrc(o, (uint32_t)L * H * DV * 4u), rp = make_rsrc(gn.ps, (uint32_t)L * H * GN_PS * 4u);
-        for (int e = tid; e < (t1 - t0) * (DV / 4); e += RT) {
-            const int t = t0 + e / (DV / 4), c4 = 4 * (e % (DV / 4));
-            const size_t th = (size_t)t * H + h;
-            const float4 ov = __builtin_bit_cast(float4, buf_b128_l2(ro, (uint32_t)((th * DV + c4) * 4), 0u));
-            const float4 pv = __builtin_bit_cast(float4, buf_b128_l2(rp, (uint32_t)(th * GN_PS * 4), 0u));
-            const f16x4 z = *reinterpret_cast<const f16x4*>(big + (size_t)t * sh.stride + sh.z_off + h * DV + c4);
-            const float4 w4 = *reinterpret_cast<const float4*>(gn.w + c4);
-            static_assert(NCG == 4, "the partial sums of 4 column workgroups");
-            const float inv = 1.0f / sqrtf((((pv.x + pv.y) + pv.z) + pv.w) / (float)DV + 1e-6f);
-            const float ow[4] = {ov.x, ov.y, ov.z, ov.w}, ww[4] = {w4.x, w4.y, w4.z, w4.w};
-            f16x4 r4;
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float zu = (float)z[u];
-                r4[u] = (f16)(ww[u] * ow[u] * inv * zu / (1.0f + expf(-zu)));
-            }
-            *reinterpret_cast<f16x4*>(gn.out + th * DV + c4) = r4;
+            for (int r = 0; r < 3; r++) hist[(size_t)r * C + ch] = hv[r];
         }
     }
 }
@@ -1292,22 +1253,18 @@ void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uin
 
 void gdn_recur(const float* qkvc, const f16* big, const GdnShape& s, const float* negA, const float* dtb, int L,
                float* state, const uint32_t* lu, int load_default, float* o, f16* hist, const Segs& sg, int nseq,
-               hipStream_t st, size_t state_off, size_t hist_off, const ConvIn& cv, const GnormOut& gn) {
+               hipStream_t st, size_t state_off, size_t hist_off, const ConvIn& cv) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
-    SD_CHECK(!gn.out || (gn.w && gn.ps && gn.ctr && gn.xs && gn.status && s.z_off % 4 == 0 && s.stride % 4 == 0),
-             "gdn_recur: the fused gated norm needs its buffers, and the gate offset and row stride multiples of 4");
     SD_CHECK(!sg.seq || (lu && sg.chunk && !hist), "gdn_recur: several sequences need lu and keep no history");
     SD_CHECK(!cv.w || (cv.hist && !hist), "gdn_recur: the conv needs the history, and updates none");
     SD_CHECK(!cv.w || (s.C % 4 == 0 && s.stride % 4 == 0), "gdn_recur: channels and row stride must be multiples of 4");
     if (!sg.seq) nseq = 1;
-    // groups (sequence, head) in runs of 8, one group per XCD, each with its DV / RC column workgroups
-    const dim3 grid(8 * (s.DV / RC) * ((s.H * nseq + 7) / 8));
     if (cv.w)
-        hipLaunchKernelGGL(k_gdn_recur<true>, grid, dim3(RT), 0, st, lu, sg.seq, state, big, qkvc, L, load_default,
-                           state_off, negA, dtb, o, sg.chunk, hist, hist_off, s, cv, gn);
+        hipLaunchKernelGGL(k_gdn_recur<true>, dim3(s.H, s.DV / RC, nseq), dim3(RT), 0, st, lu, sg.seq, state, big, qkvc,
+                           L, load_default, state_off, negA, dtb, o, sg.chunk, hist, hist_off, s, cv);
     else
-        hipLaunchKernelGGL(k_gdn_recur<false>, grid, dim3(RT), 0, st, lu, sg.seq, state, big, qkvc, L, load_default,
-                           state_off, negA, dtb, o, sg.chunk, hist, hist_off, s, cv, gn);
+        hipLaunchKernelGGL(k_gdn_recur<false>, dim3(s.H, s.DV / RC, nseq), dim3(RT), 0, st, lu, sg.seq, state, big, qkvc,
+                           L, load_default, state_off, negA, dtb, o, sg.chunk, hist, hist_off, s, cv);
     launched("gdn_recur");
 }
 

@@ -93,17 +93,12 @@ def test_forward_errors(tiny, sdamd):
 
 
 def test_profile_labels(tiny):
-    """Engine::profile's step labels.  The token-by-token delta rule (here 64 tokens) computes the gated
-    norm in its own kernel; the chunked one (300 tokens) leaves it to a gnorm launch."""
     eng, _, _ = tiny
     prof = eng.profile(ids_for(9, 64))
     labels = {k for k, _ in prof}
-    assert {"embed", "norm", "in_proj", "conv", "gdn", "out_proj", "qkv", "qk_prep", "attn", "o_proj",
+    assert {"embed", "norm", "in_proj", "conv", "gdn", "gnorm", "out_proj", "qkv", "qk_prep", "attn", "o_proj",
             "gate_up", "silu", "down"} <= labels
-    assert "gnorm" not in labels
     assert all(ms >= 0 for _, ms in prof)
-    labels = {k for k, _ in eng.profile(ids_for(9, 300))}
-    assert {"gdn", "gnorm", "out_proj"} <= labels
 
 
 @pytest.mark.parametrize("lens", [(40, 25, 70, 64, 129), (5, 12, 20), (33,), (100, 24, 30)])
