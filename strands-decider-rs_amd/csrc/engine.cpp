@@ -472,6 +472,11 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
         SD_HIP(hipMemcpy(rope, table.data(), table.size() * 4, hipMemcpyHostToDevice));
     }
     use_graphs = !env_off("SD_GRAPHS");
+    {
+        const char* c = std::getenv("STRANDS_DECIDER_CHECKED");
+        checked = c && std::strcmp(c, "1") == 0;
+        if (checked) use_graphs = false;  // every step runs eagerly
+    }
     for (const LayerW& L : layers) {
         if (L.kind == SD_LINEAR_ATTENTION) max_n = std::max(max_n, L.in_proj.N);
         if (L.kind == SD_FULL_ATTENTION) max_n = std::max(max_n, L.qkv.N);
@@ -815,9 +820,32 @@ void Engine::restore(const Snapshot* cache, size_t P) {
     }
 }
 
+void Engine::run_checked(Plan& pl) {
+    std::vector<float> xh;
+    for (size_t i = 0; i < pl.steps.size(); i++) {
+        const Step& s = pl.steps[i];
+        s.run(st);
+        const hipError_t se = hipStreamSynchronize(st);
+        const hipError_t le = hipGetLastError();
+        if (se != hipSuccess || le != hipSuccess)
+            throw Error("checked forward: step " + std::to_string(i) + " (" + s.label + "): " +
+                        hipGetErrorString(se != hipSuccess ? se : le));
+        if (std::strcmp(s.label, "norm") != 0) continue;
+        xh.resize((size_t)pl.L * cfg.d);
+        SD_HIP(hipMemcpy(xh.data(), pool.x, xh.size() * 4, hipMemcpyDeviceToHost));
+        for (size_t e = 0; e < xh.size(); e++)
+            if (!std::isfinite(xh[e]))
+                throw Error("checked forward: step " + std::to_string(i) + " (norm): the residual stream holds a "
+                            "non-finite value at row " + std::to_string(e / cfg.d) + ", column " +
+                            std::to_string(e % cfg.d));
+    }
+}
+
 void Engine::launch_and_read(Plan& pl, size_t n_rows, bool timed, bool read) {
     if (timed) SD_HIP(hipEventRecord(ev0, st));
-    if (pl.exec) {
+    if (checked) {
+        run_checked(pl);
+    } else if (pl.exec) {
         SD_HIP(hipGraphLaunch(pl.exec, st));
     } else {
         for (auto& s : pl.steps) s.run(st);

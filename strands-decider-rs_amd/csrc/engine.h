@@ -151,6 +151,11 @@ struct Engine {
     void* snap_alloc(size_t bytes);
     void snap_release(void* p, size_t bytes) const;
     bool use_graphs = true;
+    // STRANDS_DECIDER_CHECKED=1 (the reference's switch for shader runtime checks, src/engine.rs:283,
+    // 335-338): every step runs eagerly and is synchronized, a GPU error names the step that raised
+    // it, and the residual stream is checked for non-finite values after every add + RMSNorm.
+    bool checked = false;
+    void run_checked(Plan& pl);
     bool gu_il = false;  // gate_up weights interleaved in groups of 16 rows (interleave_gate_up)
     Pool pool;
     std::map<int, Plan> plans;

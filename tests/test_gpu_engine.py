@@ -340,3 +340,53 @@ def test_load_rejects_matrices_sharing_memory_with_other_shapes(sdamd, tiny_mode
         assert np.isfinite(h).all()
     finally:
         eng.free()
+
+
+def test_checked_mode(sdamd, tiny_model, tmp_path, monkeypatch):
+    """STRANDS_DECIDER_CHECKED=1 (the reference's runtime-check switch, src/engine.rs:283, 335-338):
+    every step runs eagerly and is synchronized.  Results are bit-identical to the captured graphs',
+    and a residual stream gone non-finite is reported with the step that produced it (forced from
+    the host: one layer's out_proj scales set to f16 infinity), where the unchecked engine returns
+    the non-finite rows silently."""
+    import json
+    import os
+    import shutil
+    eng = sdamd.Engine.load(tiny_model)
+    monkeypatch.setenv("STRANDS_DECIDER_CHECKED", "1")
+    chk = sdamd.Engine.load(tiny_model)
+    monkeypatch.delenv("STRANDS_DECIDER_CHECKED")
+    try:
+        for L in (7, 100):
+            ids = ids_for(70 + L, L)
+            np.testing.assert_array_equal(chk.forward(ids, [0, L - 1]).hidden, eng.forward(ids, [0, L - 1]).hidden)
+    finally:
+        chk.free()
+        eng.free()
+    d = tmp_path / "inf"
+    shutil.copytree(tiny_model, d)
+    with open(d / "manifest.json") as f:
+        man = json.load(f)
+    t = man["tensors"]["layers.1.out_proj.s"]
+    sh = next(s for s in man["shards"] if s["start"] <= t["offset"] < s["start"] + s["bytes"])
+    path = d / sdamd.model.shard_file(man["shards"].index(sh))
+    raw = bytearray(path.read_bytes())
+    off = t["offset"] - sh["start"]
+    raw[off:off + t["bytes"]] = np.full(t["bytes"] // 2, 0x7C00, np.uint16).tobytes()
+    path.write_bytes(bytes(raw))
+    bad = sdamd.Engine.load(str(d))
+    try:
+        h = bad.forward(ids_for(80, 30), [29]).hidden
+        assert not np.isfinite(h).all()
+    finally:
+        bad.free()
+    monkeypatch.setenv("STRANDS_DECIDER_CHECKED", "1")
+    bad = sdamd.Engine.load(str(d))
+    monkeypatch.delenv("STRANDS_DECIDER_CHECKED")
+    try:
+        with pytest.raises(sdamd.EngineError, match=r"step \d+ \(norm\).*non-finite"):
+            bad.forward(ids_for(80, 30), [29])
+        # the error is raised before the rows are read back; the engine still works afterwards
+        with pytest.raises(sdamd.EngineError, match="non-finite"):
+            bad.forward(ids_for(81, 5), [4])
+    finally:
+        bad.free()
