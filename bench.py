@@ -9,9 +9,12 @@ reference's Decider::ask_all (src/lib.rs:183-199) on token ids; the three questi
 independent sequences of one batched forward (the same results as three forwards), and the head
 (src/head.rs:55-77, f64) runs on the device after it.
 
-Reported: `value` = prefill tokens/s (512-token state forwards), `ms_per_step` = ask_all latency
-(state prefill + 3 questions + head), plus the per-phase times (questions_ms: the batched question
-forward with the pointer head on the device), the roofline of the dominant kernel
+Reported: `value` = prefill tokens/s (512-token state forwards), `ask_all_ms` = the latency of
+ask_all as sd_ask_ids serves it (one forward of the state with the questions as branches of it,
+then the head), `ms_per_step` = the whole step (the snapshot path below, then that ask_all), plus
+the snapshot path's phases (prefill_ms: the state's forward with keep; questions_ms: the batched
+question forward from the snapshot with the pointer head on the device; their sum
+ask_all_snapshot_path_ms), the roofline of the dominant kernel
 class (the prefill int4 GEMM, timed live with HIP events on the stream it runs on) and the CPU
 baseline (the C oracle on the host cores, a bounded prefill sample of the same model).
 """
@@ -615,12 +618,14 @@ def kernel_bench(pkg, reps=50):
     return out
 
 
-def sweep_bench(eng, head, temp, n_states=64, n_q=8, seed=4):
+def sweep_bench(pkg, eng, head, temp, n_states=64, n_q=8, seed=4):
     """64 independent states of U[128, 2048] random tokens, each encoded once
     (forward with keep), then 8 questions of U[24, 64] tokens answered from its snapshot as one
     batched forward with the device head.  Aggregate prefill tokens/s; per-question latency = the
-    wall time of the batch that answers it.  A first pass over the same inputs builds the per-length
-    plans (captured graphs) and is reported separately as the cold pass."""
+    wall time of the batch that answers it.  Then each state's ask_all as sd_ask_ids serves it (one
+    forward of the state with its 8 questions as branches): its latency per state.  A first pass over
+    the same inputs builds the per-length plans (captured graphs) and is reported separately as the
+    cold pass."""
     import numpy as np
     import sdamd.synth as synth
     rng = np.random.default_rng(seed)
@@ -633,7 +638,7 @@ def sweep_bench(eng, head, temp, n_states=64, n_q=8, seed=4):
         work.append((state, qs, opts))
 
     def run_pass():
-        pre_tok, pre_s, q_lat = 0, 0.0, []
+        pre_tok, pre_s, q_lat, a_lat = 0, 0.0, [], []
         for state, qs, opts in work:
             t0 = time.perf_counter()
             snap = eng.forward(state, [], keep=True).snapshot
@@ -641,21 +646,27 @@ def sweep_bench(eng, head, temp, n_states=64, n_q=8, seed=4):
             eng.ask_batch(head, qs, opts, [temp] * n_q, cache=snap)
             t2 = time.perf_counter()
             snap.free()
+            pkg.ask_ids(eng, head, state, qs, opts, [temp] * n_q)
+            t3 = time.perf_counter()
             pre_tok += len(state)
             pre_s += t1 - t0
             q_lat.extend([t2 - t1] * n_q)
+            a_lat.append(t3 - t2)
         q_lat.sort()
-        return pre_tok / pre_s, q_lat
+        a_lat.sort()
+        return pre_tok / pre_s, q_lat, a_lat
 
     t = time.perf_counter()
-    cold_rate, _ = run_pass()
+    cold_rate, _, _ = run_pass()
     log(f"sweep cold pass (plans built) in {time.perf_counter() - t:.1f} s")
-    rate, q_lat = run_pass()
+    rate, q_lat, a_lat = run_pass()
     return {"metric": "configs[4] sweep: aggregate prefill tokens/s, per-question latency p50/p99 (ms)",
             "prefill_tokens_per_s": round(rate, 1), "cold_pass_prefill_tokens_per_s": round(cold_rate, 1),
             "states": n_states, "questions_per_state": n_q,
             "question_p50_ms": round(1e3 * q_lat[len(q_lat) // 2], 3),
             "question_p99_ms": round(1e3 * q_lat[min(len(q_lat) - 1, int(0.99 * len(q_lat)))], 3),
+            "ask_all_p50_ms": round(1e3 * a_lat[len(a_lat) // 2], 3),
+            "ask_all_p99_ms": round(1e3 * a_lat[min(len(a_lat) - 1, int(0.99 * len(a_lat)))], 3),
             "data": "synthetic: random-init 2B, uniform-random ids; lengths U[128, 2048], questions U[24, 64], "
                     "2-5 options each"}
 
@@ -761,7 +772,7 @@ def main():
         pmc_workload(eng, head, state, questions, temp, pkg)
         return
     if args.sweep:
-        print(json.dumps(sweep_bench(eng, head, temp)), flush=True)
+        print(json.dumps(sweep_bench(pkg, eng, head, temp)), flush=True)
         return
 
     def step():
@@ -774,24 +785,31 @@ def main():
         probs, qgpu = eng.ask_batch(head, questions, OPTIONS, [temp] * N_QUESTIONS, cache=snap, timed=True)
         t2 = time.perf_counter()
         snap.free()
-        return t1 - t0, t2 - t1, out.gpu_ms, [qgpu], probs
+        # ask_all as the library serves it (sd_ask_ids): one forward of the state with the three
+        # questions as branches of it, then the device head
+        tprobs = pkg.ask_ids(eng, head, state, questions, OPTIONS, [temp] * N_QUESTIONS)
+        t3 = time.perf_counter()
+        return t1 - t0, t2 - t1, t3 - t2, out.gpu_ms, [qgpu], probs, tprobs
 
     for i in range(args.warmup):
         step()
         log(f"warmup {i + 1}/{args.warmup} done")
     torch.cuda.synchronize()
-    pre, qs, pre_gpu, q_gpu = [], [], [], []
+    pre, qs, ask, pre_gpu, q_gpu = [], [], [], [], []
     t_start = time.perf_counter()
     for i in range(args.steps):
-        a, b, g, qg, probs = step()
+        a, b, c, g, qg, probs, tprobs = step()
         pre.append(a)
         qs.append(b)
+        ask.append(c)
         pre_gpu.append(g)
         q_gpu.extend(qg)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
     log(f"timed {args.steps} steps in {wall:.3f} s")
-    ask = [a + b for a, b in zip(pre, qs)]
+    snap_ask = [a + b for a, b in zip(pre, qs)]
+    # the two ask_all paths agree (the questions' matmul sizes and summation orders differ)
+    tree_dp = max(float(abs(x - y).max()) for x, y in zip(probs, tprobs))
     value = STATE_LEN * len(pre) / sum(pre)
     res = {
         "metric": "prefill tokens/s + ask_all latency (ms), 2B hybrid, 512-tok state, 1 GPU",
@@ -811,6 +829,8 @@ def main():
                    "questions": N_QUESTIONS, "question_tokens": Q_LEN, "options": [len(o) for o in OPTIONS]},
         "ask_all_ms": round(1e3 * statistics.mean(ask), 3),
         "ask_all_p50_ms": round(1e3 * statistics.median(ask), 3),
+        "ask_all_snapshot_path_ms": round(1e3 * statistics.mean(snap_ask), 3),
+        "ask_all_paths_max_dprob": tree_dp,
         "prefill_ms": round(1e3 * statistics.mean(pre), 3),
         "prefill_gpu_ms": round(statistics.mean(pre_gpu), 3),
         "questions_ms": round(1e3 * statistics.mean(qs), 3),

@@ -149,8 +149,14 @@ int sd_head_probs(const sd_head* h, const float* hidden, size_t n_rows, size_t d
                   double* probs_out, char* err, size_t errlen);
 
 /* The engine half of `Decider::run` (src/lib.rs:183-199) on token ids: one question is a single
- * forward of state ++ question; several share one forward of the state (keep = true) and continue
- * from its snapshot (as sd_engine_ask_batch).  options[i][0..n_options[i]) are option token
+ * forward of state ++ question.  Several questions, all longer than 20 tokens, at most 31 of them,
+ * with state + questions within the 4096-token context, run as ONE forward of the state with every
+ * question as a branch of it: each branch attends the state's rows and its own, and its delta rule
+ * continues from the state's final state and conv history, which is what the reference computes
+ * from the state's snapshot.  Otherwise the state runs once (keep = true) and the questions
+ * continue from its snapshot (as sd_engine_ask_batch).  STRANDS_DECIDER_TREE=0 in the environment
+ * turns the one-forward form off.  Either form leaves no snapshot behind; the live caches hold the
+ * last forward's rows.  options[i][0..n_options[i]) are option token
  * indices into question i; probs_out receives sum(n_options) probabilities, question by question.
  * The head runs on the device (f64). */
 int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_state, size_t n_questions,

@@ -136,8 +136,10 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     __shared__ float Mm[4][16], Lm[4][16];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int fq = lane & 15, fg = lane >> 4;
-    const int P = (int)lu[1];
-    SGPR_BATCH("s"(P), "s"(rowt), "s"(big), "s"(out), "s"(pacc), "s"(pml));
+    // cache rows below Pv are every sequence's shared prefix: the cached prefix (P) and, in a forward
+    // whose sequences continue one state sequence (lu[6] > 0), that state's rows too
+    const int P = (int)lu[1], Pv = P + (int)lu[6];
+    SGPR_BATCH("s"(P), "s"(Pv), "s"(rowt), "s"(big), "s"(out), "s"(pacc), "s"(pml));
     const int t0 = blockIdx.x * 16, h = blockIdx.y, z = blockIdx.z;
     const int kh = h / (s.HQ / s.HK);
     const int nq = min(16, L - t0);
@@ -147,8 +149,12 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     const float scale = 1.0f / sqrtf((float)HD);
     const int qpos = P + t0 + fq;  // cache row of this lane's query
     const bool qok = fq < nq;
-    // first cache row of the query's own sequence: rows [P, qlo) belong to other sequences
+    // first cache row of the query's own sequence: rows [Pv, qlo) belong to other sequences
     const int qlo = P + (rowt ? (int)(rowt[t0 + min(fq, nq - 1)] >> 16) : 0);
+    // the tile's first row starts the earliest sequence among its queries: a key block inside
+    // [Pv, qlo0) belongs to other sequences for every query, is wholly masked and is skipped (its
+    // softmax update would leave the running max, sum and output unchanged)
+    const int qlo0 = rowt ? P + (int)(rowt[t0] >> 16) : 0;
 
     // Q^T fragments (B operand): lane (query fq, group fg) holds Q[fq][32s + 8fg .. +8], pre-scaled
     // by 1/sqrt(hd) and rounded to f16 as the reference does.
@@ -176,6 +182,7 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     const f16* Vb = Vt + (size_t)kh * HD * s.ctx;
 
     for (int j0 = kbeg + wv * KB; j0 < kend; j0 += 4 * KB) {
+        if (j0 >= Pv && j0 + KB <= qlo0) continue;
         // Keys are ordered inside the 32-key block so that lane (query fq, group fg) ends up with the
         // probabilities of keys j0 + 8fg .. +7: row i of S^T tile tt is key j0 + 8(i/4) + 4tt + i%4.
         // Then the V^T fragment of lane (dim fq, group fg) is those 8 keys, one 16-byte load.  The
@@ -203,13 +210,13 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         float tmax = -INFINITY;
         // a block before every query of the workgroup (and, with several sequences, inside the
         // shared prefix) needs no mask; the rows of queries past nq are computed but never stored
-        const bool open = j0 + KB <= kend && j0 + KB <= P + t0 + 1 && (!rowt || j0 + KB <= P);
+        const bool open = j0 + KB <= kend && j0 + KB <= P + t0 + 1 && (!rowt || j0 + KB <= Pv);
 #pragma unroll
         for (int tt = 0; tt < 2; tt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int j = j0 + 8 * fg + 4 * tt + r;
-                const float v = (open || (qok && j < kend && j <= qpos && (j < P || j >= qlo))) ? st2[tt][r] * LOG2E
+                const float v = (open || (qok && j < kend && j <= qpos && (j < Pv || j >= qlo))) ? st2[tt][r] * LOG2E
                                                                                                 : -INFINITY;
                 sv[tt * 4 + r] = v;
                 tmax = fmaxf(tmax, v);

@@ -1,6 +1,7 @@
 // extern "C" entry points declared in include/sdhip.h.  Every call catches C++ exceptions and
 // reports them through (err, errlen), the C form of the reference's `crate::Error(String)`.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -175,6 +176,15 @@ int sd_head_probs(const sd_head* h, const float* hidden, size_t n_rows, size_t d
 
 namespace {
 
+// STRANDS_DECIDER_TREE=0 turns the one-forward ask_all off (the snapshot path then serves every call).
+bool tree_ask_enabled() {
+    static const bool on = [] {
+        const char* v = std::getenv("STRANDS_DECIDER_TREE");
+        return !(v && std::strcmp(v, "0") == 0);
+    }();
+    return on;
+}
+
 // The questions of an ask_all, each continuing from `prefix` (src/lib.rs:192-198), with the pointer
 // head on the device.  They run as independent sequences of batched forwards (the same results as
 // one forward each; the weights stream once per batch).  A batch holds questions of one matmul
@@ -281,8 +291,31 @@ int sd_ask_ids(sd_engine* e, const sd_head* h, const uint32_t* state, size_t n_s
                            probs_out, nullptr);
             return;
         }
-        // src/lib.rs:192-198: the state once, every question continuing from its snapshot.
+        // src/lib.rs:192-198: the state once, every question continuing from it.
         if (n_state == 0) throw sd::Error("context of 0 tokens: must be 1 to " + std::to_string(SD_CONTEXT));
+        // One forward holds the state and every question as branches of it when the questions are
+        // all longer than 20 tokens (their matmuls are then the tiled kernels', as in their own
+        // forwards) and state + questions fit the context; otherwise the state's snapshot, then the
+        // questions from it in batched forwards.
+        bool tree = n_questions + 1 <= (size_t)sd::SD_MAX_SEQS && tree_ask_enabled();
+        size_t total = n_state;
+        for (size_t i = 0; i < n_questions; i++) {
+            tree = tree && q_lens[i] > 20;
+            total += q_lens[i];
+        }
+        if (tree && total <= SD_CONTEXT) {
+            std::vector<uint32_t> ids;
+            std::vector<size_t> rows;
+            for (size_t i = 0; i < n_questions; i++) {
+                const size_t base = ids.size();
+                for (size_t k = 0; k < n_options[i]; k++) rows.push_back(base + options[i][k]);
+                rows.push_back(base + q_lens[i] - 1);
+                ids.insert(ids.end(), q_ids[i], q_ids[i] + q_lens[i]);
+            }
+            eng->ask_tree(*Hd(h), state, n_state, ids.data(), q_lens, n_questions, rows.data(), n_options,
+                          temperatures, false, probs_out, nullptr);
+            return;
+        }
         sd::Snapshot* prefix = nullptr;
         eng->forward(state, n_state, nullptr, 0, nullptr, true, false, nullptr, nullptr, &prefix);
         std::unique_ptr<sd::Snapshot> hold(prefix);

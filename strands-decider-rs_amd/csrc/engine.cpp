@@ -623,8 +623,8 @@ YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, cons
     return y;
 }
 
-Plan& Engine::plan(int L, int nseq, bool short_seqs) {
-    const int key = (L << 8) | (nseq << 1) | (short_seqs ? 1 : 0);
+Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree) {
+    const uint64_t key = (uint64_t)tree << 32 | (uint64_t)L << 8 | (uint64_t)nseq << 1 | (short_seqs ? 1u : 0u);
     auto it = plans.find(key);
     if (it != plans.end()) {
         it->second.used = ++plan_clock;
@@ -674,7 +674,26 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
             // conv and the delta rule read the prefix's history and state in place (from the snapshot
             // the lu block names, else the live arena) and write the live arena
             f16* hist_upd = nseq ? nullptr : W.hist;  // several sequences leave no history
-            if (recur && nseq) {
+            if (tree) {
+                // The state (rows 0 .. tree - 1) in chunks, as its own forward without a prefix: a
+                // fresh state, the cleared history, its final state and history into the live arena.
+                // Then the branches token by token from that state and history (lu has has_cache set
+                // and names no snapshot), through the sequence tables shifted past the state.
+                const int S = tree, nbr = nseq - 1;
+                const ConvIn cs{W.conv, W.hist, nullptr, W.hist_off};
+                steps.push_back({"gdn", [=](hipStream_t s) {
+                    gdn_prep(nullptr, P.big, gs, W.negA, W.dtb, S, P.gdn, cs, Segs{}, (S + 63) / 64, nullptr, s);
+                }});
+                steps.push_back({"gdn", [=](hipStream_t s) {
+                    gdn_scan(gs, S, P.gdn, W.state, nullptr, 0, P.of, Segs{}, 0, s, W.state_off, W.hist, P.big, W.hist_off);
+                }});
+                const Segs sgb{sg.row, sg.chunk, sg.seq + 1};
+                const ConvIn cb{W.conv, W.hist, sg.row, W.hist_off};
+                steps.push_back({"gdn", [=](hipStream_t s) {
+                    gdn_recur(nullptr, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, nullptr, sgb, nbr, s,
+                              W.state_off, W.hist_off, cb);
+                }});
+            } else if (recur && nseq) {
                 // several sequences update no history: the recurrence computes the conv itself
                 const ConvIn cin{W.conv, W.hist, sg.row, W.hist_off};
                 steps.push_back({"gdn", [=](hipStream_t s) {
@@ -776,10 +795,11 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs) {
 }
 
 void Engine::upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
-                    uint32_t chunks, uint32_t nseq, const Snapshot* cache) {
+                    uint32_t chunks, uint32_t nseq, const Snapshot* cache, uint32_t tree) {
     // lu, ids and rows (and the Segs tables a batch wrote before) in one host-to-device copy; the lu
-    // block names the snapshot whose states and histories the forward reads in place
-    const uint32_t v[8] = {(uint32_t)n, (uint32_t)P, SD_CONTEXT, has_cache ? 1u : 0u, chunks, nseq, 0u, 0u};
+    // block names the snapshot whose states and histories the forward reads in place; lu[6] = the
+    // state rows every branch of a tree forward shares (attention's shared prefix past P)
+    const uint32_t v[8] = {(uint32_t)n, (uint32_t)P, SD_CONTEXT, has_cache ? 1u : 0u, chunks, nseq, tree, 0u};
     std::memcpy(up_h, v, sizeof(v));
     const void* prefix = cache ? cache->arena : nullptr;
     std::memcpy(up_h + LU_PREFIX_BYTE, &prefix, sizeof(prefix));
@@ -1069,6 +1089,11 @@ void Engine::ask_batch(const Head& head, const uint32_t* ids, const size_t* lens
     SD_CHECK(n_rows < 65536, "ask_batch: too many rows");
     attach_head(head);
     Plan& pl = prepare_batch(ids, lens, nseq, rows, n_rows, cache);
+    ask_tail(pl, nseq, n_opts, temps, n_rows, n_prob, timed, probs, gpu_ms);
+}
+
+void Engine::ask_tail(Plan& pl, size_t nseq, const size_t* n_opts, const double* temps, size_t n_rows, size_t n_prob,
+                      bool timed, double* probs, double* gpu_ms) {
     ensure_head_bufs(n_rows, nseq);
     size_t r = 0, o = 0;
     for (size_t q = 0; q < nseq; q++) {
@@ -1094,6 +1119,68 @@ void Engine::ask_batch(const Head& head, const uint32_t* ids, const size_t* lens
     if (se != hipSuccess) throw Error(std::string("GPU: ") + hipGetErrorString(se));
     std::memcpy(probs, hb.probs_h, n_prob * 8);
     finish(0, nullptr, timed, gpu_ms);
+}
+
+void Engine::ask_tree(const Head& head, const uint32_t* state, size_t n_state, const uint32_t* ids, const size_t* lens,
+                      size_t nq, const size_t* rows, const size_t* n_opts, const double* temps, bool timed,
+                      double* probs, double* gpu_ms) {
+    if (nq == 0 || nq + 1 > (size_t)SD_MAX_SEQS)
+        throw Error("a tree forward holds 1 to " + std::to_string(SD_MAX_SEQS - 1) + " questions");
+    if (n_state == 0) throw Error("context of 0 tokens: must be 1 to " + std::to_string(SD_CONTEXT));
+    size_t nb = 0, n_rows = 0, n_prob = 0;
+    for (size_t q = 0; q < nq; q++) {
+        // the questions' matmuls must be the tiled kernels' (f16 dequant) as in their own forwards
+        if (lens[q] <= 20) throw Error("a tree forward needs questions of more than 20 tokens");
+        if (n_opts[q] == 0) throw Error("question " + std::to_string(q) + " has no options");
+        nb += lens[q];
+        n_rows += n_opts[q] + 1;
+        n_prob += n_opts[q];
+    }
+    SD_CHECK(n_rows < 65536, "ask_tree: too many rows");
+    const size_t n = n_state + nb;
+    if (n > SD_CONTEXT)
+        throw Error("context of " + std::to_string(n) + " tokens (state + every question): must be at most " +
+                    std::to_string(SD_CONTEXT));
+    for (size_t r = 0; r < n_rows; r++)
+        if (rows[r] >= nb) throw Error("row " + std::to_string(rows[r]) + " out of range for " + std::to_string(nb) + " tokens");
+    for (size_t i = 0; i < n_state; i++)
+        if (state[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(state[i]) + " out of range for vocab " + std::to_string(vocab));
+    for (size_t i = 0; i < nb; i++)
+        if (ids[i] >= (uint32_t)vocab) throw Error("token id " + std::to_string(ids[i]) + " out of range for vocab " + std::to_string(vocab));
+    attach_head(head);
+    const int L = (int)n, S = (int)n_state, nseq = (int)nq + 1;
+    ensure_pool(std::max(L, (int)n_rows));
+    Plan& pl = plan(L, nseq, false, S);
+    // Sequence tables (see Segs): sequence 0 the state, q + 1 question q.  A question row's index in
+    // its sequence is S + its own index (its RoPE position); its sequence starts at its first row.
+    uint32_t* rowt = reinterpret_cast<uint32_t*>(up_h + pool.off_seg_row);
+    uint32_t* chunkt = reinterpret_cast<uint32_t*>(up_h + pool.off_seg_chunk);
+    std::vector<uint32_t> seqt(SD_MAX_SEQS + nseq);
+    uint32_t nch = 0;
+    size_t s0 = 0;
+    for (int q = 0; q < nseq; q++) {
+        const size_t len = q == 0 ? n_state : lens[q - 1];
+        const size_t base = q == 0 ? 0 : n_state;
+        seqt[SD_MAX_SEQS + q] = (uint32_t)s0 | (uint32_t)(len << 16);
+        for (size_t i = 0; i < len; i++) rowt[s0 + i] = (uint32_t)(base + i) | (uint32_t)(s0 << 16);
+        const uint32_t first = nch;
+        for (size_t k = 0; k < len; k += 64)
+            chunkt[nch++] = (uint32_t)(s0 + k) | (uint32_t)(std::min<size_t>(64, len - k) << 16);
+        seqt[q] = first | ((nch - first) << 16);
+        s0 += len;
+    }
+    SD_CHECK((int)nch <= pool.seg_chunk_cap, "ask_tree: chunk table overflow");
+    std::memcpy(up_h + pool.off_seg_seq, seqt.data(), seqt.size() * 4);
+    up_dirty = pool.off_seg_seq + seqt.size() * 4;  // sent with the ids by upload()
+    std::vector<uint32_t> all(state, state + n_state);
+    all.insert(all.end(), ids, ids + nb);
+    std::vector<size_t> grows(rows, rows + n_rows);
+    for (size_t& r : grows) r += n_state;
+    // has_cache set with no snapshot named: the branches' delta rule starts from the live state and
+    // history, which the state's scan writes earlier in the same forward
+    upload(all.data(), n, grows.data(), n_rows, 0, true, nch, (uint32_t)nseq, nullptr, (uint32_t)S);
+    restore(nullptr, 0);  // the state starts from a cleared history (the live state is overwritten)
+    ask_tail(pl, nq, n_opts, temps, n_rows, n_prob, timed, probs, gpu_ms);
 }
 
 std::vector<std::pair<const char*, double>> Engine::profile(const uint32_t* ids, size_t n) {

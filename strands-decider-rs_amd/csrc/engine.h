@@ -158,7 +158,7 @@ struct Engine {
     void run_checked(Plan& pl);
     bool gu_il = false;  // gate_up weights interleaved in groups of 16 rows (interleave_gate_up)
     Pool pool;
-    std::map<int, Plan> plans;
+    std::map<uint64_t, Plan> plans;
     uint64_t plan_clock = 0;
     // Captured plans kept at most: each holds an instantiated graph of ~230 kernel nodes (the pool's
     // buffers are shared, so a plan costs no activation memory of its own).  Traffic with more
@@ -204,6 +204,16 @@ struct Engine {
     void ask_batch(const Head& head, const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows,
                    const size_t* n_opts, const double* temps, const Snapshot* cache, bool timed, double* probs,
                    double* gpu_ms);
+    // Decider::ask_all's engine half (src/lib.rs:192-198) in one forward: the state (n_state rows)
+    // and the questions (lens[q] rows each, > 20 tokens: the tiled matmuls' f16 dequant, as their
+    // own forwards use) as branches that continue from it.  The weights stream once for all rows.
+    // Each question's hidden rows and probabilities are those of its forward from the state's
+    // snapshot (within the parity tolerances: the matmul tiles differ with the row count).  rows,
+    // n_opts, temps, probs and gpu_ms as in ask_batch; rows index the questions' concatenation.
+    // No snapshot is kept.
+    void ask_tree(const Head& head, const uint32_t* state, size_t n_state, const uint32_t* ids, const size_t* lens,
+                  size_t nq, const size_t* rows, const size_t* n_opts, const double* temps, bool timed, double* probs,
+                  double* gpu_ms);
     std::vector<std::pair<const char*, double>> profile(const uint32_t* ids, size_t n);
     // The forward of `ids` from `cache` run step by step, copying after every residual add + RMSNorm
     // of the layers (each layer's in_norm, then its post_norm) the residual x (f32) and the
@@ -222,15 +232,21 @@ struct Engine {
     void ensure_pool(int l);
     // The plan for L rows: one sequence (nseq = 0) or nseq independent ones; short: the reference's
     // GEMV dequant (each sequence <= 20 tokens).
-    Plan& plan(int L, int nseq = 0, bool short_seqs = false);
+    // tree > 0: sequence 0 is a state of `tree` rows and sequences 1 .. nseq - 1 continue from it
+    // (their own rows attend to its rows, their delta rule starts from its final state), each as its
+    // own forward from the state's snapshot would; see ask_tree.
+    Plan& plan(int L, int nseq = 0, bool short_seqs = false, int tree = 0);
     void upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
-                uint32_t chunks, uint32_t nseq, const Snapshot* cache);
+                uint32_t chunks, uint32_t nseq, const Snapshot* cache, uint32_t tree = 0);
     void restore(const Snapshot* cache, size_t P);
     void launch_and_read(Plan& pl, size_t n_rows, bool timed, bool read = true);
     // Validation, sequence tables, upload and restore of a batched forward; returns its plan.
     Plan& prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq, const size_t* rows, size_t n_rows,
                         const Snapshot* cache);
     void attach_head(const Head& head);
+    // The common tail of ask_batch and ask_tree: the head tables, the forward, the device head.
+    void ask_tail(Plan& pl, size_t nseq, const size_t* n_opts, const double* temps, size_t n_rows, size_t n_prob,
+                  bool timed, double* probs, double* gpu_ms);
     void finish(size_t n_rows, float* hidden, bool timed, double* gpu_ms);
     void mm(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, f16* Y, int L, bool short_rows);
     YIn mm_y(std::vector<Step>& steps, const char* label, const f16* A, const Mat& m, int L, bool short_rows);

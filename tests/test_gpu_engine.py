@@ -75,6 +75,48 @@ def test_ask_ids_matches_oracle(tiny, sdamd):
     assert np.abs(one - got[0]).max() < PROB_TOL
 
 
+# (state tokens, question lengths): states shorter than the conv window (1-3 tokens: the branches'
+# conv reads the history the state's scan leaves), one whole chunk, 8 mixed lengths, and 31
+# questions (state + 31 branches = the 32 sequences a forward holds)
+TREE_CASES = [(1, [21, 40]), (2, [64, 23]), (3, [30, 64, 22]), (64, [65, 21]),
+              (130, [24, 33, 64, 21, 50, 41, 29, 60]), (200, [21] * 31)]
+
+
+@pytest.mark.parametrize("case", range(len(TREE_CASES)))
+def test_ask_ids_tree_matches_snapshot_path(tiny, sdamd, case):
+    """ask_ids with every question longer than 20 tokens runs one forward of the state with every
+    question as a branch of it (the branches attend the state's rows and their own; their delta rule
+    continues from the state's final state and history).  Each question's probabilities match the
+    snapshot path's (the state's forward with keep, then the questions from the snapshot,
+    src/lib.rs:192-198) and the oracle's forward of that question from the state's snapshot."""
+    eng, head, om = tiny
+    ns, lens = TREE_CASES[case]
+    state = ids_for(900 + case, ns)
+    qs = [ids_for(1000 + 50 * case + i, L) for i, L in enumerate(lens)]
+    options = [sorted(np.random.default_rng(2000 + 50 * case + i).choice(L - 1, 3, replace=False).tolist())
+               for i, L in enumerate(lens)]
+    temps = [1.0] * len(lens)
+    snap = eng.forward(state, [], keep=True).snapshot
+    via_snap, _ = eng.ask_batch(head, qs, options, temps, cache=snap)
+    got = sdamd.ask_ids(eng, head, state, qs, options, temps)
+    # the tree forward rewrote the live K/V rows and states: the same snapshot continuation again
+    # restores its prefix and gives the same bits
+    again, _ = eng.ask_batch(head, qs, options, temps, cache=snap)
+    snap.free()
+    for i in range(len(qs)):
+        np.testing.assert_array_equal(again[i], via_snap[i])
+    _, osnap = om.forward(state, [], keep=True)
+    for i, (q, o) in enumerate(zip(qs, options)):
+        h, _ = om.forward(q, list(o) + [len(q) - 1], cache=osnap)
+        want = om.probs(h, 1.0)
+        top = np.sort(want)
+        # these seeds' top-two margins are 0.0054 to 0.50: an argmax flip is a real error
+        assert top[-1] - top[-2] > 2 * PROB_TOL
+        assert np.abs(got[i] - via_snap[i]).max() < PROB_TOL, f"question {i}"
+        assert np.abs(got[i] - want).max() < PROB_TOL, f"question {i}"
+        assert int(np.argmax(got[i])) == int(np.argmax(want)), f"question {i}"
+
+
 def test_forward_errors(tiny, sdamd):
     eng, head, om = tiny
     with pytest.raises(sdamd.EngineError, match="must be 1 to 4096"):
