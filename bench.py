@@ -456,9 +456,10 @@ def traffic_summary(fetch_dir, write_dir, cfg, state_len):
 
 def trace_summary(trace_dir):
     """Per-kernel totals of a `rocprofv3 --kernel-trace` run of this script, then the kernels of the
-    last state prefill and of the last batched question forward, then the GEMM launches of the
-    roofline's eager forwards.  Each forward starts with one k_embed launch; the forwards of a step
-    alternate prefill, questions; the roofline's forwards follow a marker kernel of torch's."""
+    last state prefill, of the last batched question forward and of the last one-forward ask_all,
+    then the GEMM launches of the roofline's eager forwards.  Each forward starts with one k_embed
+    launch; a step's forwards are prefill, questions, ask_all; the roofline's forwards follow a
+    marker kernel of torch's."""
     import csv
     import glob
     rows = []
@@ -492,7 +493,8 @@ def trace_summary(trace_dir):
     steps_rows, roof_rows = rows[:mark], [r for r in rows[mark:] if not is_marker(r[2])]
     starts = [i for i, r in enumerate(steps_rows) if "k_embed" in r[2]]
     fwd = [steps_rows[a:b] for a, b in zip(starts, starts[1:] + [len(steps_rows)])]
-    for kind, idx in (("state prefill", range(0, len(fwd), 2)), ("batched question forward", range(1, len(fwd), 2))):
+    for kind, idx in (("state prefill", range(0, len(fwd), 3)), ("batched question forward", range(1, len(fwd), 3)),
+                      ("ask_all forward (the state with the questions as its branches)", range(2, len(fwd), 3))):
         idx = list(idx)
         if not idx:
             continue

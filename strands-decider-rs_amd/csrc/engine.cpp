@@ -743,14 +743,15 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree) {
             steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.post_norm, d, nullptr, L, P.h, nullptr, s); }});
         }
         {
-            // gate_up only feeds silu * mul: from 65 rows on it runs unsplit with silu * mul in the
-            // GEMM's epilogue (measured on MI355X at 120 rows: 15.7 us against 13.7 us split in two
-            // plus 4.9 us of silu_mul); otherwise silu_mul sums the split-K partials itself.  The
+            // gate_up only feeds silu * mul: from 65 to 2560 rows it runs unsplit with silu * mul in
+            // the GEMM's epilogue (measured on MI355X at 120 rows: 15.7 us against 13.7 us split in
+            // two plus 4.9 us of silu_mul; the measured plans up to 2560 rows are of the epilogue
+            // kernels); otherwise silu_mul sums the split-K partials itself.  The
             // GEMV rows apply silu * mul in the GEMV's epilogue when the weights are interleaved.
             const Mat m = W.gate_up;
             const bool exact = gemv_rows(m, sr);
             const bool il = gu_il;
-            const int cfu = !exact && m.K % 256 == 0 && L > 64 && L <= 1024 ? gemm_w4_plan(L, m.N, m.K, false, false, 0).cfg : -1;
+            const int cfu = !exact && m.K % 256 == 0 && L > 64 && L <= 2560 ? gemm_w4_plan(L, m.N, m.K, false, false, 0).cfg : -1;
             if (exact) {
                 const bool fused = il && m.tiled;
                 const GemvPlan gp = gemv_plan(L, m.N, m.K, m.tiled, fused ? 2 : 0, 0);

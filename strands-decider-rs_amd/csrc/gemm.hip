@@ -939,6 +939,72 @@ int pick_cfg(int M, bool exact) {
     return 8;  // (4, 2): the best prefill tile on MI355X in a sweep over the 2B's shapes
 }
 
+// Configuration indices into kCfgs used by the planner: the 64-wide-step 32x32 MFMA tiles (need K a
+// multiple of 256), the same with two k halves per workgroup (K a multiple of 512), and 16x16 tiles.
+constexpr int W21 = 18, W22 = 19, W41 = 20, W31 = 21, W42 = 23, W21h = 24, W41h = 25, W31h = 26;
+constexpr int T21 = 3, T31 = 4, T41 = 5;     // 16x16 (2,1), (3,1), (4,1)
+constexpr int P21 = 30, P31 = 31, P41 = 32;  // 16x16 (2,1), (3,1), (4,1), loads three steps ahead
+
+// Measured plans for the 2B hybrid's five matmul shapes at M = 256 .. 2560 (entry i for M in
+// (192 + 64 i, 256 + 64 i]): each configuration and split timed on MI355X with the weights cold (24
+// copies rotated, more than the 256 MB last-level cache holds, as a forward streams its layers'),
+// two runs on two boxes averaged; a split plan is charged the consumer's read of its f32 slots (at
+// 5 TB/s); an entry differs from the rules below only where it was at least 3 % faster.  The grid's
+// fill of the 256 CUs decides most entries: the best tile moves with M as the workgroup count
+// crosses multiples of one or two workgroups per CU.
+constexpr int kPlanRows = 37;
+struct MeasuredPlans {
+    int N, K;
+    GemmPlan at[kPlanRows];
+};
+const MeasuredPlans kMeasured[] = {
+    // gate_up (the SiLU epilogue)
+    {12288, 2048,
+     {
+         {W41h, 1}, {W21, 1}, {W31, 1}, {W31, 1}, {W21, 1}, {W41, 1}, {W41, 1}, {W31, 1},
+         {W31, 1}, {W21, 1}, {W31, 1}, {W31, 1}, {W41, 1}, {W31, 1}, {W31, 1}, {W31, 1},
+         {W42, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1},
+         {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1},
+         {W41, 1}, {W42, 1}, {W42, 1}, {W42, 1}, {W42, 1},
+     }},
+    // in_proj
+    {8256, 2048,
+     {
+         {W31h, 1}, {W41h, 1}, {W41h, 1}, {W21h, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W21, 1},
+         {W41, 1}, {W41, 1}, {W41, 1}, {W31, 1}, {W31, 1}, {W21, 1}, {W21, 1}, {W31, 1},
+         {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W42, 1}, {W42, 1},
+         {W42, 1}, {W42, 1}, {W42, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W41, 1},
+         {W42, 1}, {W42, 1}, {W42, 1}, {W42, 1}, {W42, 1},
+     }},
+    // qkv
+    {5120, 2048,
+     {
+         {W21h, 1}, {W21h, 1}, {W21h, 1}, {W31h, 1}, {W31h, 1}, {W31h, 1}, {W41h, 1}, {W41h, 1},
+         {W41h, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W21, 1},
+         {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W31, 1}, {W31, 1}, {W31, 1},
+         {W31, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1}, {W41, 1},
+         {W41, 1}, {W41, 1}, {W41, 1}, {W42, 1}, {W42, 1},
+     }},
+    // out_proj and o_proj (split-K partials)
+    {2048, 2048,
+     {
+         {W21, 4}, {W21h, 2}, {W21h, 2}, {W21h, 2}, {W21h, 2}, {W31h, 2}, {W31h, 2}, {W31h, 2},
+         {W31h, 2}, {W21h, 1}, {W21h, 1}, {W21h, 1}, {W21h, 1}, {W31h, 1}, {W31h, 1}, {W31h, 1},
+         {W31h, 1}, {W31h, 1}, {W31h, 1}, {W31h, 1}, {W31h, 1}, {W21, 1}, {W21, 1}, {W21, 1},
+         {W21, 1}, {W21, 1}, {W21, 1}, {W21, 1}, {W21, 1}, {W31, 1}, {W31, 1}, {W31, 1},
+         {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1}, {W31, 1},
+     }},
+    // down (split-K partials)
+    {2048, 6144,
+     {
+         {W21h, 4}, {W31h, 4}, {W31h, 4}, {W21, 4}, {W21h, 2}, {W31h, 2}, {W31h, 2}, {W31h, 2},
+         {W31h, 2}, {W41h, 2}, {W41h, 2}, {W41h, 2}, {W41h, 2}, {W31, 4}, {W31, 4}, {W31h, 1},
+         {W31h, 1}, {W31h, 1}, {W31h, 1}, {W31h, 1}, {W31h, 1}, {W41h, 1}, {W41h, 1}, {W41h, 1},
+         {W41h, 1}, {W41h, 1}, {W41h, 1}, {W41h, 1}, {W41h, 1}, {W31, 2}, {W31, 2}, {W31, 2},
+         {W31, 2}, {W41, 2}, {W41, 2}, {W41, 2}, {W22, 2},
+     }},
+};
+
 }  // namespace
 
 int gemm_w4_configs() { return kNumCfgs; }
@@ -947,11 +1013,6 @@ int gemm_w4_cfg(int M, bool exact) { return pick_cfg(M, exact); }
 
 GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t max_part_elems) {
     GemmPlan p{pick_cfg(M, exact), 1};
-    // Configuration indices into kCfgs: the 64-wide-step 32x32 MFMA tiles (need K a multiple of
-    // 256), the same with two k halves per workgroup (K a multiple of 512), and 16x16 tiles.
-    constexpr int W21 = 18, W41 = 20, W31 = 21, W21h = 24, W31h = 26;
-    constexpr int T21 = 3, T31 = 4, T41 = 5;  // 16x16 (2,1), (3,1), (4,1)
-    constexpr int P21 = 30, P31 = 31, P41 = 32;  // 16x16 (2,1), (3,1), (4,1), loads three steps ahead
     const bool wide_ok = K % 256 == 0, halves_ok = K % 512 == 0;
     auto fit = [&](GemmPlan q) {  // largest usable split <= q.ks
         const int steps = K / KSTEP;
@@ -961,6 +1022,12 @@ GemmPlan gemm_w4_plan(int M, int N, int K, bool exact, bool partial_ok, size_t m
             q.ks /= 2;
         return q;
     };
+    if (!exact && M >= 256 && M <= 256 + 64 * (kPlanRows - 1))
+        for (const MeasuredPlans& t : kMeasured)
+            if (t.N == N && t.K == K) {
+                const GemmPlan q = t.at[(M - 193) / 64];
+                if (q.ks == 1 || partial_ok) return fit(q);
+            }
     if (!exact && wide_ok && M >= 256 && M <= 1024) {
         // Prefill-sized M; from a sweep of the 2B's shapes at M = 512 on MI355X (random data, tiled
         // weights): N = 12288 with the SiLU epilogue: (2,1) 33.2 us, (4,1) 34.5 us (3 runs each on

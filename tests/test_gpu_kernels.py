@@ -232,6 +232,16 @@ def split_sum(part, ks, M, N):
     (120, 2048, 2048, False, 3, 4),    # question out_proj: 16x16 (2,1), 4 splits
     (120, 2048, 2048, False, 30, 4),   # the same, loads three steps ahead
     (120, 2048, 6144, False, 32, 4),   # 16x16 (4,1) three steps ahead, 4 splits
+    # the measured plans' splits (M between 256 and 2560)
+    (256, 2048, 2048, False, 18, 4),   # o_proj: (2,1), 4 splits
+    (300, 2048, 6144, False, 26, 4),   # down: (3,1) with k halves, 4 splits
+    (640, 2048, 6144, False, 26, 2),   # down: (3,1) with k halves, 2 splits
+    (330, 2048, 6144, False, 25, 2),   # down: (4,1) with k halves, 2 splits
+    (300, 2048, 6144, False, 21, 4),   # down: (3,1), 4 splits
+    (300, 2048, 6144, False, 20, 2),   # down: (4,1), 2 splits
+    (300, 2048, 6144, False, 19, 2),   # down: (2,2), 2 splits
+    (300, 2048, 6144, False, 24, 4),   # down: (2,1) with k halves, 4 splits
+    (300, 2048, 2048, False, 26, 1),   # o_proj: (3,1) with k halves, one slot
     (8, 2048, 2048, True, -1, 2),      # GEMV partials
     (8, 2048, 6144, True, -1, 4),
     (20, 2048, 2048, True, -1, 1),
@@ -250,7 +260,10 @@ def test_split_partials(sdamd, synth, oracle, M, N, K, exact, cfg, ks):
 
 
 @pytest.mark.parametrize("M,exact,cfg", [(8, True, -1), (17, True, -1), (120, False, 24), (120, False, 30),
-                                         (120, False, 33), (200, False, 30), (512, False, 18)])
+                                         (120, False, 33), (200, False, 30), (512, False, 18),
+                                         # the measured plans' tiles: (4,1) with k halves, (4,2),
+                                         # (3,1), (4,1)
+                                         (256, False, 25), (300, False, 23), (384, False, 21), (330, False, 20)])
 def test_gate_up_silu(sdamd, synth, oracle, M, exact, cfg):
     """gate_up with silu * mul in the epilogue (the engine's fused form).  (1) Against silu_mul of the
     same kernel family's unfused gate_up output: within one f16 ulp (the epilogue itself).  (2)
