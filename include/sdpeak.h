@@ -25,7 +25,13 @@ extern "C" {
  *  variant 0: v_mfma_f32_32x32x16_f16 alone, 4 independent accumulators per wave;
  *  variant 1: the prefill GEMM's (2,1) inner loop without memory traffic: per 16-k slice one int4
  *             word dequantized as the GEMM does, 2 A fragments from LDS, 2 MFMAs;
- *  variant 2: the same with 4 A fragments and 4 MFMAs per dequantized word (the (4,1) tiles). */
+ *  variant 2: the same with 4 A fragments and 4 MFMAs per dequantized word (the (4,1) tiles);
+ *  variants 3, 4, 5: variants 0, 1, 2 on realistic operands: random f16 signs and mantissas at
+ *             magnitudes 2^-3 to 1 (an RMSNorm output's), four operand sets taken in turn so that
+ *             consecutive MFMAs see different bits, a random scale per k slice.  MI355X's clock is
+ *             power-limited under MFMA load and the power grows with the operand bits that switch:
+ *             variants 0-2 (patterned operands, few switching bits) give the instruction-rate
+ *             ceiling, variants 3-5 the ceiling a GEMM on real data can reach. */
 int sd_peak_mfma(int variant, int wg_per_cu, int iters, int launches, void* stream, double* out, char* err,
                  size_t errlen);
 

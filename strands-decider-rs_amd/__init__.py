@@ -494,7 +494,8 @@ def peak_lib():
 
 
 def peak_mfma(variant: int, wg_per_cu: int, iters: int, launches: int, stream=None) -> dict:
-    """sd_peak_mfma: 0 MFMA alone, 1 the (2,1) GEMM loop mix, 2 the (4,1) mix (include/sdpeak.h)."""
+    """sd_peak_mfma: 0 MFMA alone, 1 the (2,1) GEMM loop mix, 2 the (4,1) mix; 3, 4, 5 the same on
+    random operands (include/sdpeak.h)."""
     out = np.zeros(4, np.float64)
     _call(peak_lib().sd_peak_mfma, variant, wg_per_cu, iters, launches, _sp(stream), _ptr(out))
     return {"ms": float(out[0]), "tflops": float(out[1]), "clock_ghz": float(out[2]), "cus": int(out[3])}

@@ -39,15 +39,28 @@ __device__ __forceinline__ void stamp_end(Stamp* st) {
     }
 }
 
-template <int NACC>
-__global__ __launch_bounds__(256) void k_mfma_loop(int iters, float* __restrict__ sink, Stamp* __restrict__ st) {
+// RAND: four operand sets per lane of random f16 (random signs and mantissas, magnitudes 2^-3 to 1,
+// like an RMSNorm output's) taken in turn, so that consecutive MFMAs see different bits as they do
+// in a GEMM; otherwise one set of 3-bit patterns for every MFMA (few bits switch: the instruction
+// rate at the clock such operands allow).
+template <int NACC, bool RAND>
+__global__ __launch_bounds__(256) void k_mfma_loop(int iters, const u32x4* __restrict__ rnd, float* __restrict__ sink,
+                                                   Stamp* __restrict__ st) {
     stamp_begin(st);
     const int lane = threadIdx.x & 63;
-    f16x8 a, b;
+    f16x8 a[4], b[4];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        a[e] = (f16)(0.001f * (float)((lane + e) & 7));
-        b[e] = (f16)(0.002f * (float)((lane * 3 + e) & 7));
+    for (int u = 0; u < 4; u++) {
+        if constexpr (RAND) {
+            a[u] = __builtin_bit_cast(f16x8, rnd[(threadIdx.x * 8 + 2 * u) & 2047]);
+            b[u] = __builtin_bit_cast(f16x8, rnd[(threadIdx.x * 8 + 2 * u + 1) & 2047]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                a[u][e] = (f16)(0.001f * (float)((lane + e) & 7));
+                b[u][e] = (f16)(0.002f * (float)((lane * 3 + e) & 7));
+            }
+        }
     }
     f32x16 acc[NACC];
 #pragma unroll
@@ -58,7 +71,7 @@ __global__ __launch_bounds__(256) void k_mfma_loop(int iters, float* __restrict_
 #pragma unroll
         for (int u = 0; u < 4; u++)
 #pragma unroll
-            for (int n = 0; n < NACC; n++) acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[n], 0, 0, 0);
+            for (int n = 0; n < NACC; n++) acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[u], b[u], acc[n], 0, 0, 0);
     }
     float s = 0.f;
 #pragma unroll
@@ -69,19 +82,31 @@ __global__ __launch_bounds__(256) void k_mfma_loop(int iters, float* __restrict_
     stamp_end(st);
 }
 
-template <int MT2>
-__global__ __launch_bounds__(256) void k_gemm_mix(int iters, const uint32_t* __restrict__ words, float* __restrict__ sink,
-                                                  Stamp* __restrict__ st) {
+// RAND: the A tile in LDS holds random f16 as k_mfma_loop's, and each k slice's scale is its own
+// random f16 of a trained model's magnitude; otherwise a patterned A tile and one scale.  The
+// weight words are random either way (the nibbles are what the dequant sees).
+template <int MT2, bool RAND>
+__global__ __launch_bounds__(256) void k_gemm_mix(int iters, const uint32_t* __restrict__ words, const u32x4* __restrict__ rnd,
+                                                  float* __restrict__ sink, Stamp* __restrict__ st) {
     stamp_begin(st);
     __shared__ __attribute__((aligned(16))) uint8_t lds[MT2 * 4096];
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, g = lane >> 5;
-    for (int i = tid; i < MT2 * 1024; i += 256) reinterpret_cast<uint32_t*>(lds)[i] = 0x1C001C00u ^ (uint32_t)(i & 0x3FF);
+    if constexpr (RAND) {
+        for (int i = tid; i < MT2 * 256; i += 256) reinterpret_cast<u32x4*>(lds)[i] = rnd[i & 2047];
+    } else {
+        for (int i = tid; i < MT2 * 1024; i += 256) reinterpret_cast<uint32_t*>(lds)[i] = 0x1C001C00u ^ (uint32_t)(i & 0x3FF);
+    }
     __syncthreads();
     uint32_t w[4];
 #pragma unroll
     for (int s = 0; s < 4; s++) w[s] = words[(lane * 4 + s) & 255];
-    const f16 scv = (f16)0.01f;
-    const f16x2 sc2 = f16x2{scv, scv};
+    f16x2 scs[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const f16 v = RAND ? __builtin_bit_cast(f16, (uint16_t)(0x2000u | (words[(lane * 4 + s + 1) & 255] & 0x3FFu)))
+                           : (f16)0.01f;
+        scs[s] = f16x2{v, v};
+    }
     // the GEMM's fragment offsets: row r, k-chunk 4g + s, XOR-swizzled by row pair
     uint32_t foff[4];
 #pragma unroll
@@ -95,16 +120,17 @@ __global__ __launch_bounds__(256) void k_gemm_mix(int iters, const uint32_t* __r
     // are produced while slice s's MFMAs run, one MFMA then its share of the dequant VALU
     // instructions then a fragment read
     constexpr int VPER = (13 + MT2 - 1) / MT2;
-    auto deq = [&](uint32_t word) {
+    auto deq = [&](uint32_t word, int s) {
         f16x2 p0, p1, p2, p3;
         nib_pairs(word, p0, p1, p2, p3);
+        const f16x2 sc2 = scs[s];
         return cat4(p0 * sc2, p1 * sc2, p2 * sc2, p3 * sc2);
     };
     auto frag = [&](int s, f16x8* af) {
 #pragma unroll
         for (int a = 0; a < MT2; a++) af[a] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(lds + a * 4096 + foff[s]));
     };
-    f16x8 bf0 = deq(w[0]);
+    f16x8 bf0 = deq(w[0], 0);
     for (int it = 0; it < iters; it++) {
         f16x8 af[2][MT2], bf[2];
         bf[0] = bf0;
@@ -115,9 +141,9 @@ __global__ __launch_bounds__(256) void k_gemm_mix(int iters, const uint32_t* __r
             const int cu = s & 1, nx = cu ^ 1;
             if (s < 3) {
                 frag(s + 1, af[nx]);
-                bf[nx] = deq(w[s + 1] ^ (uint32_t)it);
+                bf[nx] = deq(w[s + 1] ^ (uint32_t)it, s + 1);
             } else {
-                bf0 = deq(w[0] ^ (uint32_t)(it + 1));
+                bf0 = deq(w[0] ^ (uint32_t)(it + 1), 0);
             }
 #pragma unroll
             for (int a = 0; a < MT2; a++) acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cu], af[cu][a], acc[a], 0, 0, 0);
@@ -247,38 +273,65 @@ extern "C" int sd_peak_mfma(int variant, int wg_per_cu, int iters, int launches,
                             size_t errlen) {
     return sd::guarded(err, errlen, [&] {
         if (!out) throw sd::Error("sd_peak_mfma: null output");
-        if (variant < 0 || variant > 2) throw sd::Error("sd_peak_mfma: variant must be 0, 1 or 2");
+        if (variant < 0 || variant > 5) throw sd::Error("sd_peak_mfma: variant must be 0 to 5");
         if (wg_per_cu < 1 || wg_per_cu > 4 || iters < 1 || launches < 1)
             throw sd::Error("sd_peak_mfma: 1 to 4 workgroups per CU, iters and launches >= 1");
         const hipStream_t s = static_cast<hipStream_t>(stream);
         const int cus = sd::device_cus(), blocks = cus * wg_per_cu;
         float* sink = nullptr;
         uint32_t* words = nullptr;
+        sd::u32x4* rnd = nullptr;
         SD_HIP(hipMalloc(&sink, (size_t)blocks * 256 * 4));
         double ms = 0.0, ghz = 0.0;
         try {
             SD_HIP(hipMalloc(&words, 256 * 4));
-            std::vector<uint32_t> hw(256);
-            for (int i = 0; i < 256; i++) hw[i] = 0x9E3779B9u * (uint32_t)(i + 1);
+            SD_HIP(hipMalloc(&rnd, 2048 * 16));
+            std::vector<uint32_t> hw(256), hr(2048 * 4);
+            uint32_t x = 0x2545F491u;  // xorshift32
+            auto next = [&] {
+                x ^= x << 13;
+                x ^= x >> 17;
+                x ^= x << 5;
+                return x;
+            };
+            for (uint32_t& v : hw) v = next();
+            // f16 pairs: random sign and mantissa, exponent field 12 to 15 (2^-3 <= |v| < 1)
+            for (uint32_t& v : hr) {
+                const uint32_t b = next();
+                const uint32_t lo = (b & 0x83FFu) | ((12u + ((b >> 10) & 3u)) << 10);
+                const uint32_t c = next();
+                const uint32_t hi = (c & 0x83FFu) | ((12u + ((c >> 10) & 3u)) << 10);
+                v = lo | hi << 16;
+            }
             SD_HIP(hipMemcpy(words, hw.data(), 256 * 4, hipMemcpyHostToDevice));
+            SD_HIP(hipMemcpy(rnd, hr.data(), hr.size() * 4, hipMemcpyHostToDevice));
             sd::timed(launches, blocks, s, [&](void* st) {
                 auto* stp = static_cast<sd::Stamp*>(st);
                 if (variant == 0)
-                    hipLaunchKernelGGL(sd::k_mfma_loop<4>, dim3(blocks), dim3(256), 0, s, iters, sink, stp);
+                    hipLaunchKernelGGL((sd::k_mfma_loop<4, false>), dim3(blocks), dim3(256), 0, s, iters, rnd, sink, stp);
                 else if (variant == 1)
-                    hipLaunchKernelGGL(sd::k_gemm_mix<2>, dim3(blocks), dim3(256), 0, s, iters, words, sink, stp);
+                    hipLaunchKernelGGL((sd::k_gemm_mix<2, false>), dim3(blocks), dim3(256), 0, s, iters, words, rnd, sink, stp);
+                else if (variant == 2)
+                    hipLaunchKernelGGL((sd::k_gemm_mix<4, false>), dim3(blocks), dim3(256), 0, s, iters, words, rnd, sink, stp);
+                else if (variant == 3)
+                    hipLaunchKernelGGL((sd::k_mfma_loop<4, true>), dim3(blocks), dim3(256), 0, s, iters, rnd, sink, stp);
+                else if (variant == 4)
+                    hipLaunchKernelGGL((sd::k_gemm_mix<2, true>), dim3(blocks), dim3(256), 0, s, iters, words, rnd, sink, stp);
                 else
-                    hipLaunchKernelGGL(sd::k_gemm_mix<4>, dim3(blocks), dim3(256), 0, s, iters, words, sink, stp);
+                    hipLaunchKernelGGL((sd::k_gemm_mix<4, true>), dim3(blocks), dim3(256), 0, s, iters, words, rnd, sink, stp);
                 SD_HIP(hipGetLastError());
             }, ms, ghz);
         } catch (...) {
             (void)hipFree(sink);
             (void)hipFree(words);
+            (void)hipFree(rnd);
             throw;
         }
         SD_HIP(hipFree(sink));
         SD_HIP(hipFree(words));
-        const int mfma_per_wave_iter = variant == 0 ? 4 * 4 : variant == 1 ? 4 * 2 : 4 * 4;
+        SD_HIP(hipFree(rnd));
+        const int v3 = variant % 3;
+        const int mfma_per_wave_iter = v3 == 0 ? 4 * 4 : v3 == 1 ? 4 * 2 : 4 * 4;
         const double flops = (double)launches * blocks * 4 * iters * mfma_per_wave_iter * 32768.0;
         out[0] = ms;
         out[1] = flops / (ms * 1e-3) / 1e12;
