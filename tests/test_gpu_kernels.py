@@ -242,6 +242,10 @@ def split_sum(part, ks, M, N):
     (300, 2048, 6144, False, 19, 2),   # down: (2,2), 2 splits
     (300, 2048, 6144, False, 24, 4),   # down: (2,1) with k halves, 4 splits
     (300, 2048, 2048, False, 26, 1),   # o_proj: (3,1) with k halves, one slot
+    (72, 2048, 2048, False, 31, 4),    # question batches: 16x16 (3,1) three steps ahead, 4 splits
+    (150, 2048, 6144, False, 31, 4),
+    (150, 2048, 2048, False, 31, 2),
+    (240, 2048, 6144, False, 24, 4),   # (2,1) with k halves, 4 splits
     (8, 2048, 2048, True, -1, 2),      # GEMV partials
     (8, 2048, 6144, True, -1, 4),
     (20, 2048, 2048, True, -1, 1),
@@ -263,7 +267,10 @@ def test_split_partials(sdamd, synth, oracle, M, N, K, exact, cfg, ks):
                                          (120, False, 33), (200, False, 30), (512, False, 18),
                                          # the measured plans' tiles: (4,1) with k halves, (4,2),
                                          # (3,1), (4,1)
-                                         (256, False, 25), (300, False, 23), (384, False, 21), (330, False, 20)])
+                                         (256, False, 25), (300, False, 23), (384, False, 21), (330, False, 20),
+                                         # question batches: 16x16 (3,2) three steps ahead, (3,1)
+                                         # with k halves
+                                         (80, False, 34), (150, False, 26)])
 def test_gate_up_silu(sdamd, synth, oracle, M, exact, cfg):
     """gate_up with silu * mul in the epilogue (the engine's fused form).  (1) Against silu_mul of the
     same kernel family's unfused gate_up output: within one f16 ulp (the epilogue itself).  (2)
