@@ -9,6 +9,7 @@
 // keys, so that the fragment loads of a key block touch whole cache lines: K as [hk][ctx / 32]
 // [hd / 32][32 keys][32 dims] (a load of 16 keys x 8 dims reads pairs of consecutive keys' 64 bytes),
 // V transposed as [hk][ctx / 32][hd][32 keys] (a block's V^T is 16 KB of consecutive bytes).
+#include <climits>
 #include <cmath>
 
 #include "common.h"
@@ -134,7 +135,8 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     constexpr int KB = 32;        // keys per block
     __shared__ float Om[4][16][HD + 4];  // per-wave unnormalised outputs [query][dim]
     __shared__ float Mm[4][16], Lm[4][16];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // wv is wave-uniform (readfirstlane): the key loop below is then a scalar loop, not a divergent one
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fq = lane & 15, fg = lane >> 4;
     // cache rows below Pv are every sequence's shared prefix: the cached prefix (P) and, in a forward
     // whose sequences continue one state sequence (lu[6] > 0), that state's rows too
@@ -149,6 +151,9 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     const float scale = 1.0f / sqrtf((float)HD);
     const int qpos = P + t0 + fq;  // cache row of this lane's query
     const bool qok = fq < nq;
+    // keys below jend can be attended by this lane's query (none past nq): the causal limit and the
+    // split's end
+    const int jend = qok ? min(kend, qpos + 1) : INT_MIN;
     // first cache row of the query's own sequence: rows [Pv, qlo) belong to other sequences
     const int qlo = P + (rowt ? (int)(rowt[t0 + min(fq, nq - 1)] >> 16) : 0);
     // the tile's first row starts the earliest sequence among its queries: a key block inside
@@ -181,23 +186,39 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     const f16* Kb = Kc + (size_t)kh * s.ctx * HD;
     const f16* Vb = Vt + (size_t)kh * HD * s.ctx;
 
-    for (int j0 = kbeg + wv * KB; j0 < kend; j0 += 4 * KB) {
-        if (j0 >= Pv && j0 + KB <= qlo0) continue;
-        // Keys are ordered inside the 32-key block so that lane (query fq, group fg) ends up with the
-        // probabilities of keys j0 + 8fg .. +7: row i of S^T tile tt is key j0 + 8(i/4) + 4tt + i%4.
-        // Then the V^T fragment of lane (dim fq, group fg) is those 8 keys, one 16-byte load.  The
-        // V loads are issued with the K loads, ahead of the S MFMAs and the softmax.
-        f16x8 kf[2][NS], vf[ND];
+    // The wave's key blocks are kbeg + 32 wv + 128 n below kend; those wholly inside [Pv, qlo0) are
+    // skipped.  A block's K and V fragments are loaded one block ahead, into the other of two
+    // register sets, while the current block's MFMAs and softmax run (one wave per SIMD: no other
+    // wave hides a block's load latency).  Every step issues the same 32 loads (past the end they
+    // re-read the last block, never used), so the explicit vmcnt wait is exact.
+    auto next_block = [&](int j) {
+        if (j >= Pv && j + KB <= qlo0) j += ((qlo0 - KB - j) / (4 * KB) + 1) * (4 * KB);
+        return j;
+    };
+    // Keys are ordered inside the 32-key block so that lane (query fq, group fg) ends up with the
+    // probabilities of keys j0 + 8fg .. +7: row i of S^T tile tt is key j0 + 8(i/4) + 4tt + i%4.
+    // Then the V^T fragment of lane (dim fq, group fg) is those 8 keys, one 16-byte load.
+    // The loads of a block stay where they are issued, ahead of the block in flight: the compiler
+    // would otherwise sink them to their first use, a block later.  A memory clobber alone does not
+    // hold them (the cache pointers are restrict: no asm without them could write their memory), so
+    // the clobbering asm takes both pointers as operands.
+    const Rsrc rk = make_rsrc(Kb, (uint32_t)s.ctx * HD * 2u), rv = make_rsrc(Vb, (uint32_t)s.ctx * HD * 2u);
+    auto load = [&](int j, f16x8 (&kf)[2][NS], f16x8 (&vf)[ND]) {
+        const int jc = min(j, kend - 1);
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
-            const int key = min(j0 + 8 * (fq >> 2) + 4 * tt + (fq & 3), kend - 1);
-            const f16* krow = Kb + (size_t)(key >> 5) * (HD * 32) + (key & 31) * 32 + fg * 8;
+            const int key = min(jc + 8 * (fq >> 2) + 4 * tt + (fq & 3), kend - 1);
+            const uint32_t ko = (uint32_t)((key >> 5) * (HD * 32) + (key & 31) * 32 + fg * 8) * 2u;
 #pragma unroll
-            for (int st = 0; st < NS; st++) kf[tt][st] = *reinterpret_cast<const f16x8*>(krow + st * 1024);
+            for (int st = 0; st < NS; st++) kf[tt][st] = __builtin_bit_cast(f16x8, buf_b128(rk, ko, (uint32_t)st * 2048u));
         }
+        const uint32_t vo = (uint32_t)((jc >> 5) * (HD * 32) + fq * 32 + fg * 8) * 2u;
 #pragma unroll
-        for (int dt = 0; dt < ND; dt++)
-            vf[dt] = *reinterpret_cast<const f16x8*>(Vb + (size_t)(j0 >> 5) * (HD * 32) + (dt * 16 + fq) * 32 + fg * 8);
+        for (int dt = 0; dt < ND; dt++) vf[dt] = __builtin_bit_cast(f16x8, buf_b128(rv, vo, (uint32_t)dt * 1024u));
+        asm volatile("" ::"s"(Kb), "s"(Vb) : "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto process = [&](int j0, const f16x8 (&kf)[2][NS], const f16x8 (&vf)[ND]) {
         f32x4 st2[2];
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
@@ -215,9 +236,11 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         for (int tt = 0; tt < 2; tt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
+                // kept: below the lane's end and outside other sequences' rows (bitwise, not
+                // short-circuit operators: the short-circuit form compiled to a branch per key)
                 const int j = j0 + 8 * fg + 4 * tt + r;
-                const float v = (open || (qok && j < kend && j <= qpos && (j < Pv || j >= qlo))) ? st2[tt][r] * LOG2E
-                                                                                                : -INFINITY;
+                const bool keep = open | ((j < jend) & ((j < Pv) | (j >= qlo)));
+                const float v = keep ? st2[tt][r] * LOG2E : -INFINITY;
                 sv[tt * 4 + r] = v;
                 tmax = fmaxf(tmax, v);
             }
@@ -245,6 +268,23 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
             a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], ph, a, 0, 0, 0);
             acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pl, a, 0, 0, 0);
         }
+    };
+    constexpr int LOADS = 2 * NS + ND;  // vector-memory loads per block
+    f16x8 kA[2][NS], vA[ND], kB[2][NS], vB[ND];
+    int j = next_block(kbeg + wv * KB);
+    load(j, kA, vA);
+    while (j < kend) {
+        int jn = next_block(j + 4 * KB);
+        load(jn, kB, vB);
+        wait_loads<vmcnt_imm(LOADS)>();  // A's loads (and all before them) have arrived
+        process(j, kA, vA);
+        j = jn;
+        if (j >= kend) break;
+        jn = next_block(j + 4 * KB);
+        load(jn, kA, vA);
+        wait_loads<vmcnt_imm(LOADS)>();
+        process(j, kB, vB);
+        j = jn;
     }
     // merge the 4 waves: acc[dt][r] is O[query fq][dim 16dt + 4fg + r]
 #pragma unroll
