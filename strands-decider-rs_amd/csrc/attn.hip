@@ -173,12 +173,16 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
             for (int e = 0; e < 8; e++) qf[st][e] = (f16)((float)v[e] * scale);
         }
     }
-    // the output gates of this block's queries (dimension tid), loaded while the keys are processed;
-    // unconditionally (queries past nq read the last one's), as a load under a branch would be
-    // waited for before the next is issued
-    float gq[16];
-#pragma unroll
-    for (int q = 0; q < 16; q++) gq[q] = (float)big[(size_t)(t0 + min(q, nq - 1)) * s.stride + h * 2 * HD + HD + tid];
+    // The epilogue gives thread tid query qe = tid / 16 and the 16 dimensions d0 .. d0 + 15: its
+    // output gates are loaded here (two 16-byte loads, unconditionally: queries past nq read the
+    // last one's), while the keys are processed.
+    const int qe = tid >> 4, d0 = (tid & 15) * 16;
+    f16x8 gv[2];
+    {
+        const f16* gp = big + (size_t)(t0 + min(qe, nq - 1)) * s.stride + h * 2 * HD + HD + d0;
+        gv[0] = *reinterpret_cast<const f16x8*>(gp);
+        gv[1] = *reinterpret_cast<const f16x8*>(gp + 8);
+    }
     f32x4 acc[ND];
 #pragma unroll
     for (int dt = 0; dt < ND; dt++) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -315,32 +319,49 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         Ml[q][1] = l;
     }
     __syncthreads();
-    const int d = tid;  // one output dimension per thread, all 16 queries
-    // every LDS read first, then the stores (a store through a generic pointer keeps the compiler
-    // from moving LDS reads past it)
-    float av[16], ml[16][2];
+    // Thread (qe, d0): the 4 waves' partial outputs of query qe at dimensions d0 .. d0 + 15, summed
+    // in wave order (16-byte LDS reads), then 16-byte stores.  Every LDS read comes first (a store
+    // through a generic pointer keeps the compiler from moving LDS reads past it).
+    float av[16];
 #pragma unroll
-    for (int q = 0; q < 16; q++) {
-        float a = 0.f;
+    for (int u = 0; u < 16; u++) av[u] = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; w++) a += Om[w][q][d] * Fw[q][w];
-        av[q] = a;
-        ml[q][0] = Ml[q][0];
-        ml[q][1] = Ml[q][1];
+    for (int w = 0; w < 4; w++) {
+        const float f = Fw[qe][w];
+#pragma unroll
+        for (int u4 = 0; u4 < 4; u4++) {
+            const float4 v = *reinterpret_cast<const float4*>(&Om[w][qe][d0 + 4 * u4]);
+            av[4 * u4] += v.x * f;
+            av[4 * u4 + 1] += v.y * f;
+            av[4 * u4 + 2] += v.z * f;
+            av[4 * u4 + 3] += v.w * f;
+        }
     }
+    const float mq = Ml[qe][0], lq = Ml[qe][1];
+    if (qe >= nq) return;
+    const int t = t0 + qe;
+    if (ks == 1) {
+        // out = acc / l * sigmoid(gate), the sigmoid on the hardware exp2 and reciprocal (within about
+        // 1 ulp in f32, rounded to f16)
+        const float inv_l = 1.0f / lq;
+        f16x8 o8[2];
 #pragma unroll
-    for (int q = 0; q < 16; q++) {
-        if (q >= nq) continue;
-        const int t = t0 + q;
-        if (ks == 1) {
-            out[(size_t)t * s.HQ * HD + h * HD + d] = (f16)(av[q] / ml[q][1] / (1.0f + expf(-gq[q])));
-        } else {
-            const size_t r = ((size_t)z * L + t) * s.HQ + h;
-            pacc[r * HD + d] = av[q];
-            if (d == 0) {
-                pml[r * 2] = ml[q][0];
-                pml[r * 2 + 1] = ml[q][1];
-            }
+        for (int u = 0; u < 16; u++) {
+            const float g = (float)gv[u >> 3][u & 7];
+            const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -LOG2E));
+            o8[u >> 3][u & 7] = (f16)(av[u] * inv_l * sg);
+        }
+        f16* op = out + (size_t)t * s.HQ * HD + h * HD + d0;
+        *reinterpret_cast<f16x8*>(op) = o8[0];
+        *reinterpret_cast<f16x8*>(op + 8) = o8[1];
+    } else {
+        const size_t r = ((size_t)z * L + t) * s.HQ + h;
+        float4* pp = reinterpret_cast<float4*>(pacc + r * HD + d0);
+#pragma unroll
+        for (int u4 = 0; u4 < 4; u4++) pp[u4] = float4{av[4 * u4], av[4 * u4 + 1], av[4 * u4 + 2], av[4 * u4 + 3]};
+        if (d0 == 0) {
+            pml[r * 2] = mq;
+            pml[r * 2 + 1] = lq;
         }
     }
 }
@@ -374,7 +395,9 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ p
             l += lz[z] * f;
             a += az[z] * f;
         }
-    out[(size_t)t * s.HQ * HD + h * HD + d] = (f16)(a / l / (1.0f + expf(-g)));
+    // as k_attn's unsplit epilogue: acc / l * sigmoid(gate), the sigmoid on exp2 and the reciprocal
+    out[(size_t)t * s.HQ * HD + h * HD + d] =
+        (f16)(a * (1.0f / l) * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -LOG2E)));
 }
 
 }  // namespace
