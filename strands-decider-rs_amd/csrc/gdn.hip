@@ -1194,6 +1194,38 @@ __global__ __launch_bounds__(256) void k_gnorm(const float* __restrict__ o, cons
     *reinterpret_cast<f16x2*>(out + b) = r;
 }
 
+// The same with 16 lanes per (t, h) row, 8 values each: 16-byte loads of o, z and w and one 16-byte
+// store, 16 rows per workgroup (z_off and stride multiples of 8).  The sum of squares runs over the
+// lane's 8 values, then over the 16 lanes of the row.
+__global__ __launch_bounds__(256) void k_gnorm8(const float* __restrict__ o, const f16* __restrict__ big,
+                                                const float* __restrict__ w, f16* __restrict__ out, int L, int H,
+                                                int stride, int z_off) {
+    constexpr int DV = 128;
+    const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int l16 = threadIdx.x & 15;
+    if (row >= L * H) return;  // a row's 16 lanes exit together; the shuffles stay inside the row
+    const int t = row / H, h = row % H;
+    const size_t b = (size_t)t * H * DV + h * DV + 8 * l16;
+    const float4 v0 = *reinterpret_cast<const float4*>(o + b), v1 = *reinterpret_cast<const float4*>(o + b + 4);
+    const f16x8 z = *reinterpret_cast<const f16x8*>(big + (size_t)t * stride + z_off + h * DV + 8 * l16);
+    const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * l16), w1 = *reinterpret_cast<const float4*>(w + 8 * l16 + 4);
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; u++) ss += v[u] * v[u];
+#pragma unroll
+    for (int s = 8; s > 0; s >>= 1) ss += __shfl_xor(ss, s);
+    const float inv = 1.0f / sqrtf(ss / (float)DV + 1e-6f);
+    f16x8 r;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const float zu = (float)z[u];
+        r[u] = (f16)(wv[u] * v[u] * inv * zu / (1.0f + expf(-zu)));
+    }
+    *reinterpret_cast<f16x8*>(out + b) = r;
+}
+
 }  // namespace
 
 // Room for the chunks of `cap` rows split into up to SD_MAX_SEQS sequences.
@@ -1272,7 +1304,10 @@ void gnorm(const float* o, const f16* big, const GdnShape& s, const float* w, in
     SD_CHECK(s.DV == 128, "gnorm: only 128-wide value heads are supported");
     SD_CHECK(s.stride % 2 == 0 && s.z_off % 2 == 0, "gnorm: gate row stride and offset must be even");
     const int rows = L * s.H;
-    hipLaunchKernelGGL(k_gnorm, dim3((rows + 3) / 4), dim3(256), 0, st, o, big, w, out, L, s.H, s.DV, s.stride, s.z_off);
+    if (s.stride % 8 == 0 && s.z_off % 8 == 0)
+        hipLaunchKernelGGL(k_gnorm8, dim3((rows + 15) / 16), dim3(256), 0, st, o, big, w, out, L, s.H, s.stride, s.z_off);
+    else
+        hipLaunchKernelGGL(k_gnorm, dim3((rows + 3) / 4), dim3(256), 0, st, o, big, w, out, L, s.H, s.DV, s.stride, s.z_off);
     launched("gnorm");
 }
 
