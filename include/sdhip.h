@@ -257,7 +257,8 @@ int sd_op_gnorm(const void* o, const void* big, int stride, int z_off, const voi
  * [32 rows][32 dims], and the V cache Vt, transposed in blocks of 32 rows [HK][ctx/32][HD][32] (f16,
  * the engine's layouts), receive rows P .. P+L-1, rows below P are the prefix; out [L][HQ*HD] f16 the gated attention output.  big [L][stride]
  * holds [q | gate] per q head, then K, V heads; rope [ctx][RD/2][2] f32 (cos, sin).  head_dim 256
- * only, ctx a multiple of 32. */
+ * only, ctx a multiple of 32.  With RD 64 the attention normalizes and rotates the queries from big
+ * itself (as the engine's forward does) and Q is written for the caller only. */
 int sd_op_attention(const void* big, int stride, const void* qw, const void* kw, const void* rope, int L, int P, int HQ,
                     int HK, int HD, int RD, void* Q, void* Kc, void* Vt, int ctx, void* out, void* stream, char* err,
                     size_t errlen);

@@ -35,7 +35,8 @@ __global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, co
     // V^T, dimension by dimension: 8 contiguous bytes per dimension.
     static_assert(HD == 256, "qk_prep is written for 256-wide heads");
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int t0 = blockIdx.x * 4, slot = blockIdx.y;
+    // without Q the grid covers the kv heads only (the attention kernel computes its queries itself)
+    const int t0 = blockIdx.x * 4, slot = Q ? (int)blockIdx.y : s.HQ + (int)blockIdx.y;
     const int P = (int)lu[1];
     const bool isq = slot < s.HQ;
     const int k_off = 2 * s.HQ * HD, v_off = k_off + s.HK * HD;
@@ -122,12 +123,13 @@ __device__ __forceinline__ float wave_sum16(float v) {
 // split into f16 hi + lo (two MFMAs) so that the product keeps the reference's f32 P.V to about 22
 // bits.  With ks > 1 the workgroups along z also split the keys
 // and write unnormalised (acc, max, sum) for k_attn_combine.
-template <int HD>
+template <int HD, int QRD>
 __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f16* __restrict__ Kc,
                                               const f16* __restrict__ Vt, const uint32_t* __restrict__ lu, int L,
                                               int HQ, int HK, int stride, int ctx, int ks,
                                               const uint32_t* __restrict__ rowt, const f16* __restrict__ big,
-                                              f16* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml) {
+                                              f16* __restrict__ out, float* __restrict__ pacc, float* __restrict__ pml,
+                                              const float* __restrict__ qw, const float* __restrict__ rope, int RD) {
     const AttnShape s{HQ, HK, HD, 0, stride, ctx};
     static_assert(HD == 256, "attention is written for 256-wide heads");
     constexpr int ND = HD / 16;   // 16 output dimension tiles
@@ -135,6 +137,7 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     constexpr int KB = 32;        // keys per block
     __shared__ float Om[4][16][HD + 4];  // per-wave unnormalised outputs [query][dim]
     __shared__ float Mm[4][16], Lm[4][16];
+    __shared__ __align__(16) f16 Qs[16][HD + 8];  // the workgroup's queries, scaled (row padding: no bank conflicts on the fragment reads)
     // wv is wave-uniform (readfirstlane): the key loop below is then a scalar loop, not a divergent one
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fq = lane & 15, fg = lane >> 4;
@@ -154,25 +157,22 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     // keys below jend can be attended by this lane's query (none past nq): the causal limit and the
     // split's end
     const int jend = qok ? min(kend, qpos + 1) : INT_MIN;
+    // The row table words of this lane's query and of the tile's first row: buffer loads, issued
+    // together and without a branch (a null table is a 0-byte buffer, whose loads read 0).
+    const Rsrc rr = make_rsrc(rowt, rowt ? (uint32_t)L * 4u : 0u);
+    const uint32_t rwq = buf_b32(rr, (uint32_t)(t0 + min(fq, nq - 1)) * 4u, 0);
+    const uint32_t rw0 = buf_b32(rr, (uint32_t)t0 * 4u, 0);
+    // and, for the fused query norm and RoPE, that of query 4 wv + lane / 16 (read for its position)
+    const uint32_t rwp = QRD ? buf_b32(rr, (uint32_t)(t0 + min(4 * wv + (lane >> 4), nq - 1)) * 4u, 0) : 0u;
     // first cache row of the query's own sequence: rows [Pv, qlo) belong to other sequences
-    const int qlo = P + (rowt ? (int)(rowt[t0 + min(fq, nq - 1)] >> 16) : 0);
+    const int qlo = P + (int)(rwq >> 16);
     // the tile's first row starts the earliest sequence among its queries: a key block inside
     // [Pv, qlo0) belongs to other sequences for every query, is wholly masked and is skipped (its
     // softmax update would leave the running max, sum and output unchanged)
-    const int qlo0 = rowt ? P + (int)(rowt[t0] >> 16) : 0;
+    const int qlo0 = P + (int)(rw0 >> 16);
 
-    // Q^T fragments (B operand): lane (query fq, group fg) holds Q[fq][32s + 8fg .. +8], pre-scaled
-    // by 1/sqrt(hd) and rounded to f16 as the reference does.
+    // Q^T fragments (B operand), filled after the first key block's loads are issued
     f16x8 qf[NS];
-    {
-        const f16* qrow = Q + ((size_t)h * L + t0 + min(fq, nq - 1)) * HD;
-#pragma unroll
-        for (int st = 0; st < NS; st++) {
-            const f16x8 v = *reinterpret_cast<const f16x8*>(qrow + st * 32 + fg * 8);
-#pragma unroll
-            for (int e = 0; e < 8; e++) qf[st][e] = (f16)((float)v[e] * scale);
-        }
-    }
     // The epilogue gives thread tid query qe = tid / 16 and the 16 dimensions d0 .. d0 + 15: its
     // output gates are loaded here (two 16-byte loads, unconditionally: queries past nq read the
     // last one's), while the keys are processed.
@@ -275,8 +275,94 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     };
     constexpr int LOADS = 2 * NS + ND;  // vector-memory loads per block
     f16x8 kA[2][NS], vA[ND], kB[2][NS], vB[ND];
+    // Q^T fragments: lane (query fq, group fg) holds Q[fq][32s + 8fg .. +8], pre-scaled by 1/sqrt(hd)
+    // and rounded to f16 as the reference does.  The 4 waves prepare them together: wave w takes
+    // queries 4w .. 4w + 3, lane (query qq, part kq) two 8-dim chunks c0, c1 of query qq, and writes
+    // them to LDS, from where every wave reads its fragments.  Their loads are issued before the
+    // first key block's and waited for alone (they are the older ones), so that the computation
+    // runs while the block is in flight.
+    //
+    // QRD = RD: the query's RMSNorm and rotate-half RoPE are done here (the reference's qk_prep for
+    // q, src/kernels.rs:400-448): q = x rsqrt(mean(x^2) + 1e-6) w, dims d < RD rotated at the row's
+    // RoPE position, rounded to f16, then scaled.  Chunk c (dims 8c .. 8c + 7) of a rotated half
+    // pairs with chunk c + NR: part kq < NR takes chunks kq and kq + NR (one cos/sin row for both),
+    // part kq >= NR the unrotated chunks 2kq and 2kq + 1 (with QRD = 0 every part: dims 16kq ..
+    // 16kq + 15 of the Q row).  The sum of squares is the 16 parts' (lanes 16 apart never mix).
+    constexpr int RD2 = QRD / 2, NR = RD2 / 8;
+    static_assert(QRD % 16 == 0 && QRD <= HD, "the fused query needs rotary_dim a multiple of 16");
+    const int qq = 4 * wv + (lane >> 4), kq = lane & 15;
+    const int tq = t0 + min(qq, nq - 1);
+    const bool rot = kq < NR;
+    const int c0 = rot ? kq : 2 * kq, c1 = rot ? kq + NR : 2 * kq + 1;
+    f16x8 xv[2];
+    float4 wq[2][2], cs4[4];
+    if constexpr (QRD == 0) {
+        const f16* qrow = Q + ((size_t)h * L + tq) * HD;
+        xv[0] = *reinterpret_cast<const f16x8*>(qrow + 8 * c0);
+        xv[1] = *reinterpret_cast<const f16x8*>(qrow + 8 * c1);
+        // (the clobber holds the loads here: it takes the pointer, so it may write their memory)
+        asm volatile("" ::"s"(Q) : "memory");
+    } else {
+        const f16* xrow = big + (size_t)tq * s.stride + h * 2 * HD;
+        // unrotated parts read a rotated part's cos/sin row and do not use it
+        xv[0] = *reinterpret_cast<const f16x8*>(xrow + 8 * c0);
+        xv[1] = *reinterpret_cast<const f16x8*>(xrow + 8 * c1);
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) wq[c][u] = *reinterpret_cast<const float4*>(qw + 8 * (c ? c1 : c0) + 4 * u);
+        const int rpos = P + (rowt ? (int)(rwp & 0xFFFFu) : tq);
+        const float* rp = rope + ((size_t)rpos * RD2 + 8 * (kq % NR)) * 2;
+#pragma unroll
+        for (int u = 0; u < 4; u++) cs4[u] = *reinterpret_cast<const float4*>(rp + 4 * u);
+        asm volatile("" ::"s"(big), "s"(qw), "s"(rope) : "memory");
+    }
+    __builtin_amdgcn_sched_barrier(0);
     int j = next_block(kbeg + wv * KB);
     load(j, kA, vA);
+    {
+        f16x8 q8[2];
+        if constexpr (QRD == 0) {
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) q8[c][e] = (f16)((float)xv[c][e] * scale);
+        } else {
+            float x[2][8], sp[2] = {0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    x[c][e] = (float)xv[c][e];
+                    sp[c] += x[c][e] * x[c][e];
+                }
+            float ss = sp[0] + sp[1];
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
+            const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const float w8[8] = {wq[c][0].x, wq[c][0].y, wq[c][0].z, wq[c][0].w,
+                                     wq[c][1].x, wq[c][1].y, wq[c][1].z, wq[c][1].w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[c][e] = x[c][e] * inv * w8[e];
+            }
+            const float cs[16] = {cs4[0].x, cs4[0].y, cs4[0].z, cs4[0].w, cs4[1].x, cs4[1].y, cs4[1].z, cs4[1].w,
+                                  cs4[2].x, cs4[2].y, cs4[2].z, cs4[2].w, cs4[3].x, cs4[3].y, cs4[3].z, cs4[3].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float c = cs[2 * e], sn = cs[2 * e + 1], a = x[0][e], bb = x[1][e];
+                const float lo = rot ? a * c - bb * sn : a, hi = rot ? bb * c + a * sn : bb;
+                q8[0][e] = (f16)((float)(f16)lo * scale);
+                q8[1][e] = (f16)((float)(f16)hi * scale);
+            }
+        }
+        *reinterpret_cast<f16x8*>(&Qs[qq][8 * c0]) = q8[0];
+        *reinterpret_cast<f16x8*>(&Qs[qq][8 * c1]) = q8[1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < NS; st++) qf[st] = *reinterpret_cast<const f16x8*>(&Qs[fq][st * 32 + fg * 8]);
     while (j < kend) {
         int jn = next_block(j + 4 * KB);
         load(jn, kB, vB);
@@ -408,8 +494,8 @@ void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* k
     SD_CHECK(s.RD % 2 == 0 && s.RD <= s.HD, "attention: bad rotary_dim");
     SD_CHECK(s.RD % 8 == 0 && s.stride % 4 == 0, "attention: rotary_dim must be a multiple of 8, the row stride of 4");
     SD_CHECK(s.ctx % 32 == 0, "attention: the cache length must be a multiple of 32");
-    hipLaunchKernelGGL(k_qk_prep<256>, dim3((L + 3) / 4, s.HQ + s.HK), dim3(256), 0, st, big, lu, L, s.HQ, s.HK, s.RD,
-                       s.stride, s.ctx, sg.row, qw, kw, rope, Q, Kc, Vc);
+    hipLaunchKernelGGL(k_qk_prep<256>, dim3((L + 3) / 4, Q ? s.HQ + s.HK : s.HK), dim3(256), 0, st, big, lu, L, s.HQ,
+                       s.HK, s.RD, s.stride, s.ctx, sg.row, qw, kw, rope, Q, Kc, Vc);
     launched("qk_prep");
 }
 
@@ -417,14 +503,20 @@ void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* k
 size_t attn_ws_floats(int rows, const AttnShape& s) { return (size_t)ATTN_KS_MAX * rows * s.HQ * (s.HD + 2); }
 
 void attention_split(const f16* Q, const f16* Kc, const f16* Vc, const f16* big, const AttnShape& s, int L,
-                     const uint32_t* lu, const Segs& sg, int ks, float* ws, f16* out, hipStream_t st) {
+                     const uint32_t* lu, const Segs& sg, int ks, float* ws, f16* out, hipStream_t st, const float* qw,
+                     const float* rope) {
     SD_CHECK(s.HD == 256 && s.HQ % s.HK == 0, "attention: unsupported head shape");
+    SD_CHECK(Q || (qw && rope && s.RD == 64), "attention: the fused query norm and RoPE take rotary_dim 64");
     SD_CHECK(ks >= 1 && ks <= ATTN_KS_MAX, "attention: 1 to 8 key splits");
     const int nb = (L + BQ - 1) / BQ;
     float* pacc = ws;
     float* pml = ws + (size_t)ks * L * s.HQ * s.HD;
-    hipLaunchKernelGGL(k_attn<256>, dim3(nb, s.HQ, ks), dim3(256), 0, st, Q, Kc, Vc, lu, L, s.HQ, s.HK, s.stride, s.ctx,
-                       ks, sg.row, big, out, pacc, pml);
+    if (Q)
+        hipLaunchKernelGGL((k_attn<256, 0>), dim3(nb, s.HQ, ks), dim3(256), 0, st, Q, Kc, Vc, lu, L, s.HQ, s.HK, s.stride,
+                           s.ctx, ks, sg.row, big, out, pacc, pml, qw, rope, s.RD);
+    else
+        hipLaunchKernelGGL((k_attn<256, 64>), dim3(nb, s.HQ, ks), dim3(256), 0, st, Q, Kc, Vc, lu, L, s.HQ, s.HK, s.stride,
+                           s.ctx, ks, sg.row, big, out, pacc, pml, qw, rope, s.RD);
     launched("attn");
     if (ks > 1) {
         hipLaunchKernelGGL(k_attn_combine<256>, dim3(L, s.HQ), dim3(256), 0, st, pacc, pml, big, out, L, ks, s.HQ,

@@ -575,9 +575,12 @@ int sd_op_attention(const void* big, int stride, const void* qw, const void* kw,
         sd::qk_prep(static_cast<const sd::f16*>(big), as, static_cast<const float*>(qw), static_cast<const float*>(kw),
                     static_cast<const float*>(rope), L, lu, sd::Segs{}, static_cast<sd::f16*>(Q), static_cast<sd::f16*>(Kc),
                     static_cast<sd::f16*>(Vt), st);
-        sd::attention_split(static_cast<const sd::f16*>(Q), static_cast<const sd::f16*>(Kc), static_cast<const sd::f16*>(Vt),
-                            static_cast<const sd::f16*>(big), as, L, lu, sd::Segs{}, ks,
-                            reinterpret_cast<float*>(static_cast<uint8_t*>(w.attn) + 256), static_cast<sd::f16*>(out), st);
+        // rotary_dim 64: the attention normalizes and rotates the queries itself, as in the engine (Q
+        // is still written above for the caller)
+        sd::attention_split(RD == 64 ? nullptr : static_cast<const sd::f16*>(Q), static_cast<const sd::f16*>(Kc),
+                            static_cast<const sd::f16*>(Vt), static_cast<const sd::f16*>(big), as, L, lu, sd::Segs{}, ks,
+                            reinterpret_cast<float*>(static_cast<uint8_t*>(w.attn) + 256), static_cast<sd::f16*>(out), st,
+                            static_cast<const float*>(qw), static_cast<const float*>(rope));
     });
 }
 

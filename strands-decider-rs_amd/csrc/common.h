@@ -232,14 +232,17 @@ void unrotate_rows(float* rows, int n_rows, int d, const double* unrot, hipStrea
 struct AttnShape {
     int HQ, HK, HD, RD, stride, ctx;
 };
-// RoPE position of row r = P + its index in its sequence; cache row = P + r.
+// RoPE position of row r = P + its index in its sequence; cache row = P + r.  Q null: the kv heads
+// only (attention_split then computes the queries itself).
 void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* kw, const float* rope, int L,
              const uint32_t* lu, const Segs& sg, f16* Q, f16* Kc, f16* Vc, hipStream_t st);
 // Workspace (floats) of the key-split path for up to `rows` query rows and 8 splits.
 size_t attn_ws_floats(int rows, const AttnShape& s);
 // ks = number of key splits (1: no workspace needed; ks > 1 needs rows = L in the workspace).
 // Row r attends the prefix (cache rows < P) and its own sequence up to itself.
+// Q null: each workgroup computes its queries' RMSNorm (qw) and RoPE (rope, rotary_dim 64) from big.
 void attention_split(const f16* Q, const f16* Kc, const f16* Vc, const f16* big, const AttnShape& s, int L,
-                     const uint32_t* lu, const Segs& sg, int ks, float* ws, f16* out, hipStream_t st);
+                     const uint32_t* lu, const Segs& sg, int ks, float* ws, f16* out, hipStream_t st,
+                     const float* qw = nullptr, const float* rope = nullptr);
 
 }  // namespace sd

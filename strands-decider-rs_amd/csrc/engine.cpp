@@ -726,15 +726,18 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree) {
             const AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, W.qkv.N, SD_CONTEXT};
             const float* rp = rope;
             mm(steps, "qkv", P.h, W.qkv, P.big, L, sr);
+            // rotary_dim 64: each attention workgroup normalizes and rotates its own queries, and
+            // qk_prep writes only the K and V cache rows (which other workgroups read)
+            f16* const qbuf = cfg.rd == 64 ? nullptr : P.q;
             steps.push_back({"qk_prep", [=](hipStream_t s) {
-                qk_prep(P.big, as, W.q_norm, W.k_norm, rp, L, luv, sg, P.q, W.kc, W.vc, s);
+                qk_prep(P.big, as, W.q_norm, W.k_norm, rp, L, luv, sg, qbuf, W.kc, W.vc, s);
             }});
             const int nb = (L + 15) / 16;
             int ks = 1;
             if (L <= P.attn_rows)
                 while (ks < 8 && nb * cfg.hq * ks < 256) ks *= 2;
             steps.push_back({"attn", [=](hipStream_t s) {
-                attention_split(P.q, W.kc, W.vc, P.big, as, L, luv, sg, ks, P.attn_ws, P.o, s);
+                attention_split(qbuf, W.kc, W.vc, P.big, as, L, luv, sg, ks, P.attn_ws, P.o, s, W.q_norm, rp);
             }});
             y = mm_y(steps, "o_proj", P.o, W.o_proj, L, sr);
         }

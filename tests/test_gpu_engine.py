@@ -289,6 +289,31 @@ def test_rotated_torso_unrotate_on_device(sdamd, synth, oracle, tmp_path_factory
         eng.free()
 
 
+def test_rotary_32_forward_and_questions(sdamd, synth, oracle, tmp_path_factory):
+    """rotary_dim 32: the attention reads the queries qk_prep wrote (with rotary_dim 64, the tiny and
+    2B configs' value, it normalizes and rotates them itself); a forward and a one-forward ask_ids
+    against the oracle."""
+    cfg = dict(synth.CONFIG_TINY, rotary_dim=32)
+    path = synth.write_model(str(tmp_path_factory.mktemp("rd32")), cfg, vocab=4096, seed=2)
+    eng, head, _ = sdamd.load_decider(path)
+    om = oracle.OracleModel(path)
+    try:
+        state, q = ids_for(90, 70), ids_for(91, 33)
+        rows = [0, 17, 32]
+        got = eng.forward(np.concatenate([state, q]), [70 + r for r in rows]).hidden
+        want, _ = om.forward(np.concatenate([state, q]), [70 + r for r in rows])
+        assert np.abs(got - want).max() < HIDDEN_TOL
+        qs = [q, ids_for(92, 25), ids_for(93, 41)]
+        options = [[4, 12], [3, 9, 20], [1, 30]]
+        probs = sdamd.ask_ids(eng, head, state, qs, options, [1.0, 1.0, 1.0])
+        _, snap = om.forward(state, [], keep=True)
+        for qq, o, g in zip(qs, options, probs):
+            h, _ = om.forward(qq, list(o) + [len(qq) - 1], cache=snap)
+            assert np.abs(g - om.probs(h, 1.0)).max() < PROB_TOL
+    finally:
+        eng.free()
+
+
 def test_interleaved_snapshots_read_in_place(tiny, sdamd):
     """Question forwards read each snapshot's GDN states and conv histories in place (no restore
     copy).  Alternating between two snapshots, batching from one, and chaining a keep-forward from a

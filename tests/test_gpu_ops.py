@@ -164,12 +164,12 @@ class AttnCase:
     """A cache shared by successive calls (a prefix, then a suffix continuing it), on the GPU and in
     the oracle's layout."""
 
-    def __init__(self, sdamd, oracle, seed):
-        self.sdamd, self.oracle = sdamd, oracle
+    def __init__(self, sdamd, oracle, seed, rd=RD):
+        self.sdamd, self.oracle, self.rd = sdamd, oracle, rd
         self.rng = np.random.default_rng(seed)
         self.qw = (1 + 0.1 * self.rng.standard_normal(HD)).astype(np.float32)
         self.kw = (1 + 0.1 * self.rng.standard_normal(HD)).astype(np.float32)
-        self.rope = oracle.rope_table(RD, 1e7)
+        self.rope = oracle.rope_table(rd, 1e7)
         self.dqw, self.dkw, self.drope = dev(self.qw), dev(self.kw), dev(self.rope)
         self.dK, self.dV = empty(HK * CTX * HD * 2), empty(HK * CTX * HD * 2)
         self.oK = np.zeros((HK, CTX, HD), np.uint16)
@@ -180,12 +180,12 @@ class AttnCase:
         big = self.rng.standard_normal((L, self.stride)).astype(np.float16)
         dbig, dQ, dout = dev(big), empty(HQ * L * HD * 2), empty(L * HQ * HD * 2)
         self.sdamd.op_attention(dbig.data_ptr(), self.stride, self.dqw.data_ptr(), self.dkw.data_ptr(),
-                                self.drope.data_ptr(), L, P, HQ, HK, HD, RD, dQ.data_ptr(), self.dK.data_ptr(),
+                                self.drope.data_ptr(), L, P, HQ, HK, HD, self.rd, dQ.data_ptr(), self.dK.data_ptr(),
                                 self.dV.data_ptr(), CTX, dout.data_ptr())
         o = self.oracle
         Q = np.empty((HQ, L, HD), np.uint16)
         o.lib().or_qk_prep(o.P(big.view(np.uint16)), I(self.stride), o.P(self.qw), o.P(self.kw), o.P(self.rope), I(L),
-                           I(P), I(CTX), I(HQ), I(HK), I(HD), I(RD), o.P(Q), o.P(self.oK), o.P(self.oV))
+                           I(P), I(CTX), I(HQ), I(HK), I(HD), I(self.rd), o.P(Q), o.P(self.oK), o.P(self.oV))
         out = np.empty((L, HQ * HD), np.uint16)
         o.lib().or_attn(o.P(Q), o.P(self.oK), o.P(self.oV), o.P(big.view(np.uint16)), I(self.stride), I(L), I(P),
                         I(CTX), I(HQ), I(HK), I(HD), o.P(out))
@@ -231,3 +231,12 @@ def test_attention_long_prefix_ragged(sdamd, oracle):
     c = AttnCase(sdamd, oracle, 3)
     c.run(1101, 0)
     c.run(47, 1101)
+
+
+def test_attention_rotary_32_reads_q_buffer(sdamd, oracle):
+    """rotary_dim 32: the attention reads the queries qk_prep wrote (with rotary_dim 64, the case of
+    the other tests, it normalizes and rotates them itself); a prefill and a key-split suffix."""
+    c = AttnCase(sdamd, oracle, 4, rd=32)
+    c.run(512, 0)
+    err = c.run(40, 512)
+    print(f"attention rotary 32, L=40 P=512: max |d out| {err:.3g}", flush=True)
