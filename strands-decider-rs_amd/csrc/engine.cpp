@@ -623,8 +623,9 @@ YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, cons
     return y;
 }
 
-Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree) {
-    const uint64_t key = (uint64_t)tree << 32 | (uint64_t)L << 8 | (uint64_t)nseq << 1 | (short_seqs ? 1u : 0u);
+Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only) {
+    const uint64_t key = (uint64_t)(cache_only ? 1u : 0u) << 63 | (uint64_t)tree << 32 | (uint64_t)L << 8 |
+                         (uint64_t)nseq << 1 | (short_seqs ? 1u : 0u);
     auto it = plans.find(key);
     if (it != plans.end()) {
         it->second.used = ++plan_clock;
@@ -656,6 +657,11 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree) {
     YIn y;  // the sublayer output the next add + norm consumes (none before layer 0)
     for (size_t i = 0; i < layers.size(); i++) {
         const LayerW W = layers[i];
+        // cache_only (a forward that reads no hidden row, such as a state encoded for its snapshot):
+        // the last layer's output feeds nothing, so it runs only the steps that write the cache (the
+        // K/V rows, or the recurrent state and conv history); an adapter writes none
+        const bool cache_end = cache_only && i + 1 == layers.size();
+        if (cache_end && W.kind == SD_ADAPTER) break;
         {
             const YIn yin = y;
             steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.in_norm, d, nullptr, L, P.h, nullptr, s); }});
@@ -720,6 +726,7 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree) {
                     gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sg, nseq, s, W.state_off, hist_upd, P.big, W.hist_off);
                 }});
             }
+            if (cache_end) break;
             steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
             y = mm_y(steps, "out_proj", P.o, W.out_proj, L, sr);
         } else {
@@ -732,6 +739,7 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree) {
             steps.push_back({"qk_prep", [=](hipStream_t s) {
                 qk_prep(P.big, as, W.q_norm, W.k_norm, rp, L, luv, sg, qbuf, W.kc, W.vc, s);
             }});
+            if (cache_end) break;
             const int nb = (L + 15) / 16;
             int ks = 1;
             if (L <= P.attn_rows)
@@ -780,7 +788,7 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree) {
         }
         y = mm_y(steps, "down", P.mid, W.down, L, sr);
     }
-    pl.last_y = y;
+    pl.last_y = y;  // (unused by a cache_only plan: no hidden row is read)
     if (use_graphs) {
         SD_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         try {
@@ -914,7 +922,7 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
     const int L = (int)n;
     SD_CHECK(n_rows <= SD_CONTEXT, "at most 4096 hidden rows per forward");
     ensure_pool(std::max(L, (int)n_rows));  // the row tables and outputs hold n_rows entries
-    Plan& pl = plan(L);
+    Plan& pl = plan(L, 0, false, 0, n_rows == 0);
     upload(ids, n, rows, n_rows, P, cache != nullptr, 0, 0, cache);
     restore(cache, P);
     launch_and_read(pl, n_rows, timed);

@@ -235,7 +235,7 @@ struct Engine {
     // tree > 0: sequence 0 is a state of `tree` rows and sequences 1 .. nseq - 1 continue from it
     // (their own rows attend to its rows, their delta rule starts from its final state), each as its
     // own forward from the state's snapshot would; see ask_tree.
-    Plan& plan(int L, int nseq = 0, bool short_seqs = false, int tree = 0);
+    Plan& plan(int L, int nseq = 0, bool short_seqs = false, int tree = 0, bool cache_only = false);
     void upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
                 uint32_t chunks, uint32_t nseq, const Snapshot* cache, uint32_t tree = 0);
     void restore(const Snapshot* cache, size_t P);

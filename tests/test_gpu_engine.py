@@ -117,6 +117,32 @@ def test_ask_ids_tree_matches_snapshot_path(tiny, sdamd, case):
         assert int(np.argmax(got[i])) == int(np.argmax(want)), f"question {i}"
 
 
+@pytest.mark.parametrize("last", ["full_attention", "linear_attention"])
+def test_cache_only_forward_leaves_the_same_snapshot(sdamd, synth, tmp_path_factory, last):
+    """A forward that reads no hidden row runs only the cache-writing steps of its last layer (qkv and
+    qk_prep, or in_proj and the delta rule): its snapshot continues exactly as that of a forward of
+    the same tokens that reads rows (the steps writing the cache are the same kernels on the same
+    inputs), for a last layer of either kind."""
+    cfg = dict(synth.CONFIG_TINY)
+    if last == "linear_attention":
+        cfg["layer_types"] = (["full_attention"] + ["linear_attention"] * 3) * 2
+    path = synth.write_model(str(tmp_path_factory.mktemp("co")), cfg, vocab=4096, seed=3)
+    eng, head, _ = sdamd.load_decider(path)
+    try:
+        for n_state in (90, 150):
+            state, q = ids_for(60 + n_state, n_state), ids_for(61, 37)
+            rows = [2, 11, 36]
+            bare = eng.forward(state, [], keep=True).snapshot
+            read = eng.forward(state, [0, n_state - 1], keep=True).snapshot
+            a = eng.forward(q, rows, cache=bare).hidden
+            b = eng.forward(q, rows, cache=read).hidden
+            np.testing.assert_array_equal(a, b)
+            bare.free()
+            read.free()
+    finally:
+        eng.free()
+
+
 def test_forward_errors(tiny, sdamd):
     eng, head, om = tiny
     with pytest.raises(sdamd.EngineError, match="must be 1 to 4096"):
