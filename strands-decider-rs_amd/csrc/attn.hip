@@ -53,6 +53,7 @@ __global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, co
             for (int i = 0; i < nt; i++) *at(P + t0 + i) = v[i];
         }
     }
+    __shared__ __align__(16) float nrow[4][HD];  // a wave's normalized row (rotary dims not a multiple of 8)
     const float* nw = isq ? qw : kw;
     const float4 w4 = *reinterpret_cast<const float4*>(nw + 4 * lane);
     const int rd2 = s.RD / 2;
@@ -71,13 +72,25 @@ __global__ __launch_bounds__(256) void k_qk_prep(const f16* __restrict__ big, co
         float n[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) n[u] = x[u] * inv * wv4[u];
-        // rotate-half RoPE on dims < RD: the partner of dim d is d +- RD/2, in lane l +- RD/8
+        // rotate-half RoPE on dims < RD: the partner of dim d is d +- RD/2.  With RD a multiple of 8
+        // it is element u of lane l +- RD/8 (a lane shuffle); otherwise it is read back from the
+        // wave's row in LDS (the wave's own stores: LDS operations of one wave complete in order).
         float pn[4];
-        const int sh = rd2 / 4;
+        if (rd2 % 4 == 0) {
+            const int sh = rd2 / 4;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float up = __shfl(n[u], (lane + sh) & 63), dn = __shfl(n[u], (lane - sh) & 63);
-            pn[u] = 4 * lane < rd2 ? up : dn;
+            for (int u = 0; u < 4; u++) {
+                const float up = __shfl(n[u], (lane + sh) & 63), dn = __shfl(n[u], (lane - sh) & 63);
+                pn[u] = 4 * lane < rd2 ? up : dn;
+            }
+        } else {
+            *reinterpret_cast<float4*>(&nrow[wv][4 * lane]) = float4{n[0], n[1], n[2], n[3]};
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int d = 4 * lane + u;
+                pn[u] = d < s.RD ? nrow[wv][d < rd2 ? d + rd2 : d - rd2] : 0.f;
+            }
         }
         f16x4 r4;
 #pragma unroll
@@ -492,7 +505,7 @@ void qk_prep(const f16* big, const AttnShape& s, const float* qw, const float* k
              const uint32_t* lu, const Segs& sg, f16* Q, f16* Kc, f16* Vc, hipStream_t st) {
     SD_CHECK(s.HD == 256, "attention: only head_dim 256 is supported");
     SD_CHECK(s.RD % 2 == 0 && s.RD <= s.HD, "attention: bad rotary_dim");
-    SD_CHECK(s.RD % 8 == 0 && s.stride % 4 == 0, "attention: rotary_dim must be a multiple of 8, the row stride of 4");
+    SD_CHECK(s.stride % 4 == 0, "attention: the row stride must be a multiple of 4");
     SD_CHECK(s.ctx % 32 == 0, "attention: the cache length must be a multiple of 32");
     hipLaunchKernelGGL(k_qk_prep<256>, dim3((L + 3) / 4, Q ? s.HQ + s.HK : s.HK), dim3(256), 0, st, big, lu, L, s.HQ,
                        s.HK, s.RD, s.stride, s.ctx, sg.row, qw, kw, rope, Q, Kc, Vc);

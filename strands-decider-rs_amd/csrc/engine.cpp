@@ -369,9 +369,9 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
             li++;
         } else {
             SD_CHECK(cfg.hd == 256, "attention: only head_dim 256 is supported");
-            // qk_prep pairs rotate-half partners with a lane shuffle over 8-element groups
-            SD_CHECK(cfg.rd >= 8 && cfg.rd % 8 == 0 && cfg.rd <= cfg.hd,
-                     "attention: rotary_dim must be a multiple of 8 from 8 to head_dim");
+            // rotate-half pairs dims d and d + rotary_dim / 2 (the reference's RD2 = rd / 2)
+            SD_CHECK(cfg.rd >= 2 && cfg.rd % 2 == 0 && cfg.rd <= cfg.hd,
+                     "attention: rotary_dim must be even, from 2 to head_dim");
             SD_CHECK(cfg.hk > 0 && cfg.hq % cfg.hk == 0, "attention: q heads must be a multiple of kv heads");
             L.qkv = mat(p + "qkv");
             SD_CHECK(L.qkv.N >= 2 * cfg.hq * cfg.hd + 2 * cfg.hk * cfg.hd, p + "qkv: too few rows");

@@ -315,12 +315,14 @@ def test_rotated_torso_unrotate_on_device(sdamd, synth, oracle, tmp_path_factory
         eng.free()
 
 
-def test_rotary_32_forward_and_questions(sdamd, synth, oracle, tmp_path_factory):
-    """rotary_dim 32: the attention reads the queries qk_prep wrote (with rotary_dim 64, the tiny and
-    2B configs' value, it normalizes and rotates them itself); a forward and a one-forward ask_ids
+@pytest.mark.parametrize("rd", [32, 12])
+def test_other_rotary_dims_forward_and_questions(sdamd, synth, oracle, tmp_path_factory, rd):
+    """rotary_dim 32 and 12: the attention reads the queries qk_prep wrote (with rotary_dim 64, the
+    tiny and 2B configs' value, it normalizes and rotates them itself; 12 is not a multiple of 8, so
+    qk_prep reads the rotate-half partners back from LDS); a forward and a one-forward ask_ids
     against the oracle."""
-    cfg = dict(synth.CONFIG_TINY, rotary_dim=32)
-    path = synth.write_model(str(tmp_path_factory.mktemp("rd32")), cfg, vocab=4096, seed=2)
+    cfg = dict(synth.CONFIG_TINY, rotary_dim=rd)
+    path = synth.write_model(str(tmp_path_factory.mktemp(f"rd{rd}")), cfg, vocab=4096, seed=2)
     eng, head, _ = sdamd.load_decider(path)
     om = oracle.OracleModel(path)
     try:
@@ -375,12 +377,14 @@ def test_interleaved_snapshots_read_in_place(tiny, sdamd):
         s.free()
 
 
-def test_rotary_dim_checked_at_load(sdamd, synth, tmp_path):
-    """qk_prep pairs rotate-half partners with a lane shuffle over groups of 8: a rotary_dim it
-    cannot rotate fails at load instead of giving wrong Q/K."""
-    cfg = dict(synth.CONFIG_TINY, rotary_dim=12)
-    d = synth.write_model(str(tmp_path / "rd12"), cfg, vocab=512, seed=5)
-    with pytest.raises(sdamd.EngineError, match="rotary_dim must be a multiple of 8"):
+@pytest.mark.parametrize("rd", [13, 0, 258])
+def test_rotary_dim_checked_at_load(sdamd, synth, tmp_path, rd):
+    """Rotate-half pairs dim d with d + rotary_dim / 2 over a table of rotary_dim / 2 (cos, sin)
+    pairs per position: an odd rotary_dim, none, or one past head_dim fails at load instead of
+    giving wrong Q/K."""
+    cfg = dict(synth.CONFIG_TINY, rotary_dim=rd)
+    d = synth.write_model(str(tmp_path / f"rd{rd}"), cfg, vocab=512, seed=5)
+    with pytest.raises(sdamd.EngineError, match="rotary_dim must be even, from 2 to head_dim"):
         sdamd.Engine.load(d)
 
 

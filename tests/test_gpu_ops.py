@@ -233,10 +233,13 @@ def test_attention_long_prefix_ragged(sdamd, oracle):
     c.run(47, 1101)
 
 
-def test_attention_rotary_32_reads_q_buffer(sdamd, oracle):
-    """rotary_dim 32: the attention reads the queries qk_prep wrote (with rotary_dim 64, the case of
-    the other tests, it normalizes and rotates them itself); a prefill and a key-split suffix."""
-    c = AttnCase(sdamd, oracle, 4, rd=32)
+@pytest.mark.parametrize("rd", [32, 12, 2])
+def test_attention_other_rotary_dims(sdamd, oracle, rd):
+    """rotary_dim other than 64: the attention reads the queries qk_prep wrote (with rotary_dim 64,
+    the case of the other tests, it normalizes and rotates them itself).  32 pairs rotate-half
+    partners with a lane shuffle; 12 and 2 (not multiples of 8) read them back from LDS.  A prefill
+    and a key-split suffix."""
+    c = AttnCase(sdamd, oracle, 4 + rd, rd=rd)
     c.run(512, 0)
     err = c.run(40, 512)
-    print(f"attention rotary 32, L=40 P=512: max |d out| {err:.3g}", flush=True)
+    print(f"attention rotary {rd}, L=40 P=512: max |d out| {err:.3g}", flush=True)
