@@ -129,6 +129,9 @@ void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* row
 // gate_up output in big (f16, [L][2I]) or as ks f32 split-K slots in part; `il`: gate and up
 // columns interleaved in groups of 16 (the layout interleave_gate_up gives the weights).
 void silu_mul(const f16* big, const float* part, int ks, int L, int I, bool il, f16* mid, hipStream_t st);
+// d0[r] = s0[rows[r]] and d1[r] = s1[rows[r]] for r < n, rows of bytes0 / bytes1 (multiples of 16)
+void gather_rows2(const void* s0, void* d0, size_t bytes0, const void* s1, void* d1, size_t bytes1, const uint32_t* rows,
+                  int n, hipStream_t st);
 void add_bias(f16* y, int L, int N, const float* c, hipStream_t st);
 void fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t st);
 // p[0..8) = v[0..8) by a kernel (a value carried in the launch, so the call may be captured)

@@ -245,6 +245,31 @@ void add_norm(float* x, const YIn& y, const float* w, int d, const uint32_t* row
     launched("add_norm");
 }
 
+// dst0 row r = src0 row rows[r] (bytes0 per row), and the same for src1/dst1: block (r, which)
+// copies one row in 16-byte pieces
+__global__ __launch_bounds__(256) void k_gather_rows2(const uint8_t* __restrict__ s0, uint8_t* __restrict__ d0,
+                                                      uint32_t b0, const uint8_t* __restrict__ s1,
+                                                      uint8_t* __restrict__ d1, uint32_t b1,
+                                                      const uint32_t* __restrict__ rows) {
+    const bool second = blockIdx.y != 0;
+    const uint8_t* const src = second ? s1 : s0;
+    uint8_t* const dst = second ? d1 : d0;
+    const uint32_t b = second ? b1 : b0;
+    const size_t r = blockIdx.x, row = rows[r];
+    for (uint32_t i = threadIdx.x * 16u; i < b; i += 256u * 16u)
+        *reinterpret_cast<u32x4*>(dst + r * b + i) = *reinterpret_cast<const u32x4*>(src + row * b + i);
+}
+
+void gather_rows2(const void* s0, void* d0, size_t bytes0, const void* s1, void* d1, size_t bytes1, const uint32_t* rows,
+                  int n, hipStream_t st) {
+    SD_CHECK(bytes0 % 16 == 0 && bytes1 % 16 == 0, "gather_rows2: rows must be multiples of 16 bytes");
+    if (n == 0) return;
+    hipLaunchKernelGGL(k_gather_rows2, dim3(n, 2), dim3(256), 0, st, static_cast<const uint8_t*>(s0),
+                       static_cast<uint8_t*>(d0), (uint32_t)bytes0, static_cast<const uint8_t*>(s1), static_cast<uint8_t*>(d1),
+                       (uint32_t)bytes1, rows);
+    launched("gather");
+}
+
 void silu_mul(const f16* big, const float* part, int ks, int L, int I, bool il, f16* mid, hipStream_t st) {
     SD_CHECK(I % 8 == 0, "silu_mul: intermediate size must be a multiple of 8");
     SD_CHECK(!il || I % 16 == 0, "silu_mul: interleaved gate/up needs I a multiple of 16");

@@ -524,6 +524,8 @@ void Engine::ensure_pool(int l) {
         attn_ws_floats(std::min(cap, 256), as) * 4,    // attention key-split workspace
         ypart * 4,                                     // split-K partials of y
         gpart * 4,                                     // split-K partials of gate_up
+        (size_t)cap * cfg.d * 4,                       // xc: a compact last layer's residual rows
+        (size_t)cap * orow * 2,                        // oc: a compact last layer's mixer output rows
     };
     size_t total = 0;
     for (size_t s : sizes) total += align256(s);
@@ -568,6 +570,8 @@ void Engine::ensure_pool(int l) {
     pool.ypart_elems = ypart;
     pool.gpart = (float*)ptrs[14];
     pool.gpart_elems = gpart;
+    pool.xc = (float*)ptrs[15];
+    pool.oc = (f16*)ptrs[16];
     SD_HIP(hipMemset(pool.x, 0, (size_t)cap * cfg.d * 4));
     SD_HIP(hipMemset(upb, 0, up.up_bytes));
     if (up_h_bytes < up.up_bytes) {
@@ -623,9 +627,17 @@ YIn Engine::mm_y(std::vector<Step>& steps, const char* label, const f16* A, cons
     return y;
 }
 
-Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only) {
-    const uint64_t key = (uint64_t)(cache_only ? 1u : 0u) << 63 | (uint64_t)tree << 32 | (uint64_t)L << 8 |
-                         (uint64_t)nseq << 1 | (short_seqs ? 1u : 0u);
+Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only, int rows_read) {
+    // A forward that reads at most half its rows runs its last layer's tail (after the token mixer:
+    // o_proj or out_proj, the residual add + norm, the MLP) on the read rows only, gathered into a
+    // compact block; the final norm then reads them there.  The mixer itself runs on every row (its
+    // output rows depend on all earlier rows).  An adapter as the last layer keeps the full tail.
+    const int compact = !cache_only && rows_read > 0 && 2 * rows_read <= L && !layers.empty() &&
+                                layers.back().kind != SD_ADAPTER
+                            ? rows_read
+                            : 0;
+    const uint64_t key = (uint64_t)(cache_only ? 1u : 0u) << 63 | (uint64_t)compact << 46 | (uint64_t)tree << 32 |
+                         (uint64_t)L << 8 | (uint64_t)nseq << 1 | (short_seqs ? 1u : 0u);
     auto it = plans.find(key);
     if (it != plans.end()) {
         it->second.used = ++plan_clock;
@@ -662,6 +674,10 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only) 
         // K/V rows, or the recurrent state and conv history); an adapter writes none
         const bool cache_end = cache_only && i + 1 == layers.size();
         if (cache_end && W.kind == SD_ADAPTER) break;
+        // this layer's tail runs on the R compact rows (the last layer of a compact plan), else on all L
+        const bool tail_c = compact > 0 && i + 1 == layers.size();
+        const int R = tail_c ? compact : L;
+        float* const xt = tail_c ? P.xc : P.x;
         {
             const YIn yin = y;
             steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.in_norm, d, nullptr, L, P.h, nullptr, s); }});
@@ -728,7 +744,11 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only) 
             }
             if (cache_end) break;
             steps.push_back({"gnorm", [=](hipStream_t s) { gnorm(P.of, P.big, gs, W.gnorm, L, P.o, s); }});
-            y = mm_y(steps, "out_proj", P.o, W.out_proj, L, sr);
+            if (tail_c) {
+                const size_t ob = (size_t)W.out_proj.K * 2, xb = (size_t)d * 4;
+                steps.push_back({"gather", [=](hipStream_t s) { gather_rows2(P.o, P.oc, ob, P.x, P.xc, xb, P.rows, R, s); }});
+            }
+            y = mm_y(steps, "out_proj", tail_c ? P.oc : P.o, W.out_proj, R, sr);
         } else {
             const AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, W.qkv.N, SD_CONTEXT};
             const float* rp = rope;
@@ -747,11 +767,15 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only) 
             steps.push_back({"attn", [=](hipStream_t s) {
                 attention_split(qbuf, W.kc, W.vc, P.big, as, L, luv, sg, ks, P.attn_ws, P.o, s, W.q_norm, rp);
             }});
-            y = mm_y(steps, "o_proj", P.o, W.o_proj, L, sr);
+            if (tail_c) {
+                const size_t ob = (size_t)W.o_proj.K * 2, xb = (size_t)d * 4;
+                steps.push_back({"gather", [=](hipStream_t s) { gather_rows2(P.o, P.oc, ob, P.x, P.xc, xb, P.rows, R, s); }});
+            }
+            y = mm_y(steps, "o_proj", tail_c ? P.oc : P.o, W.o_proj, R, sr);
         }
         {
             const YIn yin = y;
-            steps.push_back({"norm", [=](hipStream_t s) { add_norm(P.x, yin, W.post_norm, d, nullptr, L, P.h, nullptr, s); }});
+            steps.push_back({"norm", [=](hipStream_t s) { add_norm(xt, yin, W.post_norm, d, nullptr, R, P.h, nullptr, s); }});
         }
         {
             // gate_up only feeds silu * mul: from 65 to 2560 rows it runs unsplit with silu * mul in
@@ -762,33 +786,34 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only) 
             const Mat m = W.gate_up;
             const bool exact = gemv_rows(m, sr);
             const bool il = gu_il;
-            const int cfu = !exact && m.K % 256 == 0 && L > 64 && L <= 2560 ? gemm_w4_plan(L, m.N, m.K, false, false, 0).cfg : -1;
+            const int cfu = !exact && m.K % 256 == 0 && R > 64 && R <= 2560 ? gemm_w4_plan(R, m.N, m.K, false, false, 0).cfg : -1;
             if (exact) {
                 const bool fused = il && m.tiled;
-                const GemvPlan gp = gemv_plan(L, m.N, m.K, m.tiled, fused ? 2 : 0, 0);
+                const GemvPlan gp = gemv_plan(R, m.N, m.K, m.tiled, fused ? 2 : 0, 0);
                 steps.push_back({"gate_up", [=](hipStream_t s) {
-                    gemv(P.h, m.q, m.s, m.b, fused ? (void*)P.mid : (void*)P.big, fused ? 2 : 0, L, m.N, m.K, m.bits, m.group,
+                    gemv(P.h, m.q, m.s, m.b, fused ? (void*)P.mid : (void*)P.big, fused ? 2 : 0, R, m.N, m.K, m.bits, m.group,
                          m.asym, m.tiled, gp, s);
                 }});
-                if (!fused) steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, nullptr, 0, L, I, il, P.mid, s); }});
+                if (!fused) steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, nullptr, 0, R, I, il, P.mid, s); }});
             } else if (il && gemm_w4_has_silu(cfu)) {
                 const int cg = cfu;
                 steps.push_back({"gate_up", [=](hipStream_t s) {
-                    gemm_w4_silu(P.h, m.q, m.s, P.mid, L, m.N, m.K, s, cg, m.tiled);
+                    gemm_w4_silu(P.h, m.q, m.s, P.mid, R, m.N, m.K, s, cg, m.tiled);
                 }});
             } else {
-                const GemmPlan plan_ = gemm_w4_plan(L, m.N, m.K, exact, true, P.gpart_elems);
+                const GemmPlan plan_ = gemm_w4_plan(R, m.N, m.K, exact, true, P.gpart_elems);
                 const int cg = plan_.cfg, ks = plan_.ks;
                 float* gp = ks > 1 ? P.gpart : nullptr;  // unsplit: f16 straight into big
                 steps.push_back({"gate_up", [=](hipStream_t s) {
-                    gemm_w4(P.h, m.q, m.s, P.big, gp, L, m.N, m.K, exact, ks, s, cg, m.tiled);
+                    gemm_w4(P.h, m.q, m.s, P.big, gp, R, m.N, m.K, exact, ks, s, cg, m.tiled);
                 }});
-                steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, gp, ks, L, I, il, P.mid, s); }});
+                steps.push_back({"silu", [=](hipStream_t s) { silu_mul(P.big, gp, ks, R, I, il, P.mid, s); }});
             }
         }
-        y = mm_y(steps, "down", P.mid, W.down, L, sr);
+        y = mm_y(steps, "down", P.mid, W.down, R, sr);
     }
     pl.last_y = y;  // (unused by a cache_only plan: no hidden row is read)
+    pl.compact = compact;
     if (use_graphs) {
         SD_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         try {
@@ -882,7 +907,12 @@ void Engine::launch_and_read(Plan& pl, size_t n_rows, bool timed, bool read) {
     } else {
         for (auto& s : pl.steps) s.run(st);
     }
-    if (n_rows) add_norm(pool.x, pl.last_y, final_norm, cfg.d, pool.rows, (int)n_rows, nullptr, pool.out, st);
+    if (n_rows) {
+        // a compact plan's read rows are already gathered, in row order, in pool.xc
+        SD_CHECK(!pl.compact || (size_t)pl.compact == n_rows, "compact plan run with another row count");
+        if (pl.compact) add_norm(pool.xc, pl.last_y, final_norm, cfg.d, nullptr, (int)n_rows, nullptr, pool.out, st);
+        else add_norm(pool.x, pl.last_y, final_norm, cfg.d, pool.rows, (int)n_rows, nullptr, pool.out, st);
+    }
     if (!read) return;
     if (timed) SD_HIP(hipEventRecord(ev1, st));
     if (n_rows) SD_HIP(hipMemcpyAsync(out_h, pool.out, n_rows * cfg.d * 4, hipMemcpyDeviceToHost, st));
@@ -922,7 +952,7 @@ void Engine::forward(const uint32_t* ids, size_t n, const size_t* rows, size_t n
     const int L = (int)n;
     SD_CHECK(n_rows <= SD_CONTEXT, "at most 4096 hidden rows per forward");
     ensure_pool(std::max(L, (int)n_rows));  // the row tables and outputs hold n_rows entries
-    Plan& pl = plan(L, 0, false, 0, n_rows == 0);
+    Plan& pl = plan(L, 0, false, 0, n_rows == 0, (int)n_rows);
     upload(ids, n, rows, n_rows, P, cache != nullptr, 0, 0, cache);
     restore(cache, P);
     launch_and_read(pl, n_rows, timed);
@@ -993,7 +1023,7 @@ Plan& Engine::prepare_batch(const uint32_t* ids, const size_t* lens, size_t nseq
     const int L = (int)n;
     SD_CHECK(n_rows <= SD_CONTEXT, "at most 4096 hidden rows per forward");
     ensure_pool(std::max(L, (int)n_rows));  // the row tables and outputs hold n_rows entries
-    Plan& pl = plan(L, (int)nseq, any_short);
+    Plan& pl = plan(L, (int)nseq, any_short, 0, false, (int)n_rows);
     // sequence tables (see Segs): rows, chunks of <= 64 rows inside each sequence, sequences
     uint32_t* rowt = reinterpret_cast<uint32_t*>(up_h + pool.off_seg_row);
     uint32_t* chunkt = reinterpret_cast<uint32_t*>(up_h + pool.off_seg_chunk);
@@ -1162,7 +1192,7 @@ void Engine::ask_tree(const Head& head, const uint32_t* state, size_t n_state, c
     attach_head(head);
     const int L = (int)n, S = (int)n_state, nseq = (int)nq + 1;
     ensure_pool(std::max(L, (int)n_rows));
-    Plan& pl = plan(L, nseq, false, S);
+    Plan& pl = plan(L, nseq, false, S, false, (int)n_rows);
     // Sequence tables (see Segs): sequence 0 the state, q + 1 question q.  A question row's index in
     // its sequence is S + its own index (its RoPE position); its sequence starts at its first row.
     uint32_t* rowt = reinterpret_cast<uint32_t*>(up_h + pool.off_seg_row);

@@ -75,6 +75,9 @@ struct Pool {
     size_t up_bytes = 0, off_ids = 0, off_rows = 0, off_seg_row = 0, off_seg_chunk = 0, off_seg_seq = 0;
     uint32_t *ids = nullptr, *rows = nullptr;
     float *x = nullptr, *qkvc = nullptr, *of = nullptr, *out = nullptr;
+    // a compact last layer's rows: the read rows of the residual stream and of the mixer output
+    float* xc = nullptr;
+    f16* oc = nullptr;
     f16 *h = nullptr, *big = nullptr, *mid = nullptr, *o = nullptr, *y = nullptr, *q = nullptr;
     GdnWs gdn;
     float* attn_ws = nullptr;
@@ -97,6 +100,7 @@ struct Plan {
     int L = 0;
     std::vector<Step> steps;
     YIn last_y;  // where the last sublayer output lives (read by the final norm)
+    int compact = 0;  // > 0: the last layer's tail ran on this many read rows (compact, in pool.xc)
     uint64_t used = 0;  // Engine::plan_clock at the last use (least recently used plans are evicted)
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -235,7 +239,7 @@ struct Engine {
     // tree > 0: sequence 0 is a state of `tree` rows and sequences 1 .. nseq - 1 continue from it
     // (their own rows attend to its rows, their delta rule starts from its final state), each as its
     // own forward from the state's snapshot would; see ask_tree.
-    Plan& plan(int L, int nseq = 0, bool short_seqs = false, int tree = 0, bool cache_only = false);
+    Plan& plan(int L, int nseq = 0, bool short_seqs = false, int tree = 0, bool cache_only = false, int rows_read = 0);
     void upload(const uint32_t* ids, size_t n, const size_t* rows, size_t n_rows, size_t P, bool has_cache,
                 uint32_t chunks, uint32_t nseq, const Snapshot* cache, uint32_t tree = 0);
     void restore(const Snapshot* cache, size_t P);

@@ -143,6 +143,33 @@ def test_cache_only_forward_leaves_the_same_snapshot(sdamd, synth, tmp_path_fact
         eng.free()
 
 
+@pytest.mark.parametrize("last", ["full_attention", "linear_attention"])
+def test_compact_last_layer_matches_the_full_tail(sdamd, synth, oracle, tmp_path_factory, last):
+    """A forward reading at most half its rows runs its last layer's tail (o_proj or out_proj, the
+    residual add + norm, the MLP) on those rows only, gathered after the token mixer.  Rows read in
+    any order, repeated, and single: the same hidden rows (within the tolerance: the tail's matmuls
+    then have another M) as a forward reading every row, and, without the repeat, as the oracle.
+    (A repeated row is a race in the reference's final norm, which adds the sublayer output to the
+    residual row in place once per read; the oracle adds it twice, the compact tail once.)"""
+    cfg = dict(synth.CONFIG_TINY)
+    if last == "linear_attention":
+        cfg["layer_types"] = (["full_attention"] + ["linear_attention"] * 3) * 2
+    path = synth.write_model(str(tmp_path_factory.mktemp("ct")), cfg, vocab=4096, seed=4)
+    eng, head, _ = sdamd.load_decider(path)
+    om = oracle.OracleModel(path)
+    try:
+        for L, rows in ((100, [77, 3, 99, 3, 50]), (130, [129]), (41, [0, 40, 20])):
+            ids = ids_for(70 + L, L)
+            every = eng.forward(ids, list(range(L))).hidden
+            got = eng.forward(ids, rows).hidden
+            assert np.abs(got - every[rows]).max() < HIDDEN_TOL
+            uniq = list(dict.fromkeys(rows))
+            want, _ = om.forward(ids, uniq)
+            assert np.abs(eng.forward(ids, uniq).hidden - want).max() < HIDDEN_TOL
+    finally:
+        eng.free()
+
+
 def test_forward_errors(tiny, sdamd):
     eng, head, om = tiny
     with pytest.raises(sdamd.EngineError, match="must be 1 to 4096"):
