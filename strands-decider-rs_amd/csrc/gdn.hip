@@ -1043,37 +1043,50 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
         hi = __builtin_bit_cast(f16x8, buf_b128(rws, vf, so));
         lo = __builtin_bit_cast(f16x8, buf_b128(rws, vf, so + 1024u));
     };
-    auto load_wq = [&](WQ& d, int c) {
+    // W and Qg of chunk c, k step s (4 loads), and U of chunk c (4 loads): issued a few at a time
+    // between the MFMAs of the chunk before (a burst of all of them stalled the wave's issue for
+    // about 1.8 k cycles at the CU's 64 bytes per clock)
+    auto load_wq_step = [&](WQ& d, int c, int s) {
         const bool in = c < cend;
-        const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vf = in ? vfrag : OOB, vuu = in ? vu : OOB;
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            frag(slot * (uint32_t)(WF_H * 2), 4, wv, s, d.wh[s], d.wl[s], vf);
-            frag(o_qg + slot * (uint32_t)(QGF_H * 2), 4, wv, s, d.qh[s], d.ql[s], vf);
-        }
+        const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vf = in ? vfrag : OOB;
+        frag(slot * (uint32_t)(WF_H * 2), 4, wv, s, d.wh[s], d.wl[s], vf);
+        frag(o_qg + slot * (uint32_t)(QGF_H * 2), 4, wv, s, d.qh[s], d.ql[s], vf);
+    };
+    auto load_u = [&](WQ& d, int c) {
+        const bool in = c < cend;
+        const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vuu = in ? vu : OOB;
 #pragma unroll
         for (int r = 0; r < 4; r++)
             d.ur[r] = __builtin_bit_cast(
                 float, buf_b32(rws, vuu, o_u + slot * (uint32_t)(U_F * 4) + (uint32_t)(((wv * 16 + r) * DV + c0) * 4)));
     };
-    auto load_qk = [&](int c) {
+    auto load_wq = [&](WQ& d, int c) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) load_wq_step(d, c, s);
+        load_u(d, c);
+    };
+    // Qk and e^(G_last) of chunk c (part 0), or its Kg row tile 2 wv + part - 1 (parts 1, 2): each
+    // issued once the chunk before has used that register set, between its MFMAs
+    auto load_qk = [&](int c, int part) {
         const bool in = c < cend;
         const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vf = in ? vfrag : OOB;
+        if (part == 0) {
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            frag(o_qk + slot * (uint32_t)(QKF_H * 2), 2, wv, s, qkh[s], qkl[s], vf);
+            for (int s = 0; s < 2; s++) frag(o_qk + slot * (uint32_t)(QKF_H * 2), 2, wv, s, qkh[s], qkl[s], vf);
+            gl = __builtin_bit_cast(float, buf_b32(rws, in ? 0u : OOB, o_gl + slot * 4u));
+        } else {
+            const int q2 = part - 1;
 #pragma unroll
-            for (int q2 = 0; q2 < 2; q2++)
+            for (int s = 0; s < 2; s++)
                 frag(o_kg + slot * (uint32_t)(KGF_H * 2), 2, wv * 2 + q2, s, kh[q2][s], kl[q2][s], vf);
         }
-        gl = __builtin_bit_cast(float, buf_b32(rws, in ? 0u : OOB, o_gl + slot * 4u));
     };
     // o rows t0 + wv*16 + fg*4 + r (r < 4), column h*DV + c0 + fr; rows past the chunk get an
     // out-of-range offset and are not written
     const Rsrc ro = make_rsrc(o, (uint32_t)L * sh.H * DV * 4);
     const uint32_t vo = (uint32_t)((fg * 4 * sh.H * DV + fr) * 4);
     auto chunk = [&](int c, const WQ& cur, WQ& nxt) {
-        load_wq(nxt, c + 1);
+        load_u(nxt, c + 1);
         const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
         const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - c * CH);
         lds_barrier();  // St holds this chunk's starting state; Vt is free
@@ -1081,16 +1094,31 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
         // chains of 4 instead of two of 12) and are added at the end
         const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
         f32x4 av[3] = {z4, z4, z4}, ao[3] = {z4, z4, z4};
+        // k step s: its S slice (read from LDS during step s - 1), then the next chunk's W and Qg
+        // loads of step s, each step a scheduling region of its own so that those loads are issued
+        // in four groups
+        float sn[8];
+        {
+            const float* sp = &St[fr * SP + fg * 8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) sn[u] = sp[u];
+        }
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             float s8[8];
-            const float* sp = &St[fr * SP + s * 32 + fg * 8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) s8[u] = sp[u];
+            for (int u = 0; u < 8; u++) s8[u] = sn[u];
+            if (s < 3) {
+                const float* sp = &St[fr * SP + (s + 1) * 32 + fg * 8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) sn[u] = sp[u];
+            }
+            load_wq_step(nxt, c + 1, s);
             f16x8 sh8, sl8;
             split8(s8, sh8, sl8);
             mma3s(cur.wh[s], cur.wl[s], sh8, sl8, av);
             mma3s(cur.qh[s], cur.ql[s], sh8, sl8, ao);
+            __builtin_amdgcn_sched_barrier(0);
         }
         // rows wv * 16 + fg * 4 .. + 3 of column fr: one 16-byte store (conflict-free at this pitch)
         *reinterpret_cast<float4*>(&Vt[fr * VP + wv * 16 + fg * 4]) =
@@ -1109,6 +1137,9 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
         }
 #pragma unroll
         for (int s = 0; s < 2; s++) mma3s(qkh[s], qkl[s], vh[s], vl[s], ao);
+        const float g_c = gl;
+        load_qk(c + 1, 0);  // Qk and gl are consumed
+        __builtin_amdgcn_sched_barrier(0);
         // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
         f32x4 as[2][3];
 #pragma unroll
@@ -1116,9 +1147,9 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
             as[q2][0] = as[q2][1] = as[q2][2] = z4;
 #pragma unroll
             for (int s = 0; s < 2; s++) mma3s(kh[q2][s], kl[q2][s], vh[s], vl[s], as[q2]);
+            load_qk(c + 1, 1 + q2);  // Kg row tile q2 is consumed
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const float g_c = gl;
-        load_qk(c + 1);  // Qk, Kg, gl are consumed
         {
             const uint32_t so = (uint32_t)(((t0 + wv * 16) * sh.H * DV + h * DV + c0) * 4);
 #pragma unroll
@@ -1140,7 +1171,9 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
         }
     };
     load_wq(set0, cfirst);
-    load_qk(cfirst);
+    load_qk(cfirst, 0);
+    load_qk(cfirst, 1);
+    load_qk(cfirst, 2);
     int c = cfirst;
     for (; c + 1 < cend; c += 2) {  // no branch inside the loop body
         chunk(c, set0, set1);
