@@ -220,30 +220,42 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     // hold them (the cache pointers are restrict: no asm without them could write their memory), so
     // the clobbering asm takes both pointers as operands.
     const Rsrc rk = make_rsrc(Kb, (uint32_t)s.ctx * HD * 2u), rv = make_rsrc(Vb, (uint32_t)s.ctx * HD * 2u);
-    auto load = [&](int j, f16x8 (&kf)[2][NS], f16x8 (&vf)[ND]) {
-        const int jc = min(j, kend - 1);
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-            const int key = min(jc + 8 * (fq >> 2) + 4 * tt + (fq & 3), kend - 1);
-            const uint32_t ko = (uint32_t)((key >> 5) * (HD * 32) + (key & 31) * 32 + fg * 8) * 2u;
-#pragma unroll
-            for (int st = 0; st < NS; st++) kf[tt][st] = __builtin_bit_cast(f16x8, buf_b128(rk, ko, (uint32_t)st * 2048u));
-        }
-        const uint32_t vo = (uint32_t)((jc >> 5) * (HD * 32) + fq * 32 + fg * 8) * 2u;
-#pragma unroll
-        for (int dt = 0; dt < ND; dt++) vf[dt] = __builtin_bit_cast(f16x8, buf_b128(rv, vo, (uint32_t)dt * 1024u));
+    // A block's K fragments (2 NS loads) and V fragments (ND loads).  Past the end they re-read the
+    // last block (never used), so every block issues the same loads and the explicit vmcnt waits
+    // below are exact.
+    auto koff = [&](int j, int tt) {
+        const int key = min(min(j, kend - 1) + 8 * (fq >> 2) + 4 * tt + (fq & 3), kend - 1);
+        return (uint32_t)((key >> 5) * (HD * 32) + (key & 31) * 32 + fg * 8) * 2u;
+    };
+    auto voff = [&](int j) { return (uint32_t)((min(j, kend - 1) >> 5) * (HD * 32) + fq * 32 + fg * 8) * 2u; };
+    // (the clobbering asm takes both pointers, so the loads before it stay before it)
+    auto pin = [&]() {
         asm volatile("" ::"s"(Kb), "s"(Vb) : "memory");
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto process = [&](int j0, const f16x8 (&kf)[2][NS], const f16x8 (&vf)[ND]) {
-        f32x4 st2[2];
+    // Block j0 with the fragments kf, vf, and block jn's loads into kfn, vfn, issued among block
+    // j0's MFMAs (K among S = K Q^T, V among O += V^T P^T): the CU's vector memory path takes 64
+    // bytes a clock, so a burst of a block's 32 KB per wave held up the wave's issue instead of
+    // running beside its MFMAs.  A block's K is waited for before its S, its V before its P V.
+    auto process = [&](int j0, const f16x8 (&kf)[2][NS], const f16x8 (&vf)[ND], int jn, f16x8 (&kfn)[2][NS],
+                       f16x8 (&vfn)[ND]) {
+        wait_loads<vmcnt_imm(ND)>();  // block j0's K has arrived (its V may still be in flight)
+        f32x4 st2[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        const uint32_t kn0 = koff(jn, 0), kn1 = koff(jn, 1);
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-            f32x4 a = {0.f, 0.f, 0.f, 0.f};
+        for (int st = 0; st < NS; st++) {
 #pragma unroll
-            for (int st = 0; st < NS; st++) a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][st], qf[st], a, 0, 0, 0);
-            st2[tt] = a;
+            for (int tt = 0; tt < 2; tt++) {
+                st2[tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[tt][st], qf[st], st2[tt], 0, 0, 0);
+                kfn[tt][st] = __builtin_bit_cast(f16x8, buf_b128(rk, tt ? kn1 : kn0, (uint32_t)st * 2048u));
+            }
         }
+#pragma unroll
+        for (int i = 0; i < 2 * NS; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
+        }
+        pin();
         float sv[8];
         float tmax = -INFINITY;
         // a block before every query of the workgroup (and, with several sequences, inside the
@@ -278,15 +290,23 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
         l_run = l_run * alpha + wave_sum16(psum);
         m_run = m_new;
         // O^T += V^T P^T
+        wait_loads<vmcnt_imm(2 * NS)>();  // block j0's V has arrived (block jn's K may still be in flight)
+        const uint32_t vn = voff(jn);
 #pragma unroll
         for (int dt = 0; dt < ND; dt++) {
             f32x4 a = acc[dt];
             a[0] *= alpha, a[1] *= alpha, a[2] *= alpha, a[3] *= alpha;
             a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], ph, a, 0, 0, 0);
             acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[dt], pl, a, 0, 0, 0);
+            vfn[dt] = __builtin_bit_cast(f16x8, buf_b128(rv, vn, (uint32_t)dt * 1024u));
         }
+#pragma unroll
+        for (int i = 0; i < ND; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
+        }
+        pin();
     };
-    constexpr int LOADS = 2 * NS + ND;  // vector-memory loads per block
     f16x8 kA[2][NS], vA[ND], kB[2][NS], vB[ND];
     // Q^T fragments: lane (query fq, group fg) holds Q[fq][32s + 8fg .. +8], pre-scaled by 1/sqrt(hd)
     // and rounded to f16 as the reference does.  The 4 waves prepare them together: wave w takes
@@ -332,7 +352,18 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     }
     __builtin_amdgcn_sched_barrier(0);
     int j = next_block(kbeg + wv * KB);
-    load(j, kA, vA);
+    {
+        // the first block's K, then V (the order process() waits in)
+        const uint32_t k0 = koff(j, 0), k1 = koff(j, 1), v0 = voff(j);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int st = 0; st < NS; st++)
+                kA[tt][st] = __builtin_bit_cast(f16x8, buf_b128(rk, tt ? k1 : k0, (uint32_t)st * 2048u));
+#pragma unroll
+        for (int dt = 0; dt < ND; dt++) vA[dt] = __builtin_bit_cast(f16x8, buf_b128(rv, v0, (uint32_t)dt * 1024u));
+        pin();
+    }
     {
         f16x8 q8[2];
         if constexpr (QRD == 0) {
@@ -378,15 +409,11 @@ __global__ __launch_bounds__(256) void k_attn(const f16* __restrict__ Q, const f
     for (int st = 0; st < NS; st++) qf[st] = *reinterpret_cast<const f16x8*>(&Qs[fq][st * 32 + fg * 8]);
     while (j < kend) {
         int jn = next_block(j + 4 * KB);
-        load(jn, kB, vB);
-        wait_loads<vmcnt_imm(LOADS)>();  // A's loads (and all before them) have arrived
-        process(j, kA, vA);
+        process(j, kA, vA, jn, kB, vB);
         j = jn;
         if (j >= kend) break;
         jn = next_block(j + 4 * KB);
-        load(jn, kA, vA);
-        wait_loads<vmcnt_imm(LOADS)>();
-        process(j, kB, vB);
+        process(j, kB, vB, jn, kA, vA);
         j = jn;
     }
     // merge the 4 waves: acc[dt][r] is O[query fq][dim 16dt + 4fg + r]
