@@ -170,7 +170,7 @@ constexpr int PREP_T = 512;  // k_gdn_prep threads: 8 waves
 template <bool CONV>
 // Kernel arguments: the pointers and ints first, the structs last (the first 16 dwords are preloaded
 // into SGPRs, up to the first struct; the prologue needs the tables and big before anything else).
-__global__ __launch_bounds__(PREP_T) void k_gdn_prep(const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu,
+__global__ __attribute__((amdgpu_flat_work_group_size(PREP_T, PREP_T), amdgpu_waves_per_eu(4))) void k_gdn_prep(const uint32_t* __restrict__ chunkt, const uint32_t* __restrict__ lu,
                                                   const f16* __restrict__ big, const float* __restrict__ qkvc,
                                                   const float* __restrict__ negA, const float* __restrict__ dtb, int L,
                                                   GdnShape sh, GdnWs ws, ConvIn cv) {
@@ -187,7 +187,11 @@ __global__ __launch_bounds__(PREP_T) void k_gdn_prep(const uint32_t* __restrict_
     __shared__ __attribute__((aligned(16))) uint8_t RR[R1B + 2 * CH * RP * 2];
     uint8_t* const R1 = RR;
     uint8_t* const R2 = RR + R1B;
-    __shared__ __attribute__((aligned(16))) float Ts[CH * FP];
+    // T (the T side's) lives in R2: the T side stores no Q rows there, and the q side, which does,
+    // has no T (its Qk staging takes the same place).  99 KB of LDS would fit one workgroup per CU;
+    // 81.8 KB fits two (with at most 128 VGPRs), so a long input's chunks run in half the rounds.
+    static_assert((size_t)CH * FP * 4 <= (size_t)2 * CH * RP * 2, "T fits R2");
+    float* const Ts = reinterpret_cast<float*>(R2);
     __shared__ float Xs[4][16][17];
     __shared__ float Nb[6][16][17];  // the off-diagonal 16 x 16 blocks of A, (p, r) at p (p - 1) / 2 + r
     __shared__ __attribute__((aligned(16))) float beta[CH], G[CH], eG[CH], eL[CH], rkv[CH];
