@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+import threading
 import os
 from dataclasses import dataclass
 
@@ -121,15 +122,23 @@ def lib():
     return _lib
 
 
+_tls = threading.local()
+
+
 def _call(fn, *args):
-    buf = C.create_string_buffer(1024)
-    rc = fn(*args, buf, len(buf))
+    # one error buffer per thread, reused (a call's message is read before the thread's next call)
+    buf = getattr(_tls, "err", None)
+    if buf is None:
+        buf = _tls.err = C.create_string_buffer(1024)
+    rc = fn(*args, buf, 1024)
     if rc != 0:
         raise EngineError(buf.value.decode(errors="replace"))
 
 
 def _ptr(a):
-    return None if a is None else a.ctypes.data_as(C.c_void_p)
+    # the address as an int: the c_void_p argument types take it as it is (data_as builds a
+    # ctypes object per call)
+    return None if a is None else a.ctypes.data
 
 
 class Snapshot:

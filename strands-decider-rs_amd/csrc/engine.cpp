@@ -236,8 +236,10 @@ void Engine::load(const sd_config* c, const sd_tensor* ts, size_t nt, const char
     SD_HIP(hipGetDeviceProperties(&prop, dev));
     adapter = std::string(prop.name) + " (" + prop.gcnArchName + ", HIP)";
     SD_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
-    SD_HIP(hipEventCreate(&ev0));
-    SD_HIP(hipEventCreate(&ev1));
+    // timing only (the stream is synchronized before any result is read): no system-scope fence,
+    // whose cache write-back and invalidation would be part of what the events time
+    SD_HIP(hipEventCreateWithFlags(&ev0, hipEventDisableSystemFence));
+    SD_HIP(hipEventCreateWithFlags(&ev1, hipEventDisableSystemFence));
 
     // Shards: one device buffer each, streamed from the file through a pinned staging buffer.
     const size_t chunk = size_t(64) << 20;
