@@ -766,6 +766,27 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only, 
         } else {
             const AttnShape as{cfg.hq, cfg.hk, cfg.hd, cfg.rd, W.qkv.N, SD_CONTEXT};
             const float* rp = rope;
+            if (cache_end && W.qkv.tiled && W.qkv.N == 2 * cfg.hq * cfg.hd + 2 * cfg.hk * cfg.hd && !gemv_rows(W.qkv, sr)) {
+                // Only the cache rows are needed: K and V, the last 2 hk hd output columns (in the
+                // tiled layout a column range starts n0 K / 32 blocks in), then qk_prep over a view
+                // with no q heads.  The GEMM runs the full qkv GEMM's configuration, whose sums per
+                // output element do not depend on N: the cache rows are those a forward reading rows
+                // writes, bit for bit.
+                const int n0 = 2 * cfg.hq * cfg.hd;
+                Mat kv = W.qkv;
+                kv.q += (size_t)n0 * kv.K / 8;
+                kv.s += (size_t)n0 * (kv.K / 32);
+                kv.N -= n0;
+                const int cf = gemm_w4_plan(L, W.qkv.N, W.qkv.K, false, false, 0).cfg;
+                steps.push_back({"qkv", [=](hipStream_t s) {
+                    gemm_w4(P.h, kv.q, kv.s, P.big, nullptr, L, kv.N, kv.K, false, 1, s, cf, true);
+                }});
+                const AttnShape akv{0, cfg.hk, cfg.hd, cfg.rd, kv.N, SD_CONTEXT};
+                steps.push_back({"qk_prep", [=](hipStream_t s) {
+                    qk_prep(P.big, akv, W.q_norm, W.k_norm, rp, L, luv, sg, nullptr, W.kc, W.vc, s);
+                }});
+                break;
+            }
             mm(steps, "qkv", P.h, W.qkv, P.big, L, sr);
             // rotary_dim 64: each attention workgroup normalizes and rotates its own queries, and
             // qk_prep writes only the K and V cache rows (which other workgroups read)

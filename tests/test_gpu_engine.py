@@ -122,14 +122,16 @@ def test_cache_only_forward_leaves_the_same_snapshot(sdamd, synth, tmp_path_fact
     """A forward that reads no hidden row runs only the cache-writing steps of its last layer (qkv and
     qk_prep, or in_proj and the delta rule): its snapshot continues exactly as that of a forward of
     the same tokens that reads rows (the steps writing the cache are the same kernels on the same
-    inputs), for a last layer of either kind."""
+    inputs; an attention layer's K/V-only GEMM runs the full qkv GEMM's configuration on fewer
+    columns), for a last layer of either kind, at state lengths on the short-input and the prefill
+    GEMM plans."""
     cfg = dict(synth.CONFIG_TINY)
     if last == "linear_attention":
         cfg["layer_types"] = (["full_attention"] + ["linear_attention"] * 3) * 2
     path = synth.write_model(str(tmp_path_factory.mktemp("co")), cfg, vocab=4096, seed=3)
     eng, head, _ = sdamd.load_decider(path)
     try:
-        for n_state in (90, 150):
+        for n_state in (90, 150, 300, 700):
             state, q = ids_for(60 + n_state, n_state), ids_for(61, 37)
             rows = [2, 11, 36]
             bare = eng.forward(state, [], keep=True).snapshot
