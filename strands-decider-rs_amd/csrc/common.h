@@ -202,21 +202,9 @@ void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float*
 // state is written to `state` only for a single sequence (sg.seq null).  nseq = sequence grid size.
 // hist (nullable) is updated from big at the end (the reference's hist_update; single sequence
 // only), its old rows from the prefix's history.
-// A one-forward ask_all's branch tokens (the rows past the state's S): their causal conv + SiLU
-// into out ([L][C] f32, as conv_silu writes it), computed by extra workgroups of the state's scan
-// launch, on the CUs its chains leave idle.  A branch row's conv reads the rows before it in its
-// own sequence, then the state's last rows, then zeros (the state starts from a cleared history).
-struct BranchConv {
-    const float* w = nullptr;        // [C][4] taps; null: no branch conv
-    const uint32_t* lu = nullptr;    // lu[4]: the forward's chunk count (the state's, then the branches')
-    const uint32_t* chunkt = nullptr, *rowt = nullptr;  // the forward's chunk and row tables
-    int S = 0, L = 0;                // the state's rows; the forward's rows
-    float* out = nullptr;
-    int planes = 0;                  // grid z planes of (head, 8 branch chunks)
-};
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
               const Segs& sg, int nseq, hipStream_t st, size_t state_off = 0, f16* hist = nullptr,
-              const f16* big = nullptr, size_t hist_off = 0, const BranchConv& bcv = BranchConv{});
+              const f16* big = nullptr, size_t hist_off = 0);
 // The same recurrence token by token (the reference's own order), for short inputs: every
 // sequence starts from the prefix state as gdn_scan; with one sequence the final state is written
 // to `state` and hist (nullable) updated afterwards, as gdn_prep + gdn_scan do.

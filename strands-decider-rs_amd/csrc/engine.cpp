@@ -701,33 +701,22 @@ Plan& Engine::plan(int L, int nseq, bool short_seqs, int tree, bool cache_only, 
             if (tree) {
                 // The state (rows 0 .. tree - 1) in chunks, as its own forward without a prefix: a
                 // fresh state, the cleared history, its final state and history into the live arena.
-                // Then the branches token by token from that state (lu has has_cache set and names
-                // no snapshot), through the sequence tables shifted past the state, their conv
-                // already in qkvc.
+                // The branches in chunks too, each from that state: their chunks' prep runs in the
+                // state's prep launch (a branch's rows before its first are the state's last ones),
+                // then, after the state's scan, a scan of the branches as sequences starting from the
+                // live state (lu has has_cache set and names no snapshot), through the sequence
+                // tables shifted past the state; it keeps no state.
                 const int S = tree, nbr = nseq - 1;
-                const ConvIn cs{W.conv, W.hist, nullptr, W.hist_off};
+                const ConvIn cin{W.conv, W.hist, sg.row, W.hist_off};
                 steps.push_back({"gdn", [=](hipStream_t s) {
-                    gdn_prep(nullptr, P.big, gs, W.negA, W.dtb, S, P.gdn, cs, Segs{}, (S + 63) / 64, nullptr, s);
+                    gdn_prep(nullptr, P.big, gs, W.negA, W.dtb, L, P.gdn, cin, sg, nch, luv, s);
                 }});
-                // the branches' conv runs in the scan's launch, beside the state's chunk chains (at most
-                // (L - S + 63) / 64 + nbr chunks, 8 per z plane of the grid), into qkvc for the recurrence
-                BranchConv bcv;
-                bcv.w = W.conv;
-                bcv.lu = luv;
-                bcv.chunkt = sg.chunk;
-                bcv.rowt = sg.row;
-                bcv.S = S;
-                bcv.L = L;
-                bcv.out = P.qkvc;
-                bcv.planes = ((L - S + 63) / 64 + nbr + 7) / 8;
                 steps.push_back({"gdn", [=](hipStream_t s) {
-                    gdn_scan(gs, S, P.gdn, W.state, nullptr, 0, P.of, Segs{}, 0, s, W.state_off, W.hist, P.big, W.hist_off,
-                             bcv);
+                    gdn_scan(gs, S, P.gdn, W.state, nullptr, 0, P.of, Segs{}, 0, s, W.state_off, W.hist, P.big, W.hist_off);
                 }});
                 const Segs sgb{sg.row, sg.chunk, sg.seq + 1};
                 steps.push_back({"gdn", [=](hipStream_t s) {
-                    gdn_recur(P.qkvc, P.big, gs, W.negA, W.dtb, L, W.state, luv, 0, P.of, nullptr, sgb, nbr, s,
-                              W.state_off, W.hist_off);
+                    gdn_scan(gs, L, P.gdn, W.state, luv, 0, P.of, sgb, nbr, s, W.state_off, nullptr, P.big, W.hist_off);
                 }});
             } else if (recur && nseq) {
                 // several sequences update no history: the recurrence computes the conv itself

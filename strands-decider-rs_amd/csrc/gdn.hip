@@ -208,9 +208,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(PREP_T, PREP_T), amdgpu_wa
     // the pointers are selected first, with `big` standing in for a null table (values then unused).
     const uint32_t* lp = lu ? lu : reinterpret_cast<const uint32_t*>(big);
     const uint32_t* cp = chunkt ? chunkt + c : lp;
-    const uint32_t lu_chunks = lp[4], ce = *cp;
+    const uint32_t lu_chunks = lp[4], ce = *cp, lu_tree = lp[6];
     const uint8_t* const lu_pre = *reinterpret_cast<const uint8_t* const*>(lp + 8);
-    SGPR_BATCH("s"(lu_chunks), "s"(ce), "s"(lu_pre), "s"(H), "s"(sh.C), "s"(sh.stride), "s"(sh.a_off), "s"(sh.b_off),
+    SGPR_BATCH("s"(lu_chunks), "s"(ce), "s"(lu_tree), "s"(lu_pre), "s"(H), "s"(sh.C), "s"(sh.stride), "s"(sh.a_off), "s"(sh.b_off),
                "s"(sh.z_off), "s"(ws.wf), "s"(ws.qgf), "s"(ws.qkf), "s"(ws.kgf), "s"(ws.u), "s"(ws.gl), "s"(cv.w),
                "s"(cv.hist), "s"(cv.rowt), "s"(cv.hist_off), "s"(negA), "s"(dtb));
     if (chunkt && c >= (int)lu_chunks) return;  // the grid is sized for the most chunks L can split into
@@ -270,7 +270,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(PREP_T, PREP_T), amdgpu_wa
     } else {
         // conv view: wave w takes tokens 8w..8w+7, lane l 4 channels of matrix l / 32 (q side: q, k;
         // T side: k, v); the 11 rows a wave's tokens read are the same for all its lanes, so whether
-        // a row comes from big or from the history is wave-uniform.
+        // a row comes from big or from the history is wave-uniform.  A sequence's rows before its
+        // first come from the history, except for a branch of a tree forward (lu[6] = the state's
+        // length, a sequence starting past row 0), whose rows before its first are the state's last
+        // rows (and before the state's first, the cleared history).
         const int wvu = __builtin_amdgcn_readfirstlane(wv);
         const int mat = lane >> 5, c4 = (lane & 31) * 4;
         const int m0 = qside ? (mat == 0 ? h * DK : sh.H * DK + h * DK) : (mat == 0 ? sh.H * DK + h * DK : 2 * sh.H * DK + h * DV);
@@ -278,19 +281,24 @@ __global__ __attribute__((amdgpu_flat_work_group_size(PREP_T, PREP_T), amdgpu_wa
         float4 wk[4];  // taps of the 4 channels
 #pragma unroll
         for (int u = 0; u < 4; u++) wk[u] = *reinterpret_cast<const float4*>(cv.w + 4 * (cg + u));
-        const uint32_t rt0 = cv.rowt ? cv.rowt[t0] : (uint32_t)t0;  // index in the sequence | start row << 16
-        const int i0 = (int)(rt0 & 0xFFFFu), s0 = (int)(rt0 >> 16);
+        // the start row of the chunk's sequence (row table: index in the sequence | start row << 16)
+        const int s0 = (int)((cv.rowt ? cv.rowt[t0] : (uint32_t)t0) >> 16);
+        const int i0 = t0 - s0;  // the chunk's first row in its sequence
+        const int tS = lu ? (int)lu_tree : 0;
+        const bool branch = tS > 0 && s0 > 0;
         const uint8_t* pre = lu ? lu_pre : nullptr;
         const f16* hsrc = pre ? reinterpret_cast<const f16*>(pre + cv.hist_off) : cv.hist;
-        const Rsrc rb = make_rsrc(big, (uint32_t)(s0 + i0 + Lc) * (uint32_t)sh.stride * 2u);
+        const Rsrc rb = make_rsrc(big, (uint32_t)(t0 + Lc) * (uint32_t)sh.stride * 2u);
         const Rsrc rh = make_rsrc(hsrc, 3u * (uint32_t)C * 2u);
         f16x4 xr[11];
 #pragma unroll
         for (int m = 0; m < 11; m++) {
-            const int ii = min(i0 + 8 * wvu - 3 + m, i0 + Lc - 1);  // sequence index of the row (uniform)
-            const bool fromh = ii < 0;
+            const int ii = min(i0 + 8 * wvu - 3 + m, i0 + Lc - 1);  // row of the sequence (uniform)
+            // big's row, or (negative) history row rr + 3
+            const int rr = ii >= 0 ? s0 + ii : branch ? tS + ii : ii;
+            const bool fromh = rr < 0;
             const Rsrc r = fromh ? rh : rb;
-            const uint32_t so = fromh ? (uint32_t)((ii + 3) * C) * 2u : (uint32_t)(s0 + ii) * (uint32_t)sh.stride * 2u;
+            const uint32_t so = fromh ? (uint32_t)((rr + 3) * C) * 2u : (uint32_t)rr * (uint32_t)sh.stride * 2u;
             xr[m] = __builtin_bit_cast(f16x4, buf_b64(r, (uint32_t)cg * 2u, so));
         }
         float* X = reinterpret_cast<float*>(RR);
@@ -951,64 +959,13 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     }
 }
 
-// The branch conv of a one-forward ask_all (BranchConv): workgroup (head, y) of z plane z takes
-// branch chunk 8 (z - z0) + y; thread (group g, half) 4 channels of the head's q, k or v for 32 of
-// the chunk's rows, from a window of 35 rows (3 before), as the token-by-token kernel's conv
-// (sum over the 4 taps in order, f32, then SiLU).
-__device__ __forceinline__ void branch_conv(const BranchConv& bc, const f16* __restrict__ big, const GdnShape& sh,
-                                            int chunk) {
-    constexpr int DK = 128, DV = 128;
-    const int h = blockIdx.x, H = sh.H, C = sh.C, tid = threadIdx.x;
-    const int sch = (bc.S + 63) / 64;  // the state's chunks come first in the table
-    if (sch + chunk >= (int)bc.lu[4] || tid >= 192) return;
-    const uint32_t ce = bc.chunkt[sch + chunk];
-    const int t0 = (int)(ce & 0xFFFFu), Lc = (int)(ce >> 16);
-    const int s0 = (int)(bc.rowt[t0] >> 16);  // the branch's first row
-    const int i0 = t0 - s0;                   // the chunk's first row in its branch
-    const int g = tid % 96, r0 = 32 * (tid / 96);
-    const int ch = g < 32 ? h * DK + 4 * g : g < 64 ? H * DK + h * DK + 4 * (g - 32) : 2 * H * DK + h * DV + 4 * (g - 64);
-    float4 wk[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) wk[u] = *reinterpret_cast<const float4*>(bc.w + 4 * (ch + u));
-    // window row m is the branch's row i0 + r0 - 3 + m (clamped to the chunk: rows past it feed no
-    // output); before the branch, the state's row S + index; before the state, zero (an
-    // out-of-range offset)
-    const Rsrc rb = make_rsrc(big, (uint32_t)bc.L * (uint32_t)sh.stride * 2u);
-    f16x4 xr[35];
-#pragma unroll
-    for (int m = 0; m < 35; m++) {
-        const int ii = i0 + min(r0 - 3 + m, Lc - 1);
-        const int row = ii >= 0 ? s0 + ii : bc.S + ii;
-        const uint32_t off = row >= 0 ? (uint32_t)row * (uint32_t)sh.stride * 2u + (uint32_t)ch * 2u : OOB;
-        xr[m] = __builtin_bit_cast(f16x4, buf_b64(rb, off, 0u));
-    }
-#pragma unroll
-    for (int t = 0; t < 32; t++) {
-        float o4[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float kj[4] = {wk[u].x, wk[u].y, wk[u].z, wk[u].w};
-            float a = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; j++) a += kj[j] * (float)xr[t + j][u];
-            o4[u] = silu(a);
-        }
-        if (r0 + t < Lc) *reinterpret_cast<float4*>(bc.out + (size_t)(t0 + r0 + t) * C + ch) = float4{o4[0], o4[1], o4[2], o4[3]};
-    }
-}
-
 // Sequential over chunks for one head and 16 value columns; wave w owns rows 16w..16w+15 of the
-// chunk (and state rows 32w..32w+31 for the update).  z planes from bcz on (when bcv.w is set) are
-// the branch conv's.
+// chunk (and state rows 32w..32w+31 for the update).
 __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ lu, const uint32_t* __restrict__ seqt,
                                                   const uint32_t* __restrict__ chunkt, float* __restrict__ state,
                                                   int L, int load_default, size_t state_off, float* __restrict__ o,
                                                   const f16* __restrict__ big, f16* hist, size_t hist_off, GdnShape sh,
-                                                  GdnWs ws, BranchConv bcv, int bcz) {
-    if (bcv.w && (int)blockIdx.z >= bcz) {
-        branch_conv(bcv, big, sh, ((int)blockIdx.z - bcz) * (int)gridDim.y + (int)blockIdx.y);
-        return;
-    }
+                                                  GdnWs ws) {
     constexpr int DK = 128, DV = 128;
     constexpr int SP = DK + 4, VP = CH + 4;
     __shared__ __attribute__((aligned(16))) float St[DVS * SP];  // S^T: [column][k]
@@ -1361,18 +1318,13 @@ void gdn_prep(const float* qkvc, const f16* big, const GdnShape& s, const float*
 }
 
 void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uint32_t* lu, int load_default, float* o,
-              const Segs& sg, int nseq, hipStream_t st, size_t state_off, f16* hist, const f16* big, size_t hist_off,
-              const BranchConv& bcv) {
+              const Segs& sg, int nseq, hipStream_t st, size_t state_off, f16* hist, const f16* big, size_t hist_off) {
     SD_CHECK(s.DK == 128 && s.DV == 128, "gated delta net: only 128-wide key/value heads are supported");
     SD_CHECK(!sg.seq || (lu && sg.chunk), "gdn_scan: several sequences need lu and the chunk table");
     SD_CHECK(!hist || (!sg.seq && big), "gdn_scan: the history update needs one sequence and big");
-    SD_CHECK(!bcv.w || (big && bcv.lu && bcv.chunkt && bcv.rowt && bcv.out && bcv.planes > 0 && s.C % 4 == 0 &&
-                        s.stride % 4 == 0 && bcv.L >= bcv.S),
-             "gdn_scan: the branch conv needs big, lu, the chunk and row tables and an output");
     if (!sg.seq) nseq = 1;
-    const int planes = bcv.w ? bcv.planes : 0;
-    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq + planes), dim3(256), 0, st, lu, sg.seq, sg.chunk, state, L,
-                       load_default, state_off, o, big, hist, hist_off, s, ws, bcv, nseq);
+    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(256), 0, st, lu, sg.seq, sg.chunk, state, L,
+                       load_default, state_off, o, big, hist, hist_off, s, ws);
     launched("gdn_scan");
 }
 
