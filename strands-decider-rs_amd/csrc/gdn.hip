@@ -22,7 +22,8 @@
 //    The workgroups also perform the reference's hist_update, each on a slice of the channels (the
 //    conv already consumed the old history).
 //  * gdn_scan: one workgroup per (head, 16 value columns), sequential over chunks; the state slice
-//    lives in LDS (transposed, the B operand of every product).
+//    lives in LDS (transposed, the B operand of every product); 4 waves carry the recurrence and 4
+//    compute the output beside them.
 #include "common.h"
 #include "device.h"
 
@@ -959,18 +960,29 @@ __global__ __launch_bounds__(RT) void k_gdn_recur(const uint32_t* __restrict__ l
     }
 }
 
-// Sequential over chunks for one head and 16 value columns; wave w owns rows 16w..16w+15 of the
-// chunk (and state rows 32w..32w+31 for the update).
-__global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ lu, const uint32_t* __restrict__ seqt,
-                                                  const uint32_t* __restrict__ chunkt, float* __restrict__ state,
-                                                  int L, int load_default, size_t state_off, float* __restrict__ o,
-                                                  const f16* __restrict__ big, f16* hist, size_t hist_off, GdnShape sh,
-                                                  GdnWs ws) {
+// Sequential over chunks for one head and 16 value columns, in two roles of 4 waves each.  The
+// state role (waves 0-3) carries the recurrence: V' = U - W S, then S <- e^(G_last) S + KgT V';
+// the output role (waves 4-7) computes o = Qg S + Qk V' from the same chunk's S and V'.  Both
+// pass the same two LDS barriers per chunk: after the first, S of chunk c is in St[p]; between
+// the two, the state role forms W S and V' while the output role forms Qg S; after the second, the
+// state role forms KgT V' and writes chunk c + 1's S into St[p ^ 1] while the output role adds
+// Qk V' and stores o.  So o's products and operand loads run beside the recurrence instead of on
+// its chain, and each role's CU time goes to its own half of the chunk's operands.  Wave w of a
+// role owns rows 16w..16w+15 of the chunk (and the state role state rows 32w..32w+31 for the
+// update).  The arithmetic of every product is the single-role form's: the same split operands,
+// the same three-chain MFMA sums in the same order.
+constexpr int SCAN_T = 512;
+__global__ __launch_bounds__(SCAN_T) void k_gdn_scan(const uint32_t* __restrict__ lu, const uint32_t* __restrict__ seqt,
+                                                     const uint32_t* __restrict__ chunkt, float* __restrict__ state,
+                                                     int L, int load_default, size_t state_off, float* __restrict__ o,
+                                                     const f16* __restrict__ big, f16* hist, size_t hist_off, GdnShape sh,
+                                                     GdnWs ws) {
     constexpr int DK = 128, DV = 128;
     constexpr int SP = DK + 4, VP = CH + 4;
-    __shared__ __attribute__((aligned(16))) float St[DVS * SP];  // S^T: [column][k]
-    __shared__ __attribute__((aligned(16))) float Vt[DVS * VP];  // V'^T: [column][token]
-    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __shared__ __attribute__((aligned(16))) float St[2][DVS * SP];  // S^T: [column][k], chunk parity p
+    __shared__ __attribute__((aligned(16))) float Vt[DVS * VP];     // V'^T: [column][token]
+    const int tid = threadIdx.x, lane = tid & 63, w8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int role = w8 >> 2, wv = w8 & 3;
     const int fr = lane & 15, fg = lane >> 4;
     const int h = blockIdx.x, sl = blockIdx.y, H = sh.H, q = blockIdx.z;
     // The lu fields and the sequence's chunk range in one batch of scalar loads, issued before any
@@ -991,18 +1003,18 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
         // The slice through a buffer resource, every load issued before the first LDS store (a load
         // under a branch, or a flat one, would be waited for before the next is issued); a fresh
         // state gets an empty resource, whose loads return 0 without touching memory.
-        static_assert(DK * DVS % 256 == 0, "whole passes of the workgroup");
+        static_assert(DK * DVS % SCAN_T == 0, "whole passes of the workgroup");
         const Rsrc rs = make_rsrc(S0, load ? (uint32_t)(DK * DV * 4) : 0u);
-        float sv[DK * DVS / 256];
+        float sv[DK * DVS / SCAN_T];
 #pragma unroll
-        for (int i = 0; i < DK * DVS / 256; i++) {
-            const int e = tid + 256 * i, k = e / DVS, cc = e % DVS;
+        for (int i = 0; i < DK * DVS / SCAN_T; i++) {
+            const int e = tid + SCAN_T * i, k = e / DVS, cc = e % DVS;
             sv[i] = __builtin_bit_cast(float, buf_b32(rs, (uint32_t)((k * DV + c0 + cc) * 4), 0u));
         }
 #pragma unroll
-        for (int i = 0; i < DK * DVS / 256; i++) {
-            const int e = tid + 256 * i, k = e / DVS, cc = e % DVS;
-            St[cc * SP + k] = sv[i];
+        for (int i = 0; i < DK * DVS / SCAN_T; i++) {
+            const int e = tid + SCAN_T * i, k = e / DVS, cc = e % DVS;
+            St[0][cc * SP + k] = sv[i];
         }
     }
     // the reference's hist_update (src/kernels.rs:173-190): the last 3 rows of (the prefix's history
@@ -1022,19 +1034,20 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
     }
     const int cfirst = seqt ? (int)(se & 0xFFFFu) : 0;
     const int cend = seqt ? cfirst + (int)(se >> 16) : (L + CH - 1) / CH;
-    // A chunk's operands (prep's output, not written here) are loaded ahead of their use: W, Qg and
-    // U of chunk c + 1 into a second register set when chunk c starts, its Qk, Kg and e^(G_last)
-    // once chunk c has used its own, so the load latency overlaps a chunk's MFMA work instead of
-    // following it.  Vector memory operations retire in issue order (vmcnt), so chunk c's o stores
-    // are issued after those loads: a wait for the loads never waits for the stores to be acked.
-    // e^(G_last) is a vector load too, so no scalar load is outstanding at an LDS barrier.
-    struct WQ {
-        f16x8 wh[4], wl[4], qh[4], ql[4];
+    // A chunk's operands (prep's output, not written here) are loaded ahead of their use, each by
+    // the role that uses it: W (state) and Qg (output) of chunk c + 1 into a second register set
+    // during chunk c's first half, U of chunk c + 1 at chunk c's start; Kg and e^(G_last) (state)
+    // and Qk (output) once chunk c has used its own.  Vector memory operations retire in issue
+    // order (vmcnt), so the output role's o stores are issued after its loads: a wait for the loads
+    // never waits for the stores to be acked.  e^(G_last) is a vector load too, so no scalar load is
+    // outstanding at an LDS barrier.
+    struct WS {  // state role
+        f16x8 wh[4], wl[4];
         float ur[4];
     };
-    WQ set0, set1;
-    f16x8 kh[2][2], kl[2][2], qkh[2], qkl[2];
-    float gl = 0.f;
+    struct QS {  // output role
+        f16x8 qh[4], ql[4];
+    };
     // The workspace is one allocation (W | Qg | Qk | Kg | U | e^G_last regions): every operand load
     // is a buffer load of it with this lane's fixed offset in a VGPR and the region, slot and
     // fragment offsets in SGPRs, so no per-load address arithmetic runs on the VALU.
@@ -1045,100 +1058,25 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
                    o_kg = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.kgf) - wsb),
                    o_u = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.u) - wsb),
                    o_gl = (uint32_t)(reinterpret_cast<const uint8_t*>(ws.gl) - wsb);
-    const uint32_t vfrag = (uint32_t)lane * 16u;                              // fragment layout
+    const uint32_t vfrag = (uint32_t)lane * 16u;             // fragment layout
     const uint32_t vu = (uint32_t)((fg * 4 * DV + fr) * 4);  // U rows fg*4 + r, column fr
     // Every chunk issues the same loads with no branch around any of them: a chunk past the last
     // one gets out-of-range offsets (zeros, no memory access).  The compiler then counts exactly
     // which loads a wait must cover; a load under a branch leaves it unsure and it waits for more.
+    auto slot_of = [&](int c) { return (uint32_t)((c < cend ? c : cfirst) * H + h); };
     auto frag = [&](uint32_t region, int KS, int rt, int s, f16x8& hi, f16x8& lo, uint32_t vf) {
         const uint32_t so = region + (uint32_t)((rt * KS + s) * 2) * 1024u;
         hi = __builtin_bit_cast(f16x8, buf_b128(rws, vf, so));
         lo = __builtin_bit_cast(f16x8, buf_b128(rws, vf, so + 1024u));
     };
-    // W and Qg of chunk c, k step s (4 loads), and U of chunk c (4 loads): issued a few at a time
-    // between the MFMAs of the chunk before (a burst of all of them stalled the wave's issue for
-    // about 1.8 k cycles at the CU's 64 bytes per clock)
-    auto load_wq_step = [&](WQ& d, int c, int s) {
-        const bool in = c < cend;
-        const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vf = in ? vfrag : OOB;
-        frag(slot * (uint32_t)(WF_H * 2), 4, wv, s, d.wh[s], d.wl[s], vf);
-        frag(o_qg + slot * (uint32_t)(QGF_H * 2), 4, wv, s, d.qh[s], d.ql[s], vf);
+    // S^T slice of k step s for this lane (column fr, k = 32 s + 8 fg ..), from St[p]
+    auto s_slice = [&](int p, int s, float* v8) {
+        const float* spp = &St[p][fr * SP + s * 32 + fg * 8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v8[u] = spp[u];
     };
-    auto load_u = [&](WQ& d, int c) {
-        const bool in = c < cend;
-        const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vuu = in ? vu : OOB;
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            d.ur[r] = __builtin_bit_cast(
-                float, buf_b32(rws, vuu, o_u + slot * (uint32_t)(U_F * 4) + (uint32_t)(((wv * 16 + r) * DV + c0) * 4)));
-    };
-    auto load_wq = [&](WQ& d, int c) {
-#pragma unroll
-        for (int s = 0; s < 4; s++) load_wq_step(d, c, s);
-        load_u(d, c);
-    };
-    // Qk and e^(G_last) of chunk c (part 0), or its Kg row tile 2 wv + part - 1 (parts 1, 2): each
-    // issued once the chunk before has used that register set, between its MFMAs
-    auto load_qk = [&](int c, int part) {
-        const bool in = c < cend;
-        const uint32_t slot = (uint32_t)((in ? c : cfirst) * H + h), vf = in ? vfrag : OOB;
-        if (part == 0) {
-#pragma unroll
-            for (int s = 0; s < 2; s++) frag(o_qk + slot * (uint32_t)(QKF_H * 2), 2, wv, s, qkh[s], qkl[s], vf);
-            gl = __builtin_bit_cast(float, buf_b32(rws, in ? 0u : OOB, o_gl + slot * 4u));
-        } else {
-            const int q2 = part - 1;
-#pragma unroll
-            for (int s = 0; s < 2; s++)
-                frag(o_kg + slot * (uint32_t)(KGF_H * 2), 2, wv * 2 + q2, s, kh[q2][s], kl[q2][s], vf);
-        }
-    };
-    // o rows t0 + wv*16 + fg*4 + r (r < 4), column h*DV + c0 + fr; rows past the chunk get an
-    // out-of-range offset and are not written
-    const Rsrc ro = make_rsrc(o, (uint32_t)L * sh.H * DV * 4);
-    const uint32_t vo = (uint32_t)((fg * 4 * sh.H * DV + fr) * 4);
-    auto chunk = [&](int c, const WQ& cur, WQ& nxt) {
-        load_u(nxt, c + 1);
-        const int t0 = chunkt ? (int)(chunkt[c] & 0xFFFFu) : c * CH;
-        const int Lc = chunkt ? (int)(chunkt[c] >> 16) : min(CH, L - c * CH);
-        lds_barrier();  // St holds this chunk's starting state; Vt is free
-        // the three terms of each split product accumulate separately (six independent MFMA
-        // chains of 4 instead of two of 12) and are added at the end
-        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-        f32x4 av[3] = {z4, z4, z4}, ao[3] = {z4, z4, z4};
-        // k step s: its S slice (read from LDS during step s - 1), then the next chunk's W and Qg
-        // loads of step s, each step a scheduling region of its own so that those loads are issued
-        // in four groups
-        float sn[8];
-        {
-            const float* sp = &St[fr * SP + fg * 8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) sn[u] = sp[u];
-        }
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            float s8[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) s8[u] = sn[u];
-            if (s < 3) {
-                const float* sp = &St[fr * SP + (s + 1) * 32 + fg * 8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) sn[u] = sp[u];
-            }
-            load_wq_step(nxt, c + 1, s);
-            f16x8 sh8, sl8;
-            split8(s8, sh8, sl8);
-            mma3s(cur.wh[s], cur.wl[s], sh8, sl8, av);
-            mma3s(cur.qh[s], cur.ql[s], sh8, sl8, ao);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // rows wv * 16 + fg * 4 .. + 3 of column fr: one 16-byte store (conflict-free at this pitch)
-        *reinterpret_cast<float4*>(&Vt[fr * VP + wv * 16 + fg * 4]) =
-            float4{cur.ur[0] - (av[0][0] + av[1][0] + av[2][0]), cur.ur[1] - (av[0][1] + av[1][1] + av[2][1]),
-                   cur.ur[2] - (av[0][2] + av[1][2] + av[2][2]), cur.ur[3] - (av[0][3] + av[1][3] + av[2][3])};
-        lds_barrier();
-        // V'^T fragments (B operand), used by Qk V' and by the state update
-        f16x8 vh[2], vl[2];
+    // V'^T fragments (B operand) of the chunk, both k steps
+    auto v_frags = [&](f16x8 (&vh)[2], f16x8 (&vl)[2]) {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             float v8[8];
@@ -1147,22 +1085,138 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
             for (int u = 0; u < 8; u++) v8[u] = vp[u];
             split8(v8, vh[s], vl[s]);
         }
+    };
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    int c = cfirst;
+    if (role == 0) {
+        // ---- state role: V' = U - W S; S <- e^(G_last) S + KgT V'
+        WS set0, set1;
+        f16x8 kh[2][2], kl[2][2];
+        float gl = 0.f;
+        auto load_w_step = [&](WS& d, int cc, int s) {
+            const uint32_t vf = cc < cend ? vfrag : OOB;
+            frag(slot_of(cc) * (uint32_t)(WF_H * 2), 4, wv, s, d.wh[s], d.wl[s], vf);
+        };
+        auto load_u = [&](WS& d, int cc) {
+            const uint32_t vuu = cc < cend ? vu : OOB, slot = slot_of(cc);
 #pragma unroll
-        for (int s = 0; s < 2; s++) mma3s(qkh[s], qkl[s], vh[s], vl[s], ao);
-        const float g_c = gl;
-        load_qk(c + 1, 0);  // Qk and gl are consumed
-        __builtin_amdgcn_sched_barrier(0);
-        // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
-        f32x4 as[2][3];
+            for (int r = 0; r < 4; r++)
+                d.ur[r] = __builtin_bit_cast(
+                    float, buf_b32(rws, vuu, o_u + slot * (uint32_t)(U_F * 4) + (uint32_t)(((wv * 16 + r) * DV + c0) * 4)));
+        };
+        auto load_gl = [&](int cc) { gl = __builtin_bit_cast(float, buf_b32(rws, cc < cend ? 0u : OOB, o_gl + slot_of(cc) * 4u)); };
+        auto load_kg = [&](int cc, int q2) {
+            const uint32_t vf = cc < cend ? vfrag : OOB, slot = slot_of(cc);
 #pragma unroll
-        for (int q2 = 0; q2 < 2; q2++) {
-            as[q2][0] = as[q2][1] = as[q2][2] = z4;
+            for (int s = 0; s < 2; s++)
+                frag(o_kg + slot * (uint32_t)(KGF_H * 2), 2, wv * 2 + q2, s, kh[q2][s], kl[q2][s], vf);
+        };
+        auto chunk = [&](int cc, int p, const WS& cur, WS& nxt) {
+            load_u(nxt, cc + 1);
+            lds_barrier();  // St[p] holds this chunk's starting state; Vt is free
+            f32x4 av[3] = {z4, z4, z4};
+            // k step s: its S slice (read from LDS during step s - 1), then the next chunk's W loads
+            // of step s, each step a scheduling region of its own so that those loads are issued
+            // in four groups
+            float sn[8];
+            s_slice(p, 0, sn);
 #pragma unroll
-            for (int s = 0; s < 2; s++) mma3s(kh[q2][s], kl[q2][s], vh[s], vl[s], as[q2]);
-            load_qk(c + 1, 1 + q2);  // Kg row tile q2 is consumed
-            __builtin_amdgcn_sched_barrier(0);
+            for (int s = 0; s < 4; s++) {
+                float s8[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) s8[u] = sn[u];
+                if (s < 3) s_slice(p, s + 1, sn);
+                load_w_step(nxt, cc + 1, s);
+                f16x8 sh8, sl8;
+                split8(s8, sh8, sl8);
+                mma3s(cur.wh[s], cur.wl[s], sh8, sl8, av);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            // rows wv * 16 + fg * 4 .. + 3 of column fr: one 16-byte store (conflict-free at this pitch)
+            *reinterpret_cast<float4*>(&Vt[fr * VP + wv * 16 + fg * 4]) =
+                float4{cur.ur[0] - (av[0][0] + av[1][0] + av[2][0]), cur.ur[1] - (av[0][1] + av[1][1] + av[2][1]),
+                       cur.ur[2] - (av[0][2] + av[1][2] + av[2][2]), cur.ur[3] - (av[0][3] + av[1][3] + av[2][3])};
+            lds_barrier();  // V' complete
+            f16x8 vh[2], vl[2];
+            v_frags(vh, vl);
+            const float g_c = gl;
+            load_gl(cc + 1);  // e^(G_last) is consumed
+            // S <- e^(G_last) S + KgT V': state row tiles 2w, 2w+1
+            f32x4 as[2][3];
+#pragma unroll
+            for (int q2 = 0; q2 < 2; q2++) {
+                as[q2][0] = as[q2][1] = as[q2][2] = z4;
+#pragma unroll
+                for (int s = 0; s < 2; s++) mma3s(kh[q2][s], kl[q2][s], vh[s], vl[s], as[q2]);
+                load_kg(cc + 1, q2);  // Kg row tile q2 is consumed
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int q2 = 0; q2 < 2; q2++) {
+                // state rows k0 .. k0 + 3 of column fr: one 16-byte read of S_c and one write of S_c+1
+                const int so = fr * SP + (wv * 2 + q2) * 16 + fg * 4;
+                const float4 s4 = *reinterpret_cast<const float4*>(&St[p][so]);
+                *reinterpret_cast<float4*>(&St[p ^ 1][so]) =
+                    float4{g_c * s4.x + (as[q2][0][0] + as[q2][1][0] + as[q2][2][0]),
+                           g_c * s4.y + (as[q2][0][1] + as[q2][1][1] + as[q2][2][1]),
+                           g_c * s4.z + (as[q2][0][2] + as[q2][1][2] + as[q2][2][2]),
+                           g_c * s4.w + (as[q2][0][3] + as[q2][1][3] + as[q2][2][3])};
+            }
+        };
+#pragma unroll
+        for (int s = 0; s < 4; s++) load_w_step(set0, cfirst, s);
+        load_u(set0, cfirst);
+        load_gl(cfirst);
+        load_kg(cfirst, 0);
+        load_kg(cfirst, 1);
+        for (; c + 1 < cend; c += 2) {  // no branch inside the loop body
+            chunk(c, 0, set0, set1);
+            chunk(c + 1, 1, set1, set0);
         }
-        {
+        if (c < cend) chunk(c, 0, set0, set1);
+    } else {
+        // ---- output role: o = Qg S + Qk V'
+        QS set0, set1;
+        f16x8 qkh[2], qkl[2];
+        auto load_q_step = [&](QS& d, int cc, int s) {
+            const uint32_t vf = cc < cend ? vfrag : OOB;
+            frag(o_qg + slot_of(cc) * (uint32_t)(QGF_H * 2), 4, wv, s, d.qh[s], d.ql[s], vf);
+        };
+        auto load_qk = [&](int cc) {
+            const uint32_t vf = cc < cend ? vfrag : OOB, slot = slot_of(cc);
+#pragma unroll
+            for (int s = 0; s < 2; s++) frag(o_qk + slot * (uint32_t)(QKF_H * 2), 2, wv, s, qkh[s], qkl[s], vf);
+        };
+        // o rows t0 + wv*16 + fg*4 + r (r < 4), column h*DV + c0 + fr; rows past the chunk get an
+        // out-of-range offset and are not written
+        const Rsrc ro = make_rsrc(o, (uint32_t)L * sh.H * DV * 4);
+        const uint32_t vo = (uint32_t)((fg * 4 * sh.H * DV + fr) * 4);
+        auto chunk = [&](int cc, int p, const QS& cur, QS& nxt) {
+            const int t0 = chunkt ? (int)(chunkt[cc] & 0xFFFFu) : cc * CH;
+            const int Lc = chunkt ? (int)(chunkt[cc] >> 16) : min(CH, L - cc * CH);
+            lds_barrier();  // St[p] holds this chunk's starting state
+            f32x4 ao[3] = {z4, z4, z4};
+            float sn[8];
+            s_slice(p, 0, sn);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                float s8[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) s8[u] = sn[u];
+                if (s < 3) s_slice(p, s + 1, sn);
+                load_q_step(nxt, cc + 1, s);
+                f16x8 sh8, sl8;
+                split8(s8, sh8, sl8);
+                mma3s(cur.qh[s], cur.ql[s], sh8, sl8, ao);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            lds_barrier();  // V' complete
+            f16x8 vh[2], vl[2];
+            v_frags(vh, vl);
+#pragma unroll
+            for (int s = 0; s < 2; s++) mma3s(qkh[s], qkl[s], vh[s], vl[s], ao);
+            load_qk(cc + 1);  // Qk is consumed
+            __builtin_amdgcn_sched_barrier(0);
             const uint32_t so = (uint32_t)(((t0 + wv * 16) * sh.H * DV + h * DV + c0) * 4);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
@@ -1170,40 +1224,29 @@ __global__ __launch_bounds__(256) void k_gdn_scan(const uint32_t* __restrict__ l
                 buf_st32(ro, in ? vo + (uint32_t)(r * sh.H * DV * 4) : OOB, so,
                          __builtin_bit_cast(uint32_t, ao[0][r] + ao[1][r] + ao[2][r]));
             }
-        }
+        };
 #pragma unroll
-        for (int q2 = 0; q2 < 2; q2++) {
-            // state rows k0 .. k0 + 3 of column fr: one 16-byte read-modify-write
-            float4* sp4 = reinterpret_cast<float4*>(&St[fr * SP + (wv * 2 + q2) * 16 + fg * 4]);
-            const float4 s4 = *sp4;
-            *sp4 = float4{g_c * s4.x + (as[q2][0][0] + as[q2][1][0] + as[q2][2][0]),
-                          g_c * s4.y + (as[q2][0][1] + as[q2][1][1] + as[q2][2][1]),
-                          g_c * s4.z + (as[q2][0][2] + as[q2][1][2] + as[q2][2][2]),
-                          g_c * s4.w + (as[q2][0][3] + as[q2][1][3] + as[q2][2][3])};
+        for (int s = 0; s < 4; s++) load_q_step(set0, cfirst, s);
+        load_qk(cfirst);
+        for (; c + 1 < cend; c += 2) {
+            chunk(c, 0, set0, set1);
+            chunk(c + 1, 1, set1, set0);
         }
-    };
-    load_wq(set0, cfirst);
-    load_qk(cfirst, 0);
-    load_qk(cfirst, 1);
-    load_qk(cfirst, 2);
-    int c = cfirst;
-    for (; c + 1 < cend; c += 2) {  // no branch inside the loop body
-        chunk(c, set0, set1);
-        chunk(c + 1, set1, set0);
+        if (c < cend) chunk(c, 0, set0, set1);
     }
-    if (c < cend) chunk(c, set0, set1);
     if (seqt) return;  // several sequences: their final states are not kept
     __syncthreads();
-    for (int e = tid; e < DK * DVS; e += 256) {
+    const int pf = (cend - cfirst) & 1;  // the buffer holding the final state
+    for (int e = tid; e < DK * DVS; e += SCAN_T) {
         const int k = e / DVS, cc = e % DVS;
-        Sg[k * DV + c0 + cc] = St[cc * SP + k];
+        Sg[k * DV + c0 + cc] = St[pf][cc * SP + k];
     }
     if (hist) {
         if (hlo + tid < hhi) {
 #pragma unroll
             for (int r = 0; r < 3; r++) hist[(size_t)r * hC + hlo + tid] = hv[r];
         }
-        for (int ch = hlo + tid + 256; ch < hhi; ch += 256) {
+        for (int ch = hlo + tid + SCAN_T; ch < hhi; ch += SCAN_T) {
             f16 v3[3];
 #pragma unroll
             for (int r = 0; r < 3; r++) {
@@ -1323,7 +1366,7 @@ void gdn_scan(const GdnShape& s, int L, const GdnWs& ws, float* state, const uin
     SD_CHECK(!sg.seq || (lu && sg.chunk), "gdn_scan: several sequences need lu and the chunk table");
     SD_CHECK(!hist || (!sg.seq && big), "gdn_scan: the history update needs one sequence and big");
     if (!sg.seq) nseq = 1;
-    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(256), 0, st, lu, sg.seq, sg.chunk, state, L,
+    hipLaunchKernelGGL(k_gdn_scan, dim3(s.H, s.DV / DVS, nseq), dim3(SCAN_T), 0, st, lu, sg.seq, sg.chunk, state, L,
                        load_default, state_off, o, big, hist, hist_off, s, ws);
     launched("gdn_scan");
 }
